@@ -1,0 +1,121 @@
+/*
+ * pkm_hip.h — C ABI of the MI355X (gfx950) product-key-memory lookup library
+ * (libpkm_hip.so).
+ *
+ * Every entry point:
+ *   - takes borrowed device pointers and plain sizes (no framework types);
+ *   - writes only into caller-provided outputs / workspace (no allocation);
+ *   - enqueues its kernels on `stream` (a hipStream_t passed as void*, NULL =
+ *     the null stream) and returns without synchronising;
+ *   - returns PKM_OK (0) or a nonzero pkm_status_t; the message of the last
+ *     failure on the calling thread is returned by pkm_last_error_string().
+ *
+ * Index tensors are int64 (torch.long), row-major [bags, bag_size].
+ * Indices outside [0, num_rows) do not fault: they read nothing, contribute
+ * zero to outputs and get a zero per-sample-weight gradient.
+ * pkm_count_invalid_indices() reports how many there are.
+ */
+#ifndef PKM_HIP_H_
+#define PKM_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes (tables, gradients, per-sample weights). */
+enum pkm_dtype_t {
+  PKM_DTYPE_NONE = -1, /* pointer is NULL: unweighted bag (all weights 1) */
+  PKM_DTYPE_F32 = 0,
+  PKM_DTYPE_BF16 = 1,
+  PKM_DTYPE_F16 = 2
+};
+
+enum pkm_status_t {
+  PKM_OK = 0,
+  PKM_ERR_INVALID_ARGUMENT = 1, /* bad shape, dtype, null pointer, overflow */
+  PKM_ERR_UNSUPPORTED = 2,      /* valid request this build has no kernel for */
+  PKM_ERR_WORKSPACE = 3,        /* workspace smaller than the size query returned */
+  PKM_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
+};
+
+/* Library version, (major << 16) | minor. */
+int pkm_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* pkm_last_error_string(void);
+
+/*
+ * Weighted embedding bag, forward (mode "sum").
+ *   out[b, :] = sum_{j < bag_size} psw[b, j] * weight[indices[b, j], :]
+ * Accumulates in float32 in j order and rounds once to weight's dtype.
+ * psw may be NULL (psw_dtype PKM_DTYPE_NONE): all weights are 1.
+ * out: [bags, dim] in weight_dtype.
+ *
+ * Replaces embedding_bag_triton / embedding_bag_k
+ *   (pkm/xformer_embeddingbag.py:97-138, fwpkm/xformer_embeddingbag_legacy.py:33-74)
+ * and the index_select+sum forward of _XEmbeddingBagFn
+ *   (fwpkm/xformer_embeddingbag_grad_wrapper.py:98-103).
+ */
+int pkm_eb_fwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+               const int64_t* indices, const void* psw, int psw_dtype,
+               int64_t bags, int64_t bag_size, void* out, void* stream);
+
+/* Workspace bytes pkm_eb_bwd needs for these sizes. */
+size_t pkm_eb_bwd_workspace_size(int64_t num_rows, int64_t dim, int64_t bags, int64_t bag_size);
+
+/*
+ * Weighted embedding bag, backward. Deterministic (no float atomics; the
+ * float32 sums run in a fixed order independent of the launch).
+ *   grad_weight[r, :] = sum_{(b,j): indices[b,j] == r} psw[b, j] * grad_out[b, :]
+ *       dense [num_rows, dim] in weight_dtype; untouched rows are written as 0.
+ *   grad_psw[b, j]    = <weight[indices[b, j], :], grad_out[b, :]>   (float32 dot)
+ *       [bags, bag_size] in psw_dtype; not written when psw is NULL.
+ * grad_out: [bags, dim] in grad_dtype.
+ * workspace: device buffer of at least pkm_eb_bwd_workspace_size() bytes.
+ *
+ * Replaces embedding_bag_bw_rev_indices
+ *   (pkm/xformer_embeddingbag.py:331-386, fwpkm/xformer_embeddingbag_legacy.py:170-227),
+ * i.e. count_per_embedding_k + argsort/cumsum + map_embeddings_and_outputs_k
+ * + aggregate_gradient_for_embedding_k (pkm/xformer_embeddingbag.py:261-328),
+ * and the CPU fallback _embedding_bag_bw_native (legacy:147-167).
+ */
+int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+               const int64_t* indices, const void* psw, int psw_dtype,
+               const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
+               void* grad_weight, void* grad_psw,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Double backward of the embedding bag: the VJP of
+ *   grad_weight = EBbwd(indices, a, grad_out)
+ * with respect to grad_out and a, given gbar = dLoss/d(grad_weight):
+ *   d_grad_out[b, :] = sum_j a[b, j] * gbar[indices[b, j], :]     [bags, dim], grad_dtype
+ *   d_a[b, j]        = <gbar[indices[b, j], :], grad_out[b, :]>   [bags, bag_size], a_dtype
+ * a may be NULL (unweighted): then d_a is not written.
+ * gbar: [num_rows, dim] in gbar_dtype.
+ *
+ * Replaces EmbeddingBagBW.backward (fwpkm/xformer_embeddingbag_grad_wrapper.py:42-74).
+ */
+int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int gbar_dtype,
+                const int64_t* indices, const void* a, int a_dtype,
+                const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
+                void* d_grad_out, void* d_a, void* stream);
+
+/*
+ * Counts indices outside [0, num_rows) into *count_out (a device int64),
+ * which the call overwrites. No counterpart in the reference (its Triton
+ * kernels do no bounds check; its CPU path raises from F.embedding_bag,
+ * pkm/xformer_embeddingbag.py:436-437): it lets a caller turn bad indices
+ * into an error.
+ */
+int pkm_count_invalid_indices(const int64_t* indices, int64_t n, int64_t num_rows,
+                              int64_t* count_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PKM_HIP_H_ */

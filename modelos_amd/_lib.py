@@ -1,0 +1,122 @@
+"""ctypes binding of libpkm_hip.so, the C ABI declared in include/pkm_hip.h.
+
+The library is loaded after torch, so it binds to the HIP runtime torch has
+already loaded (one runtime per process: streams and device pointers are
+shared). A missing library is an error, never a silent fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_char_p, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (must be imported before the HIP library is opened)
+
+LIB_PATH = Path(os.environ.get("PKM_HIP_LIB", Path(__file__).with_name("libpkm_hip.so")))
+
+# name -> (restype, argtypes); mirrors include/pkm_hip.h
+SIGNATURES = {
+    "pkm_version": (c_int, []),
+    "pkm_last_error_string": (c_char_p, []),
+    "pkm_eb_fwd": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p],
+    ),
+    "pkm_eb_bwd_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int64]),
+    "pkm_eb_bwd": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64, c_int,  # weight, num_rows, dim, weight_dtype
+            c_void_p, c_void_p, c_int,  # indices, psw, psw_dtype
+            c_void_p, c_int,  # grad_out, grad_dtype
+            c_int64, c_int64,  # bags, bag_size
+            c_void_p, c_void_p,  # grad_weight, grad_psw
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+    "pkm_eb_bwd2": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64, c_int,  # gbar, num_rows, dim, gbar_dtype
+            c_void_p, c_void_p, c_int,  # indices, a, a_dtype
+            c_void_p, c_int,  # grad_out, grad_dtype
+            c_int64, c_int64,  # bags, bag_size
+            c_void_p, c_void_p, c_void_p,  # d_grad_out, d_a, stream
+        ],
+    ),
+    "pkm_count_invalid_indices": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+}
+
+# pkm_dtype_t
+DTYPE_NONE = -1
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+STATUS_NAMES = {
+    1: "invalid argument",
+    2: "unsupported",
+    3: "workspace too small",
+    4: "HIP error",
+}
+
+
+class PkmError(RuntimeError):
+    """A libpkm_hip call returned a nonzero status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        self.fn = fn
+        self.status = status
+        super().__init__(f"{fn} failed ({STATUS_NAMES.get(status, status)}): {message}")
+
+
+class PkmLibraryMissing(RuntimeError):
+    """libpkm_hip.so is not built / not loadable."""
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Opens libpkm_hip.so once and declares every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise PkmLibraryMissing(
+            f"{LIB_PATH} is missing: build it with `python -m modelos_amd.build_lib` "
+            "(the PKM lookup path has no CPU fallback)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Calls an int-status entry point and raises PkmError on failure."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        msg = lib.pkm_last_error_string().decode(errors="replace")
+        raise PkmError(name, status, msg)
+
+
+def dtype_code(t: torch.Tensor | None) -> int:
+    if t is None:
+        return DTYPE_NONE
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype} (float32, bfloat16 and float16 are supported)") from None
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    """Raw hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream

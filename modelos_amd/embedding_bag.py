@@ -1,0 +1,166 @@
+"""Host side of the weighted embedding bag: torch tensors in, HIP kernels run.
+
+Functions here validate shapes/dtypes, allocate outputs with torch's caching
+allocator on the inputs' device, and call libpkm_hip.so on torch's current
+stream (no host synchronisation). They are the building blocks of the
+drop-in autograd functions in modelos_amd.pkm / modelos_amd.fwpkm.
+
+There is no CPU path: CPU tensors raise.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+
+def _require_device(*tensors: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"PKM HIP kernels need ROCm device tensors, got a tensor on {t.device} "
+                "(this implementation has no CPU path)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    assert dev is not None
+    return dev
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the kernels read rows with 16-byte loads)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _check_bag_inputs(indices: torch.Tensor, table: torch.Tensor, psw: Optional[torch.Tensor], fn: str) -> None:
+    if indices.dtype != torch.long:
+        raise TypeError(f"{fn}: indices must be int64 (torch.long), got {indices.dtype}")
+    if indices.dim() != 2:
+        raise ValueError(f"{fn}: indices must be [bags, bag_size], got shape {tuple(indices.shape)}")
+    if table.dim() != 2:
+        raise ValueError(f"{fn}: table must be [num_rows, dim], got shape {tuple(table.shape)}")
+    if psw is not None and psw.shape != indices.shape:
+        raise ValueError(
+            f"{fn}: per_sample_weights shape {tuple(psw.shape)} != indices shape {tuple(indices.shape)}"
+        )
+
+
+def eb_forward(
+    indices: torch.Tensor, weight: torch.Tensor, per_sample_weights: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """out[b, :] = sum_j psw[b, j] * weight[indices[b, j], :], in weight.dtype.
+
+    float32 accumulation in j order (pkm/xformer_embeddingbag.py:97-113).
+    """
+    _check_bag_inputs(indices, weight, per_sample_weights, "eb_forward")
+    dev = _require_device(indices, weight, per_sample_weights)
+    indices = indices.contiguous()
+    weight = _aligned(weight)
+    psw = per_sample_weights.contiguous() if per_sample_weights is not None else None
+    B, L = indices.shape
+    K, D = weight.shape
+    out = torch.empty((B, D), dtype=weight.dtype, device=dev)
+    _lib.call(
+        "pkm_eb_fwd",
+        _lib.ptr(weight), K, D, _lib.dtype_code(weight),
+        _lib.ptr(indices), _lib.ptr(psw), _lib.dtype_code(psw),
+        B, L, _lib.ptr(out), _lib.stream_of(dev),
+    )
+    return out
+
+
+def eb_backward_workspace_bytes(num_rows: int, dim: int, bags: int, bag_size: int) -> int:
+    return int(_lib.load().pkm_eb_bwd_workspace_size(num_rows, dim, bags, bag_size))
+
+
+def eb_backward(
+    indices: torch.Tensor,
+    weight: torch.Tensor,
+    per_sample_weights: Optional[torch.Tensor],
+    grad_output: torch.Tensor,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Deterministic backward: (grad_weight [K, D] dense in weight.dtype,
+    grad_psw [B, L] in psw.dtype or None when psw is None).
+
+    Same outputs as embedding_bag_bw_rev_indices (pkm/xformer_embeddingbag.py:331-386).
+    """
+    _check_bag_inputs(indices, weight, per_sample_weights, "eb_backward")
+    dev = _require_device(indices, weight, per_sample_weights, grad_output)
+    B, L = indices.shape
+    K, D = weight.shape
+    if grad_output.shape != (B, D):
+        raise ValueError(f"eb_backward: grad_output shape {tuple(grad_output.shape)} != {(B, D)}")
+    indices = indices.contiguous()
+    weight = _aligned(weight)
+    psw = per_sample_weights.contiguous() if per_sample_weights is not None else None
+    grad_output = _aligned(grad_output.to(weight.dtype))
+    grad_weight = torch.empty_like(weight, memory_format=torch.contiguous_format)
+    grad_psw = torch.empty_like(psw, memory_format=torch.contiguous_format) if psw is not None else None
+    ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
+    workspace = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    _lib.call(
+        "pkm_eb_bwd",
+        _lib.ptr(weight), K, D, _lib.dtype_code(weight),
+        _lib.ptr(indices), _lib.ptr(psw), _lib.dtype_code(psw),
+        _lib.ptr(grad_output), _lib.dtype_code(grad_output),
+        B, L,
+        _lib.ptr(grad_weight), _lib.ptr(grad_psw),
+        _lib.ptr(workspace), ws_bytes, _lib.stream_of(dev),
+    )
+    return grad_weight, grad_psw
+
+
+def eb_double_backward(
+    indices: torch.Tensor,
+    a: Optional[torch.Tensor],
+    grad_output: torch.Tensor,
+    g_bar: torch.Tensor,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """VJP of grad_weight = EBbwd(indices, a, grad_output) given g_bar = dL/d(grad_weight):
+    (d_grad_output [B, D], d_a [B, L] or None).
+
+    Same outputs as EmbeddingBagBW.backward
+    (fwpkm/xformer_embeddingbag_grad_wrapper.py:42-74).
+    """
+    _check_bag_inputs(indices, g_bar, a, "eb_double_backward")
+    dev = _require_device(indices, a, grad_output, g_bar)
+    B, L = indices.shape
+    K, D = g_bar.shape
+    if grad_output.shape != (B, D):
+        raise ValueError(f"eb_double_backward: grad_output shape {tuple(grad_output.shape)} != {(B, D)}")
+    indices = indices.contiguous()
+    out_dtype = grad_output.dtype
+    g_bar = _aligned(g_bar.to(out_dtype))
+    grad_output = _aligned(grad_output)
+    a = a.contiguous() if a is not None else None
+    d_grad_output = torch.empty((B, D), dtype=out_dtype, device=dev)
+    d_a = torch.empty_like(a, memory_format=torch.contiguous_format) if a is not None else None
+    _lib.call(
+        "pkm_eb_bwd2",
+        _lib.ptr(g_bar), K, D, _lib.dtype_code(g_bar),
+        _lib.ptr(indices), _lib.ptr(a), _lib.dtype_code(a),
+        _lib.ptr(grad_output), _lib.dtype_code(grad_output),
+        B, L,
+        _lib.ptr(d_grad_output), _lib.ptr(d_a), _lib.stream_of(dev),
+    )
+    return d_grad_output, d_a
+
+
+def count_invalid_indices(indices: torch.Tensor, num_rows: int) -> int:
+    """Number of entries outside [0, num_rows) (synchronises)."""
+    dev = _require_device(indices)
+    indices = indices.contiguous()
+    out = torch.empty((1,), dtype=torch.int64, device=dev)
+    _lib.call(
+        "pkm_count_invalid_indices",
+        _lib.ptr(indices), indices.numel(), num_rows, _lib.ptr(out), _lib.stream_of(dev),
+    )
+    return int(out.item())

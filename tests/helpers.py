@@ -1,0 +1,45 @@
+"""Shared input generators and comparison helpers for the tests."""
+from __future__ import annotations
+
+import torch
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def eb_inputs(B, L, K, D, dtype, seed=0, psw=True, psw_dtype=None, softmax=True, with_grad=True, scale=None):
+    """Seeded CPU inputs for an embedding-bag case, drawn in a fixed order:
+    weight, indices, psw, grad."""
+    g = gen(seed)
+    scale = (D**-0.5) if scale is None else scale
+    W = (torch.randn((K, D), generator=g) * scale).to(dtype)
+    idx = torch.randint(0, max(K, 1), (B, L), generator=g, dtype=torch.long)
+    p = None
+    if psw:
+        logits = torch.randn((B, L), generator=g)
+        p = (torch.softmax(logits, -1) if softmax else logits).to(psw_dtype or dtype)
+    grad = torch.randn((B, D), generator=g).to(dtype) if with_grad else None
+    return W, idx, p, grad
+
+
+REL_TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3, torch.float64: 1e-12}
+
+
+def assert_rel_close(actual: torch.Tensor, expected: torch.Tensor, rel: float, what: str = ""):
+    """Element-wise |a - e| <= rel * |e| + rel * max|e|: relative error with an
+    absolute floor at the tensor's scale (sums with cancellation)."""
+    a = actual.detach().to("cpu", torch.float64)
+    e = expected.detach().to("cpu", torch.float64)
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    scale = e.abs().max().item() if e.numel() else 0.0
+    err = (a - e).abs()
+    bound = rel * e.abs() + rel * scale + 1e-30
+    bad = err > bound
+    if bad.any():
+        i = int(bad.reshape(-1).nonzero()[0])
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} / {a.numel()} elements off; first at flat {i}: "
+            f"got {a.reshape(-1)[i].item()!r} expected {e.reshape(-1)[i].item()!r} "
+            f"(max abs err {err.max().item():.3e}, scale {scale:.3e}, rel {rel})"
+        )

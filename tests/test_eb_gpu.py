@@ -1,0 +1,297 @@
+"""Parity of the HIP embedding-bag kernels (through the C ABI) with the oracle.
+
+Small and ragged sizes are compared element-wise with oracle/eb.py on the same
+seeded inputs; the full standalone size (16384 bags x 128 lookups into a
+2^20 x 1024 bf16 table) is checked on sampled bags / rows against the oracle
+plus size-independent properties (column-sum checksum, untouched rows exactly
+zero, bitwise run-to-run determinism). Tolerances: 1e-5 relative (fp32),
+2e-2 (bf16), 2e-3 (fp16), relative to each tensor's scale.
+"""
+import pytest
+import torch
+
+from oracle import eb as ref
+from tests.helpers import REL_TOL, assert_rel_close, eb_inputs
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+# (B, L, K, D): row lengths hit every lane-group shape (LPG 1..64, VPL 1..8),
+# bag sizes around the 64-entry batch, tiny and empty cases.
+SHAPES = [
+    (33, 17, 1000, 1024),
+    (7, 64, 500, 512),
+    (9, 65, 300, 256),
+    (5, 128, 2000, 2048),
+    (3, 3, 50, 4096),
+    (17, 31, 100, 128),
+    (21, 5, 64, 64),
+    (4, 2, 10, 32),
+    (6, 1, 9, 16),
+    (2, 7, 40, 8),
+]
+
+
+def _dev(*ts, device):
+    return [t.to(device) if t is not None else None for t in ts]
+
+
+def _reduce_supported(D, dtype):
+    """The backward / double-backward kernels hold a whole row per lane group:
+    dim / (16 B / element size) must be LPG * VPL with VPL <= 8."""
+    epv = 4 if dtype == torch.float32 else 8
+    return (D // epv) <= 512
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("B,L,K,D", SHAPES)
+def test_forward_parity(B, L, K, D, dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    if dtype == torch.float32 and D == 8:
+        D = 12  # not a multiple of 8 for 16-bit, exercises fp32 LPG=1; 16-bit uses the scalar fallback below
+    W, idx, p, _ = eb_inputs(B, L, K, D, dtype, seed=B * 1000 + L, with_grad=False)
+    out = eb.eb_forward(*_dev(idx, W, p, device=device))
+    assert out.dtype == dtype and out.shape == (B, D)
+    assert_rel_close(out, ref.eb_forward(idx, W, p), REL_TOL[dtype], f"forward {dtype} {B,L,K,D}")
+
+
+@pytest.mark.parametrize("D", [12, 20, 6])
+def test_forward_scalar_fallback(D, device):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, _ = eb_inputs(5, 9, 30, D, torch.bfloat16, seed=D, with_grad=False)
+    out = eb.eb_forward(*_dev(idx, W, p, device=device))
+    assert_rel_close(out, ref.eb_forward(idx, W, p), 2e-2, "scalar fallback")
+
+
+def test_forward_unweighted_mixed_dtypes_and_invalid(device):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, _ = eb_inputs(19, 40, 700, 1024, torch.bfloat16, seed=5, psw_dtype=torch.float32, with_grad=False)
+    idx[0, 0] = -5
+    idx[3, 39] = 700
+    idx[7, 12] = 1 << 40
+    dW, didx, dp = _dev(W, idx, p, device=device)
+    assert_rel_close(eb.eb_forward(didx, dW, dp), ref.eb_forward(idx, W, p), 2e-2, "fp32 psw on bf16 table")
+    assert_rel_close(eb.eb_forward(didx, dW, None), ref.eb_forward(idx, W, None), 2e-2, "unweighted")
+    assert eb.count_invalid_indices(didx, 700) == 3
+
+
+def test_forward_empty(device):
+    from modelos_amd import embedding_bag as eb
+
+    W = torch.randn(10, 64, device=device)
+    assert eb.eb_forward(torch.zeros(0, 3, dtype=torch.long, device=device), W, None).shape == (0, 64)
+    out = eb.eb_forward(torch.zeros(4, 0, dtype=torch.long, device=device), W, torch.zeros(4, 0, device=device))
+    assert (out == 0).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("B,L,K,D", SHAPES)
+def test_backward_parity(B, L, K, D, dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, g = eb_inputs(B, L, K, D, dtype, seed=B * 7 + L)
+    if not _reduce_supported(D, dtype):
+        from modelos_amd._lib import PkmError
+
+        with pytest.raises(PkmError, match="not supported"):
+            eb.eb_backward(*_dev(idx, W, p, g, device=device))
+        return
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    assert gW.dtype == dtype and gp.dtype == p.dtype
+    assert_rel_close(gW, eW, REL_TOL[dtype], f"grad_weight {dtype} {B,L,K,D}")
+    assert_rel_close(gp, ep, REL_TOL[dtype], f"grad_psw {dtype} {B,L,K,D}")
+
+
+def _hot_indices(B, L, K, seed):
+    """Indices with heavy rows: row 3 takes ~1/3 of all lookups, rows 4 and 5
+    ~600 each (adjacent heavy rows share chunks), the rest uniform, plus a few
+    out-of-range entries."""
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, K, (B, L), generator=g)
+    u = torch.rand((B, L), generator=g)
+    idx[u < 1 / 3] = 3
+    flat = idx.view(-1)
+    pos = torch.randperm(B * L, generator=g)
+    flat[pos[:600]] = 4
+    flat[pos[600:1200]] = 5
+    flat[pos[1200:1205]] = -1
+    return idx
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("D", [1024, 64])
+def test_backward_heavy_rows(D, dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K = 97, 64, 5000
+    W, _, p, g = eb_inputs(B, L, K, D, dtype, seed=21)
+    idx = _hot_indices(B, L, K, seed=22)
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    assert_rel_close(gW, eW, REL_TOL[dtype], "heavy grad_weight")
+    assert_rel_close(gp, ep, REL_TOL[dtype], "heavy grad_psw")
+    assert (gp.cpu()[idx < 0] == 0).all()
+
+
+def test_backward_unweighted_and_deterministic(device):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, _, g = eb_inputs(64, 48, 3000, 512, torch.float32, seed=23, psw=False)
+    idx = _hot_indices(64, 48, 3000, seed=24)
+    dW, didx, dg = _dev(W, idx, g, device=device)
+    gW1, gp1 = eb.eb_backward(didx, dW, None, dg)
+    gW2, _ = eb.eb_backward(didx, dW, None, dg)
+    assert gp1 is None
+    eW, _ = ref.eb_backward(idx, W, None, g)
+    assert_rel_close(gW1, eW, 1e-5, "unweighted grad_weight")
+    assert torch.equal(gW1, gW2), "backward is not bitwise deterministic"
+
+
+def test_backward_empty_bags_zero_grad(device):
+    from modelos_amd import embedding_bag as eb
+
+    W = torch.randn(100, 256, device=device)
+    gW, gp = eb.eb_backward(
+        torch.zeros(0, 4, dtype=torch.long, device=device), W, torch.zeros(0, 4, device=device),
+        torch.zeros(0, 256, device=device),
+    )
+    assert (gW == 0).all() and gp.shape == (0, 4)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("B,L,K,D", SHAPES)
+@pytest.mark.parametrize("with_a", [True, False])
+def test_double_backward_parity(B, L, K, D, dtype, with_a, device):
+    from modelos_amd import embedding_bag as eb
+
+    _, idx, a, g = eb_inputs(B, L, K, D, dtype, seed=B + L + D, psw=with_a)
+    gbar = torch.randn((K, D), generator=torch.Generator().manual_seed(3)).to(dtype)
+    if not _reduce_supported(D, dtype):
+        from modelos_amd._lib import PkmError
+
+        with pytest.raises(PkmError, match="not supported"):
+            eb.eb_double_backward(*_dev(idx, a, g, gbar, device=device))
+        return
+    d_g, d_a = eb.eb_double_backward(*_dev(idx, a, g, gbar, device=device))
+    e_g, e_a = ref.eb_double_backward(idx, a, g, gbar)
+    assert_rel_close(d_g, e_g, REL_TOL[dtype], f"d_grad_output {dtype}")
+    if with_a:
+        assert_rel_close(d_a, e_a, REL_TOL[dtype], f"d_a {dtype}")
+    else:
+        assert d_a is None
+
+
+def test_autograd_dropin_pkm(device):
+    from modelos_amd.pkm.xformer_embeddingbag import xformers_embedding_bag
+
+    W, idx, p, g = eb_inputs(40, 32, 900, 1024, torch.bfloat16, seed=31)
+    dW, didx, dp, dg = _dev(W, idx, p, g, device=device)
+    dW.requires_grad_(True)
+    dp.requires_grad_(True)
+    out = xformers_embedding_bag(didx, dW, dp)
+    out.backward(dg)
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    assert_rel_close(out, ref.eb_forward(idx, W, p), 2e-2, "pkm drop-in forward")
+    assert_rel_close(dW.grad, eW, 2e-2, "pkm drop-in weight grad")
+    assert_rel_close(dp.grad, ep, 2e-2, "pkm drop-in psw grad")
+
+
+def test_autograd_dropin_fwpkm_double_backward(device):
+    """Outer gradient through one inner SGD step on the table, the fwpkm pattern
+    (fwpkm/fwpkm.py:308-365): compared with the same computation done by
+    autograd on the oracle's differentiable forward in float64."""
+    from modelos_amd.fwpkm.xformer_embeddingbag_grad_wrapper import xformers_embedding_bag
+
+    B, L, K, D = 24, 16, 300, 256
+    W, idx, a, _ = eb_inputs(B, L, K, D, torch.float32, seed=41)
+    tgt = torch.randn((B, D), generator=torch.Generator().manual_seed(42))
+    idx2 = torch.randint(0, K, (B, L), generator=torch.Generator().manual_seed(43))
+    a2 = torch.softmax(torch.randn((B, L), generator=torch.Generator().manual_seed(44)), -1)
+
+    def run(eb_fn, W0, a0, dev_or_none):
+        hyp = eb_fn(idx if dev_or_none is None else idx.to(dev_or_none), W0, a0)
+        t = tgt if dev_or_none is None else tgt.to(dev_or_none)
+        inner = 0.5 * ((hyp - t) ** 2).mean()
+        (gV,) = torch.autograd.grad(inner, W0, create_graph=True)
+        W1 = W0 - 0.1 * gV * (B * D)
+        i2 = idx2 if dev_or_none is None else idx2.to(dev_or_none)
+        p2 = a2 if dev_or_none is None else a2.to(dev_or_none)
+        out = eb_fn(i2, W1, p2)
+        return (out**2).sum()
+
+    Wd = W.to(device).requires_grad_(True)
+    ad = a.to(device).requires_grad_(True)
+    loss = run(lambda i, w, p: xformers_embedding_bag(i, w, p), Wd, ad, device)
+    gW, ga = torch.autograd.grad(loss, (Wd, ad))
+
+    We = W.double().requires_grad_(True)
+    ae = a.double().requires_grad_(True)
+    loss_e = run(lambda i, w, p: ref.eb_forward(i, w, p.double()), We, ae, None)
+    eW, ea = torch.autograd.grad(loss_e, (We, ae))
+    assert_rel_close(loss.detach(), loss_e.detach(), 1e-5, "outer loss")
+    assert_rel_close(gW, eW, 1e-5, "outer grad wrt table")
+    assert_rel_close(ga, ea, 1e-5, "outer grad wrt per-sample weights")
+
+
+# ---------------------------------------------------------------------------
+# Full standalone size: 16384 bags x 128 lookups, 2^20 x 1024 bf16 table
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def full_case(device):
+    B, L, K, D = 16384, 128, 1 << 20, 1024
+    g = torch.Generator(device=device).manual_seed(0)
+    W = (torch.randn((K, D), generator=g, device=device) * 0.03).to(torch.bfloat16)
+    idx = torch.randint(0, K, (B, L), generator=g, device=device)
+    p = torch.softmax(torch.randn((B, L), generator=g, device=device), -1).to(torch.bfloat16)
+    gr = torch.randn((B, D), generator=g, device=device).to(torch.bfloat16)
+    return W, idx, p, gr
+
+
+def test_full_size_forward_sampled(full_case):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, _ = full_case
+    out = eb.eb_forward(idx, W, p)
+    sel = torch.randperm(idx.shape[0], generator=torch.Generator().manual_seed(1))[:256].to(idx.device)
+    si, sp = idx[sel].cpu(), p[sel].cpu()
+    rows = W[si.reshape(-1)].cpu()
+    local = torch.arange(si.numel()).view(si.shape)
+    expect = ref.eb_forward(local, rows, sp)
+    assert_rel_close(out[sel], expect, 2e-2, "full-size forward (sampled bags)")
+
+
+def test_full_size_backward_sampled_and_properties(full_case):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, gr = full_case
+    K, D = W.shape
+    gW, gp = eb.eb_backward(idx, W, p, gr)
+    gW2, gp2 = eb.eb_backward(idx, W, p, gr)
+    assert torch.equal(gW, gW2) and torch.equal(gp, gp2), "not bitwise deterministic"
+    # untouched rows exactly zero
+    touched = torch.zeros(K, dtype=torch.bool, device=idx.device)
+    touched[idx.reshape(-1)] = True
+    assert (gW[~touched] == 0).all()
+    # checksum over all rows: sum_r gW[r] = sum_b (sum_j p[b,j]) g[b]
+    colsum = gW.float().sum(0)
+    expect = (p.float().sum(1, keepdim=True) * gr.float()).sum(0)
+    assert_rel_close(colsum, expect, 2e-2, "column-sum checksum")
+    # sampled rows against the oracle
+    rows = torch.randperm(K, generator=torch.Generator().manual_seed(2))[:512].to(idx.device)
+    flat = idx.reshape(-1)
+    hit = torch.isin(flat, rows)
+    pos = hit.nonzero().squeeze(1)
+    b = pos // idx.shape[1]
+    occ_rows = flat[pos]
+    contrib = p.reshape(-1)[pos].float()[:, None] * gr[b].float()
+    exp_rows = torch.zeros(K, D, device=idx.device).index_add_(0, occ_rows, contrib)[rows]
+    assert_rel_close(gW[rows], exp_rows, 2e-2, "sampled grad_weight rows")
+    # sampled psw gradients
+    sb = torch.randperm(idx.shape[0], generator=torch.Generator().manual_seed(3))[:128].to(idx.device)
+    e_gp = (W[idx[sb]].float() * gr[sb].float()[:, None, :]).sum(-1)
+    assert_rel_close(gp[sb], e_gp, 2e-2, "sampled grad_psw")
