@@ -116,6 +116,11 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument(
+        "--copy-probe-mib", type=int, default=0,
+        help="run one plain elementwise copy (torch.neg, fp32) of this many MiB after warm-up; "
+        "its FETCH_SIZE / WRITE_SIZE calibrate the HBM counters of the kernels",
+    )
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -151,6 +156,13 @@ def main():
         step()
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
+    if args.copy_probe_mib:
+        src = torch.ones(args.copy_probe_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]

@@ -10,22 +10,27 @@
 // reading W and writing gW for all K rows.
 //
 // This design (own):
-//  1. count:   rows histogram with integer atomics (exact), indices outside
-//              [0, K) go to a sentinel row K;
-//  2. scan:    exclusive scan of the counts -> row offsets (K+2 entries);
-//  3. sort:    stable LSD radix sort (8-bit digits) of (row, flat position)
-//              pairs. The input is in position order and every pass is stable,
-//              so each row's occurrences end up in increasing position order:
-//              the float32 sums below have a fixed order, independent of the
-//              launch (no float atomics anywhere);
-//  4. heavy:   rows with more than T occurrences are cut into fixed chunks of
+//  1. sort:    stable LSD radix sort of (row, flat position) pairs, 2 passes of
+//              10/11-bit digits for up to 2^22 rows. Lookups whose index is out
+//              of [0, K) are dropped here (their psw-gradient is written as 0).
+//              The input is in position order and every pass is stable, so each
+//              row's occurrences end up in increasing position order: the
+//              float32 sums below have a fixed order, independent of the launch
+//              (no float atomics anywhere).
+//  2. offsets: row r starts at the first sorted position whose key is >= r:
+//              run starts scatter their position, a suffix-min scan fills the
+//              untouched rows.
+//  3. heavy:   rows with more than T occurrences are cut into fixed chunks of
 //              T sorted occurrences; each chunk writes a float32 partial sum
 //              (2 slots per chunk: the row running in from the previous chunk
-//              and the row starting inside this one);
-//  5. rows:    one lane group per row, rows in order: untouched rows get zeros,
-//              light rows are reduced in position order while the group holds
-//              W[r] in registers for the psw-gradient dot products, heavy rows
-//              add their chunk partials in chunk order.
+//              and the row starting inside this one).
+//  4. rows:    a wave owns 64 consecutive rows and walks them in order with the
+//              row offsets and a 64-entry window of occurrence metadata
+//              (position, bag, weight) in lane registers: one memory round trip
+//              per touched row. Untouched rows get zeros, light rows are reduced
+//              in position order while the wave holds W[r] in registers for the
+//              psw-gradient dot products, heavy rows add their chunk partials in
+//              chunk order.
 // HBM traffic: W is read once per distinct row, gW written once per row, the
 // upstream gradient g (B x D, tens of MB) is re-read per occurrence from
 // L2 / Infinity Cache.
@@ -43,15 +48,6 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, int64_t n)
     p[i] = v;
 }
 
-__device__ __forceinline__ uint32_t row_key(int64_t r, int64_t K) {
-  return (r >= 0 && r < K) ? (uint32_t)r : (uint32_t)K;
-}
-
-__global__ void count_rows_kernel(const int64_t* __restrict__ idx, int64_t N, int64_t K, uint32_t* __restrict__ counts) {
-  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < N; p += (int64_t)gridDim.x * blockDim.x)
-    atomicAdd(&counts[row_key(idx[p], K)], 1u);
-}
-
 __global__ void count_invalid_kernel(const int64_t* __restrict__ idx, int64_t n, int64_t K,
                                      unsigned long long* __restrict__ out) {
   uint32_t c = 0;
@@ -67,14 +63,15 @@ __global__ void count_invalid_kernel(const int64_t* __restrict__ idx, int64_t n,
 __global__ void zero_i64_kernel(unsigned long long* p) { *p = 0; }
 
 // ---------------------------------------------------------------------------
-// Device-wide exclusive scan of uint32 (tiles of 4096 = 256 threads x 16).
+// Device-wide scans of uint32 (tiles of 4096 = 256 threads x 16):
+//   exclusive prefix sum (radix digit offsets), inclusive suffix min (row offsets).
 // ---------------------------------------------------------------------------
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;
 
-// Exclusive scan of one value per thread across a 256-thread block.
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* total, uint32_t* lds4) {
+// Exclusive prefix sum of one value per thread across a 256-thread block.
+__device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* total, uint32_t* lds4) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   uint32_t x = v;
@@ -97,6 +94,33 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* t
   return pre + x - v;
 }
 
+// Exclusive suffix min across a 256-thread block (threads with a larger index
+// are to the right); *total gets the block min.
+__device__ __forceinline__ uint32_t block_exclusive_suffix_min(uint32_t v, uint32_t* total, uint32_t* lds4) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_down(x, o);
+    if (lane + o < 64) x = x < y ? x : y;
+  }
+  if (lane == 0) lds4[w] = x;
+  __syncthreads();
+  uint32_t right = 0xFFFFFFFFu, tot = 0xFFFFFFFFu;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t t = lds4[i];
+    if (i > w) right = right < t ? right : t;
+    tot = tot < t ? tot : t;
+  }
+  __syncthreads();
+  uint32_t in_wave = __shfl_down(x, 1);
+  if (lane == 63) in_wave = 0xFFFFFFFFu;
+  *total = tot;
+  return in_wave < right ? in_wave : right;
+}
+
 __global__ __launch_bounds__(256) void scan_reduce_kernel(const uint32_t* __restrict__ in, int64_t n,
                                                           uint32_t* __restrict__ parts) {
   __shared__ uint32_t lds4[4];
@@ -108,11 +132,11 @@ __global__ __launch_bounds__(256) void scan_reduce_kernel(const uint32_t* __rest
     s += p < n ? in[p] : 0u;
   }
   uint32_t tot;
-  block_exclusive_scan(s, &tot, lds4);
+  block_exclusive_sum(s, &tot, lds4);
   if (threadIdx.x == 0) parts[blockIdx.x] = tot;
 }
 
-// Single block: exclusive scan of the per-tile sums, in place.
+// Single block: exclusive prefix sum of the per-tile sums, in place.
 __global__ __launch_bounds__(256) void scan_parts_kernel(uint32_t* __restrict__ parts, int64_t nparts) {
   __shared__ uint32_t lds4[4];
   uint32_t carry = 0;
@@ -126,7 +150,7 @@ __global__ __launch_bounds__(256) void scan_parts_kernel(uint32_t* __restrict__ 
       s += v[i];
     }
     uint32_t tot;
-    uint32_t run = carry + block_exclusive_scan(s, &tot, lds4);
+    uint32_t run = carry + block_exclusive_sum(s, &tot, lds4);
 #pragma unroll
     for (int i = 0; i < kScanItems; ++i) {
       if (p0 + i < nparts) parts[p0 + i] = run;
@@ -136,7 +160,7 @@ __global__ __launch_bounds__(256) void scan_parts_kernel(uint32_t* __restrict__ 
   }
 }
 
-// data[i] <- tile prefix + exclusive scan inside the tile; data[n] <- total.
+// data[i] <- tile prefix + exclusive sum inside the tile; data[n] <- total.
 __global__ __launch_bounds__(256) void scan_apply_kernel(uint32_t* __restrict__ data, int64_t n,
                                                          const uint32_t* __restrict__ parts) {
   __shared__ uint32_t lds4[4];
@@ -149,7 +173,7 @@ __global__ __launch_bounds__(256) void scan_apply_kernel(uint32_t* __restrict__ 
     s += v[i];
   }
   uint32_t tot;
-  uint32_t run = parts[blockIdx.x] + block_exclusive_scan(s, &tot, lds4);
+  uint32_t run = parts[blockIdx.x] + block_exclusive_sum(s, &tot, lds4);
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) {
     if (p0 + i < n) data[p0 + i] = run;
@@ -158,62 +182,154 @@ __global__ __launch_bounds__(256) void scan_apply_kernel(uint32_t* __restrict__ 
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) data[n] = parts[blockIdx.x] + tot;
 }
 
+__global__ __launch_bounds__(256) void smin_reduce_kernel(const uint32_t* __restrict__ in, int64_t n,
+                                                          uint32_t* __restrict__ parts) {
+  __shared__ uint32_t lds4[4];
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+  uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    const int64_t p = base + (int64_t)i * kScanThreads + threadIdx.x;
+    const uint32_t x = p < n ? in[p] : 0xFFFFFFFFu;
+    m = m < x ? m : x;
+  }
+  uint32_t tot;
+  block_exclusive_suffix_min(m, &tot, lds4);
+  if (threadIdx.x == 0) parts[blockIdx.x] = tot;
+}
+
+// Single block: exclusive suffix min of the per-tile mins, in place.
+__global__ __launch_bounds__(256) void smin_parts_kernel(uint32_t* __restrict__ parts, int64_t nparts) {
+  __shared__ uint32_t lds4[4];
+  uint32_t carry = 0xFFFFFFFFu;
+  const int64_t nchunks = (nparts + kScanTile - 1) / kScanTile;
+  for (int64_t ch = nchunks - 1; ch >= 0; --ch) {
+    const int64_t p0 = ch * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    uint32_t v[kScanItems];
+    uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+      v[i] = (p0 + i < nparts) ? parts[p0 + i] : 0xFFFFFFFFu;
+      m = m < v[i] ? m : v[i];
+    }
+    uint32_t tot;
+    const uint32_t ex = block_exclusive_suffix_min(m, &tot, lds4);
+    uint32_t run = carry < ex ? carry : ex;
+#pragma unroll
+    for (int i = kScanItems - 1; i >= 0; --i) {
+      if (p0 + i < nparts) parts[p0 + i] = run;
+      run = run < v[i] ? run : v[i];
+    }
+    carry = carry < tot ? carry : tot;
+  }
+}
+
+// data[i] <- min(data[i..n)) using the exclusive suffix mins of the tiles.
+__global__ __launch_bounds__(256) void smin_apply_kernel(uint32_t* __restrict__ data, int64_t n,
+                                                         const uint32_t* __restrict__ parts) {
+  __shared__ uint32_t lds4[4];
+  const int64_t p0 = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+  uint32_t v[kScanItems];
+  uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    v[i] = (p0 + i < n) ? data[p0 + i] : 0xFFFFFFFFu;
+    m = m < v[i] ? m : v[i];
+  }
+  uint32_t tot;
+  const uint32_t ex = block_exclusive_suffix_min(m, &tot, lds4);
+  const uint32_t right = parts[blockIdx.x];
+  uint32_t run = ex < right ? ex : right;
+#pragma unroll
+  for (int i = kScanItems - 1; i >= 0; --i) {
+    run = run < v[i] ? run : v[i];
+    if (p0 + i < n) data[p0 + i] = run;
+  }
+}
+
 // ---------------------------------------------------------------------------
-// Stable LSD radix sort pass, 8-bit digit, tiles of 4096 (4 waves x 16 x 64).
-// Item order inside a tile: wave-major, then round, then lane, so a wave's
-// rounds cover consecutive 64-item runs and ranks stay stable.
+// Stable LSD radix sort pass with BITS-bit digits over tiles of 4096 items
+// (4 waves x 16 rounds x 64 lanes). Item order inside a tile: wave-major,
+// then round, then lane, so ranks stay stable. The first pass reads the int64
+// indices (dropping out-of-range ones); later passes read nvalid items.
 // ---------------------------------------------------------------------------
-constexpr int kRadix = 256;
 constexpr int kRadixItems = 16;
 constexpr int kRadixTile = 256 * kRadixItems;
 
 template <bool FIRST>
+__device__ __forceinline__ bool radix_item(int64_t p, int64_t N, uint32_t nv, const int64_t* __restrict__ idx,
+                                           const uint32_t* __restrict__ keys, int64_t K, uint32_t* k) {
+  if (FIRST) {
+    if (p >= N) return false;
+    const int64_t r = idx[p];
+    *k = (uint32_t)r;
+    return r >= 0 && r < K;
+  }
+  if (p >= (int64_t)nv) return false;
+  *k = keys[p];
+  return true;
+}
+
+template <bool FIRST, int BITS>
 __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restrict__ idx,
-                                                         const uint32_t* __restrict__ keys, int64_t N, int64_t K,
-                                                         int shift, uint32_t* __restrict__ hist, int64_t ntiles) {
-  __shared__ uint32_t h[kRadix];
-  h[threadIdx.x] = 0;
+                                                         const uint32_t* __restrict__ keys, int64_t N,
+                                                         const uint32_t* __restrict__ nvalid, int64_t K, int shift,
+                                                         uint32_t* __restrict__ hist, int64_t ntiles,
+                                                         void* __restrict__ gpsw, int pdt) {
+  constexpr int R = 1 << BITS;
+  __shared__ uint32_t h[R];
+  for (int d = threadIdx.x; d < R; d += 256) h[d] = 0;
   __syncthreads();
+  const uint32_t nv = FIRST ? 0u : *nvalid;
   const int64_t base = (int64_t)blockIdx.x * kRadixTile;
 #pragma unroll 4
   for (int i = 0; i < kRadixItems; ++i) {
     const int64_t p = base + (int64_t)i * 256 + threadIdx.x;
-    if (p < N) {
-      const uint32_t k = FIRST ? row_key(idx[p], K) : keys[p];
-      atomicAdd(&h[(k >> shift) & (kRadix - 1)], 1u);
+    uint32_t k;
+    if (radix_item<FIRST>(p, N, nv, idx, keys, K, &k)) {
+      atomicAdd(&h[(k >> shift) & (R - 1)], 1u);
+    } else if (FIRST && p < N && gpsw != nullptr) {
+      store_scalar(gpsw, pdt, p, 0.f);  // out-of-range index: zero psw-gradient
     }
   }
   __syncthreads();
-  hist[(int64_t)threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+  for (int d = threadIdx.x; d < R; d += 256) hist[(int64_t)d * ntiles + blockIdx.x] = h[d];
 }
 
-template <bool FIRST>
+template <bool FIRST, int BITS>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __restrict__ idx,
                                                             const uint32_t* __restrict__ keys_in,
                                                             const uint32_t* __restrict__ vals_in, int64_t N,
-                                                            int64_t K, int shift, const uint32_t* __restrict__ ofs,
+                                                            const uint32_t* __restrict__ nvalid, int64_t K,
+                                                            int shift, const uint32_t* __restrict__ ofs,
                                                             int64_t ntiles, uint32_t* __restrict__ keys_out,
                                                             uint32_t* __restrict__ vals_out) {
-  __shared__ uint32_t wcnt[4][kRadix];
+  constexpr int R = 1 << BITS;
+  __shared__ uint32_t wcnt[4][R];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
+  for (int d = threadIdx.x; d < R; d += 256) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wcnt[i][threadIdx.x] = 0;
+    for (int i = 0; i < 4; ++i) wcnt[i][d] = 0;
+  }
   __syncthreads();
 
+  const uint32_t nv = FIRST ? 0u : *nvalid;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int64_t base = (int64_t)blockIdx.x * kRadixTile + (int64_t)w * (kRadixItems * 64);
   uint32_t k[kRadixItems], v[kRadixItems], pre[kRadixItems];
+  uint32_t validmask = 0;
 #pragma unroll
   for (int i = 0; i < kRadixItems; ++i) {
     const int64_t p = base + (int64_t)i * 64 + lane;
-    const bool valid = p < N;
-    k[i] = valid ? (FIRST ? row_key(idx[p], K) : keys_in[p]) : 0u;
+    k[i] = 0;
+    const bool valid = radix_item<FIRST>(p, N, nv, idx, keys_in, K, &k[i]);
     v[i] = valid ? (FIRST ? (uint32_t)p : vals_in[p]) : 0u;
-    const uint32_t d = (k[i] >> shift) & (kRadix - 1);
+    validmask |= valid ? (1u << i) : 0u;
+    const uint32_t d = (k[i] >> shift) & (R - 1);
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int bit = 0; bit < 8; ++bit) {
+    for (int bit = 0; bit < BITS; ++bit) {
       const bool on = (d >> bit) & 1u;
       const uint64_t bb = __ballot(on);
       peers &= on ? bb : ~bb;
@@ -224,8 +340,7 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
     pre[i] = old + rank;
   }
   __syncthreads();
-  {
-    const int d = threadIdx.x;
+  for (int d = threadIdx.x; d < R; d += 256) {
     uint32_t run = ofs[(int64_t)d * ntiles + blockIdx.x];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -237,9 +352,8 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kRadixItems; ++i) {
-    const int64_t p = base + (int64_t)i * 64 + lane;
-    if (p < N) {
-      const uint32_t d = (k[i] >> shift) & (kRadix - 1);
+    if (validmask & (1u << i)) {
+      const uint32_t d = (k[i] >> shift) & (R - 1);
       const uint32_t dst = wcnt[w][d] + pre[i];
       keys_out[dst] = k[i];
       vals_out[dst] = v[i];
@@ -247,8 +361,20 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
   }
 }
 
+// offs[key] <- position of each run start of the sorted keys; offs[K] <- nvalid.
+__global__ void run_starts_kernel(const uint32_t* __restrict__ skeys, const uint32_t* __restrict__ nvalid, int64_t N,
+                                  int64_t K, uint32_t* __restrict__ offs) {
+  const uint32_t nv = *nvalid;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N; i += (int64_t)gridDim.x * blockDim.x) {
+    if (i >= (int64_t)nv) break;
+    const uint32_t k = skeys[i];
+    if (i == 0 || skeys[i - 1] != k) offs[k] = (uint32_t)i;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) offs[K] = nv;
+}
+
 // ---------------------------------------------------------------------------
-// Segmented reduction over sorted occurrences.
+// Segmented reduction over sorted occurrences (generic lane groups).
 // ---------------------------------------------------------------------------
 template <int VPL>
 struct BwdUnroll {
@@ -262,7 +388,8 @@ __device__ __forceinline__ void reduce_occurrences(uint32_t i_beg, uint32_t i_en
                                                    const void* __restrict__ psw, int pdt,
                                                    const TW* __restrict__ g, int64_t D, uint32_t L32,
                                                    int64_t col0, int glane, const float* wv, bool want_dot,
-                                                   void* __restrict__ gpsw, float* acc) {
+                                                   void* __restrict__ gpsw, float* acc,
+                                                   float* __restrict__ dsorted = nullptr) {
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   constexpr int U = BwdUnroll<VPL>::U;
@@ -309,7 +436,12 @@ __device__ __forceinline__ void reduce_occurrences(uint32_t i_beg, uint32_t i_en
         }
       }
     }
-    if (want_dot && glane < n) store_scalar(gpsw, pdt, my_p, my_dot);
+    if (want_dot && glane < n) {
+      if (dsorted != nullptr)
+        dsorted[i0 + glane] = my_dot;  // sorted order, scattered by position later
+      else
+        store_scalar(gpsw, pdt, my_p, my_dot);
+    }
   }
 }
 
@@ -320,6 +452,28 @@ __device__ __forceinline__ void load_row_f32(const TW* __restrict__ row, int64_t
   for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(ld16(row + col0 + v * LPG * EPV), f + v * EPV);
 }
 
+// acc += partial sums of a heavy row [beg, end) in chunk order.
+template <int LPG, int VPL, int EPV>
+__device__ __forceinline__ void add_heavy_partials(uint32_t beg, uint32_t end, const float* __restrict__ partials,
+                                                   int64_t D, int64_t col0, float* acc) {
+  constexpr int VSTRIDE = LPG * EPV;
+  const uint32_t c_first = beg / kHeavyT, c_last = (end - 1) / kHeavyT;
+  for (uint32_t c = c_first; c <= c_last; ++c) {
+    const int slot = (c == c_first && beg != c * (uint32_t)kHeavyT) ? 1 : 0;
+    const float* prow = partials + (2 * (int64_t)c + slot) * D + col0;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+#pragma unroll
+      for (int h = 0; h < EPV; h += 4) {
+        float f[4];
+        VecTraits<float>::unpack(ld16(prow + v * VSTRIDE + h), f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[v * EPV + h + e] += f[e];
+      }
+    }
+  }
+}
+
 // Heavy rows: chunk c = sorted occurrences [c*T, (c+1)*T). A row with more
 // than T occurrences always contains the chunk's first or last occurrence.
 template <typename TW, int LPG, int VPL>
@@ -328,9 +482,10 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
                                                            const TW* __restrict__ g, uint32_t L32,
                                                            const uint32_t* __restrict__ offs,
                                                            const uint32_t* __restrict__ skeys,
-                                                           const uint32_t* __restrict__ svals, uint32_t N,
-                                                           int64_t nchunks, float* __restrict__ partials,
-                                                           void* __restrict__ gpsw) {
+                                                           const uint32_t* __restrict__ svals,
+                                                           const uint32_t* __restrict__ nvalid, int64_t nchunks,
+                                                           float* __restrict__ partials, void* __restrict__ gpsw,
+                                                           float* __restrict__ dsorted) {
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   constexpr int GPW = 64 / LPG;
@@ -338,8 +493,10 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
   const int glane = lane & (LPG - 1);
   const int64_t c = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * GPW + (lane / LPG);
   if (c >= nchunks) return;
+  const uint32_t nv = *nvalid;
   const uint32_t i_beg = (uint32_t)(c * kHeavyT);
-  const uint32_t i_end = (uint32_t)((int64_t)i_beg + kHeavyT < (int64_t)N ? i_beg + kHeavyT : N);
+  if (i_beg >= nv) return;
+  const uint32_t i_end = (uint32_t)((int64_t)i_beg + kHeavyT < (int64_t)nv ? i_beg + kHeavyT : nv);
   const int64_t col0 = (int64_t)glane * EPV;
   const bool want_dot = psw != nullptr;
   const uint32_t cand[2] = {skeys[i_beg], skeys[i_end - 1]};
@@ -347,7 +504,6 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
   for (int t = 0; t < 2; ++t) {
     const uint32_t r = cand[t];
     if (t == 1 && r == cand[0]) break;
-    if (r >= (uint32_t)K) continue;  // sentinel row: handled by the rows kernel
     const uint32_t rb = offs[r], re = offs[r + 1];
     if (re - rb <= (uint32_t)kHeavyT) continue;
     const uint32_t s_beg = rb > i_beg ? rb : i_beg;
@@ -358,7 +514,8 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
-    reduce_occurrences<TW, LPG, VPL>(s_beg, s_end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw, acc);
+    reduce_occurrences<TW, LPG, VPL>(s_beg, s_end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw, acc,
+                                     dsorted);
     float* prow = partials + (2 * c + slot) * D + col0;
 #pragma unroll
     for (int v = 0; v < VPL; ++v)
@@ -367,6 +524,7 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
   }
 }
 
+// Generic rows kernel (lane groups smaller than a wave, small rows).
 template <typename TW, int LPG, int VPL>
 __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__ W, int64_t K, int64_t D,
                                                           const void* __restrict__ psw, int pdt,
@@ -383,39 +541,19 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
   const int glane = lane & (LPG - 1);
   const int64_t grp = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * GPW + (lane / LPG);
   const int64_t r0 = grp * rows_per_group;
-  if (r0 > K) return;
-  const int64_t r1 = (r0 + rows_per_group < K + 1) ? r0 + rows_per_group : K + 1;
+  if (r0 >= K) return;
+  const int64_t r1 = (r0 + rows_per_group < K) ? r0 + rows_per_group : K;
   const int64_t col0 = (int64_t)glane * EPV;
   const bool want_dot = psw != nullptr;
 
   for (int64_t r = r0; r < r1; ++r) {
     const uint32_t beg = offs[r], end = offs[r + 1];
     const uint32_t cnt = end - beg;
-    if (r == K) {
-      // occurrences whose index was out of range: zero psw-gradient
-      if (want_dot)
-        for (uint32_t i = beg + glane; i < end; i += LPG) store_scalar(gpsw, pdt, svals[i], 0.f);
-      continue;
-    }
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
     if (cnt > (uint32_t)kHeavyT) {
-      const uint32_t c_first = beg / kHeavyT, c_last = (end - 1) / kHeavyT;
-      for (uint32_t c = c_first; c <= c_last; ++c) {
-        const int slot = (c == c_first && beg != c * (uint32_t)kHeavyT) ? 1 : 0;
-        const float* prow = partials + (2 * (int64_t)c + slot) * D + col0;
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) {
-#pragma unroll
-          for (int h = 0; h < EPV; h += 4) {
-            float f[4];
-            VecTraits<float>::unpack(ld16(prow + v * VSTRIDE + h), f);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[v * EPV + h + e] += f[e];
-          }
-        }
-      }
+      add_heavy_partials<LPG, VPL, EPV>(beg, end, partials, D, col0, acc);
     } else if (cnt > 0) {
       float wv[NE];
       if (want_dot) load_row_f32<TW, LPG, VPL>(W + r * D, col0, wv);
@@ -427,22 +565,226 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
   }
 }
 
+// Wave-per-64-rows kernel (rows of 64*VPL 16-byte vectors), software-pipelined.
+//
+// Row i+1's W row and its first U gradient rows are in flight while row i is
+// reduced and stored. gfx9 counts loads and stores in one in-order vmcnt, so
+// the loads must be issued before the current row's stores, and every row
+// issues the same number of vector loads (unused slots read a zero row, tail
+// rows past K write a dummy row) so the compiler's waits stay partial.
+// Occurrence metadata comes from an LDS window (lgkmcnt, not vmcnt); the
+// psw-gradient dots of a row leave in one store into sorted order and are
+// scattered by position afterwards.
+constexpr int kMetaChunk = 256;  // per-wave LDS window of occurrence metadata (entries)
+
+template <int VPL, int U>
+struct RowData {
+  uint4 wraw[VPL];
+  uint4 gvec[U][VPL];
+};
+template <int U>
+struct RowMeta {
+  uint32_t beg, end, nh;  // nh: occurrences served by the prefetch (0 for empty / heavy rows)
+  uint32_t b[U];
+  float w[U];
+};
+
+template <typename TW, int VPL, int U>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 && U <= 4) ? 5 : ((VPL == 1 || (VPL == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows64_kernel(
+    const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TW* __restrict__ g,
+    const uint32_t* __restrict__ offs, const uint4* __restrict__ meta, const float* __restrict__ partials,
+    const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
+    uint32_t dummy_slot) {
+  __shared__ uint4 smeta[4][kMetaChunk];
+  constexpr int EPV = VecTraits<TW>::EPV;
+  constexpr int NE = VPL * EPV;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + wv) * 64;
+  if (r0 >= K) return;
+  const int nrows = (int)((K - r0) < 64 ? (K - r0) : 64);
+  const int64_t col0 = (int64_t)lane * EPV;
+  const uint32_t lane_byte = (uint32_t)lane * 16u;  // lane's byte offset inside a row
+  const uint64_t rowbytes = (uint64_t)D * sizeof(TW);
+  const char* Wb = (const char*)W;
+  const char* gb = (const char*)g;
+  const char* zb = (const char*)zrow;
+
+  // lane i: [begin, end) of row r0 + i in the sorted stream; lanes past the
+  // last row describe an empty row at the end of the wave's stream
+  const uint32_t tail = offs[r0 + nrows];
+  uint32_t my_beg = tail, my_end = tail;
+  if (lane < nrows) {
+    my_beg = offs[r0 + lane];
+    my_end = offs[r0 + lane + 1];
+  }
+
+  uint4* sm = smeta[wv];
+  uint32_t cbase = (uint32_t)__builtin_amdgcn_readlane((int)my_beg, 0);
+  auto load_chunk = [&](uint32_t start) {
+    cbase = start;
+#pragma unroll
+    for (int k = 0; k < kMetaChunk / 64; ++k) sm[lane + 64 * k] = meta[start + lane + 64 * k];
+  };
+  load_chunk(cbase);
+
+  auto get_meta = [&](int i, RowMeta<U>& M) {
+    if (i < 64) {
+      M.beg = (uint32_t)__builtin_amdgcn_readlane((int)my_beg, i);
+      M.end = (uint32_t)__builtin_amdgcn_readlane((int)my_end, i);
+    } else {
+      M.beg = M.end = tail;
+    }
+    const uint32_t cnt = M.end - M.beg;
+    M.nh = cnt > (uint32_t)kHeavyT ? 0u : (cnt < (uint32_t)U ? cnt : (uint32_t)U);
+    if (M.beg + U > cbase + kMetaChunk) load_chunk(M.beg);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint4 m = sm[M.beg - cbase + u];
+      M.b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)m.y);
+      M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readfirstlane((int)m.z)) : 0.f;
+    }
+  };
+  auto issue = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
+    const char* wrow = (want_dot && M.nh) ? Wb + (uint64_t)(r0 + i) * rowbytes : zb;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16(wrow + lane_byte + v * 1024u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * rowbytes : zb;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+    }
+  };
+  // acc += sum_u w[u] * gvec[u]; lane u of the returned value holds <wraw, gvec[u]>
+  auto accumulate = [&](const RowData<VPL, U>& R, const float* w, float* acc) {
+    float mydot = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float f[NE];
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.gvec[u][v], f + v * EPV);
+#pragma unroll
+      for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
+      if (want_dot) {
+        float d = 0.f;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) d = vec_dot<TW>(R.wraw[v], R.gvec[u][v], d);
+        d = group_sum<64>(d);
+        mydot = lane == u ? d : mydot;
+      }
+    }
+    return mydot;
+  };
+  auto process = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
+    float acc[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) acc[e] = 0.f;
+    float mydot = accumulate(R, M.w, acc);
+    if (want_dot) dsorted[(uint32_t)lane < M.nh ? M.beg + lane : dummy_slot] = mydot;
+    const uint32_t cnt = M.end - M.beg;
+    if (cnt > (uint32_t)kHeavyT) {
+      add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
+    } else if (cnt > (uint32_t)U) {
+      // rows longer than the prefetch: U more occurrences at a time, in order
+      for (uint32_t s = M.beg + U; s < M.end; s += U) {
+        const uint32_t nh = (M.end - s) < (uint32_t)U ? (M.end - s) : (uint32_t)U;
+        float w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint4 m = meta[s + u];
+          const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.y * rowbytes : zb;
+          w[u] = (uint32_t)u < nh ? __uint_as_float(m.z) : 0.f;
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+        }
+        mydot = accumulate(R, w, acc);
+        if (want_dot) dsorted[(uint32_t)lane < nh ? s + lane : dummy_slot] = mydot;
+      }
+    }
+    char* orow = (r0 + i < K) ? (char*)gW + (uint64_t)(r0 + i) * rowbytes : (char*)dummy_row;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
+  };
+
+  RowMeta<U> MA, MB;
+  RowData<VPL, U> DA, DB;
+  get_meta(0, MA);
+  issue(0, MA, DA);
+  get_meta(1, MB);
+  for (int i = 0; i < 64; i += 2) {
+    issue(i + 1, MB, DB);
+    process(i, MA, DA);
+    get_meta(i + 2, MA);
+    issue(i + 2, MA, DA);
+    process(i + 1, MB, DB);
+    get_meta(i + 3, MB);
+  }
+}
+
+// meta[i] = {position, bag, weight as float32 bits, 0} in sorted order;
+// entries past the valid count (padding included) are zero.
+__global__ void occ_meta_kernel(const uint32_t* __restrict__ svals, const uint32_t* __restrict__ nvalid,
+                                int64_t n_total, uint32_t L32, const void* __restrict__ psw, int pdt,
+                                uint4* __restrict__ meta) {
+  const uint32_t nv = *nvalid;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_total; i += (int64_t)gridDim.x * blockDim.x) {
+    uint4 m = make_uint4(0u, 0u, 0u, 0u);
+    if (i < (int64_t)nv) {
+      const uint32_t p = svals[i];
+      m.x = p;
+      m.y = p / L32;
+      m.z = __float_as_uint(psw ? load_scalar(psw, pdt, p) : 1.f);
+    }
+    meta[i] = m;
+  }
+}
+
+// gpsw[position] <- psw-gradient dots computed in sorted order.
+__global__ void gpsw_scatter_kernel(const uint4* __restrict__ meta, const float* __restrict__ dsorted,
+                                    const uint32_t* __restrict__ nvalid, int64_t N, void* __restrict__ gpsw, int pdt) {
+  const uint32_t nv = *nvalid;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N; i += (int64_t)gridDim.x * blockDim.x) {
+    if (i >= (int64_t)nv) break;
+    store_scalar(gpsw, pdt, meta[i].x, dsorted[i]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-struct BwdLayout {
-  size_t counts, keys0, vals0, keys1, vals1, hist, parts, partials, total;
-  int64_t ntiles, nchunks;
-};
-
+static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+struct RadixPlan {
+  int passes;
+  int bits;
+};
+
+// Digit plan for keys in [0, K).
+static RadixPlan radix_plan(int64_t K) {
+  int tb = 0;
+  if (K > 1)
+    while (tb < 31 && ((uint64_t)(K - 1) >> tb) != 0) ++tb;
+  if (tb <= 8) return {1, 8};
+  if (tb <= 16) return {2, 8};
+  if (tb <= 20) return {2, 10};
+  if (tb <= 22) return {2, 11};
+  if (tb <= 30) return {3, 10};
+  return {3, 11};
+}
+
+struct BwdLayout {
+  size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, total;
+  int64_t ntiles, nbins, nchunks, nmeta;
+  RadixPlan plan;
+};
 
 static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   BwdLayout l;
+  l.plan = radix_plan(K);
   size_t off = 0;
-  l.counts = off;
+  l.offs = off;
   off += align256((size_t)(K + 2) * 4);
   l.keys0 = off;
   off += align256((size_t)N * 4);
@@ -453,24 +795,45 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   l.vals1 = off;
   off += align256((size_t)N * 4);
   l.ntiles = cdiv(N, kRadixTile);
+  l.nbins = ((int64_t)1 << l.plan.bits) * l.ntiles;
   l.hist = off;
-  off += align256((size_t)(kRadix * l.ntiles + 1) * 4);
-  const int64_t scan_n = (K + 1) > kRadix * l.ntiles ? (K + 1) : kRadix * l.ntiles;
+  off += align256((size_t)(l.nbins + 1) * 4);
+  const int64_t scan_n = (K + 1) > l.nbins ? (K + 1) : l.nbins;
   l.parts = off;
   off += align256((size_t)(cdiv(scan_n, kScanTile) + 1) * 4);
   l.nchunks = cdiv(N, kHeavyT);
   l.partials = off;
   off += align256((size_t)(2 * l.nchunks) * (size_t)D * 4);
+  // wave-per-64-rows path: sorted occurrence metadata (padded so a wave can read
+  // a full LDS window past any row start), dots in sorted order (+1 dummy slot),
+  // a zero row read by unused prefetch slots and a dummy row written by tail rows
+  l.nmeta = N + kMetaChunk + 16;
+  l.meta = off;
+  off += align256((size_t)l.nmeta * 16);
+  l.dsorted = off;
+  off += align256((size_t)(N + 1) * 4);
+  l.zrow = off;
+  off += align256((size_t)D * 4);
+  l.dummy_row = off;
+  off += align256((size_t)D * 4);
   l.total = off;
   return l;
 }
 
-// In-place exclusive scan of data[0..n) with data[n] <- total.
-static void device_exclusive_scan(uint32_t* data, int64_t n, uint32_t* parts, hipStream_t st) {
+// In-place exclusive prefix sum of data[0..n) with data[n] <- total.
+static void device_exclusive_sum(uint32_t* data, int64_t n, uint32_t* parts, hipStream_t st) {
   const int64_t tiles = cdiv(n, kScanTile);
   hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
   hipLaunchKernelGGL(scan_parts_kernel, dim3(1), dim3(kScanThreads), 0, st, parts, tiles);
   hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
+}
+
+// In-place inclusive suffix min of data[0..n).
+static void device_suffix_min(uint32_t* data, int64_t n, uint32_t* parts, hipStream_t st) {
+  const int64_t tiles = cdiv(n, kScanTile);
+  hipLaunchKernelGGL(smin_reduce_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
+  hipLaunchKernelGGL(smin_parts_kernel, dim3(1), dim3(kScanThreads), 0, st, parts, tiles);
+  hipLaunchKernelGGL(smin_apply_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
 }
 
 static unsigned grid_for(int64_t n, int threads, int64_t cap = 65536) {
@@ -479,33 +842,114 @@ static unsigned grid_for(int64_t n, int threads, int64_t cap = 65536) {
   return (unsigned)(b < cap ? b : cap);
 }
 
+template <int BITS>
+static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], uint32_t* const vals[2], int cur,
+                       int nxt, int64_t N, int64_t K, const BwdLayout& l, uint32_t* hist, uint32_t* parts,
+                       void* gpsw, int pdt, hipStream_t st) {
+  const int shift = pass * BITS;
+  const uint32_t* nvalid = hist + l.nbins;  // total of the previous pass's scan
+  const dim3 grid((unsigned)l.ntiles), block(256);
+  if (pass == 0) {
+    hipLaunchKernelGGL((radix_hist_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr, N,
+                       (const uint32_t*)nullptr, K, shift, hist, l.ntiles, gpsw, pdt);
+    device_exclusive_sum(hist, l.nbins, parts, st);
+    hipLaunchKernelGGL((radix_scatter_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr,
+                       (const uint32_t*)nullptr, N, (const uint32_t*)nullptr, K, shift, (const uint32_t*)hist,
+                       l.ntiles, keys[nxt], vals[nxt]);
+  } else {
+    // the previous scan's total (nvalid) lives at hist[nbins]; this pass's hist
+    // kernel reads it before the scan below rewrites it with the same value
+    hipLaunchKernelGGL((radix_hist_kernel<false, BITS>), grid, block, 0, st, (const int64_t*)nullptr,
+                       (const uint32_t*)keys[cur], N, nvalid, K, shift, hist, l.ntiles, (void*)nullptr, 0);
+    device_exclusive_sum(hist, l.nbins, parts, st);
+    hipLaunchKernelGGL((radix_scatter_kernel<false, BITS>), grid, block, 0, st, (const int64_t*)nullptr,
+                       (const uint32_t*)keys[cur], (const uint32_t*)vals[cur], N, nvalid, K, shift,
+                       (const uint32_t*)hist, l.ntiles, keys[nxt], vals[nxt]);
+  }
+}
+
+template <typename TW, int VPL, int U>
+static void launch_rows64(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
+                          const uint4* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
+                          float* dsorted, uint32_t dummy_slot, hipStream_t st) {
+  const unsigned rb = (unsigned)cdiv(K, 4 * 64);
+  hipLaunchKernelGGL((eb_bwd_rows64_kernel<TW, VPL, U>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, want_dot,
+                     (const TW*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW, dsorted,
+                     dummy_slot);
+}
+
 template <typename TW, int LPG, int VPL>
 static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, int pdt, const void* g, int64_t L,
-                          const uint32_t* offs, const uint32_t* skeys, const uint32_t* svals, int64_t N,
-                          const BwdLayout& l, float* partials, void* gW, void* gpsw, hipStream_t st) {
+                          const uint32_t* offs, const uint32_t* skeys, const uint32_t* svals, const uint32_t* nvalid,
+                          int64_t N, const BwdLayout& l, char* ws, void* gW, void* gpsw, hipStream_t st) {
   constexpr int GPW = 64 / LPG;
   const int64_t groups_per_block = 4 * GPW;
-  if (N > 0) {
-    const unsigned hb = (unsigned)cdiv(l.nchunks, groups_per_block);
-    hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D, psw, pdt,
-                       (const TW*)g, (uint32_t)L, offs, skeys, svals, (uint32_t)N, l.nchunks, partials, gpsw);
+  float* partials = (float*)(ws + l.partials);
+  const unsigned hb = (unsigned)cdiv(l.nchunks, groups_per_block);
+  if constexpr (LPG == 64) {
+    uint4* meta = (uint4*)(ws + l.meta);
+    float* dsorted = (float*)(ws + l.dsorted);
+    void* zrow = ws + l.zrow;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(D, 256, 64)), dim3(256), 0, st, (uint32_t*)zrow, 0u, D);
+    if (N > 0) {
+      hipLaunchKernelGGL(occ_meta_kernel, dim3(grid_for(l.nmeta, 256, 16384)), dim3(256), 0, st, svals, nvalid,
+                         l.nmeta, (uint32_t)L, psw, pdt, meta);
+      hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D, psw,
+                         pdt, (const TW*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
+                         dsorted);
+    } else {
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(4 * l.nmeta, 256, 4096)), dim3(256), 0, st,
+                         (uint32_t*)meta, 0u, 4 * l.nmeta);
+    }
+    if (K > 0) {
+      const int want_dot = psw != nullptr ? 1 : 0;
+      const bool dense = N > 3 * K;  // more than ~3 lookups per row on average: prefetch 8
+      const uint32_t dslot = (uint32_t)N;
+      void* dummy = ws + l.dummy_row;
+      if constexpr (VPL == 1) {
+        if (dense)
+          launch_rows64<TW, 1, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+        else
+          launch_rows64<TW, 1, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+      } else if constexpr (VPL == 2) {
+        if (dense)
+          launch_rows64<TW, 2, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+        else
+          launch_rows64<TW, 2, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+      } else if constexpr (VPL == 4) {
+        launch_rows64<TW, 4, 2>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+      } else {
+        launch_rows64<TW, 8, 1>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+      }
+    }
+    if (N > 0 && psw != nullptr)
+      hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, (const uint4*)meta,
+                         (const float*)dsorted, nvalid, N, gpsw, pdt);
+  } else {
+    if (N > 0)
+      hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D, psw,
+                         pdt, (const TW*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
+                         (float*)nullptr);
+    if (K == 0) return;
+    const int rows_per_group = 4;
+    const int64_t groups = cdiv(K, rows_per_group);
+    const unsigned rb = (unsigned)cdiv(groups, groups_per_block);
+    hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, LPG, VPL>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, psw, pdt,
+                       (const TW*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW,
+                       gpsw);
   }
-  const int rows_per_group = 4;
-  const int64_t groups = cdiv(K + 1, rows_per_group);
-  const unsigned rb = (unsigned)cdiv(groups, groups_per_block);
-  hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, LPG, VPL>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, psw, pdt,
-                     (const TW*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW, gpsw);
 }
 
 template <typename TW>
 static bool dispatch_reduce(const GroupCfg& c, const void* W, int64_t K, int64_t D, const void* psw, int pdt,
                             const void* g, int64_t L, const uint32_t* offs, const uint32_t* skeys,
-                            const uint32_t* svals, int64_t N, const BwdLayout& l, float* partials, void* gW,
-                            void* gpsw, hipStream_t st) {
-#define PKM_RED_CASE(LPG_, VPL_)                                                                           \
-  if (c.lpg == LPG_ && c.vpl == VPL_) {                                                                    \
-    launch_reduce<TW, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, N, l, partials, gW, gpsw, st); \
-    return true;                                                                                           \
+                            const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l,
+                            char* ws, void* gW, void* gpsw, hipStream_t st) {
+#define PKM_RED_CASE(LPG_, VPL_)                                                                                  \
+  if (c.lpg == LPG_ && c.vpl == VPL_) {                                                                           \
+    launch_reduce<TW, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, gpsw, \
+                                  st);                                                                            \
+    return true;                                                                                                  \
   }
   PKM_RED_CASE(64, 1)
   PKM_RED_CASE(64, 2)
@@ -539,18 +983,16 @@ extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int
   PKM_REQUIRE(valid_dt(weight_dtype), PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: bad weight dtype %d", weight_dtype);
   PKM_REQUIRE(grad_dtype == weight_dtype, PKM_ERR_UNSUPPORTED,
               "pkm_eb_bwd: grad_out dtype %d differs from weight dtype %d", grad_dtype, weight_dtype);
-  PKM_REQUIRE(psw == nullptr ? psw_dtype == PKM_DTYPE_NONE : valid_dt(psw_dtype), PKM_ERR_INVALID_ARGUMENT,
-              "pkm_eb_bwd: psw pointer / dtype %d mismatch", psw_dtype);
+  PKM_REQUIRE(psw_dtype == PKM_DTYPE_NONE ? psw == nullptr
+                                          : (valid_dt(psw_dtype) && (psw != nullptr || bags * bag_size == 0)),
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: psw pointer / dtype %d mismatch", psw_dtype);
   PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd: bad sizes num_rows=%lld dim=%lld bags=%lld bag_size=%lld", (long long)num_rows,
               (long long)dim, (long long)bags, (long long)bag_size);
   const int64_t N = bags * bag_size;
-  PKM_REQUIRE(N < ((int64_t)1 << 32) - 1 && num_rows < ((int64_t)1 << 31) - 1, PKM_ERR_INVALID_ARGUMENT,
-              "pkm_eb_bwd: bags*bag_size=%lld or num_rows=%lld too large", (long long)N, (long long)num_rows);
-  if (num_rows == 0) {
-    // nothing to write for the weight; every lookup is out of range
-    PKM_REQUIRE(psw == nullptr || N == 0 || grad_psw != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_psw");
-  }
+  PKM_REQUIRE(N < ((int64_t)1 << 31) && num_rows < ((int64_t)1 << 31) - 1, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd: bags*bag_size=%lld must be < 2^31 and num_rows=%lld < 2^31-1", (long long)N,
+              (long long)num_rows);
   PKM_REQUIRE(grad_weight != nullptr || num_rows == 0, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_weight");
   PKM_REQUIRE(N == 0 || (indices != nullptr && grad_out != nullptr), PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd: null indices / grad_out");
@@ -570,60 +1012,48 @@ extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int
 
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  uint32_t* counts = (uint32_t*)(ws + l.counts);
+  uint32_t* offs = (uint32_t*)(ws + l.offs);
   uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
   uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
   uint32_t* hist = (uint32_t*)(ws + l.hist);
   uint32_t* parts = (uint32_t*)(ws + l.parts);
   float* partials = (float*)(ws + l.partials);
   const int64_t K = num_rows;
+  const uint32_t* nvalid = hist + l.nbins;
+  void* gpsw = psw != nullptr ? grad_psw : nullptr;
 
-  // 1-2. row counts -> offsets[0..K+1]
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 2, 256, 4096)), dim3(256), 0, st, counts, 0u, K + 2);
-  if (N > 0)
-    hipLaunchKernelGGL(count_rows_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, indices, N, K, counts);
-  device_exclusive_scan(counts, K + 1, parts, st);
-
-  // 3. stable LSD radix sort of (row, position)
   int cur = 0;
   if (N > 0) {
-    int bits = 0;
-    while (bits < 32 && ((uint64_t)K >> bits) != 0) ++bits;  // keys are in [0, K]
-    const int passes = bits == 0 ? 1 : (bits + 7) / 8;
-    for (int pass = 0; pass < passes; ++pass) {
-      const int shift = pass * 8;
+    // 1. stable LSD radix sort of (row, position); invalid lookups dropped
+    for (int pass = 0; pass < l.plan.passes; ++pass) {
       const int nxt = pass == 0 ? 0 : 1 - cur;
-      if (pass == 0) {
-        hipLaunchKernelGGL(radix_hist_kernel<true>, dim3((unsigned)l.ntiles), dim3(256), 0, st, indices,
-                           (const uint32_t*)nullptr, N, K, shift, hist, l.ntiles);
-        device_exclusive_scan(hist, kRadix * l.ntiles, parts, st);
-        hipLaunchKernelGGL(radix_scatter_kernel<true>, dim3((unsigned)l.ntiles), dim3(256), 0, st, indices,
-                           (const uint32_t*)nullptr, (const uint32_t*)nullptr, N, K, shift, (const uint32_t*)hist,
-                           l.ntiles, keys[0], vals[0]);
-        cur = 0;
-      } else {
-        hipLaunchKernelGGL(radix_hist_kernel<false>, dim3((unsigned)l.ntiles), dim3(256), 0, st,
-                           (const int64_t*)nullptr, (const uint32_t*)keys[cur], N, K, shift, hist, l.ntiles);
-        device_exclusive_scan(hist, kRadix * l.ntiles, parts, st);
-        hipLaunchKernelGGL(radix_scatter_kernel<false>, dim3((unsigned)l.ntiles), dim3(256), 0, st,
-                           (const int64_t*)nullptr, (const uint32_t*)keys[cur], (const uint32_t*)vals[cur], N, K,
-                           shift, (const uint32_t*)hist, l.ntiles, keys[nxt], vals[nxt]);
-        cur = nxt;
+      switch (l.plan.bits) {
+        case 8: radix_pass<8>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st); break;
+        case 10: radix_pass<10>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st); break;
+        default: radix_pass<11>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st); break;
       }
+      cur = nxt;
     }
+    // 2. row offsets: run starts + suffix min
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 1, 256, 4096)), dim3(256), 0, st, offs, 0xFFFFFFFFu, K + 1);
+    hipLaunchKernelGGL(run_starts_kernel, dim3(grid_for(N, 256, 8192)), dim3(256), 0, st, (const uint32_t*)keys[cur],
+                       nvalid, N, K, offs);
+    device_suffix_min(offs, K + 1, parts, st);
+  } else {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 1, 256, 4096)), dim3(256), 0, st, offs, 0u, K + 1);
   }
 
-  // 4-5. heavy-row chunk partials, then every row once
+  // 3-4. heavy-row chunk partials, then every row once
   bool ok;
   if (weight_dtype == PKM_DTYPE_F32)
-    ok = dispatch_reduce<float>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, counts, keys[cur], vals[cur], N,
-                                l, partials, grad_weight, grad_psw, st);
+    ok = dispatch_reduce<float>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, offs, keys[cur], vals[cur],
+                                nvalid, N, l, ws, grad_weight, gpsw, st);
   else if (weight_dtype == PKM_DTYPE_BF16)
-    ok = dispatch_reduce<bf16_t>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, counts, keys[cur], vals[cur],
-                                 N, l, partials, grad_weight, grad_psw, st);
+    ok = dispatch_reduce<bf16_t>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, offs, keys[cur], vals[cur],
+                                 nvalid, N, l, ws, grad_weight, gpsw, st);
   else
-    ok = dispatch_reduce<f16_t>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, counts, keys[cur], vals[cur],
-                                N, l, partials, grad_weight, grad_psw, st);
+    ok = dispatch_reduce<f16_t>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, offs, keys[cur], vals[cur],
+                                nvalid, N, l, ws, grad_weight, gpsw, st);
   PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
   return pkm_check_launch("pkm_eb_bwd");
 }

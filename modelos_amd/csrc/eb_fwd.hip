@@ -237,7 +237,7 @@ extern "C" int pkm_eb_fwd(const void* weight, int64_t num_rows, int64_t dim, int
                           const int64_t* indices, const void* psw, int psw_dtype, int64_t bags, int64_t bag_size,
                           void* out, void* stream) {
   PKM_REQUIRE(valid_dtype(weight_dtype), PKM_ERR_INVALID_ARGUMENT, "pkm_eb_fwd: bad weight dtype %d", weight_dtype);
-  PKM_REQUIRE(psw == nullptr ? psw_dtype == PKM_DTYPE_NONE : valid_dtype(psw_dtype), PKM_ERR_INVALID_ARGUMENT,
+  PKM_REQUIRE(psw_dtype == PKM_DTYPE_NONE ? psw == nullptr : (valid_dtype(psw_dtype) && (psw != nullptr || bags * bag_size == 0)), PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_fwd: psw pointer / dtype %d mismatch", psw_dtype);
   PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_fwd: bad sizes num_rows=%lld dim=%lld bags=%lld bag_size=%lld", (long long)num_rows,
@@ -283,7 +283,7 @@ extern "C" int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int 
   PKM_REQUIRE(valid_dtype(gbar_dtype), PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd2: bad gbar dtype %d", gbar_dtype);
   PKM_REQUIRE(grad_dtype == gbar_dtype, PKM_ERR_UNSUPPORTED,
               "pkm_eb_bwd2: grad_out dtype %d differs from gbar dtype %d", grad_dtype, gbar_dtype);
-  PKM_REQUIRE(a == nullptr ? a_dtype == PKM_DTYPE_NONE : valid_dtype(a_dtype), PKM_ERR_INVALID_ARGUMENT,
+  PKM_REQUIRE(a_dtype == PKM_DTYPE_NONE ? a == nullptr : (valid_dtype(a_dtype) && (a != nullptr || bags * bag_size == 0)), PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd2: a pointer / dtype %d mismatch", a_dtype);
   PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd2: bad sizes");

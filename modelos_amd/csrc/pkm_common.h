@@ -11,7 +11,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/pkm_hip.h"
+#include "pkm_hip.h"
 
 namespace pkm {
 
@@ -115,14 +115,50 @@ struct VecTraits<f16_t> {
   }
 };
 
+// Float32 dot product of two packed bf16 pairs accumulated into c
+// (v_dot2_f32_bf16: the bf16 products are exact in float32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// d + <a, b> over the elements of two 16-byte vectors, float32 accumulation
+// (packed dot instructions for 16-bit types).
+template <typename T>
+__device__ __forceinline__ float vec_dot(const uint4& a, const uint4& b, float d);
+template <>
+__device__ __forceinline__ float vec_dot<float>(const uint4& a, const uint4& b, float d) {
+  d = __builtin_fmaf(__uint_as_float(a.x), __uint_as_float(b.x), d);
+  d = __builtin_fmaf(__uint_as_float(a.y), __uint_as_float(b.y), d);
+  d = __builtin_fmaf(__uint_as_float(a.z), __uint_as_float(b.z), d);
+  return __builtin_fmaf(__uint_as_float(a.w), __uint_as_float(b.w), d);
+}
+template <>
+__device__ __forceinline__ float vec_dot<bf16_t>(const uint4& a, const uint4& b, float d) {
+  d = dot2_bf16(a.x, b.x, d);
+  d = dot2_bf16(a.y, b.y, d);
+  d = dot2_bf16(a.z, b.z, d);
+  return dot2_bf16(a.w, b.w, d);
+}
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+template <>
+__device__ __forceinline__ float vec_dot<f16_t>(const uint4& a, const uint4& b, float d) {
+  d = dot2_f16(a.x, b.x, d);
+  d = dot2_f16(a.y, b.y, d);
+  d = dot2_f16(a.z, b.z, d);
+  return dot2_f16(a.w, b.w, d);
+}
+
 __device__ __forceinline__ uint4 ld16(const void* p) { return *(const uint4*)p; }
 __device__ __forceinline__ void st16(void* p, const uint4& v) { *(uint4*)p = v; }
 // Streaming store for write-once outputs (dense weight gradient).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void st16_nt(void* p, const uint4& v) {
-  __builtin_nontemporal_store(v.x, (uint32_t*)p + 0);
-  __builtin_nontemporal_store(v.y, (uint32_t*)p + 1);
-  __builtin_nontemporal_store(v.z, (uint32_t*)p + 2);
-  __builtin_nontemporal_store(v.w, (uint32_t*)p + 3);
+  const u32x4_t x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, (u32x4_t*)p);
 }
 
 // ---------------------------------------------------------------------------
@@ -151,14 +187,35 @@ __device__ __forceinline__ int64_t bcast_i64(int64_t v, int src) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// v + (v moved by a DPP pattern); lanes whose row is masked off add 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
 // Sum over the LPG lanes of a group; every lane of the group gets the total.
-// The butterfly order is fixed, so the result is deterministic.
+// DPP lane permutes (no LDS traffic) in a fixed order, so the result is
+// deterministic: quad swaps, half-row and row mirrors (16-lane rows), then
+// row broadcasts across the wave.
 template <int LPG>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = LPG / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, LPG);
+  if constexpr (LPG >= 2) v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (LPG >= 4) v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (LPG >= 8) v = dpp_add<0x141>(v);  // row_half_mirror
+  if constexpr (LPG >= 16) v = dpp_add<0x140>(v); // row_mirror: every lane holds its row's sum
+  if constexpr (LPG == 32) {
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    v = (threadIdx.x & 32) ? hi : lo;
+  } else if constexpr (LPG == 64) {
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  }
   return v;
 }
+
 
 // ---------------------------------------------------------------------------
 // Row split over lane groups (host side, defined in eb_fwd.hip): a row of D
