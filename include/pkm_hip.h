@@ -104,6 +104,40 @@ int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int gbar_dtype,
                 const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
                 void* d_grad_out, void* d_a, void* stream);
 
+/* Sub-key score of pkm_score_topk. */
+enum pkm_score_t {
+  PKM_SCORE_DOT = 0, /* <q, k> */
+  PKM_SCORE_IDW = 1  /* -log(1e-3 + max(|q|^2 + |k|^2 - 2 <q, k>, 0)) */
+};
+
+/*
+ * Product-key retrieval: sub-key scores, per-half top-knn and the top-knn of
+ * the knn x knn cartesian sums, for every (token t, head h).
+ *   query: [num_tokens, heads, 2 * half], keys: [2 * heads * n_keys, half]
+ *   (key (h, c, i) is row (2h + c) * n_keys + i), both in dtype (F32 or BF16).
+ *   s_c[i]          = score(query[t, h, c*half : (c+1)*half], key (h, c, i))
+ *                     in float32, rounded to dtype
+ *   (v_c, i_c)      = top-knn of s_c, best first
+ *   out_scores      = top-knn of dtype(v_0[a] + v_1[b]), best first  [num_tokens*heads, knn], dtype
+ *   out_indices     = i_0[a] * n_keys + i_1[b] of those              [num_tokens*heads, knn], int64
+ * Optional (NULL = not written):
+ *   out_sub_indices1/2 = i_0 / i_1                                    [num_tokens, heads, knn], int64
+ *   out_sub_scores1/2  = s_0 / s_1 (every key)                        [num_tokens, heads, n_keys], dtype
+ * Equal scores are ordered by the smaller sub-key index (per half) and by
+ * the smaller a * knn + b (cartesian); the result is deterministic.
+ * Limits: knn <= 64, n_keys a multiple of 64 up to 2048, half a multiple of
+ * 32 (BF16) or 4 (F32); query and keys 16-byte aligned.
+ *
+ * Replaces HashingMemory.get_indices (pkm/memory.py:250-289; score_type DOT,
+ * no sub outputs) and FastWeightProductKeyMemory.get_indices +
+ * compute_qk_scores (fwpkm/fwpkm.py:853-934; DOT or IDW, all outputs).
+ */
+int pkm_score_topk(const void* query, const void* keys, int64_t num_tokens, int64_t heads,
+                   int64_t n_keys, int64_t half, int64_t knn, int score_type, int dtype,
+                   void* out_scores, int64_t* out_indices,
+                   int64_t* out_sub_indices1, int64_t* out_sub_indices2,
+                   void* out_sub_scores1, void* out_sub_scores2, void* stream);
+
 /*
  * Counts indices outside [0, num_rows) into *count_out (a device int64),
  * which the call overwrites. No counterpart in the reference (its Triton

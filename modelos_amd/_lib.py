@@ -46,7 +46,22 @@ SIGNATURES = {
         ],
     ),
     "pkm_count_invalid_indices": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "pkm_score_topk": (
+        c_int,
+        [
+            c_void_p, c_void_p,  # query, keys
+            c_int64, c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, half, knn
+            c_int, c_int,  # score_type, dtype
+            c_void_p, c_void_p,  # out_scores, out_indices
+            c_void_p, c_void_p,  # out_sub_indices1, out_sub_indices2
+            c_void_p, c_void_p,  # out_sub_scores1, out_sub_scores2
+            c_void_p,  # stream
+        ],
+    ),
 }
+
+# pkm_score_t
+SCORE_CODES = {"dot": 0, "idw": 1}
 
 # pkm_dtype_t
 DTYPE_NONE = -1
