@@ -110,10 +110,54 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+class CallTimer:
+    """Brackets every entry-point call with a pair of timing events on torch's
+    current stream (the stream the call enqueues on). Use as a context
+    manager; `summary()` synchronises and returns {name: [ms, ...]}."""
+
+    def __init__(self):
+        self.events = []
+
+    def __enter__(self):
+        global _timer
+        self._prev, _timer = _timer, self
+        return self
+
+    def __exit__(self, *exc):
+        global _timer
+        _timer = self._prev
+        return False
+
+    def summary(self) -> dict:
+        """{(entry point, leading integer arguments): [ms per call]}."""
+        torch.cuda.synchronize()
+        out: dict = {}
+        for key, a, b in self.events:
+            out.setdefault(key, []).append(a.elapsed_time(b))
+        return out
+
+
+_timer: CallTimer | None = None
+# positions of the size arguments that name a call's shape in CallTimer keys
+_SIZE_ARGS = {
+    "pkm_eb_fwd": (1, 2),  # num_rows, dim
+    "pkm_eb_bwd": (1, 2),
+    "pkm_eb_bwd2": (1, 2),
+    "pkm_score_topk": (2, 3, 4, 5),  # num_tokens, heads, n_keys, half
+}
+
+
 def call(name: str, *args) -> None:
     """Calls an int-status entry point and raises PkmError on failure."""
     lib = load()
+    timer = _timer
+    if timer is not None:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
     status = getattr(lib, name)(*args)
+    if timer is not None:
+        end.record()
+        timer.events.append(((name, tuple(args[i] for i in _SIZE_ARGS.get(name, ()))), start, end))
     if status != 0:
         msg = lib.pkm_last_error_string().decode(errors="replace")
         raise PkmError(name, status, msg)

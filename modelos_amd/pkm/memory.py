@@ -1,0 +1,263 @@
+"""Drop-in for the reference's pkm/memory.py: the product-key memory layer.
+
+HashingMemory keeps the reference's constructor arguments, parameter names
+and shapes (so state dicts load unchanged), reset_parameters, and its forward
+contract x [B, T, C] -> (out [B, T, output_dim], indices [B, T, heads * knn]).
+The two hot steps run on gfx950 HIP kernels:
+
+  * get_indices: sub-key scores on MFMA, per-half top-k and the cartesian
+    top-k fused in one kernel (modelos_amd.product_keys), with a sparse
+    backward through the embedding-bag kernels on the key table;
+  * the value read: the weighted embedding bag (xFormerEmbeddingBag).
+
+The query network, softmax and the swilu/value projections are ordinary
+torch ops around them (GEMMs on the vendor BLAS).
+
+Reference: pkm/memory.py:15-28 (ProductKeyArgs), :37-248 (HashingMemory),
+:250-289 (get_indices), :292-349 (QueryMLP).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from logging import getLogger
+from typing import Optional
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from ..product_keys import product_key_topk
+from .colwise_embedding_bag import xFormerEmbeddingBag
+
+logger = getLogger()
+
+
+@dataclass
+class ProductKeyArgs:
+    """Model-config block of the PKM layers (pkm/memory.py:15-28)."""
+
+    is_enabled: bool = False
+    layers: str = ""
+    mem_n_keys: int = 1024
+    mem_heads: int = 4
+    mem_knn: int = 32
+    mem_share_values: bool = True
+    mem_k_dim: int = 512
+    mem_v_dim: int = -1
+    swilu_projection: bool = True
+    value_fixed_lr: Optional[float] = 0.001
+    mem_gated: bool = False
+    peer_variant: bool = False
+
+
+class AttrDict(dict):
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.__dict__ = self
+
+
+class HashingMemory(nn.Module):
+    """Product-key memory read (pkm/memory.py:37-248)."""
+
+    VALUES = None
+    EVAL_MEMORY = True
+
+    def __init__(
+        self,
+        input_dim,
+        output_dim,
+        value_fixed_lr=0.001,
+        mem_k_dim=512,
+        mem_v_dim=-1,
+        mem_heads=4,
+        mem_knn=32,
+        mem_share_values=True,
+        mem_n_keys=1024,
+        mem_query_bias=True,
+        mem_query_batchnorm=False,
+        mem_query_rmsnorm=True,
+        mem_gated=False,
+        mem_input_dropout=0.0,
+        mem_query_dropout=0.0,
+        mem_value_dropout=0.0,
+        peer_variant=False,
+        swilu_projection=True,
+    ):
+        # argument checks of the reference (memory.py:71-95)
+        assert mem_k_dim >= 2 and mem_k_dim % 2 == 0
+        assert 0 <= mem_input_dropout < 1 and 0 <= mem_query_dropout < 1 and 0 <= mem_value_dropout < 1
+        assert not (peer_variant and mem_v_dim > 0), (
+            "Cannot use PEER variant with a value dimension different from the input dimension (mem_v_dim=-1)"
+        )
+        assert mem_heads >= 2
+        if mem_query_batchnorm:
+            logger.warning(
+                "WARNING: if you use batch normalization, be sure that you use batches of sentences with the same "
+                "size at training time. Otherwise, the padding token will result in incorrect mean/variance "
+                "estimations in the BatchNorm layer."
+            )
+        assert not (mem_query_batchnorm and mem_query_rmsnorm), "Cannot use both batchnorm and rmsnorm"
+        super().__init__()
+        self.use_peer_variant = peer_variant
+        self.input_dim = input_dim
+        self.output_dim = output_dim
+        self.size = mem_n_keys**2
+        self.k_dim = mem_k_dim
+        self.v_dim = mem_v_dim if mem_v_dim > 0 else output_dim
+        self.swilu_proj = swilu_projection
+        self.v_proj = mem_v_dim > 0 or self.swilu_proj
+        self.heads = mem_heads
+        self.knn = mem_knn
+        self.input_dropout = mem_input_dropout
+        self.query_dropout = mem_query_dropout
+        self.value_dropout = mem_value_dropout
+
+        # keys: [2 * heads * n_keys, k_dim / 2]; key (h, c, i) is row (2h + c) * n_keys + i
+        self.keys = nn.Parameter(torch.zeros(2 * self.heads * int(self.size**0.5), self.k_dim // 2))
+
+        self.mem_share_values = mem_share_values
+        self.original = not self.mem_share_values or HashingMemory.VALUES is None
+        if self.original:
+            if not self.use_peer_variant:
+                self.values = xFormerEmbeddingBag(self.size, self.v_dim)
+            else:
+                self.values_u = nn.Embedding(self.size, self.v_dim)
+                self.values_v = nn.Embedding(self.size, self.v_dim)
+        else:
+            if not self.use_peer_variant:
+                self.values = None
+            else:
+                self.values_u = None
+                self.values_v = None
+        self.value_fixed_lr = value_fixed_lr
+
+        if self.v_proj:
+            proj_input = mem_v_dim
+            if self.swilu_proj and proj_input < 0:
+                proj_input = output_dim
+            self.value_proj = nn.Linear(proj_input, output_dim)
+        if self.swilu_proj:
+            self.swilu_projection = nn.Linear(self.input_dim, proj_input)
+        self.gating = nn.Linear(input_dim, 1) if mem_gated else None
+
+        self.query_proj = QueryMLP(
+            self.input_dim,
+            self.heads,
+            self.k_dim,
+            (self.input_dim, self.heads * self.k_dim),
+            bias=mem_query_bias,
+            batchnorm=mem_query_batchnorm,
+            rmsnorm=mem_query_rmsnorm,
+        )
+
+    def reset_parameters(self, init_std=None, factor=1.0):
+        """Initialisation of the reference (memory.py:169-188)."""
+        bound = 1 / math.sqrt(self.k_dim)
+        nn.init.uniform_(self.keys, a=-bound, b=bound)
+        if self.original:
+            if not self.use_peer_variant:
+                nn.init.normal_(self.values.weight, mean=0, std=self.v_dim**-0.5)
+            else:
+                nn.init.normal_(self.values_u.weight, mean=0, std=self.v_dim**-0.5)
+                nn.init.normal_(self.values_v.weight, mean=0, std=self.v_dim**-0.5)
+        nn.init.xavier_uniform_(self.query_proj.query_mlps[0].weight)
+        if self.v_proj:
+            nn.init.normal_(self.value_proj.weight, mean=0, std=self.output_dim**-0.5)
+        if self.swilu_proj:
+            nn.init.normal_(self.swilu_projection.weight, mean=0, std=self.output_dim**-0.5)
+        if self.gating is not None:
+            nn.init.normal_(self.gating.weight, mean=0, std=self.input_dim**-0.5)
+
+    def forward(self, input):
+        """x [B, T, C] -> (out [B, T, output_dim], indices [B, T, heads * knn]) (memory.py:190-248)."""
+        B, T, C = input.shape
+        input = input.view(-1, self.input_dim)
+        bs = input.shape[0]
+        input = F.dropout(input, p=self.input_dropout, training=self.training)
+        query = self.query_proj(input)  # [bs * heads, k_dim]
+        query = F.dropout(query, p=self.query_dropout, training=self.training)
+        assert query.shape == (bs * self.heads, self.k_dim)
+
+        knn = self.knn
+        scores, indices = self.get_indices(query, knn)  # [bs * heads, knn] each
+
+        if not self.training and HashingMemory.EVAL_MEMORY:
+            # usage statistics, eval mode only (memory.py:212-215)
+            self.last_indices = indices.view(bs, self.heads, knn).detach().cpu()
+            self.last_scores = scores.view(bs, self.heads, knn).detach().cpu().float()
+
+        # softmax over each head's knn scores in float32 (memory.py:218)
+        scores = F.softmax(scores.float(), dim=-1).type_as(scores)
+        indices = indices.view(bs, self.heads * knn)
+        scores = scores.view(bs, self.heads * knn)
+
+        if not self.use_peer_variant:
+            output = self.values(indices, scores)  # [bs, v_dim]
+            if self.v_proj and not self.swilu_proj:
+                output = self.value_proj(output)
+            if self.swilu_proj:
+                output = self.value_proj(output * F.silu(self.swilu_projection(input)))
+        else:
+            # PEER variant (memory.py:231-237): per-slot expert vectors
+            u = self.values_u(indices)  # [bs, heads * knn, v_dim]
+            x = torch.bmm(u, input.unsqueeze(-1)).squeeze(-1)
+            x = F.gelu(x) * scores
+            v = self.values_v(indices)
+            output = torch.bmm(x.unsqueeze(1), v).squeeze(1)
+
+        output = F.dropout(output, p=self.value_dropout, training=self.training)
+        output = output.view(B, T, self.v_dim)
+        if self.gating:
+            output = F.sigmoid(self.gating(input)).view(B, T, 1) * output
+        return output.view(B, T, -1), indices.view(B, T, -1)
+
+    def get_indices(self, query, knn):
+        """(scores, indices) [bs * heads, knn]: the best knn product keys per
+        (token, head), best first (memory.py:250-289). One fused HIP kernel;
+        equal scores are ordered by the smaller sub-key position."""
+        assert query.dim() == 2 and query.size(1) == self.k_dim
+        return product_key_topk(query, self.keys, self.heads, knn, "dot")
+
+
+class QueryMLP(nn.Module):
+    """Query network: Linear (+ReLU chain) then BatchNorm / RMSNorm (memory.py:292-349)."""
+
+    def __init__(self, input_dim, heads, k_dim, sizes, bias=False, batchnorm=False, rmsnorm=False):
+        super().__init__()
+        self.input_dim = input_dim
+        self.heads = heads
+        self.k_dim = k_dim
+        self.sizes = sizes
+        assert sizes[0] == input_dim
+        assert sizes[-1] == (heads * k_dim)
+        self.query_mlps = QueryMLP.mlp(list(sizes), bias=bias)
+        if batchnorm:
+            self.norm = nn.BatchNorm1d(sizes[-1], affine=True, eps=1e-6, momentum=0.1)
+        elif rmsnorm:
+            from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+            self.norm = Qwen3RMSNorm(sizes[-1], eps=1e-6)
+        else:
+            self.norm = None
+
+    @staticmethod
+    def mlp(sizes, bias=True):
+        assert len(sizes) >= 2
+        layers = []
+        n = len(sizes) - 1
+        for i in range(n):
+            layers.append(nn.Linear(sizes[i], sizes[i + 1], bias=bias))
+            if i < n - 1:
+                layers.append(nn.ReLU())
+        return nn.Sequential(*layers)
+
+    def forward(self, input):
+        assert input.shape[-1] == self.input_dim
+        input = input.contiguous().view(-1, self.input_dim) if input.dim() > 2 else input
+        bs = len(input)
+        query = self.query_mlps(input)
+        if self.norm is not None:
+            query = self.norm(query)
+        assert query.shape == (bs, self.heads * self.k_dim)
+        return query.view(bs * self.heads, self.k_dim)

@@ -37,8 +37,8 @@ def sub_scores(query: torch.Tensor, keys: torch.Tensor, heads: int, score_type: 
     """Sub-key scores s_0, s_1 [N, H, n], computed in float64 from the stored
     inputs and rounded once to out_dtype (default: the input dtype).
     Reference: memory.py:262-268 (dot), fwpkm.py:853-869 (dot / idw)."""
-    N = query.shape[0]
     k = query.shape[-1]
+    N = query.numel() // (heads * k)  # query [N, H, k] or [N * H, k]
     half = k // 2
     q = query.reshape(N, heads, k).to(torch.float64)
     K = keys.to(torch.float64).reshape(heads, 2, -1, half)

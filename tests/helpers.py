@@ -26,15 +26,16 @@ def eb_inputs(B, L, K, D, dtype, seed=0, psw=True, psw_dtype=None, softmax=True,
 REL_TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3, torch.float64: 1e-12}
 
 
-def assert_rel_close(actual: torch.Tensor, expected: torch.Tensor, rel: float, what: str = ""):
-    """Element-wise |a - e| <= rel * |e| + rel * max|e|: relative error with an
-    absolute floor at the tensor's scale (sums with cancellation)."""
+def assert_rel_close(actual: torch.Tensor, expected: torch.Tensor, rel: float, what: str = "", atol: float = 0.0):
+    """Element-wise |a - e| <= rel * |e| + rel * max|e| + atol: relative error
+    with an absolute floor at the tensor's scale (sums with cancellation);
+    atol covers tensors that are zero up to rounding."""
     a = actual.detach().to("cpu", torch.float64)
     e = expected.detach().to("cpu", torch.float64)
     assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
     scale = e.abs().max().item() if e.numel() else 0.0
     err = (a - e).abs()
-    bound = rel * e.abs() + rel * scale + 1e-30
+    bound = rel * e.abs() + rel * scale + atol + 1e-30
     bad = err > bound
     if bad.any():
         i = int(bad.reshape(-1).nonzero()[0])

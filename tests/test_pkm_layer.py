@@ -1,0 +1,162 @@
+"""HashingMemory (the PKM layer) against the reference's own outputs.
+
+tests/golden/pkm_layer_*.pt were written by the reference's HashingMemory
+(pkm/memory.py) on the CPU by tests/golden/make_pkm_layer_golden.py: explicit
+parameters, input, upstream gradient, outputs, indices and every gradient.
+
+CPU: the oracle's functional restatement (oracle/pkm_layer.py) reproduces
+the fixtures; the drop-in module has the reference's parameter names/shapes.
+GPU: the drop-in HashingMemory on the HIP kernels reproduces the fixtures
+(float32, 1e-5 relative; indices exact), and matches the oracle in bf16 at a
+larger shape (2e-2 relative, evaluated at the kernel's selection).
+"""
+from __future__ import annotations
+
+import hashlib
+from pathlib import Path
+
+import pytest
+import torch
+
+from modelos_amd.pkm.memory import HashingMemory
+from oracle import pkm_layer
+from tests.helpers import REL_TOL, assert_rel_close, gen
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+CASES = ["rmsnorm", "batchnorm"]
+
+
+def _load(case):
+    rec = torch.load(GOLDEN / f"pkm_layer_{case}.pt", weights_only=True)
+    cfg = rec["config"].tolist()
+    kw = dict(input_dim=cfg[0], output_dim=cfg[1], mem_k_dim=cfg[2], mem_heads=cfg[3], mem_knn=cfg[4],
+              mem_n_keys=cfg[5], mem_query_batchnorm=bool(cfg[6]), mem_query_rmsnorm=not bool(cfg[6]))
+    params = {k[len("param."):]: v for k, v in rec.items() if k.startswith("param.")}
+    return rec, kw, params
+
+
+def _atol(name, kw, rec):
+    """The query bias feeds a train-mode BatchNorm, which removes it: its
+    gradient is zero up to rounding, so it is compared on the scale of the
+    query weight's gradient."""
+    if kw["mem_query_batchnorm"] and name == "query_proj.query_mlps.0.bias":
+        return 1e-5 * rec["grad.query_proj.query_mlps.0.weight"].abs().max().item()
+    return 0.0
+
+
+def _dense_grad(rec, name, like):
+    if "grad_rows." + name in rec:
+        g = torch.zeros_like(like)
+        g[rec["grad_rows." + name]] = rec["grad." + name]
+        return g
+    return rec["grad." + name]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_golden_integrity(case):
+    rec, _, _ = _load(case)
+    digest = hashlib.sha256(rec["x"].contiguous().numpy().tobytes()).digest()
+    assert bytes(rec["sha256.x"].tolist()) == digest
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_oracle_matches_reference_golden(case):
+    rec, kw, params = _load(case)
+    P = {k: v.clone().requires_grad_(True) for k, v in params.items()}
+    x = rec["x"].clone().requires_grad_(True)
+    out, idx = pkm_layer.hashing_memory_forward(x, P, kw["mem_heads"], kw["mem_knn"], kw["mem_query_batchnorm"])
+    assert torch.equal(idx, rec["indices"])
+    assert_rel_close(out, rec["out"], 1e-5, "out")
+    out.backward(rec["dout"])
+    assert_rel_close(x.grad, rec["dx"], 1e-5, "dx")
+    for name, p in P.items():
+        assert_rel_close(p.grad, _dense_grad(rec, name, p), 1e-5, f"grad {name}", _atol(name, kw, rec))
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_module_state_dict_matches_reference(case):
+    _, kw, params = _load(case)
+    mem = HashingMemory(**kw)
+    names = {n: tuple(p.shape) for n, p in mem.named_parameters()}
+    assert names == {n: tuple(v.shape) for n, v in params.items()}
+    mem.load_state_dict(params, strict=False)  # BatchNorm buffers are not parameters
+
+
+def _module_from_golden(case, device):
+    rec, kw, params = _load(case)
+    mem = HashingMemory(**kw).to(device)
+    with torch.no_grad():
+        for n, p in mem.named_parameters():
+            p.copy_(params[n])
+    mem.train()
+    return rec, kw, mem
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES)
+def test_layer_matches_reference_golden(device, case):
+    rec, kw, mem = _module_from_golden(case, device)
+    x = rec["x"].to(device).requires_grad_(True)
+    out, idx = mem(x)
+    assert torch.equal(idx.cpu(), rec["indices"])
+    assert_rel_close(out.cpu(), rec["out"], 1e-5, "out")
+    out.backward(rec["dout"].to(device))
+    assert_rel_close(x.grad.cpu(), rec["dx"], 1e-5, "dx")
+    for name, p in mem.named_parameters():
+        assert_rel_close(p.grad.cpu(), _dense_grad(rec, name, p.detach().cpu()), 1e-5, f"grad {name}",
+                         _atol(name, kw, rec))
+
+
+@pytest.mark.gpu
+def test_layer_bf16_vs_oracle(device):
+    """bf16 layer at 8 heads x 256 keys/half, k_dim 512, knn 32 (the layer's
+    head shape on a smaller table), RMSNorm query: outputs and every gradient
+    within 2e-2 of the float64 oracle evaluated at the kernel's selection."""
+    torch.manual_seed(0)
+    kw = dict(input_dim=256, output_dim=256, mem_k_dim=512, mem_heads=8, mem_knn=32, mem_n_keys=256)
+    mem = HashingMemory(**kw)
+    mem.reset_parameters()
+    mem = mem.to(device=device, dtype=torch.bfloat16).train()
+    g = gen(21)
+    x = torch.randn((2, 64, 256), generator=g).to(torch.bfloat16)
+    dout = torch.randn((2, 64, 256), generator=g).to(torch.bfloat16)
+    xd = x.to(device).requires_grad_(True)
+    out, idx = mem(xd)
+    out.backward(dout.to(device))
+
+    P = {n: p.detach().cpu().double().requires_grad_(True) for n, p in mem.named_parameters()}
+    x64 = x.double().requires_grad_(True)
+    e_out, _ = pkm_layer.hashing_memory_forward(x64, P, 8, 32, idx=idx.cpu().view(-1, 32))
+    e_out.backward(dout.double())
+    tol = REL_TOL[torch.bfloat16]
+    assert_rel_close(out.cpu(), e_out, tol, "out")
+    assert_rel_close(xd.grad.cpu(), x64.grad, tol, "dx")
+    for name, p in mem.named_parameters():
+        assert_rel_close(p.grad.cpu(), P[name].grad, tol, f"grad {name}")
+
+
+@pytest.mark.gpu
+def test_layer_eval_mode_records_usage(device):
+    _, kw, mem = _module_from_golden("rmsnorm", device)
+    mem.eval()
+    rec, _, _ = _load("rmsnorm")
+    with torch.no_grad():
+        _, idx = mem(rec["x"].to(device))
+    assert mem.last_indices.shape == (rec["x"].shape[0] * rec["x"].shape[1], kw["mem_heads"], kw["mem_knn"])
+    assert torch.equal(mem.last_indices.view(idx.shape), idx.cpu())
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_reference_op_sequence_matches_golden(case):
+    """The op-for-op CPU path timed as the CPU baseline reproduces the fixtures."""
+    rec, kw, params = _load(case)
+    P = {k: v.clone().requires_grad_(True) for k, v in params.items()}
+    x = rec["x"].clone().requires_grad_(True)
+    out, idx = pkm_layer.hashing_memory_forward(x, P, kw["mem_heads"], kw["mem_knn"], kw["mem_query_batchnorm"],
+                                                reference_ops=True)
+    assert torch.equal(idx, rec["indices"])
+    assert_rel_close(out, rec["out"], 1e-5, "out")
+    out.backward(rec["dout"])
+    assert_rel_close(x.grad, rec["dx"], 1e-5, "dx")
+    for name, p in P.items():
+        assert_rel_close(p.grad, _dense_grad(rec, name, p), 1e-5, f"grad {name}", _atol(name, kw, rec))
