@@ -2,77 +2,90 @@
 //
 // For every (token t, head h):
 //   s_c[i] = score(q[t, h, c*half:(c+1)*half], keys[(2h+c)*n + i, :])   c = 0, 1; i < n
-//            score = dot product, or idw: -log(1e-3 + |q - k|^2)
+//            score = dot product, or idw: -log(1e-3 + max(|q|^2 + |k|^2 - 2<q,k>, 0))
 //   (v_c, i_c) = top-knn of s_c, sorted best first
-//   cand[a, c'] = v_0[a] + v_1[c'],  id = i_0[a] * n + i_1[c']
+//   cand[a, b] = v_0[a] + v_1[b],  id = i_0[a] * n + i_1[b]
 //   (scores, ids) = top-knn of cand, sorted best first
 // Reference: HashingMemory.get_indices (pkm/memory.py:250-289) and
 // FastWeightProductKeyMemory.get_indices / compute_qk_scores (fwpkm/fwpkm.py:853-934).
 // Rounding follows the reference's tensors: sub-scores are stored in the
 // input dtype (a bf16 einsum output), the cartesian sums are rounded to it
 // again (bf16 + bf16 in ATen), and top-k selects on the rounded values.
-// Ties are broken by the smaller index (sub-key index, then flat a*knn + c'),
-// which only matters for inputs the reference's topk leaves unspecified.
+// Equal values are ordered by the smaller index (sub-key index, then flat
+// a*knn + b), an order the reference's topk leaves unspecified.
 //
-// One workgroup (4 waves) owns TM tokens of one head:
-//   A. scores of one half for all n keys on MFMA (16x16x32 bf16 / 16x16x4 f32),
-//      rounded and parked in LDS ([TM][n]);
-//   B. exact top-knn of each row by one wave: bit-by-bit threshold search with
-//      wave ballots, compaction of the selected entries, 64-lane bitonic sort;
-//   C. per token, the cartesian candidates restricted to (a+1)(c+1) <= knn —
-//      every other pair is dominated by at least knn pairs that precede it in
-//      (value, flat index) order, so this is exact, ties included — and the
-//      same exact top-knn.
+// One workgroup (8 waves) owns TM tokens of one head; per half:
+//   A. The half of the TM queries is staged in LDS. Each wave streams its own
+//      1/8 of the key tiles from L2 (16-byte loads, keys read once per
+//      workgroup) and computes the [TM x 16] score tiles on MFMA
+//      (16x16x32 bf16 / 16x16x4 f32); the epilogue rounds the scores into the
+//      LDS score tile [TM][n] and keeps, per row, the exact maximum of each of
+//      G = min(n, 128) column groups (group = column mod 128) in registers.
+//   B. Per row (one wave): T0 = knn-th largest group maximum is a lower bound
+//      of the knn-th largest score (knn groups each hold a score >= T0), so
+//      the top-knn are among the scores >= T0 — about 1.1 knn of them on
+//      random data. They are compacted with wave ballots as unique 32-bit keys
+//      (order-preserving value bits, then the inverted index), and one 64-lane
+//      bitonic sort orders them; with more than 64 (128) candidates an exact
+//      threshold search over all of the row's keys takes over.
+//   C. (after the second half) per token, the cartesian candidates restricted
+//      to the pairs (a+1)(b+1) <= knn — every other pair is preceded, in
+//      (value, flat index) order, by at least knn pairs — keyed the same way
+//      and selected by an exact threshold search plus the bitonic sort.
+// Workgroups map head-fastest onto the grid, so with 8 heads each XCD (and its
+// L2) serves one head's keys.
 #include <atomic>
 
 #include "pkm_common.h"
 
 namespace pkm {
 
-// Order-preserving map float -> uint32 (a < b  <=>  key(a) < key(b)); key 0 is below every number.
-__device__ __forceinline__ uint32_t float_key(float f) {
-  const uint32_t b = __float_as_uint(f);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float key_float(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-template <typename T>
-struct ScoreIO;
-template <>
-struct ScoreIO<float> {
-  static constexpr int LO_BIT = 0;  // all 32 key bits are significant
-  static __device__ __forceinline__ float round(float x) { return x; }
-  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
-  static __device__ __forceinline__ void store(float* p, int64_t i, float x) { p[i] = x; }
-};
-template <>
-struct ScoreIO<bf16_t> {
-  static constexpr int LO_BIT = 16;  // bf16 values: the low 16 bits of the float are zero
-  static __device__ __forceinline__ float round(float x) { return bf16_to_f32(f32_to_bf16_bits(x)); }
-  static __device__ __forceinline__ float load(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i].x); }
-  static __device__ __forceinline__ void store(bf16_t* p, int64_t i, float x) { p[i].x = (uint16_t)f32_to_bf16_bits(x); }
-};
-
-// MFMA fragments along k for C[16 x 16] += A[16 x KSTEP] * B[KSTEP x 16]:
-// lane l holds row/col l % 16 and the k chunk (l / 16).
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-template <typename T>
-struct Mfma;
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxNV = 32;        // n_keys <= 2048 (32 keys per lane in a 64-lane row scan)
+constexpr int kMaxPairSlots = 5;  // knn = 64 -> 280 candidate pairs
+constexpr int kCandCap = 128;     // row candidates kept before the exact fallback
+constexpr int kMaxLds = 160 * 1024;
+
+// ---------------------------------------------------------------------------
+// Order keys: monotone maps of the stored score bits to unsigned integers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t okey16(uint32_t b) { return b ^ ((b & 0x8000u) ? 0xFFFFu : 0x8000u); }
+__device__ __forceinline__ uint32_t okey16_inv(uint32_t k) { return k ^ ((k & 0x8000u) ? 0x8000u : 0xFFFFu); }
+__device__ __forceinline__ uint32_t okey32(uint32_t b) {
+  return b ^ ((b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
+}
+__device__ __forceinline__ uint32_t okey32_inv(uint32_t k) {
+  return k ^ ((k & 0x80000000u) ? 0x80000000u : 0xFFFFFFFFu);
+}
+
+// Per storage type: score tile element, unique selection key, MFMA step.
+template <typename TIN>
+struct Sel;
+
 template <>
-struct Mfma<bf16_t> {
-  static constexpr int KSTEP = 32;
-  typedef uint4 frag;
-  static __device__ __forceinline__ frag load(const bf16_t* row, int k0, int lane) {
-    return ld16(row + k0 + 8 * (lane >> 4));
+struct Sel<bf16_t> {
+  typedef uint16_t Store;
+  typedef uint32_t Key;  // (16-bit order key << 16) | (0xFFFF - index)
+  static constexpr int KSTEP = 32;  // k per 16-byte fragment: one 16x16x32 MFMA
+  static __device__ __forceinline__ Store to_store(float v) { return (Store)f32_to_bf16_bits(v + 0.0f); }
+  static __device__ __forceinline__ uint32_t okey(Store s) { return okey16(s); }
+  static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok; }  // 16-bit threshold key
+  static __device__ __forceinline__ Key make(uint32_t ok, uint32_t idx) { return (ok << 16) | (0xFFFFu - idx); }
+  static __device__ __forceinline__ uint32_t key_okey(Key k) { return k >> 16; }
+  static __device__ __forceinline__ uint32_t key_idx(Key k) { return 0xFFFFu - (k & 0xFFFFu); }
+  static __device__ __forceinline__ float value(uint32_t ok) { return bf16_to_f32(okey16_inv(ok)); }
+  static __device__ __forceinline__ uint32_t okey_of(float v) { return okey16(f32_to_bf16_bits(v + 0.0f)); }
+  static __device__ __forceinline__ void put(bf16_t* p, int64_t i, uint32_t ok) { p[i].x = (uint16_t)okey16_inv(ok); }
+  static __device__ __forceinline__ void put_store(bf16_t* p, int64_t i, Store s) { p[i].x = s; }
+  static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                0, 0, 0);
   }
-  static __device__ __forceinline__ f32x4_t mma(const frag& a, const frag& b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ float sumsq(const frag& a) {
+  static __device__ __forceinline__ float sumsq(const uint4& a) {
     float f[8];
     VecTraits<bf16_t>::unpack(a, f);
     float s = 0.f;
@@ -81,255 +94,459 @@ struct Mfma<bf16_t> {
     return s;
   }
 };
+
 template <>
-struct Mfma<float> {
-  static constexpr int KSTEP = 4;
-  typedef float frag;
-  static __device__ __forceinline__ frag load(const float* row, int k0, int lane) { return row[k0 + (lane >> 4)]; }
-  static __device__ __forceinline__ f32x4_t mma(const frag& a, const frag& b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+struct Sel<float> {
+  typedef float Store;
+  typedef uint64_t Key;  // (32-bit order key << 32) | (0xFFFFFFFF - index)
+  static constexpr int KSTEP = 16;  // k per 16-byte fragment: four 16x16x4 MFMAs
+  static __device__ __forceinline__ Store to_store(float v) { return v + 0.0f; }
+  static __device__ __forceinline__ uint32_t okey(Store s) { return okey32(__float_as_uint(s)); }
+  static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok >> 16; }  // truncated: a lower bound
+  static __device__ __forceinline__ Key make(uint32_t ok, uint32_t idx) {
+    return ((uint64_t)ok << 32) | (uint64_t)(0xFFFFFFFFu - idx);
   }
-  static __device__ __forceinline__ float sumsq(const frag& a) { return a * a; }
+  static __device__ __forceinline__ uint32_t key_okey(Key k) { return (uint32_t)(k >> 32); }
+  static __device__ __forceinline__ uint32_t key_idx(Key k) { return 0xFFFFFFFFu - (uint32_t)k; }
+  static __device__ __forceinline__ float value(uint32_t ok) { return __uint_as_float(okey32_inv(ok)); }
+  static __device__ __forceinline__ uint32_t okey_of(float v) { return okey32(__float_as_uint(v + 0.0f)); }
+  static __device__ __forceinline__ void put(float* p, int64_t i, uint32_t ok) { p[i] = __uint_as_float(okey32_inv(ok)); }
+  static __device__ __forceinline__ void put_store(float* p, int64_t i, Store s) { p[i] = s; }
+  // The 16 k values of a fragment pair: lane group g holds k = 4g + s in
+  // step s, for A and B alike (a permutation of the summation order).
+  static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float sumsq(const uint4& a) {
+    float s = __uint_as_float(a.x) * __uint_as_float(a.x);
+    s = __builtin_fmaf(__uint_as_float(a.y), __uint_as_float(a.y), s);
+    s = __builtin_fmaf(__uint_as_float(a.z), __uint_as_float(a.z), s);
+    return __builtin_fmaf(__uint_as_float(a.w), __uint_as_float(a.w), s);
+  }
 };
 
-// 64-lane bitonic sort, best first: larger key, then smaller index.
-__device__ __forceinline__ void bitonic64(uint32_t& key, uint32_t& idx) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const uint32_t pk = (uint32_t)__shfl_xor((int)key, j);
-      const uint32_t pi = (uint32_t)__shfl_xor((int)idx, j);
-      const bool p_better = pk > key || (pk == key && pi < idx);
-      const bool lower = (lane & j) == 0;
-      const bool best_first = (lane & k) == 0;
-      const bool take = (lower == best_first) ? p_better : !p_better;
-      if (take) {
-        key = pk;
-        idx = pi;
-      }
-    }
-  }
+// ---------------------------------------------------------------------------
+// Wave-level selection on unique keys (larger = better).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t shfl_key(uint32_t v, int src) { return (uint32_t)__shfl((int)v, src); }
+__device__ __forceinline__ uint64_t shfl_key(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src), hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t xor_key(uint32_t v, int m) { return (uint32_t)__shfl_xor((int)v, m); }
+__device__ __forceinline__ uint64_t xor_key(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
 }
 
-// Exact top-knn (knn <= 64) of NV keys per lane. Slot (v, lane) has index
-// v * 64 + lane and slots must be ordered like indices (ties go to the smaller
-// index). Lane j < knn returns the j-th best (key, slot index); other lanes key 0.
-template <int NVMAX>
-__device__ __forceinline__ void wave_topk(const uint32_t* key, int NV, int knn, int lo_bit, uint2* scratch,
-                                          uint32_t& okey, uint32_t& oslot) {
+// Sorts one key per lane, largest first (lane 0 = best).
+template <typename Key>
+__device__ __forceinline__ Key bitonic64_desc(Key k) {
   const int lane = threadIdx.x & 63;
-  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-  // Bits below lo_bit carry no order (keys of bf16 values: 0 for positive,
-  // all ones for negative values); compare on the masked keys.
-  const uint32_t mask = ~((1u << lo_bit) - 1u);
-  // T = the largest masked value with at least knn keys >= T
-  uint32_t T = 0;
-  for (int bit = 31; bit >= lo_bit; --bit) {
-    const uint32_t trial = T | (1u << bit);
+#pragma unroll
+  for (int kk = 2; kk <= 64; kk <<= 1) {
+#pragma unroll
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      const Key p = xor_key(k, j);
+      const bool keep_max = ((lane & j) == 0) == ((lane & kk) == 0);
+      k = keep_max ? (p > k ? p : k) : (p < k ? p : k);
+    }
+  }
+  return k;
+}
+
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int lane = threadIdx.x & 63;
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
+
+// Exact top-knn (knn <= 64) of the unique keys keys[s] (slots s < ns, key 0 =
+// empty, at least knn nonzero keys). Returns the lane's rank in best-first
+// order (lanes >= knn: 0). scr: 64 keys of this wave's LDS scratch.
+template <typename Key, int NS>
+__device__ __forceinline__ Key wave_topk_unique(const Key* keys, int ns, int knn, Key* scr) {
+  constexpr int BITS = 8 * (int)sizeof(Key);
+  Key T = 0;
+  for (int bit = BITS - 1; bit >= 0; --bit) {
+    const Key trial = T | ((Key)1 << bit);
     uint32_t c = 0;
 #pragma unroll
-    for (int v = 0; v < NVMAX; ++v)
-      if (v < NV) c += (uint32_t)__popcll(__ballot(key[v] >= trial));
-    if (c >= (uint32_t)knn) T = trial;
+    for (int s = 0; s < NS; ++s)
+      if (s < ns) c += (uint32_t)__popcll(__ballot(keys[s] >= trial));
+    if (c >= (uint32_t)knn) {
+      T = trial;
+      if (c == (uint32_t)knn) break;  // {keys >= T} is exactly the top-knn
+    }
   }
-  uint32_t gt = 0;
+  const uint64_t below = lanes_below();
+  uint32_t base = 0;
 #pragma unroll
-  for (int v = 0; v < NVMAX; ++v)
-    if (v < NV) gt += (uint32_t)__popcll(__ballot((key[v] & mask) > T));
-  const uint32_t need_eq = (uint32_t)knn - gt;
-  // compaction in slot order: every key > T and the first need_eq keys == T
-  uint32_t base = 0, eq_seen = 0;
-#pragma unroll
-  for (int v = 0; v < NVMAX; ++v) {
-    if (v < NV) {
-      const uint32_t km = key[v] & mask;
-      const bool is_gt = km > T, is_eq = km == T;
-      const uint64_t me = __ballot(is_eq);
-      const bool sel = is_gt || (is_eq && eq_seen + (uint32_t)__popcll(me & below) < need_eq);
-      const uint64_t ms = __ballot(sel);
-      if (sel) scratch[base + (uint32_t)__popcll(ms & below)] = make_uint2(key[v], (uint32_t)(v * 64 + lane));
-      base += (uint32_t)__popcll(ms);
-      eq_seen += (uint32_t)__popcll(me);
+  for (int s = 0; s < NS; ++s) {
+    if (s < ns) {
+      const bool sel = keys[s] >= T;
+      const uint64_t m = __ballot(sel);
+      if (sel) scr[base + (uint32_t)__popcll(m & below)] = keys[s];
+      base += (uint32_t)__popcll(m);
     }
   }
   __builtin_amdgcn_wave_barrier();
-  okey = 0;
-  oslot = 0xFFFFFFFFu;
-  if (lane < knn) {
-    const uint2 e = scratch[lane];
-    okey = e.x;
-    oslot = e.y;
-  }
+  const int lane = threadIdx.x & 63;
+  Key k = lane < knn ? scr[lane] : (Key)0;
   __builtin_amdgcn_wave_barrier();
-  bitonic64(okey, oslot);
+  return bitonic64_desc(k);
 }
 
-constexpr int kMaxNV = 32;  // n <= 2048 keys per half
-constexpr int kMaxPairSlots = 5;  // knn = 64 -> 280 candidate pairs
-constexpr int kMaxLds = 160 * 1024;  // LDS per CU on gfx950
+// The same selection over a whole row of the LDS score tile (NV keys per
+// lane, recomputed from the tile in every pass instead of held in registers):
+// the exact path for rows whose threshold admits more than kCandCap scores.
+template <typename TIN>
+__device__ __noinline__ typename Sel<TIN>::Key wave_topk_row(const typename Sel<TIN>::Store* Srow, int row, int NV,
+                                                             int knn, typename Sel<TIN>::Key* scr);
 
-template <typename TIN, int IDW>
-__global__ __launch_bounds__(256) void pkm_score_topk_kernel(const TIN* __restrict__ Q, const TIN* __restrict__ Kt,
-                                                             int64_t Ntok, int H, int n, int half, int knn, int TM,
-                                                             TIN* __restrict__ out_scores,
-                                                             int64_t* __restrict__ out_idx,
-                                                             int64_t* __restrict__ out_i1, int64_t* __restrict__ out_i2,
-                                                             TIN* __restrict__ out_s1, TIN* __restrict__ out_s2) {
+// ---------------------------------------------------------------------------
+// LDS layout (host and device agree through score_lds_layout).
+// ---------------------------------------------------------------------------
+struct ScoreLds {
+  int s_bytes;     // score tile [TM][n]
+  int r_bytes;     // shared region: query stage, later group maxima + scratch
+  int gmax_bytes;  // [TM][G] uint16 threshold keys of the group maxima
+  int total;
+};
+
+__host__ __device__ inline int score_groups(int n) { return n < 128 ? n : 128; }
+
+__host__ __device__ inline ScoreLds score_lds_layout(int TM, int n, int half, int esz, int key_bytes) {
+  ScoreLds L;
+  L.s_bytes = ((TM * n * esz) + 15) & ~15;
+  L.gmax_bytes = ((TM * score_groups(n) * 2) + 15) & ~15;
+  const int q_bytes = TM * half * esz;
+  const int sel_bytes = L.gmax_bytes + kWaves * kCandCap * key_bytes;
+  L.r_bytes = q_bytes > sel_bytes ? q_bytes : sel_bytes;
+  L.total = L.s_bytes + L.r_bytes;
+  return L;
+}
+
+// Largest power of two (<= 8) dividing `chunks`, minus one: the XOR mask of
+// the query-stage chunk swizzle (stays inside the row).
+__host__ __device__ inline int chunk_swizzle_mask(int chunks) {
+  int m = 1;
+  while (m < 8 && chunks % (2 * m) == 0) m *= 2;
+  return m - 1;
+}
+
+// Column swizzle of the score tile: the 4 rows an MFMA store writes at once
+// (rows 4g + e, g = 0..3) land in different LDS banks.
+__device__ __forceinline__ int s_phys(int row, int col) { return col ^ (((row >> 2) & 3) << 4); }
+
+template <typename TIN>
+__device__ __noinline__ typename Sel<TIN>::Key wave_topk_row(const typename Sel<TIN>::Store* Srow, int row, int NV,
+                                                             int knn, typename Sel<TIN>::Key* scr) {
+  typedef Sel<TIN> SL;
+  typedef typename SL::Key Key;
+  constexpr int BITS = 8 * (int)sizeof(Key);
+  const int lane = threadIdx.x & 63;
+  Key T = 0;
+  for (int bit = BITS - 1; bit >= 0; --bit) {
+    const Key trial = T | ((Key)1 << bit);
+    uint32_t c = 0;
+    for (int e = 0; e < NV; ++e) {
+      const int col = 64 * e + lane;
+      const Key k = SL::make(SL::okey(Srow[s_phys(row, col)]), (uint32_t)col);
+      c += (uint32_t)__popcll(__ballot(k >= trial));
+    }
+    if (c >= (uint32_t)knn) {
+      T = trial;
+      if (c == (uint32_t)knn) break;
+    }
+  }
+  const uint64_t below = lanes_below();
+  uint32_t base = 0;
+  for (int e = 0; e < NV; ++e) {
+    const int col = 64 * e + lane;
+    const Key k = SL::make(SL::okey(Srow[s_phys(row, col)]), (uint32_t)col);
+    const bool sel = k >= T;
+    const uint64_t m = __ballot(sel);
+    if (sel) scr[base + (uint32_t)__popcll(m & below)] = k;
+    base += (uint32_t)__popcll(m);
+  }
+  __builtin_amdgcn_wave_barrier();
+  Key k = lane < knn ? scr[lane] : (Key)0;
+  __builtin_amdgcn_wave_barrier();
+  return bitonic64_desc(k);
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.
+// ---------------------------------------------------------------------------
+template <typename TIN, int IDW, int TM>
+__global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
+    const TIN* __restrict__ Q, const TIN* __restrict__ Kt, int64_t Ntok, int H, int n, int half, int knn,
+    TIN* __restrict__ out_scores, int64_t* __restrict__ out_idx, int64_t* __restrict__ out_i1,
+    int64_t* __restrict__ out_i2, TIN* __restrict__ out_s1, TIN* __restrict__ out_s2) {
+  typedef Sel<TIN> SL;
+  typedef typename SL::Store Store;
+  typedef typename SL::Key Key;
+  constexpr int RT = TM / 16;  // row tiles
+  constexpr int CB = 4;        // column tiles per batch
   extern __shared__ __align__(16) unsigned char smem[];
-  typedef Mfma<TIN> M;
+
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  const int64_t t0 = (int64_t)blockIdx.x * TM;
-  const int h = blockIdx.y;
+  const int h = (int)(blockIdx.x % (unsigned)H);
+  const int64_t t0 = (int64_t)(blockIdx.x / (unsigned)H) * TM;
+  const int esz = (int)sizeof(Store);
+  const ScoreLds L = score_lds_layout(TM, n, half, esz, (int)sizeof(Key));
+  Store* S = (Store*)smem;
+  unsigned char* R = smem + L.s_bytes;
+  uint4* QS = (uint4*)R;                               // phase A: query stage
+  uint16_t* GM = (uint16_t*)R;                         // phase B: group maxima
+  Key* scr = (Key*)(R + L.gmax_bytes) + w * kCandCap;  // phase B/C: this wave's scratch
+
   const int kdim = 2 * half;
-  TIN* S = (TIN*)smem;  // [TM][n] rounded scores of the current half
-  const size_t s_bytes = (((size_t)TM * n * sizeof(TIN)) + 15) & ~(size_t)15;
-  uint2* lists = (uint2*)(smem + s_bytes);    // [TM][2][64] (key, sub-key index), best first
-  uint2* scratch = lists + (size_t)TM * 2 * 64;  // [4][64]
-  uint32_t* pairs = (uint32_t*)(scratch + 4 * 64);  // candidate pairs (a << 16 | c), a-major
-
-  // candidate pair table: all (a, c) with (a + 1) * (c + 1) <= knn
-  int npairs = 0;
-  for (int a = 0; a < knn; ++a) npairs += knn / (a + 1);
-  if (w == 0) {
-    const int cnt = lane < knn ? knn / (lane + 1) : 0;
-    int x = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o);
-      if (lane >= o) x += y;
-    }
-    const int off = x - cnt;
-    for (int c = 0; c < cnt; ++c) pairs[off + c] = ((uint32_t)lane << 16) | (uint32_t)c;
-  }
-
-  const int RT = TM / 16;
+  const int EPC = 16 / esz;        // elements per 16-byte chunk
+  const int CH = half / EPC;       // chunks per query half row
+  const int cmask = chunk_swizzle_mask(CH);
+  const int KS = half / SL::KSTEP;
   const int ncol = n / 16;
-  for (int hc = 0; hc < 2; ++hc) {
-    const TIN* Kc = Kt + (int64_t)(2 * h + hc) * n * half;  // [n][half]
-    // --- A: scores -> LDS
-    float qn[2] = {0.f, 0.f};  // squared norms of rows (lane % 16) of row tiles 0, 1 (idw)
-    if (IDW) {
-      for (int r = 0; r < RT; ++r) {
-        const int64_t t = t0 + r * 16 + (lane & 15);
-        float s = 0.f;
-        if (t < Ntok) {
-          const TIN* qrow = Q + (t * H + h) * kdim + hc * half;
-          for (int k0 = 0; k0 < half; k0 += M::KSTEP) s += M::sumsq(M::load(qrow, k0, lane));
-        }
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
-        qn[r] = s;
+  const int G = score_groups(n);
+  const int NV = n / 64;
+
+  // candidate pairs of the cartesian step: slot s -> (a, b), a-major, (a+1)(b+1) <= knn
+  int pa[kMaxPairSlots], pb[kMaxPairSlots];
+  int npairs = 0;
+#pragma unroll
+  for (int s = 0; s < kMaxPairSlots; ++s) pa[s] = pb[s] = 0;
+  for (int a = 0; a < knn; ++a) {
+    const int cnt = knn / (a + 1);
+#pragma unroll
+    for (int s = 0; s < kMaxPairSlots; ++s) {
+      const int slot = 64 * s + lane;
+      if (slot >= npairs && slot < npairs + cnt) {
+        pa[s] = a;
+        pb[s] = slot - npairs;
       }
     }
-    for (int j = w; j < ncol; j += 4) {
-      const TIN* krow = Kc + (int64_t)(j * 16 + (lane & 15)) * half;
-      f32x4_t acc[2];
-      acc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      float kn = 0.f;
-      for (int k0 = 0; k0 < half; k0 += M::KSTEP) {
-        const typename M::frag b = M::load(krow, k0, lane);
-        if (IDW) kn += M::sumsq(b);
-        for (int r = 0; r < RT; ++r) {
-          const int64_t t = t0 + r * 16 + (lane & 15);
-          typename M::frag a;
-          if (t < Ntok)
-            a = M::load(Q + (t * H + h) * kdim + hc * half, k0, lane);
-          else
-            a = typename M::frag{};
-          acc[r] = M::mma(a, b, acc[r]);
+    npairs += cnt;
+  }
+  const int NP = (npairs + 63) / 64;
+
+  for (int hc = 0; hc < 2; ++hc) {
+    const TIN* Kc = Kt + (int64_t)(2 * h + hc) * n * half;
+    // ---- A0: stage the query half [TM][half] (zeros past the last token)
+    for (int i = threadIdx.x; i < TM * CH; i += kThreads) {
+      const int r = i / CH, c = i - (i / CH) * CH;
+      const int64_t t = t0 + r;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (t < Ntok) v = ld16(Q + (t * H + h) * kdim + hc * half + c * EPC);
+      QS[r * CH + (c ^ (r & cmask))] = v;
+    }
+    __syncthreads();
+
+    // ---- A: scores of this wave's column tiles (w, w+8, ...), batches of CB
+    float gmax[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gmax[rt][e] = -__builtin_inff();
+    float qn[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) qn[rt] = 0.f;
+    bool have_qn = false;
+    for (int jb = 0;; ++jb) {
+      int tile[CB];
+      bool tv[CB];
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        tile[k] = w + kWaves * (CB * jb + k);
+        tv[k] = tile[k] < ncol;
+      }
+      if (!tv[0]) break;
+      const TIN* krow[CB];
+#pragma unroll
+      for (int k = 0; k < CB; ++k) krow[k] = Kc + (int64_t)(16 * (tv[k] ? tile[k] : 0) + (lane & 15)) * half;
+      f32x4_t acc[RT][CB];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int k = 0; k < CB; ++k) acc[rt][k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      float kn[CB] = {0.f, 0.f, 0.f, 0.f};
+      float qp[RT];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) qp[rt] = 0.f;
+      uint4 bnext[CB];
+#pragma unroll
+      for (int k = 0; k < CB; ++k)
+        bnext[k] = tv[k] ? ld16(krow[k] + (lane >> 4) * EPC) : make_uint4(0u, 0u, 0u, 0u);
+      for (int ks = 0; ks < KS; ++ks) {
+        uint4 b[CB];
+#pragma unroll
+        for (int k = 0; k < CB; ++k) b[k] = bnext[k];
+        if (ks + 1 < KS) {
+#pragma unroll
+          for (int k = 0; k < CB; ++k)
+            bnext[k] = tv[k] ? ld16(krow[k] + ((ks + 1) * 4 + (lane >> 4)) * EPC) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        const int c = ks * 4 + (lane >> 4);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const int r = rt * 16 + (lane & 15);
+          const uint4 a = QS[r * CH + (c ^ (r & cmask))];
+          if (IDW && !have_qn) qp[rt] += SL::sumsq(a);
+#pragma unroll
+          for (int k = 0; k < CB; ++k) SL::mma(a, b[k], acc[rt][k]);
+        }
+        if (IDW) {
+#pragma unroll
+          for (int k = 0; k < CB; ++k) kn[k] += SL::sumsq(b[k]);
         }
       }
       if (IDW) {
-        kn += __shfl_xor(kn, 16);
-        kn += __shfl_xor(kn, 32);  // every lane: norm of key (lane % 16) = its C column
-      }
-      const int col = j * 16 + (lane & 15);
-      for (int r = 0; r < RT; ++r) {
+        if (!have_qn) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = 4 * (lane >> 4) + e;  // row inside the tile
-          float s = acc[r][e];
-          if (IDW) {
-            const float qrow_n = __shfl(qn[r], row);
-            float d2 = qrow_n + kn - 2.f * s;
-            d2 = d2 > 0.f ? d2 : 0.f;
-            s = -logf(1e-3f + d2);
+          for (int rt = 0; rt < RT; ++rt) {
+            float s = qp[rt];
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            qn[rt] = s;  // squared norm of row rt*16 + (lane & 15)
           }
-          ScoreIO<TIN>::store(S, (int64_t)(r * 16 + row) * n + col, s);
+          have_qn = true;
+        }
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+          kn[k] += __shfl_xor(kn[k], 16);
+          kn[k] += __shfl_xor(kn[k], 32);  // squared norm of key 16*tile + (lane & 15)
+        }
+      }
+      // epilogue: round into the score tile, track the group maxima
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        if (!tv[k]) continue;
+        const int col = 16 * tile[k] + (lane & 15);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int rr = 4 * (lane >> 4) + e;  // row inside the tile
+            const int row = rt * 16 + rr;
+            float s = acc[rt][k][e];
+            if (IDW) {
+              float d2 = __shfl(qn[rt], rr) + kn[k] - 2.f * s;
+              d2 = d2 > 0.f ? d2 : 0.f;
+              s = -logf(1e-3f + d2);
+            }
+            gmax[rt][e] = s > gmax[rt][e] ? s : gmax[rt][e];
+            S[row * n + s_phys(row, col)] = SL::to_store(s);
+          }
         }
       }
     }
+    __syncthreads();  // score tile complete; the query stage is free
+    if (16 * w < G) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = rt * 16 + 4 * (lane >> 4) + e;
+          GM[row * G + 16 * w + (lane & 15)] = (uint16_t)SL::coarse(SL::okey(SL::to_store(gmax[rt][e])));
+        }
+    }
     __syncthreads();
-    // full sub-scores, when asked for (fast-weight PKM returns them)
+
+    // ---- B: exact top-knn of each row (and C after the second half)
     TIN* out_s = hc == 0 ? out_s1 : out_s2;
-    if (out_s != nullptr) {
-      for (int idx = threadIdx.x; idx < TM * n; idx += 256) {
-        const int r = idx / n, col = idx - (idx / n) * n;
-        const int64_t t = t0 + r;
-        if (t < Ntok) out_s[(t * H + h) * n + col] = S[idx];
+    for (int r = w; r < TM; r += kWaves) {
+      const int64_t t = t0 + r;
+      if (t >= Ntok) continue;
+      const int64_t th = t * H + h;
+      // T0: knn-th largest group maximum
+      const uint32_t gk0 = GM[r * G + lane];
+      const uint32_t gk1 = G > 64 ? GM[r * G + 64 + lane] : 0u;
+      uint32_t T0 = 0;
+      for (int bit = 15; bit >= 0; --bit) {
+        const uint32_t trial = T0 | (1u << bit);
+        uint32_t c = (uint32_t)__popcll(__ballot(gk0 >= trial));
+        if (G > 64) c += (uint32_t)__popcll(__ballot(gk1 >= trial));
+        if (c >= (uint32_t)knn) T0 = trial;
       }
-    }
-    // --- B: exact top-knn of every row
-    const int NV = n / 64;
-    for (int r = w; r < TM; r += 4) {
-      if (t0 + r >= Ntok) continue;
-      uint32_t key[kMaxNV];
-#pragma unroll
-      for (int v = 0; v < kMaxNV; ++v)
-        key[v] = v < NV ? float_key(ScoreIO<TIN>::load(S, (int64_t)r * n + v * 64 + lane)) : 0u;
-      uint32_t okey, oslot;
-      wave_topk<kMaxNV>(key, NV, knn, ScoreIO<TIN>::LO_BIT, scratch + w * 64, okey, oslot);
-      if (lane < knn) lists[((size_t)r * 2 + hc) * 64 + lane] = make_uint2(okey, oslot);
-    }
-    __syncthreads();
-  }
+      // candidates: scores whose threshold key is >= T0
+      const uint64_t below = lanes_below();
+      uint32_t total = 0;
+      for (int e = 0; e < NV; ++e) {
+        const int col = 64 * e + lane;
+        const Store v = S[r * n + s_phys(r, col)];
+        if (out_s != nullptr) SL::put_store(out_s, th * n + col, v);
+        const uint32_t ok = SL::okey(v);
+        const bool cand = SL::coarse(ok) >= T0;
+        const uint64_t m = __ballot(cand);
+        if (m) {
+          const uint32_t pos = total + (uint32_t)__popcll(m & below);
+          if (cand && pos < (uint32_t)kCandCap) scr[pos] = SL::make(ok, (uint32_t)col);
+          total += (uint32_t)__popcll(m);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      Key best;
+      if (total <= 64u) {
+        const Key k = lane < (int)total ? scr[lane] : (Key)0;
+        __builtin_amdgcn_wave_barrier();
+        best = bitonic64_desc(k);
+      } else if (total <= (uint32_t)kCandCap) {
+        Key k2[2];
+        k2[0] = scr[lane];
+        k2[1] = lane + 64 < (int)total ? scr[lane + 64] : (Key)0;
+        __builtin_amdgcn_wave_barrier();
+        best = wave_topk_unique<Key, 2>(k2, 2, knn, scr);
+      } else {
+        best = wave_topk_row<TIN>(S + r * n, r, NV, knn, scr);
+      }
+      const int64_t orow = th * knn;
+      if (hc == 0) {
+        // park the first half's list in the index output until the cartesian step
+        if (lane < knn) out_idx[orow + lane] = (int64_t)best;
+        if (out_i1 != nullptr && lane < knn) out_i1[orow + lane] = (int64_t)SL::key_idx(best);
+        continue;
+      }
+      if (out_i2 != nullptr && lane < knn) out_i2[orow + lane] = (int64_t)SL::key_idx(best);
 
-  // --- C: cartesian top-knn per token
-  for (int r = w; r < TM; r += 4) {
-    const int64_t t = t0 + r;
-    if (t >= Ntok) continue;
-    const uint2* L1 = lists + ((size_t)r * 2 + 0) * 64;
-    const uint2* L2 = lists + ((size_t)r * 2 + 1) * 64;
-    uint32_t key[kMaxPairSlots];
-    const int NP = (npairs + 63) / 64;
+      // ---- C: cartesian top-knn of this token
+      const Key l0 = lane < knn ? (Key)out_idx[orow + lane] : (Key)0;
+      const Key l1 = best;
+      Key keys[kMaxPairSlots];
 #pragma unroll
-    for (int v = 0; v < kMaxPairSlots; ++v) {
-      key[v] = 0u;
-      const int s = v * 64 + lane;
-      if (v < NP && s < npairs) {
-        const uint32_t pr = pairs[s];
-        const float v1 = key_float(L1[pr >> 16].x), v2 = key_float(L2[pr & 0xFFFFu].x);
-        key[v] = float_key(ScoreIO<TIN>::round(v1 + v2));
+      for (int s = 0; s < kMaxPairSlots; ++s) {
+        keys[s] = 0;
+        if (s < NP) {
+          const Key k0 = shfl_key(l0, pa[s]);
+          const Key k1 = shfl_key(l1, pb[s]);
+          const float v = SL::value(SL::key_okey(k0)) + SL::value(SL::key_okey(k1));
+          if (64 * s + lane < npairs) keys[s] = SL::make(SL::okey_of(v), (uint32_t)(pa[s] * knn + pb[s]));
+        }
+      }
+      const Key top = wave_topk_unique<Key, kMaxPairSlots>(keys, NP, knn, scr);
+      const uint32_t flat = SL::key_idx(top);
+      int a = (int)(flat / (uint32_t)knn);
+      int b = (int)(flat - (uint32_t)a * (uint32_t)knn);
+      a = a < 63 ? a : 63;
+      b = b < 63 ? b : 63;
+      const uint32_t i0 = SL::key_idx(shfl_key(l0, a));
+      const uint32_t i1 = SL::key_idx(shfl_key(l1, b));
+      if (lane < knn) {
+        SL::put(out_scores, orow + lane, SL::key_okey(top));
+        out_idx[orow + lane] = (int64_t)i0 * n + (int64_t)i1;
       }
     }
-    uint32_t okey, oslot;
-    wave_topk<kMaxPairSlots>(key, NP, knn, ScoreIO<TIN>::LO_BIT, scratch + w * 64, okey, oslot);
-    const int64_t orow = (t * H + h) * knn;
-    if (lane < knn) {
-      const uint32_t pr = pairs[oslot < (uint32_t)npairs ? oslot : 0u];
-      const uint32_t a = pr >> 16, c = pr & 0xFFFFu;
-      ScoreIO<TIN>::store(out_scores, orow + lane, key_float(okey));
-      out_idx[orow + lane] = (int64_t)L1[a].y * n + (int64_t)L2[c].y;
-      if (out_i1 != nullptr) out_i1[orow + lane] = (int64_t)L1[lane].y;
-      if (out_i2 != nullptr) out_i2[orow + lane] = (int64_t)L2[lane].y;
-    }
+    __syncthreads();  // before the next half overwrites the score tile and the shared region
   }
 }
 
-static size_t score_lds_bytes(int TM, int n, int esz) {
-  const size_t s_bytes = (((size_t)TM * n * esz) + 15) & ~(size_t)15;
-  return s_bytes + (size_t)TM * 2 * 64 * 8 + 4 * 64 * 8 + 64 * kMaxPairSlots * 4;
-}
-
-template <typename TIN, int IDW>
-static int launch_score(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn, int TM,
-                        void* out_scores, int64_t* out_idx, int64_t* out_i1, int64_t* out_i2, void* out_s1,
-                        void* out_s2, hipStream_t st) {
-  const size_t lds = score_lds_bytes(TM, n, (int)sizeof(TIN));
+template <typename TIN, int IDW, int TM>
+static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
+                           size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1, int64_t* out_i2,
+                           void* out_s1, void* out_s2, hipStream_t st) {
   // Dynamic LDS above 64 KiB is enabled once per device (idempotent, so a
   // race between threads only repeats the call).
   static std::atomic<uint64_t> lds_enabled{0};
@@ -338,17 +555,34 @@ static int launch_score(const void* q, const void* keys, int64_t Ntok, int H, in
   if (e != hipSuccess) return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: hipGetDevice failed: %s", hipGetErrorString(e));
   const uint64_t bit = 1ull << (dev & 63);
   if (!(lds_enabled.load(std::memory_order_relaxed) & bit)) {
-    e = hipFuncSetAttribute((const void*)pkm_score_topk_kernel<TIN, IDW>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kMaxLds);
+    e = hipFuncSetAttribute((const void*)pkm_score_topk_kernel<TIN, IDW, TM>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
     if (e != hipSuccess)
       return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
     lds_enabled.fetch_or(bit, std::memory_order_relaxed);
   }
-  const dim3 grid((unsigned)((Ntok + TM - 1) / TM), (unsigned)H);
-  hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW>), grid, dim3(256), lds, st, (const TIN*)q, (const TIN*)keys,
-                     Ntok, H, n, half, knn, TM, (TIN*)out_scores, out_idx, out_i1, out_i2, (TIN*)out_s1,
-                     (TIN*)out_s2);
+  const int64_t blocks = ((Ntok + TM - 1) / TM) * H;
+  hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
+                     (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
+                     out_i2, (TIN*)out_s1, (TIN*)out_s2);
   return PKM_OK;
+}
+
+template <typename TIN, int IDW>
+static int launch_score(int TM, const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
+                        size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1, int64_t* out_i2,
+                        void* out_s1, void* out_s2, hipStream_t st) {
+  switch (TM) {
+    case 64:
+      return launch_score_tm<TIN, IDW, 64>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1, out_i2,
+                                           out_s1, out_s2, st);
+    case 32:
+      return launch_score_tm<TIN, IDW, 32>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1, out_i2,
+                                           out_s1, out_s2, st);
+    default:
+      return launch_score_tm<TIN, IDW, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1, out_i2,
+                                           out_s1, out_s2, st);
+  }
 }
 
 }  // namespace pkm
@@ -370,7 +604,7 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
   PKM_REQUIRE(knn <= 64 && n_keys % 64 == 0 && n_keys <= 64 * kMaxNV, PKM_ERR_UNSUPPORTED,
               "pkm_score_topk: need knn <= 64 and n_keys a multiple of 64 up to %d (got knn %lld, n_keys %lld)",
               64 * kMaxNV, (long long)knn, (long long)n_keys);
-  const int kstep = dtype == PKM_DTYPE_BF16 ? 32 : 4;
+  const int kstep = dtype == PKM_DTYPE_BF16 ? Sel<bf16_t>::KSTEP : Sel<float>::KSTEP;
   PKM_REQUIRE(half % kstep == 0, PKM_ERR_UNSUPPORTED, "pkm_score_topk: half key dim %lld must be a multiple of %d",
               (long long)half, kstep);
   if (num_tokens == 0) return PKM_OK;
@@ -378,31 +612,35 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
   PKM_REQUIRE((uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
               "pkm_score_topk: query and keys must be 16-byte aligned");
   const int esz = dtype == PKM_DTYPE_BF16 ? 2 : 4;
+  const int key_bytes = dtype == PKM_DTYPE_BF16 ? 4 : 8;
   int dev = 0, lds_max = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (e != hipSuccess)
     return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: device query failed: %s", hipGetErrorString(e));
   if (lds_max > kMaxLds) lds_max = kMaxLds;
-  int TM = 32;
-  if (score_lds_bytes(TM, (int)n_keys, esz) > (size_t)lds_max) TM = 16;
-  PKM_REQUIRE(score_lds_bytes(TM, (int)n_keys, esz) <= (size_t)lds_max, PKM_ERR_UNSUPPORTED,
-              "pkm_score_topk: n_keys %lld needs %zu bytes of LDS, the device allows %d", (long long)n_keys,
-              score_lds_bytes(TM, (int)n_keys, esz), lds_max);
+  int TM = 64;
+  while (TM > 16 && score_lds_layout(TM, (int)n_keys, (int)half, esz, key_bytes).total > lds_max) TM /= 2;
+  const int lds = score_lds_layout(TM, (int)n_keys, (int)half, esz, key_bytes).total;
+  PKM_REQUIRE(lds <= lds_max, PKM_ERR_UNSUPPORTED,
+              "pkm_score_topk: n_keys %lld / half %lld need %d bytes of LDS, the device allows %d", (long long)n_keys,
+              (long long)half, lds, lds_max);
+  const int64_t blocks = ((num_tokens + TM - 1) / TM) * heads;
+  PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: grid too large");
   hipStream_t st = (hipStream_t)stream;
   int rc;
   const int H = (int)heads, n = (int)n_keys, hf = (int)half, k = (int)knn;
   if (dtype == PKM_DTYPE_BF16) {
     rc = score_type == PKM_SCORE_DOT
-             ? launch_score<bf16_t, 0>(query, keys, num_tokens, H, n, hf, k, TM, out_scores, out_indices,
+             ? launch_score<bf16_t, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
                                        out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st)
-             : launch_score<bf16_t, 1>(query, keys, num_tokens, H, n, hf, k, TM, out_scores, out_indices,
+             : launch_score<bf16_t, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
                                        out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st);
   } else {
     rc = score_type == PKM_SCORE_DOT
-             ? launch_score<float, 0>(query, keys, num_tokens, H, n, hf, k, TM, out_scores, out_indices,
+             ? launch_score<float, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
                                       out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st)
-             : launch_score<float, 1>(query, keys, num_tokens, H, n, hf, k, TM, out_scores, out_indices,
+             : launch_score<float, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
                                       out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st);
   }
   if (rc != PKM_OK) return rc;

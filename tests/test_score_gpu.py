@@ -29,6 +29,7 @@ SHAPES = [
     (5, 2, 64, 32, 64),  # knn == n_keys
     (3, 1, 64, 32, 1),  # knn 1
     (33, 3, 192, 64, 7),  # odd knn
+    (24, 2, 1024, 64, 64),  # knn 64 on 1024 keys: 65-128 threshold candidates per row
 ]
 
 
@@ -84,6 +85,20 @@ def test_random_inputs(device, shape, dtype, score_type):
     assert torch.equal(i1, e_i1) and torch.equal(i2, e_i2)
     assert torch.equal(idx.view(N, H, knn), e_idx)
     assert torch.equal(scores.view(N, H, knn), e_scores)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_all_scores_equal(device, dtype):
+    """A zero query makes every score equal: the order is the index order
+    (per half 0..knn-1, then the cartesian flat positions)."""
+    N, H, n, half, knn = 9, 2, 256, 64, 16
+    q = torch.zeros((N, H, 2 * half), dtype=dtype)
+    _, k = _random_inputs(N, H, n, half, dtype, seed=19)
+    scores, idx, i1, i2, s1, s2 = _run(q, k, H, knn, "dot", device)
+    e_scores, e_idx, e_i1, e_i2, e_s1, e_s2 = ref.get_indices(q, k, H, knn)
+    assert torch.equal(i1, e_i1) and torch.equal(i2, e_i2)
+    assert torch.equal(idx.view(N, H, knn), e_idx) and torch.equal(scores.view(N, H, knn), e_scores)
+    assert torch.equal(i1[0, 0], torch.arange(knn))
 
 
 def test_sub_outputs_optional_and_query_views(device):
