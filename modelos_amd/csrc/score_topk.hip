@@ -14,24 +14,30 @@
 // Equal values are ordered by the smaller index (sub-key index, then flat
 // a*knn + b), an order the reference's topk leaves unspecified.
 //
+// Selection works on unique keys: (order-preserving bits of the rounded value
+// << index bits) | (inverted index), so "larger key" is "better", ties
+// included, and a rank is a count of larger keys.
+//
 // One workgroup (8 waves) owns TM tokens of one head; per half:
 //   A. The half of the TM queries is staged in LDS. Each wave streams its own
 //      1/8 of the key tiles from L2 (16-byte loads, keys read once per
 //      workgroup) and computes the [TM x 16] score tiles on MFMA
-//      (16x16x32 bf16 / 16x16x4 f32); the epilogue rounds the scores into the
-//      LDS score tile [TM][n] and keeps, per row, the exact maximum of each of
-//      G = min(n, 128) column groups (group = column mod 128) in registers.
+//      (16x16x32 bf16 / 16x16x4 f32); the epilogue writes the order keys of
+//      the rounded scores into the LDS score tile [TM][n] and keeps, per row,
+//      the exact maximum of each of G = min(n, 128) column groups
+//      (group = column mod 128) in registers.
 //   B. Per row (one wave): T0 = knn-th largest group maximum is a lower bound
 //      of the knn-th largest score (knn groups each hold a score >= T0), so
-//      the top-knn are among the scores >= T0 — about 1.1 knn of them on
-//      random data. They are compacted with wave ballots as unique 32-bit keys
-//      (order-preserving value bits, then the inverted index), and one 64-lane
-//      bitonic sort orders them; with more than 64 (128) candidates an exact
-//      threshold search over all of the row's keys takes over.
+//      the top-knn are among the scores >= T0 (about 1.1 knn of them on
+//      random data). 8-score chunks whose maximum (packed 16-bit max) is
+//      below T0 are dropped, the scores of the remaining chunks are compacted
+//      with wave ballots, and each candidate's rank is counted. More than
+//      kCandCap candidates fall back to an exact threshold search over the row.
 //   C. (after the second half) per token, the cartesian candidates restricted
 //      to the pairs (a+1)(b+1) <= knn — every other pair is preceded, in
-//      (value, flat index) order, by at least knn pairs — keyed the same way
-//      and selected by an exact threshold search plus the bitonic sort.
+//      (value, flat index) order, by at least knn pairs. The knn pairs (a, 0)
+//      and the knn pairs (0, b) bound the knn-th value from below, which again
+//      leaves a few dozen candidates to rank.
 // Workgroups map head-fastest onto the grid, so with 8 heads each XCD (and its
 // L2) serves one head's keys.
 #include <atomic>
@@ -42,12 +48,14 @@ namespace pkm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kMaxNV = 32;        // n_keys <= 2048 (32 keys per lane in a 64-lane row scan)
+constexpr int kMaxN = 2048;       // n_keys limit
 constexpr int kMaxPairSlots = 5;  // knn = 64 -> 280 candidate pairs
-constexpr int kCandCap = 128;     // row candidates kept before the exact fallback
+constexpr int kCandCap = 128;     // candidates ranked per row before the exact fallback
+constexpr int kChunk = 8;         // scores per culling chunk
 constexpr int kMaxLds = 160 * 1024;
 
 // ---------------------------------------------------------------------------
@@ -62,25 +70,31 @@ __device__ __forceinline__ uint32_t okey32_inv(uint32_t k) {
   return k ^ ((k & 0x80000000u) ? 0x80000000u : 0xFFFFFFFFu);
 }
 
-// Per storage type: score tile element, unique selection key, MFMA step.
+// Per score type: score-tile element (an order key), unique selection key,
+// MFMA step. coarse() is the 16-bit key the thresholds compare.
 template <typename TIN>
 struct Sel;
 
 template <>
 struct Sel<bf16_t> {
-  typedef uint16_t Store;
-  typedef uint32_t Key;  // (16-bit order key << 16) | (0xFFFF - index)
+  typedef uint16_t Store;  // order key of the bf16 score
+  typedef uint32_t Key;    // (order key << 16) | (0xFFFF - index)
   static constexpr int KSTEP = 32;  // k per 16-byte fragment: one 16x16x32 MFMA
-  static __device__ __forceinline__ Store to_store(float v) { return (Store)f32_to_bf16_bits(v + 0.0f); }
-  static __device__ __forceinline__ uint32_t okey(Store s) { return okey16(s); }
-  static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok; }  // 16-bit threshold key
+  static __device__ __forceinline__ uint32_t okey_of(float v) { return okey16(f32_to_bf16_bits(v + 0.0f)); }
+  static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok; }
   static __device__ __forceinline__ Key make(uint32_t ok, uint32_t idx) { return (ok << 16) | (0xFFFFu - idx); }
   static __device__ __forceinline__ uint32_t key_okey(Key k) { return k >> 16; }
   static __device__ __forceinline__ uint32_t key_idx(Key k) { return 0xFFFFu - (k & 0xFFFFu); }
   static __device__ __forceinline__ float value(uint32_t ok) { return bf16_to_f32(okey16_inv(ok)); }
-  static __device__ __forceinline__ uint32_t okey_of(float v) { return okey16(f32_to_bf16_bits(v + 0.0f)); }
   static __device__ __forceinline__ void put(bf16_t* p, int64_t i, uint32_t ok) { p[i].x = (uint16_t)okey16_inv(ok); }
-  static __device__ __forceinline__ void put_store(bf16_t* p, int64_t i, Store s) { p[i].x = s; }
+  // maximum coarse key of one 8-score chunk (16 bytes)
+  static __device__ __forceinline__ uint32_t chunk_max(const Store* p) {
+    const uint4 v = *(const uint4*)p;
+    u16x2_t m = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, v.x), __builtin_bit_cast(u16x2_t, v.y));
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, v.z));
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, v.w));
+    return m.x > m.y ? m.x : m.y;
+  }
   static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                 0, 0, 0);
@@ -97,11 +111,10 @@ struct Sel<bf16_t> {
 
 template <>
 struct Sel<float> {
-  typedef float Store;
-  typedef uint64_t Key;  // (32-bit order key << 32) | (0xFFFFFFFF - index)
+  typedef uint32_t Store;  // order key of the float32 score
+  typedef uint64_t Key;    // (order key << 32) | (0xFFFFFFFF - index)
   static constexpr int KSTEP = 16;  // k per 16-byte fragment: four 16x16x4 MFMAs
-  static __device__ __forceinline__ Store to_store(float v) { return v + 0.0f; }
-  static __device__ __forceinline__ uint32_t okey(Store s) { return okey32(__float_as_uint(s)); }
+  static __device__ __forceinline__ uint32_t okey_of(float v) { return okey32(__float_as_uint(v + 0.0f)); }
   static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok >> 16; }  // truncated: a lower bound
   static __device__ __forceinline__ Key make(uint32_t ok, uint32_t idx) {
     return ((uint64_t)ok << 32) | (uint64_t)(0xFFFFFFFFu - idx);
@@ -109,9 +122,18 @@ struct Sel<float> {
   static __device__ __forceinline__ uint32_t key_okey(Key k) { return (uint32_t)(k >> 32); }
   static __device__ __forceinline__ uint32_t key_idx(Key k) { return 0xFFFFFFFFu - (uint32_t)k; }
   static __device__ __forceinline__ float value(uint32_t ok) { return __uint_as_float(okey32_inv(ok)); }
-  static __device__ __forceinline__ uint32_t okey_of(float v) { return okey32(__float_as_uint(v + 0.0f)); }
   static __device__ __forceinline__ void put(float* p, int64_t i, uint32_t ok) { p[i] = __uint_as_float(okey32_inv(ok)); }
-  static __device__ __forceinline__ void put_store(float* p, int64_t i, Store s) { p[i] = s; }
+  static __device__ __forceinline__ uint32_t chunk_max(const Store* p) {
+    const uint4 a = *(const uint4*)p, b = *(const uint4*)(p + 4);
+    uint32_t m = a.x > a.y ? a.x : a.y;
+    m = m > a.z ? m : a.z;
+    m = m > a.w ? m : a.w;
+    m = m > b.x ? m : b.x;
+    m = m > b.y ? m : b.y;
+    m = m > b.z ? m : b.z;
+    m = m > b.w ? m : b.w;
+    return m >> 16;
+  }
   // The 16 k values of a fragment pair: lane group g holds k = 4g + s in
   // step s, for A and B alike (a permutation of the summation order).
   static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
@@ -136,84 +158,116 @@ __device__ __forceinline__ uint64_t shfl_key(uint64_t v, int src) {
   const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src), hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src);
   return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint32_t xor_key(uint32_t v, int m) { return (uint32_t)__shfl_xor((int)v, m); }
-__device__ __forceinline__ uint64_t xor_key(uint64_t v, int m) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+__device__ __forceinline__ uint32_t lane_key(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
+}
+__device__ __forceinline__ uint64_t lane_key(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src);
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Sorts one key per lane, largest first (lane 0 = best).
+__device__ __forceinline__ uint32_t lanes_below_count(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Appends the keys of the lanes with `cand` to scr[total...] (positions
+// >= cap are dropped, total still counts them).
 template <typename Key>
-__device__ __forceinline__ Key bitonic64_desc(Key k) {
+__device__ __forceinline__ void wave_append(bool cand, Key key, Key* scr, uint32_t& total) {
+  const uint64_t m = __ballot(cand);
+  if (m) {
+    const uint32_t pos = total + lanes_below_count(m);
+    if (cand && pos < (uint32_t)kCandCap) scr[pos] = key;
+    total += (uint32_t)__popcll(m);
+  }
+}
+
+// Best-first top-knn of the total (knn <= total <= kCandCap) unique keys in
+// scr, by counting for each key the keys above it. Returns lane j's rank-j
+// key (lanes >= knn: 0); scr is reused as the output list.
+template <typename Key>
+__device__ __forceinline__ Key rank_select(Key* scr, uint32_t total, int knn) {
   const int lane = threadIdx.x & 63;
+  const Key k0 = lane < (int)total ? scr[lane] : (Key)0;
+  const Key k1 = lane + 64 < (int)total ? scr[lane + 64] : (Key)0;
+  uint32_t r0 = 0, r1 = 0;
+  constexpr int PER16 = 16 / (int)sizeof(Key);
+  const uint32_t full = total & ~(uint32_t)(PER16 - 1);
+  if (total <= 64u) {
+    for (uint32_t j = 0; j < full; j += PER16) {
+      const uint4 q = *(const uint4*)(scr + j);
+      const Key* kq = (const Key*)&q;
 #pragma unroll
-  for (int kk = 2; kk <= 64; kk <<= 1) {
+      for (int i = 0; i < PER16; ++i) r0 += kq[i] > k0 ? 1u : 0u;
+    }
+    for (uint32_t j = full; j < total; ++j) r0 += scr[j] > k0 ? 1u : 0u;
+  } else {
+    for (uint32_t j = 0; j < full; j += PER16) {
+      const uint4 q = *(const uint4*)(scr + j);
+      const Key* kq = (const Key*)&q;
 #pragma unroll
-    for (int j = kk >> 1; j > 0; j >>= 1) {
-      const Key p = xor_key(k, j);
-      const bool keep_max = ((lane & j) == 0) == ((lane & kk) == 0);
-      k = keep_max ? (p > k ? p : k) : (p < k ? p : k);
+      for (int i = 0; i < PER16; ++i) {
+        r0 += kq[i] > k0 ? 1u : 0u;
+        r1 += kq[i] > k1 ? 1u : 0u;
+      }
+    }
+    for (uint32_t j = full; j < total; ++j) {
+      r0 += scr[j] > k0 ? 1u : 0u;
+      r1 += scr[j] > k1 ? 1u : 0u;
     }
   }
-  return k;
+  __builtin_amdgcn_wave_barrier();
+  if (lane < (int)total && r0 < (uint32_t)knn) scr[r0] = k0;
+  if (lane + 64 < (int)total && r1 < (uint32_t)knn) scr[r1] = k1;
+  __builtin_amdgcn_wave_barrier();
+  const Key out = lane < knn ? scr[lane] : (Key)0;
+  __builtin_amdgcn_wave_barrier();
+  return out;
 }
 
-__device__ __forceinline__ uint64_t lanes_below() {
-  const int lane = threadIdx.x & 63;
-  return lane ? (~0ull >> (64 - lane)) : 0ull;
-}
-
-// Exact top-knn (knn <= 64) of the unique keys keys[s] (slots s < ns, key 0 =
-// empty, at least knn nonzero keys). Returns the lane's rank in best-first
-// order (lanes >= knn: 0). scr: 64 keys of this wave's LDS scratch.
-template <typename Key, int NS>
-__device__ __forceinline__ Key wave_topk_unique(const Key* keys, int ns, int knn, Key* scr) {
+// Exact best-first top-knn of the nonzero keys produced by key_at(slot) for
+// slot < nslots (at least knn of them): bit-by-bit threshold search with wave
+// ballots, then compaction and ranking. The path for inputs whose cheap
+// thresholds leave more than kCandCap candidates (e.g. many equal scores).
+template <typename Key, typename F>
+__device__ __forceinline__ Key exact_topk(F key_at, int nslots, int knn, Key* scr) {
   constexpr int BITS = 8 * (int)sizeof(Key);
+  const int lane = threadIdx.x & 63;
+  const int nv = (nslots + 63) / 64;
   Key T = 0;
   for (int bit = BITS - 1; bit >= 0; --bit) {
     const Key trial = T | ((Key)1 << bit);
     uint32_t c = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      if (s < ns) c += (uint32_t)__popcll(__ballot(keys[s] >= trial));
+    for (int v = 0; v < nv; ++v) {
+      const int slot = 64 * v + lane;
+      const Key k = slot < nslots ? key_at(slot) : (Key)0;
+      c += (uint32_t)__popcll(__ballot(k >= trial));
+    }
     if (c >= (uint32_t)knn) {
       T = trial;
       if (c == (uint32_t)knn) break;  // {keys >= T} is exactly the top-knn
     }
   }
-  const uint64_t below = lanes_below();
-  uint32_t base = 0;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    if (s < ns) {
-      const bool sel = keys[s] >= T;
-      const uint64_t m = __ballot(sel);
-      if (sel) scr[base + (uint32_t)__popcll(m & below)] = keys[s];
-      base += (uint32_t)__popcll(m);
-    }
+  uint32_t total = 0;
+  for (int v = 0; v < nv; ++v) {
+    const int slot = 64 * v + lane;
+    const Key k = slot < nslots ? key_at(slot) : (Key)0;
+    wave_append(k >= T && k != 0, k, scr, total);
   }
   __builtin_amdgcn_wave_barrier();
-  const int lane = threadIdx.x & 63;
-  Key k = lane < knn ? scr[lane] : (Key)0;
-  __builtin_amdgcn_wave_barrier();
-  return bitonic64_desc(k);
+  return rank_select(scr, total, knn);
 }
-
-// The same selection over a whole row of the LDS score tile (NV keys per
-// lane, recomputed from the tile in every pass instead of held in registers):
-// the exact path for rows whose threshold admits more than kCandCap scores.
-template <typename TIN>
-__device__ __noinline__ typename Sel<TIN>::Key wave_topk_row(const typename Sel<TIN>::Store* Srow, int row, int NV,
-                                                             int knn, typename Sel<TIN>::Key* scr);
 
 // ---------------------------------------------------------------------------
 // LDS layout (host and device agree through score_lds_layout).
 // ---------------------------------------------------------------------------
 struct ScoreLds {
-  int s_bytes;     // score tile [TM][n]
-  int r_bytes;     // shared region: query stage, later group maxima + scratch
-  int gmax_bytes;  // [TM][G] uint16 threshold keys of the group maxima
+  int s_bytes;     // score tile [TM][n] of order keys
+  int r_bytes;     // shared region: query stage in phase A, else the three below
+  int gmax_bytes;  // [TM][G] uint16 coarse keys of the group maxima
+  int scr_bytes;   // per wave: kCandCap selection keys
+  int list_bytes;  // per wave: n / kChunk uint16 chunk ids
   int total;
 };
 
@@ -223,8 +277,10 @@ __host__ __device__ inline ScoreLds score_lds_layout(int TM, int n, int half, in
   ScoreLds L;
   L.s_bytes = ((TM * n * esz) + 15) & ~15;
   L.gmax_bytes = ((TM * score_groups(n) * 2) + 15) & ~15;
-  const int q_bytes = TM * half * esz;
-  const int sel_bytes = L.gmax_bytes + kWaves * kCandCap * key_bytes;
+  L.scr_bytes = kCandCap * key_bytes;
+  L.list_bytes = (((n / kChunk) * 2) + 15) & ~15;
+  const int q_bytes = TM * half * (esz == 2 ? 2 : 4);
+  const int sel_bytes = L.gmax_bytes + kWaves * (L.scr_bytes + L.list_bytes);
   L.r_bytes = q_bytes > sel_bytes ? q_bytes : sel_bytes;
   L.total = L.s_bytes + L.r_bytes;
   return L;
@@ -239,45 +295,9 @@ __host__ __device__ inline int chunk_swizzle_mask(int chunks) {
 }
 
 // Column swizzle of the score tile: the 4 rows an MFMA store writes at once
-// (rows 4g + e, g = 0..3) land in different LDS banks.
+// (rows 4g + e, g = 0..3) land in different LDS banks. It permutes 16-score
+// blocks inside 64-score blocks, so 8-score chunks stay contiguous.
 __device__ __forceinline__ int s_phys(int row, int col) { return col ^ (((row >> 2) & 3) << 4); }
-
-template <typename TIN>
-__device__ __noinline__ typename Sel<TIN>::Key wave_topk_row(const typename Sel<TIN>::Store* Srow, int row, int NV,
-                                                             int knn, typename Sel<TIN>::Key* scr) {
-  typedef Sel<TIN> SL;
-  typedef typename SL::Key Key;
-  constexpr int BITS = 8 * (int)sizeof(Key);
-  const int lane = threadIdx.x & 63;
-  Key T = 0;
-  for (int bit = BITS - 1; bit >= 0; --bit) {
-    const Key trial = T | ((Key)1 << bit);
-    uint32_t c = 0;
-    for (int e = 0; e < NV; ++e) {
-      const int col = 64 * e + lane;
-      const Key k = SL::make(SL::okey(Srow[s_phys(row, col)]), (uint32_t)col);
-      c += (uint32_t)__popcll(__ballot(k >= trial));
-    }
-    if (c >= (uint32_t)knn) {
-      T = trial;
-      if (c == (uint32_t)knn) break;
-    }
-  }
-  const uint64_t below = lanes_below();
-  uint32_t base = 0;
-  for (int e = 0; e < NV; ++e) {
-    const int col = 64 * e + lane;
-    const Key k = SL::make(SL::okey(Srow[s_phys(row, col)]), (uint32_t)col);
-    const bool sel = k >= T;
-    const uint64_t m = __ballot(sel);
-    if (sel) scr[base + (uint32_t)__popcll(m & below)] = k;
-    base += (uint32_t)__popcll(m);
-  }
-  __builtin_amdgcn_wave_barrier();
-  Key k = lane < knn ? scr[lane] : (Key)0;
-  __builtin_amdgcn_wave_barrier();
-  return bitonic64_desc(k);
-}
 
 // ---------------------------------------------------------------------------
 // The kernel.
@@ -292,28 +312,29 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
   typedef typename SL::Key Key;
   constexpr int RT = TM / 16;  // row tiles
   constexpr int CB = 4;        // column tiles per batch
+  constexpr int ESZ = (int)sizeof(TIN);
+  constexpr int EPC = 16 / ESZ;  // input elements per 16-byte chunk
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int h = (int)(blockIdx.x % (unsigned)H);
   const int64_t t0 = (int64_t)(blockIdx.x / (unsigned)H) * TM;
-  const int esz = (int)sizeof(Store);
-  const ScoreLds L = score_lds_layout(TM, n, half, esz, (int)sizeof(Key));
+  const ScoreLds L = score_lds_layout(TM, n, half, (int)sizeof(Store), (int)sizeof(Key));
   Store* S = (Store*)smem;
   unsigned char* R = smem + L.s_bytes;
-  uint4* QS = (uint4*)R;                               // phase A: query stage
-  uint16_t* GM = (uint16_t*)R;                         // phase B: group maxima
-  Key* scr = (Key*)(R + L.gmax_bytes) + w * kCandCap;  // phase B/C: this wave's scratch
+  uint4* QS = (uint4*)R;        // phase A: query stage
+  uint16_t* GM = (uint16_t*)R;  // phases B, C: group maxima
+  Key* scr = (Key*)(R + L.gmax_bytes + w * L.scr_bytes);
+  uint16_t* clist = (uint16_t*)(R + L.gmax_bytes + kWaves * L.scr_bytes + w * L.list_bytes);
 
   const int kdim = 2 * half;
-  const int EPC = 16 / esz;        // elements per 16-byte chunk
-  const int CH = half / EPC;       // chunks per query half row
+  const int CH = half / EPC;  // 16-byte chunks per query half row
   const int cmask = chunk_swizzle_mask(CH);
   const int KS = half / SL::KSTEP;
   const int ncol = n / 16;
   const int G = score_groups(n);
-  const int NV = n / 64;
+  const int NC = n / kChunk;  // culling chunks per row
 
   // candidate pairs of the cartesian step: slot s -> (a, b), a-major, (a+1)(b+1) <= knn
   int pa[kMaxPairSlots], pb[kMaxPairSlots];
@@ -352,10 +373,21 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) gmax[rt][e] = -__builtin_inff();
-    float qn[RT];
+    float qn[RT];  // idw: squared norm of query row rt*16 + (lane & 15)
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) qn[rt] = 0.f;
-    bool have_qn = false;
+    for (int rt = 0; rt < RT; ++rt) {
+      float s = 0.f;
+      if (IDW) {
+        const int r = rt * 16 + (lane & 15);
+        for (int j = 0; j < KS; ++j) {
+          const int c = j * 4 + (lane >> 4);
+          s += SL::sumsq(QS[r * CH + (c ^ (r & cmask))]);
+        }
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+      }
+      qn[rt] = s;
+    }
     for (int jb = 0;; ++jb) {
       int tile[CB];
       bool tv[CB];
@@ -365,63 +397,74 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
         tv[k] = tile[k] < ncol;
       }
       if (!tv[0]) break;
-      const TIN* krow[CB];
+      // keys of tiles past the end are read from tile 0 (in range) and their scores dropped
+      const uint4* kb[CB];
 #pragma unroll
-      for (int k = 0; k < CB; ++k) krow[k] = Kc + (int64_t)(16 * (tv[k] ? tile[k] : 0) + (lane & 15)) * half;
+      for (int k = 0; k < CB; ++k)
+        kb[k] = (const uint4*)(Kc + (int64_t)(16 * (tv[k] ? tile[k] : 0) + (lane & 15)) * half) + (lane >> 4);
       f32x4_t acc[RT][CB];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int k = 0; k < CB; ++k) acc[rt][k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       float kn[CB] = {0.f, 0.f, 0.f, 0.f};
-      float qp[RT];
+      // k-step ks: 16-byte chunk 4*ks + (lane >> 4) of the query and key rows
+      auto load_b = [&](uint4* b, int ks) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) qp[rt] = 0.f;
-      uint4 bnext[CB];
-#pragma unroll
-      for (int k = 0; k < CB; ++k)
-        bnext[k] = tv[k] ? ld16(krow[k] + (lane >> 4) * EPC) : make_uint4(0u, 0u, 0u, 0u);
-      for (int ks = 0; ks < KS; ++ks) {
-        uint4 b[CB];
-#pragma unroll
-        for (int k = 0; k < CB; ++k) b[k] = bnext[k];
-        if (ks + 1 < KS) {
-#pragma unroll
-          for (int k = 0; k < CB; ++k)
-            bnext[k] = tv[k] ? ld16(krow[k] + ((ks + 1) * 4 + (lane >> 4)) * EPC) : make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int k = 0; k < CB; ++k) b[k] = kb[k][4 * ks];
+      };
+      auto load_a = [&](uint4* a, int ks) {
         const int c = ks * 4 + (lane >> 4);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const int r = rt * 16 + (lane & 15);
-          const uint4 a = QS[r * CH + (c ^ (r & cmask))];
-          if (IDW && !have_qn) qp[rt] += SL::sumsq(a);
-#pragma unroll
-          for (int k = 0; k < CB; ++k) SL::mma(a, b[k], acc[rt][k]);
+          a[rt] = QS[r * CH + (c ^ (r & cmask))];
         }
+      };
+      auto step = [&](const uint4* a, const uint4* b) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int k = 0; k < CB; ++k) SL::mma(a[rt], b[k], acc[rt][k]);
         if (IDW) {
 #pragma unroll
           for (int k = 0; k < CB; ++k) kn[k] += SL::sumsq(b[k]);
         }
+      };
+      // two k-steps per iteration on ping-pong registers: the key loads for
+      // step ks+2 are issued while steps ks+1 runs, with no branch between a
+      // load and its use (the clamped loads past the last step are unused)
+      // (scheduling barriers keep the loads where they are issued: the
+      // scheduler would otherwise sink them next to their use)
+      uint4 b0[CB], b1[CB], a0[RT], a1[RT];
+      load_b(b0, 0);
+      load_b(b1, KS > 1 ? 1 : 0);
+      load_a(a0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      int ks = 0;
+      for (; ks + 1 < KS; ks += 2) {
+        load_a(a1, ks + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        step(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        const int k2 = ks + 2 < KS ? ks + 2 : KS - 1;
+        load_b(b0, k2);
+        load_a(a0, k2);
+        __builtin_amdgcn_sched_barrier(0);
+        step(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b1, ks + 3 < KS ? ks + 3 : KS - 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (ks < KS) step(a0, b0);
       if (IDW) {
-        if (!have_qn) {
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            float s = qp[rt];
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
-            qn[rt] = s;  // squared norm of row rt*16 + (lane & 15)
-          }
-          have_qn = true;
-        }
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
           kn[k] += __shfl_xor(kn[k], 16);
           kn[k] += __shfl_xor(kn[k], 32);  // squared norm of key 16*tile + (lane & 15)
         }
       }
-      // epilogue: round into the score tile, track the group maxima
+      // epilogue: order keys of the rounded scores into the tile, group maxima
 #pragma unroll
       for (int k = 0; k < CB; ++k) {
         if (!tv[k]) continue;
@@ -439,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
               s = -logf(1e-3f + d2);
             }
             gmax[rt][e] = s > gmax[rt][e] ? s : gmax[rt][e];
-            S[row * n + s_phys(row, col)] = SL::to_store(s);
+            S[row * n + s_phys(row, col)] = (Store)SL::okey_of(s);
           }
         }
       }
@@ -451,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = rt * 16 + 4 * (lane >> 4) + e;
-          GM[row * G + 16 * w + (lane & 15)] = (uint16_t)SL::coarse(SL::okey(SL::to_store(gmax[rt][e])));
+          GM[row * G + 16 * w + (lane & 15)] = (uint16_t)SL::coarse(SL::okey_of(gmax[rt][e]));
         }
     }
     __syncthreads();
@@ -462,6 +505,10 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
       const int64_t t = t0 + r;
       if (t >= Ntok) continue;
       const int64_t th = t * H + h;
+      const Store* Srow = S + r * n;
+      if (out_s != nullptr) {
+        for (int col = lane; col < n; col += 64) SL::put(out_s, th * n + col, Srow[s_phys(r, col)]);
+      }
       // T0: knn-th largest group maximum
       const uint32_t gk0 = GM[r * G + lane];
       const uint32_t gk1 = G > 64 ? GM[r * G + 64 + lane] : 0u;
@@ -472,36 +519,35 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
         if (G > 64) c += (uint32_t)__popcll(__ballot(gk1 >= trial));
         if (c >= (uint32_t)knn) T0 = trial;
       }
-      // candidates: scores whose threshold key is >= T0
-      const uint64_t below = lanes_below();
+      // chunks whose maximum reaches T0
+      uint32_t nact = 0;
+      for (int c = lane; c - lane < NC; c += 64) {
+        const bool act = c < NC && SL::chunk_max(Srow + s_phys(r, kChunk * c)) >= T0;
+        const uint64_t m = __ballot(act);
+        if (act) clist[nact + lanes_below_count(m)] = (uint16_t)c;
+        nact += (uint32_t)__popcll(m);
+      }
+      __builtin_amdgcn_wave_barrier();
+      // their scores >= T0, 64 per ballot
       uint32_t total = 0;
-      for (int e = 0; e < NV; ++e) {
-        const int col = 64 * e + lane;
-        const Store v = S[r * n + s_phys(r, col)];
-        if (out_s != nullptr) SL::put_store(out_s, th * n + col, v);
-        const uint32_t ok = SL::okey(v);
-        const bool cand = SL::coarse(ok) >= T0;
-        const uint64_t m = __ballot(cand);
-        if (m) {
-          const uint32_t pos = total + (uint32_t)__popcll(m & below);
-          if (cand && pos < (uint32_t)kCandCap) scr[pos] = SL::make(ok, (uint32_t)col);
-          total += (uint32_t)__popcll(m);
+      for (uint32_t base = 0; base < nact * kChunk; base += 64) {
+        const uint32_t slot = base + lane;
+        bool cand = false;
+        Key key = 0;
+        if (slot < nact * kChunk) {
+          const int col = kChunk * clist[slot / kChunk] + (int)(slot % kChunk);
+          const uint32_t ok = Srow[s_phys(r, col)];
+          cand = SL::coarse(ok) >= T0;
+          key = SL::make(ok, (uint32_t)col);
         }
+        wave_append(cand, key, scr, total);
       }
       __builtin_amdgcn_wave_barrier();
       Key best;
-      if (total <= 64u) {
-        const Key k = lane < (int)total ? scr[lane] : (Key)0;
-        __builtin_amdgcn_wave_barrier();
-        best = bitonic64_desc(k);
-      } else if (total <= (uint32_t)kCandCap) {
-        Key k2[2];
-        k2[0] = scr[lane];
-        k2[1] = lane + 64 < (int)total ? scr[lane + 64] : (Key)0;
-        __builtin_amdgcn_wave_barrier();
-        best = wave_topk_unique<Key, 2>(k2, 2, knn, scr);
+      if (total <= (uint32_t)kCandCap) {
+        best = rank_select(scr, total, knn);
       } else {
-        best = wave_topk_row<TIN>(S + r * n, r, NV, knn, scr);
+        best = exact_topk<Key>([&](int col) { return SL::make(Srow[s_phys(r, col)], (uint32_t)col); }, n, knn, scr);
       }
       const int64_t orow = th * knn;
       if (hc == 0) {
@@ -515,18 +561,41 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
       // ---- C: cartesian top-knn of this token
       const Key l0 = lane < knn ? (Key)out_idx[orow + lane] : (Key)0;
       const Key l1 = best;
+      // lower bound of the knn-th pair value: the knn pairs (a, 0) and the knn pairs (0, b)
+      const float v0 = SL::value(SL::key_okey(lane_key(l0, 0)));
+      const float w0 = SL::value(SL::key_okey(lane_key(l1, 0)));
+      const uint32_t ta = SL::okey_of(SL::value(SL::key_okey(lane_key(l0, knn - 1))) + w0);
+      const uint32_t tb = SL::okey_of(v0 + SL::value(SL::key_okey(lane_key(l1, knn - 1))));
+      const uint32_t Tc = ta > tb ? ta : tb;
       Key keys[kMaxPairSlots];
+      uint32_t ctotal = 0;
 #pragma unroll
       for (int s = 0; s < kMaxPairSlots; ++s) {
         keys[s] = 0;
         if (s < NP) {
           const Key k0 = shfl_key(l0, pa[s]);
           const Key k1 = shfl_key(l1, pb[s]);
-          const float v = SL::value(SL::key_okey(k0)) + SL::value(SL::key_okey(k1));
-          if (64 * s + lane < npairs) keys[s] = SL::make(SL::okey_of(v), (uint32_t)(pa[s] * knn + pb[s]));
+          const uint32_t ok = SL::okey_of(SL::value(SL::key_okey(k0)) + SL::value(SL::key_okey(k1)));
+          const bool valid = 64 * s + lane < npairs;
+          if (valid) keys[s] = SL::make(ok, (uint32_t)(pa[s] * knn + pb[s]));
+          wave_append(valid && ok >= Tc, keys[s], scr, ctotal);
         }
       }
-      const Key top = wave_topk_unique<Key, kMaxPairSlots>(keys, NP, knn, scr);
+      __builtin_amdgcn_wave_barrier();
+      Key top;
+      if (ctotal <= (uint32_t)kCandCap) {
+        top = rank_select(scr, ctotal, knn);
+      } else {
+        top = exact_topk<Key>(
+            [&](int slot) {
+              Key k = 0;
+#pragma unroll
+              for (int s = 0; s < kMaxPairSlots; ++s)
+                if (slot >> 6 == s) k = keys[s];
+              return k;
+            },
+            64 * NP, knn, scr);
+      }
       const uint32_t flat = SL::key_idx(top);
       int a = (int)(flat / (uint32_t)knn);
       int b = (int)(flat - (uint32_t)a * (uint32_t)knn);
@@ -545,8 +614,8 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
 
 template <typename TIN, int IDW, int TM>
 static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
-                           size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1, int64_t* out_i2,
-                           void* out_s1, void* out_s2, hipStream_t st) {
+                           size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
+                           int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
   // Dynamic LDS above 64 KiB is enabled once per device (idempotent, so a
   // race between threads only repeats the call).
   static std::atomic<uint64_t> lds_enabled{0};
@@ -570,18 +639,18 @@ static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H,
 
 template <typename TIN, int IDW>
 static int launch_score(int TM, const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
-                        size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1, int64_t* out_i2,
-                        void* out_s1, void* out_s2, hipStream_t st) {
+                        size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
+                        int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
   switch (TM) {
     case 64:
-      return launch_score_tm<TIN, IDW, 64>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1, out_i2,
-                                           out_s1, out_s2, st);
+      return launch_score_tm<TIN, IDW, 64>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+                                           out_i2, out_s1, out_s2, st);
     case 32:
-      return launch_score_tm<TIN, IDW, 32>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1, out_i2,
-                                           out_s1, out_s2, st);
+      return launch_score_tm<TIN, IDW, 32>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+                                           out_i2, out_s1, out_s2, st);
     default:
-      return launch_score_tm<TIN, IDW, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1, out_i2,
-                                           out_s1, out_s2, st);
+      return launch_score_tm<TIN, IDW, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+                                           out_i2, out_s1, out_s2, st);
   }
 }
 
@@ -601,9 +670,9 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
               PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: bad sizes");
   PKM_REQUIRE(knn <= n_keys, PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: knn %lld > n_keys %lld", (long long)knn,
               (long long)n_keys);
-  PKM_REQUIRE(knn <= 64 && n_keys % 64 == 0 && n_keys <= 64 * kMaxNV, PKM_ERR_UNSUPPORTED,
+  PKM_REQUIRE(knn <= 64 && n_keys % 64 == 0 && n_keys <= kMaxN, PKM_ERR_UNSUPPORTED,
               "pkm_score_topk: need knn <= 64 and n_keys a multiple of 64 up to %d (got knn %lld, n_keys %lld)",
-              64 * kMaxNV, (long long)knn, (long long)n_keys);
+              kMaxN, (long long)knn, (long long)n_keys);
   const int kstep = dtype == PKM_DTYPE_BF16 ? Sel<bf16_t>::KSTEP : Sel<float>::KSTEP;
   PKM_REQUIRE(half % kstep == 0, PKM_ERR_UNSUPPORTED, "pkm_score_topk: half key dim %lld must be a multiple of %d",
               (long long)half, kstep);
@@ -611,7 +680,7 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
   PKM_REQUIRE(query && keys && out_scores && out_indices, PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: null pointer");
   PKM_REQUIRE((uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
               "pkm_score_topk: query and keys must be 16-byte aligned");
-  const int esz = dtype == PKM_DTYPE_BF16 ? 2 : 4;
+  const int esz = dtype == PKM_DTYPE_BF16 ? 2 : 4;  // score-tile element = order key of the input dtype
   const int key_bytes = dtype == PKM_DTYPE_BF16 ? 4 : 8;
   int dev = 0, lds_max = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -632,16 +701,20 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
   const int H = (int)heads, n = (int)n_keys, hf = (int)half, k = (int)knn;
   if (dtype == PKM_DTYPE_BF16) {
     rc = score_type == PKM_SCORE_DOT
-             ? launch_score<bf16_t, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
-                                       out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st)
-             : launch_score<bf16_t, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
-                                       out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st);
+             ? launch_score<bf16_t, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+                                       out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
+                                       out_sub_scores2, st)
+             : launch_score<bf16_t, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+                                       out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
+                                       out_sub_scores2, st);
   } else {
     rc = score_type == PKM_SCORE_DOT
-             ? launch_score<float, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
-                                      out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st)
-             : launch_score<float, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores, out_indices,
-                                      out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st);
+             ? launch_score<float, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+                                      out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
+                                      out_sub_scores2, st)
+             : launch_score<float, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+                                      out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
+                                      out_sub_scores2, st);
   }
   if (rc != PKM_OK) return rc;
   return pkm_check_launch("pkm_score_topk");
