@@ -139,6 +139,27 @@ int pkm_score_topk(const void* query, const void* keys, int64_t num_tokens, int6
                    void* out_sub_scores1, void* out_sub_scores2, void* stream);
 
 /*
+ * Dense gradient of the two sub-score matrices from the gradient of the
+ * selected scores (scores[t,h,j] = s_0[i_0] + s_1[i_1], id = i_0 * n_keys + i_1):
+ *   d_sub_dense[h, c, t, i] = sum_{j : i_c(indices[t,h,j]) == i} d_scores[t,h,j]
+ *                             + d_sub_scores_c[t, h, i]          (when not NULL)
+ * float32 sums in j order, rounded once to dtype (F32 or BF16).
+ *   indices, d_scores: [num_tokens, heads, knn];  d_sub_scores1/2: [num_tokens, heads, n_keys]
+ *   d_sub_dense: [heads, 2, num_tokens, n_keys], fully written; 16-byte aligned.
+ * Limits: knn <= 64, n_keys a multiple of 4 up to 2048. Ids outside [0, n_keys^2) are ignored.
+ * With it, dq = d_sub_dense[h, c] @ keys_c and dkeys_c = d_sub_dense[h, c]^T @ q_c are
+ * plain batched GEMMs.
+ *
+ * Replaces the autograd backward of topk + gather + expand-add in
+ * HashingMemory.get_indices (pkm/memory.py:267-285) and
+ * FastWeightProductKeyMemory.get_indices (fwpkm/fwpkm.py:904-921).
+ */
+int pkm_score_grad_dense(const int64_t* indices, const void* d_scores, int dtype,
+                         int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t knn,
+                         const void* d_sub_scores1, const void* d_sub_scores2,
+                         void* d_sub_dense, void* stream);
+
+/*
  * Counts indices outside [0, num_rows) into *count_out (a device int64),
  * which the call overwrites. No counterpart in the reference (its Triton
  * kernels do no bounds check; its CPU path raises from F.embedding_bag,

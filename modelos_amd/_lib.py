@@ -58,6 +58,15 @@ SIGNATURES = {
             c_void_p,  # stream
         ],
     ),
+    "pkm_score_grad_dense": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_int,  # indices, d_scores, dtype
+            c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, knn
+            c_void_p, c_void_p,  # d_sub_scores1, d_sub_scores2
+            c_void_p, c_void_p,  # d_sub_dense, stream
+        ],
+    ),
 }
 
 # pkm_score_t

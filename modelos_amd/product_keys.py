@@ -3,13 +3,12 @@
 `score_topk` runs the fused HIP kernel (pkm_score_topk) on torch's current
 stream. `product_key_topk` wraps it in autograd:
 
-  * the returned top-knn scores are differentiable w.r.t. query and keys;
-    their gradient is sparse (each score touches one key row per half) and is
-    computed with the embedding-bag kernels on the key table:
-      dq[t,h,c]  = sum_j dscore[t,h,j] * d s_c / d q      (an embedding-bag forward)
-      dkeys[row] = sum_{(t,h,j) -> row} dscore * d s / d k (an embedding-bag backward)
-  * the optional full sub-score matrices s_1, s_2 (fast-weight PKM) are
-    differentiable too; their dense gradient goes through batched GEMMs.
+  * the returned top-knn scores, and the optional full sub-score matrices
+    s_1, s_2 (fast-weight PKM), are differentiable w.r.t. query and keys. The
+    backward scatters the selected scores' gradient into dense sub-score
+    gradients (pkm_score_grad_dense, deterministic, dense upstream gradients
+    of s_1, s_2 added) and takes dq = dS @ K and dK = dS^T @ q as batched
+    GEMMs per (head, half), as autograd does for the reference's einsum.
 
 Reference: HashingMemory.get_indices (pkm/memory.py:250-289),
 FastWeightProductKeyMemory.compute_qk_scores / get_indices
@@ -25,7 +24,7 @@ from typing import Tuple
 import torch
 
 from . import _lib
-from .embedding_bag import _aligned, _require_device, eb_backward, eb_forward
+from .embedding_bag import _aligned, _require_device
 
 SCORE_TYPES = ("dot", "idw")
 
@@ -91,70 +90,50 @@ def score_topk(
     return scores, indices
 
 
-def _key_rows(indices: torch.Tensor, heads: int, n: int) -> torch.Tensor:
-    """Key-table rows of the two halves of every selected slot:
-    [tokens * heads * 2, knn], bag (t, h, c) = (t * heads + h) * 2 + c, row
-    (2h + c) * n + i_c with i_0 = id // n, i_1 = id % n (memory.py:278-281)."""
+def score_grad_dense(indices: torch.Tensor, d_scores: torch.Tensor, heads: int, n_keys: int,
+                     d_sub1: torch.Tensor | None = None, d_sub2: torch.Tensor | None = None) -> torch.Tensor:
+    """Dense gradient of the sub-score matrices, [heads, 2, tokens, n_keys] in
+    d_scores.dtype, from the gradient of the selected scores (and optional
+    dense upstream gradients of s1, s2 [tokens, heads, n_keys])."""
+    dev = _require_device(indices, d_scores, d_sub1, d_sub2)
     NH, knn = indices.shape
-    h = (torch.arange(NH, device=indices.device) % heads)[:, None]
-    r0 = (2 * h) * n + torch.div(indices, n, rounding_mode="floor")
-    r1 = (2 * h + 1) * n + torch.remainder(indices, n)
-    return torch.stack((r0, r1), dim=1).reshape(NH * 2, knn)
+    N = NH // heads
+    dt = d_scores.dtype
+    d_sub1 = _aligned(d_sub1.to(dt)) if d_sub1 is not None else None
+    d_sub2 = _aligned(d_sub2.to(dt)) if d_sub2 is not None else None
+    dS = torch.empty((heads, 2, N, n_keys), dtype=dt, device=dev)
+    _lib.call(
+        "pkm_score_grad_dense",
+        _lib.ptr(indices.contiguous()), _lib.ptr(d_scores.contiguous()), _lib.dtype_code(d_scores),
+        N, heads, n_keys, knn, _lib.ptr(d_sub1), _lib.ptr(d_sub2), _lib.ptr(dS), _lib.stream_of(dev),
+    )
+    return dS
 
 
-def _sparse_grads(query, keys, indices, d_scores, heads, n, score_type):
-    """Gradient of the selected top-knn scores w.r.t. query ([N*H*2, half]
-    float32) and keys ([2Hn, half] float32)."""
-    NH, knn = indices.shape
+def _grads_from_dense(query, keys, dS, heads, n, score_type):
+    """dq [tokens, heads, k_dim] and dkeys [2*heads*n, half] from the dense
+    sub-score gradient dS [heads, 2, tokens, n] with one pair of batched GEMMs
+    per (head, half) — the products autograd forms for the reference's einsum
+    (dot) or cdist (idw) on the full score matrices."""
     half = keys.shape[1]
-    rows = _key_rows(indices, heads, n)
-    q2 = query.reshape(NH * 2, half)
-    w = d_scores.float()[:, None, :].expand(NH, 2, knn).reshape(NH * 2, knn)
+    N = dS.shape[2]
+    Kh = keys.reshape(heads * 2, n, half)
+    qh = query.reshape(N, heads, 2, half).permute(1, 2, 0, 3).reshape(heads * 2, N, half)
+    D = dS.view(heads * 2, N, n)
     if score_type == "dot":
-        # s = <q, k>: dq = sum_j w_j k_j, dk_r = sum_{j -> r} w_j q_j
-        dq = eb_forward(rows, keys, w).float()
-        dk, _ = eb_backward(rows, keys, w, q2)
-        return dq, dk.float()
-    # s = -log(1e-3 + max(d2, 0)), d2 = |q - k|^2:
-    #   ds/dq = 2 u (k - q), ds/dk = 2 u (q - k), u = 1 / (1e-3 + d2) (0 where d2 < 0)
-    keys32, q32 = keys.float(), q2.float()
-    _, dots = eb_backward(rows, keys32, torch.zeros_like(w), q32)  # <k_row, q> per slot
-    qn = (q32 * q32).sum(-1)
-    kn = (keys32 * keys32).sum(-1)
-    d2 = qn[:, None] + kn[rows] - 2.0 * dots
-    u = torch.where(d2 >= 0, w / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
-    dq = 2.0 * eb_forward(rows, keys32, u) - 2.0 * q32 * u.sum(-1, keepdim=True)
-    gk, _ = eb_backward(rows, keys32, u, q32)
-    usum = torch.zeros(keys.shape[0], dtype=torch.float32, device=keys.device)
-    usum.index_add_(0, rows.reshape(-1), u.reshape(-1))
-    dk = 2.0 * gk - 2.0 * keys32 * usum[:, None]
-    return dq, dk
-
-
-def _dense_grads(query, keys, d_s, heads, n, score_type, dq, dk):
-    """Adds the gradient of the full sub-score matrices s_c [N, H, n] (float32,
-    batched GEMMs per head) to dq [N, H, 2, half] and dk [H, 2, n, half]."""
-    half = keys.shape[1]
-    N = query.numel() // (heads * 2 * half)
-    q = query.reshape(N, heads, 2, half).float()
-    K = keys.reshape(heads, 2, n, half).float()
-    for c, g in enumerate(d_s):
-        if g is None:
-            continue
-        G = g.float().permute(1, 0, 2).contiguous()  # [H, N, n]
-        qc = q[:, :, c].permute(1, 0, 2).contiguous()  # [H, N, half]
-        Kc = K[:, c].contiguous()  # [H, n, half]
-        if score_type == "idw":
-            dots = torch.bmm(qc, Kc.transpose(1, 2).contiguous())  # [H, N, n]
-            d2 = (qc * qc).sum(-1)[:, :, None] + (Kc * Kc).sum(-1)[:, None, :] - 2.0 * dots
-            U = torch.where(d2 >= 0, G / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
-            gq = 2.0 * (torch.bmm(U, Kc) - qc * U.sum(-1, keepdim=True))
-            gk = 2.0 * (torch.bmm(U.transpose(1, 2).contiguous(), qc) - Kc * U.sum(1)[:, :, None])
-        else:
-            gq = torch.bmm(G, Kc)
-            gk = torch.bmm(G.transpose(1, 2).contiguous(), qc)
-        dq[:, :, c] += gq.permute(1, 0, 2)
-        dk[:, c] += gk
+        dqh = torch.bmm(D, Kh)  # [2H, N, half]
+        dk = torch.bmm(D.transpose(1, 2), qh)  # [2H, n, half]
+    else:
+        # s = -log(1e-3 + max(d2, 0)), d2 = |q|^2 + |k|^2 - 2<q,k>:
+        #   ds/dq = 2 u (k - q), ds/dk = 2 u (q - k), u = 1 / (1e-3 + d2) (0 where d2 < 0)
+        q32, k32 = qh.float(), Kh.float()
+        dots = torch.bmm(q32, k32.transpose(1, 2).contiguous())
+        d2 = (q32 * q32).sum(-1)[:, :, None] + (k32 * k32).sum(-1)[:, None, :] - 2.0 * dots
+        U = torch.where(d2 >= 0, D.float() / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
+        dqh = 2.0 * (torch.bmm(U, k32) - q32 * U.sum(-1, keepdim=True))
+        dk = 2.0 * (torch.bmm(U.transpose(1, 2).contiguous(), q32) - k32 * U.sum(1)[:, :, None])
+    dq = dqh.view(heads, 2, N, half).permute(2, 0, 1, 3).reshape(N, heads, 2 * half)
+    return dq, dk.reshape(keys.shape)
 
 
 class ProductKeyTopK(torch.autograd.Function):
@@ -174,23 +153,14 @@ class ProductKeyTopK(torch.autograd.Function):
     def backward(ctx, d_scores, d_indices, *rest):
         query, keys, indices = ctx.saved_tensors
         heads, n = ctx.heads, ctx.n
-        half = keys.shape[1]
-        NH = indices.shape[0]
-        N = NH // heads
-        qc = _aligned(query)
-        kc = _aligned(keys)
-        dq = torch.zeros((N, heads, 2, half), dtype=torch.float32, device=query.device)
-        dk = torch.zeros((heads, 2, n, half), dtype=torch.float32, device=keys.device)
-        if d_scores is not None and NH > 0:
-            sq, sk = _sparse_grads(qc, kc, indices, d_scores.contiguous(), heads, n, ctx.score_type)
-            dq += sq.reshape(N, heads, 2, half)
-            dk += sk.reshape(heads, 2, n, half)
-        if ctx.sub_outputs and N > 0:
-            d_s = (rest[2], rest[3])
-            if any(g is not None for g in d_s):
-                _dense_grads(qc, kc, d_s, heads, n, ctx.score_type, dq, dk)
+        d_s1 = rest[2] if ctx.sub_outputs else None
+        d_s2 = rest[3] if ctx.sub_outputs else None
+        if d_scores is None:
+            d_scores = torch.zeros(indices.shape, dtype=query.dtype, device=query.device)
+        dS = score_grad_dense(indices, d_scores.to(query.dtype), heads, n, d_s1, d_s2)
+        dq, dk = _grads_from_dense(_aligned(query), _aligned(keys), dS, heads, n, ctx.score_type)
         d_query = dq.to(query.dtype).reshape(ctx.query_shape) if ctx.needs_input_grad[0] else None
-        d_keys = dk.to(keys.dtype).reshape(keys.shape) if ctx.needs_input_grad[1] else None
+        d_keys = dk.to(keys.dtype) if ctx.needs_input_grad[1] else None
         return d_query, d_keys, None, None, None, None
 
 
@@ -206,9 +176,4 @@ def product_key_topk(
     return ProductKeyTopK.apply(query, keys, heads, knn, score_type, sub_outputs)
 
 
-def sparse_key_rows(indices: torch.Tensor, heads: int, n_keys: int) -> torch.Tensor:
-    """Public form of the key-row mapping used by the backward (for tests)."""
-    return _key_rows(indices, heads, n_keys)
-
-
-__all__ = ["score_topk", "product_key_topk", "ProductKeyTopK", "sparse_key_rows", "SCORE_TYPES"]
+__all__ = ["score_topk", "product_key_topk", "ProductKeyTopK", "score_grad_dense", "SCORE_TYPES"]

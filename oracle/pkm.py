@@ -129,3 +129,24 @@ def brute_force_topk_pairs(s1: torch.Tensor, s2: torch.Tensor, knn: int):
             vals.append((float(v), i * n + j))
     vals.sort(key=lambda t: (-t[0], t[1]))
     return vals[:knn]
+
+
+def score_grad_dense(idx: torch.Tensor, d: torch.Tensor, n: int, d_s1: torch.Tensor | None = None,
+                     d_s2: torch.Tensor | None = None) -> torch.Tensor:
+    """Gradient of the full sub-score matrices [H, 2, N, n] from the gradient d
+    [N, H, knn] of scores = s1[id // n] + s2[id % n] (memory.py:274-285 with
+    the selection fixed), plus optional dense gradients of s1, s2 [N, H, n]:
+    float32 sums in j order, then the dense term, rounded once to d's dtype."""
+    N, H, knn = idx.shape
+    out = torch.zeros((H, 2, N, n), dtype=torch.float32)
+    i1, i2 = idx // n, idx % n
+    df = d.float()
+    for j in range(knn):  # j order, as the reference's index accumulation of a row
+        for c, ic in ((0, i1), (1, i2)):
+            view = out[:, c]  # [H, N, n]
+            view.scatter_add_(2, ic[:, :, j].t().reshape(H, N, 1), df[:, :, j].t().reshape(H, N, 1))
+    if d_s1 is not None:
+        out[:, 0] += d_s1.float().permute(1, 0, 2)
+    if d_s2 is not None:
+        out[:, 1] += d_s2.float().permute(1, 0, 2)
+    return out.to(d.dtype)

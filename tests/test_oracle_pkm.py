@@ -178,3 +178,23 @@ def test_integer_inputs_are_exact_in_bf16():
     q, k = _int_inputs(4, 2, 64, 256, torch.bfloat16, 8)
     s1, _ = ref.sub_scores(q, k, 2, out_dtype=torch.float64)
     assert torch.equal(s1, s1.round()) and s1.abs().max() <= 2 * 256
+
+
+def test_score_grad_dense_matches_autograd():
+    """The dense sub-score gradient is what autograd gives through
+    s1.gather + s2.gather (duplicate sub-keys included), float64."""
+    N, H, n, knn = 7, 3, 40, 9
+    g = gen(9)
+    s1 = torch.randn((N, H, n), generator=g, dtype=torch.float64, requires_grad=True)
+    s2 = torch.randn((N, H, n), generator=g, dtype=torch.float64, requires_grad=True)
+    _, idx, _, _ = ref.select(s1.detach(), s2.detach(), knn)
+    d = torch.randn((N, H, knn), generator=g, dtype=torch.float64)
+    ds1 = torch.randn((N, H, n), generator=g, dtype=torch.float64)
+    ds2 = torch.randn((N, H, n), generator=g, dtype=torch.float64)
+    sel = s1.gather(2, idx // n) + s2.gather(2, idx % n)
+    ((sel * d).sum() + (s1 * ds1).sum() + (s2 * ds2).sum()).backward()
+    got = ref.score_grad_dense(idx, d, n, ds1, ds2).double()
+    torch.testing.assert_close(got[:, 0].permute(1, 0, 2), s1.grad, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(got[:, 1].permute(1, 0, 2), s2.grad, rtol=1e-6, atol=1e-6)
+    # duplicates really occur: some sub-key is shared by several selected pairs
+    assert any(len(set((idx[t, h] // n).tolist())) < knn for t in range(N) for h in range(H))

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from modelos_amd import _lib
-from modelos_amd.product_keys import product_key_topk, score_topk
+from modelos_amd.product_keys import product_key_topk, score_grad_dense, score_topk
 from oracle import pkm as ref
 from tests.helpers import REL_TOL, assert_rel_close, gen
 
@@ -211,3 +211,21 @@ def test_full_size_layer_shape_sampled(device):
     assert int(idx.min()) >= 0 and int(idx.max()) < n * n
     srt = idx.sort(dim=1).values
     assert bool((srt[:, 1:] != srt[:, :-1]).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dense", [False, True], ids=["sparse", "sparse+dense"])
+def test_score_grad_dense_bit_exact(device, dtype, dense):
+    """pkm_score_grad_dense equals the oracle bit for bit (float32 sums in j
+    order, one rounding), on selections with shared sub-keys."""
+    N, H, n, half, knn = 37, 4, 512, 64, 32
+    q, k = _random_inputs(N, H, n, half, dtype, seed=20)
+    _, idx, _, _, _, _ = _run(q, k, H, knn, "dot", device)
+    g = gen(21)
+    d = torch.randn((N, H, knn), generator=g).to(dtype)
+    ds1 = torch.randn((N, H, n), generator=g).to(dtype) if dense else None
+    ds2 = torch.randn((N, H, n), generator=g).to(dtype) if dense else None
+    got = score_grad_dense(idx.view(N * H, knn).to(device), d.view(N * H, knn).to(device), H, n,
+                           ds1.to(device) if dense else None, ds2.to(device) if dense else None)
+    exp = ref.score_grad_dense(idx.view(N, H, knn), d, n, ds1, ds2)
+    assert torch.equal(got.cpu(), exp)
