@@ -229,3 +229,29 @@ def test_score_grad_dense_bit_exact(device, dtype, dense):
                            ds1.to(device) if dense else None, ds2.to(device) if dense else None)
     exp = ref.score_grad_dense(idx.view(N, H, knn), d, n, ds1, ds2)
     assert torch.equal(got.cpu(), exp)
+
+
+@pytest.mark.parametrize("score_type", ["dot_product", "idw"])
+def test_fwpkm_drop_in(device, score_type):
+    """fwpkm get_indices / compute_qk_scores drop-ins (fwpkm/fwpkm.py:853-934):
+    the 6-tuple's shapes, the selection bit-exact from the returned
+    sub-scores, and compute_qk_scores within tolerance of the oracle."""
+    from modelos_amd.fwpkm.fwpkm import ProductKeyIndexMixin
+
+    class Mem(ProductKeyIndexMixin):
+        heads, k_dim, topk, subsize, qk_score_type = 4, 256, 16, 512, score_type
+
+    m = Mem()
+    BT = 50
+    q, k = _random_inputs(BT, m.heads, m.subsize, m.k_dim // 2, torch.float32, seed=22)
+    scores, idx, i1, i2, s1, s2 = m.get_indices(q.to(device), k.to(device))
+    assert scores.shape == idx.shape == i1.shape == i2.shape == (BT, m.heads, m.topk)
+    assert s1.shape == s2.shape == (BT, m.heads, m.subsize)
+    e = ref.select(s1.cpu(), s2.cpu(), m.topk)
+    assert torch.equal(idx.cpu(), e[1]) and torch.equal(scores.cpu(), e[0])
+    st = "dot" if score_type == "dot_product" else "idw"
+    e_s1, _ = ref.sub_scores(q, k, m.heads, st)
+    assert_rel_close(s1.cpu(), e_s1, REL_TOL[torch.float32], "s1")
+    kv = k.view(m.heads, 2, m.subsize, m.k_dim // 2)[:, 0].contiguous().to(device)
+    dense = m.compute_qk_scores(q[:, :, : m.k_dim // 2].contiguous().to(device), kv)
+    assert_rel_close(dense.cpu(), e_s1, 1e-4, "compute_qk_scores")
