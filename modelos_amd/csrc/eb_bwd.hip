@@ -656,22 +656,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
       for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
     }
   };
-  // acc += sum_u w[u] * gvec[u]; lane u of the returned value holds <wraw, gvec[u]>
-  auto accumulate = [&](const RowData<VPL, U>& R, const float* w, float* acc) {
-    float mydot = 0.f;
+  // acc += sum_{u < nh} w[u] * gvec[u]; lane u of the returned value holds
+  // <wraw, gvec[u]> (slots u >= nh, wave-uniform, are skipped)
+  auto accumulate = [&](const RowData<VPL, U>& R, const float* w, uint32_t nh, float* acc) {
+    float d[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float f[NE];
+      d[u] = 0.f;
+      if ((uint32_t)u < nh) {
+        float f[NE];
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.gvec[u][v], f + v * EPV);
+        for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.gvec[u][v], f + v * EPV);
 #pragma unroll
-      for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
-      if (want_dot) {
-        float d = 0.f;
+        for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
+        if (want_dot) {
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) d = vec_dot<TW>(R.wraw[v], R.gvec[u][v], d);
-        d = group_sum<64>(d);
-        mydot = lane == u ? d : mydot;
+          for (int v = 0; v < VPL; ++v) d[u] = vec_dot<TW>(R.wraw[v], R.gvec[u][v], d[u]);
+        }
+      }
+    }
+    float mydot = 0.f;
+    if (want_dot) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if ((uint32_t)u < nh) {
+          const float t = group_sum<64>(d[u]);
+          mydot = lane == u ? t : mydot;
+        }
       }
     }
     return mydot;
@@ -680,7 +691,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
-    float mydot = accumulate(R, M.w, acc);
+    float mydot = accumulate(R, M.w, M.nh, acc);
     if (want_dot) dsorted[(uint32_t)lane < M.nh ? M.beg + lane : dummy_slot] = mydot;
     const uint32_t cnt = M.end - M.beg;
     if (cnt > (uint32_t)kHeavyT) {
@@ -698,7 +709,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
 #pragma unroll
           for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
         }
-        mydot = accumulate(R, w, acc);
+        mydot = accumulate(R, w, nh, acc);
         if (want_dot) dsorted[(uint32_t)lane < nh ? s + lane : dummy_slot] = mydot;
       }
     }

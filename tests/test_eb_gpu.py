@@ -295,3 +295,42 @@ def test_full_size_backward_sampled_and_properties(full_case):
     sb = torch.randperm(idx.shape[0], generator=torch.Generator().manual_seed(3))[:128].to(idx.device)
     e_gp = (W[idx[sb]].float() * gr[sb].float()[:, None, :]).sum(-1)
     assert_rel_close(gp[sb], e_gp, 2e-2, "sampled grad_psw")
+
+
+# Upstream gradients larger than the L2 of one XCD (the g rows of every
+# occurrence are re-read from the Infinity Cache): full parity at moderate
+# sizes, with heavy rows, invalid indices, unweighted bags and bitwise
+# determinism.
+LARGE_G = [
+    (4200, 16, 50000, 1024, torch.bfloat16),  # 8.6 MB of upstream gradient
+    (2200, 24, 20000, 2048, torch.bfloat16),
+    (2200, 8, 30000, 1024, torch.float32),
+    (8800, 4, 9000, 512, torch.float16),
+]
+
+
+@pytest.mark.parametrize("B,L,K,D,dtype", LARGE_G, ids=lambda v: str(v).replace("torch.", ""))
+def test_backward_large_gradient_parity(B, L, K, D, dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    assert B * D * torch.tensor([], dtype=dtype).element_size() > 8 << 20
+    W, _, p, g = eb_inputs(B, L, K, D, dtype, seed=31 + D)
+    idx = _hot_indices(B, L, K, seed=32 + D)
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    assert_rel_close(gW, eW, REL_TOL[dtype], "grad_weight")
+    assert_rel_close(gp, ep, REL_TOL[dtype], "grad_psw")
+    assert (gp.cpu()[idx < 0] == 0).all()
+    gW2, gp2 = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
+
+
+def test_backward_large_gradient_unweighted(device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K, D = 4200, 8, 20000, 1024
+    W, idx, _, g = eb_inputs(B, L, K, D, torch.bfloat16, seed=41, psw=False)
+    gW, gp = eb.eb_backward(*_dev(idx, W, None, g, device=device))
+    assert gp is None
+    eW, _ = ref.eb_backward(idx, W, None, g)
+    assert_rel_close(gW, eW, REL_TOL[torch.bfloat16], "unweighted grad_weight")
