@@ -126,7 +126,7 @@ enum pkm_score_t {
  * Equal scores are ordered by the smaller sub-key index (per half) and by
  * the smaller a * knn + b (cartesian); the result is deterministic.
  * Limits: knn <= 64, n_keys a multiple of 64 up to 2048, half a multiple of
- * 32 (BF16) or 4 (F32); query and keys 16-byte aligned.
+ * 32 (BF16) or 16 (F32); query and keys 16-byte aligned.
  *
  * Replaces HashingMemory.get_indices (pkm/memory.py:250-289; score_type DOT,
  * no sub outputs) and FastWeightProductKeyMemory.get_indices +

@@ -20,27 +20,29 @@
 //
 // One workgroup (8 waves) owns TM tokens of one head; per half:
 //   A. The half of the TM queries is staged in LDS. Each wave streams its own
-//      1/8 of the key tiles from L2 (16-byte loads, keys read once per
-//      workgroup) and computes the [TM x 16] score tiles on MFMA
+//      1/8 of the key tiles from L2 (16-byte loads two k-steps ahead, keys
+//      read once per workgroup) and computes [TM x 16] score tiles on MFMA
 //      (16x16x32 bf16 / 16x16x4 f32); the epilogue writes the order keys of
-//      the rounded scores into the LDS score tile [TM][n] and keeps, per row,
-//      the exact maximum of each of G = min(n, 128) column groups
-//      (group = column mod 128) in registers.
-//   B. Per row (one wave): T0 = knn-th largest group maximum is a lower bound
-//      of the knn-th largest score (knn groups each hold a score >= T0), so
-//      the top-knn are among the scores >= T0 (about 1.1 knn of them on
-//      random data). 8-score chunks whose maximum (packed 16-bit max) is
-//      below T0 are dropped, the scores of the remaining chunks are compacted
-//      with wave ballots, and each candidate's rank is counted. More than
-//      kCandCap candidates fall back to an exact threshold search over the row.
-//   C. (after the second half) per token, the cartesian candidates restricted
-//      to the pairs (a+1)(b+1) <= knn — every other pair is preceded, in
-//      (value, flat index) order, by at least knn pairs. The knn pairs (a, 0)
-//      and the knn pairs (0, b) bound the knn-th value from below, which again
-//      leaves a few dozen candidates to rank.
+//      the rounded scores into the LDS score tile [TM][n], each row laid out
+//      so that the columns g, g + G, g + 2G, ... (one threshold group) are
+//      adjacent (a 16-byte chunk for n >= 1024).
+//   B. Each row is selected by a group of LPR = 512 / TM lanes, all rows at
+//      once: T0 = the knn-th largest chunk maximum (a bit search with DPP
+//      group sums) is a lower bound of the knn-th largest score, since knn
+//      disjoint chunks each hold a score >= T0; the scores >= T0 (about 1.1
+//      knn of them on random data) are compacted with a group prefix sum and
+//      ranked by counting. More candidates than the row's buffer holds (e.g.
+//      many equal scores) leave the row to an exact bit search by its wave.
+//   C. (after the second half) per token and lane group, the cartesian
+//      candidates are the pairs (a+1)(b+1) <= knn, every other pair being
+//      preceded, in (value, flat index) order, by at least knn of them. The
+//      knn-th pair value is found by a bit search between the bound given by
+//      the pairs (a, 0) and (0, b) and the best pair, and the pairs reaching
+//      it are ranked.
 // Workgroups map head-fastest onto the grid, so with 8 heads each XCD (and its
 // L2) serves one head's keys.
 #include <atomic>
+#include <type_traits>
 
 #include "pkm_common.h"
 
@@ -48,14 +50,11 @@ namespace pkm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxN = 2048;       // n_keys limit
-constexpr int kMaxPairSlots = 5;  // knn = 64 -> 280 candidate pairs
 constexpr int kCandCap = 128;     // candidates ranked per row before the exact fallback
-constexpr int kChunk = 8;         // scores per culling chunk
 constexpr int kMaxLds = 160 * 1024;
 
 // ---------------------------------------------------------------------------
@@ -63,6 +62,13 @@ constexpr int kMaxLds = 160 * 1024;
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t okey16(uint32_t b) { return b ^ ((b & 0x8000u) ? 0xFFFFu : 0x8000u); }
 __device__ __forceinline__ uint32_t okey16_inv(uint32_t k) { return k ^ ((k & 0x8000u) ? 0x8000u : 0xFFFFu); }
+// okey16 of both halves of a word: the sign of each half (arithmetic shift)
+// selects its mask 0xFFFF or 0x8000
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t okey16x2(uint32_t b) {
+  const uint32_t sgn = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2_t, b) >> (short)15);
+  return b ^ ((sgn & 0x7FFF7FFFu) | 0x80008000u);
+}
 __device__ __forceinline__ uint32_t okey32(uint32_t b) {
   return b ^ ((b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
 }
@@ -71,7 +77,7 @@ __device__ __forceinline__ uint32_t okey32_inv(uint32_t k) {
 }
 
 // Per score type: score-tile element (an order key), unique selection key,
-// MFMA step. coarse() is the 16-bit key the thresholds compare.
+// MFMA step.
 template <typename TIN>
 struct Sel;
 
@@ -81,21 +87,12 @@ struct Sel<bf16_t> {
   typedef uint32_t Key;    // (order key << 16) | (0xFFFF - index)
   static constexpr int KSTEP = 32;  // k per 16-byte fragment: one 16x16x32 MFMA
   static __device__ __forceinline__ uint32_t okey_of(float v) { return okey16(f32_to_bf16_bits(v + 0.0f)); }
-  static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok; }
   static __device__ __forceinline__ Key make(uint32_t ok, uint32_t idx) { return (ok << 16) | (0xFFFFu - idx); }
   static __device__ __forceinline__ uint32_t key_okey(Key k) { return k >> 16; }
   static __device__ __forceinline__ uint32_t key_idx(Key k) { return 0xFFFFu - (k & 0xFFFFu); }
   static __device__ __forceinline__ float value(uint32_t ok) { return bf16_to_f32(okey16_inv(ok)); }
   static __device__ __forceinline__ void put(bf16_t* p, int64_t i, uint32_t ok) { p[i].x = (uint16_t)okey16_inv(ok); }
-  // maximum coarse key of one 8-score chunk (16 bytes)
-  static __device__ __forceinline__ uint32_t chunk_max(const Store* p) {
-    const uint4 v = *(const uint4*)p;
-    u16x2_t m = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, v.x), __builtin_bit_cast(u16x2_t, v.y));
-    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, v.z));
-    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, v.w));
-    return m.x > m.y ? m.x : m.y;
-  }
-  static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
+    static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                 0, 0, 0);
   }
@@ -115,7 +112,6 @@ struct Sel<float> {
   typedef uint64_t Key;    // (order key << 32) | (0xFFFFFFFF - index)
   static constexpr int KSTEP = 16;  // k per 16-byte fragment: four 16x16x4 MFMAs
   static __device__ __forceinline__ uint32_t okey_of(float v) { return okey32(__float_as_uint(v + 0.0f)); }
-  static __device__ __forceinline__ uint32_t coarse(uint32_t ok) { return ok >> 16; }  // truncated: a lower bound
   static __device__ __forceinline__ Key make(uint32_t ok, uint32_t idx) {
     return ((uint64_t)ok << 32) | (uint64_t)(0xFFFFFFFFu - idx);
   }
@@ -123,17 +119,6 @@ struct Sel<float> {
   static __device__ __forceinline__ uint32_t key_idx(Key k) { return 0xFFFFFFFFu - (uint32_t)k; }
   static __device__ __forceinline__ float value(uint32_t ok) { return __uint_as_float(okey32_inv(ok)); }
   static __device__ __forceinline__ void put(float* p, int64_t i, uint32_t ok) { p[i] = __uint_as_float(okey32_inv(ok)); }
-  static __device__ __forceinline__ uint32_t chunk_max(const Store* p) {
-    const uint4 a = *(const uint4*)p, b = *(const uint4*)(p + 4);
-    uint32_t m = a.x > a.y ? a.x : a.y;
-    m = m > a.z ? m : a.z;
-    m = m > a.w ? m : a.w;
-    m = m > b.x ? m : b.x;
-    m = m > b.y ? m : b.y;
-    m = m > b.z ? m : b.z;
-    m = m > b.w ? m : b.w;
-    return m >> 16;
-  }
   // The 16 k values of a fragment pair: lane group g holds k = 4g + s in
   // step s, for A and B alike (a permutation of the summation order).
   static __device__ __forceinline__ void mma(const uint4& a, const uint4& b, f32x4_t& c) {
@@ -153,20 +138,6 @@ struct Sel<float> {
 // ---------------------------------------------------------------------------
 // Wave-level selection on unique keys (larger = better).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t shfl_key(uint32_t v, int src) { return (uint32_t)__shfl((int)v, src); }
-__device__ __forceinline__ uint64_t shfl_key(uint64_t v, int src) {
-  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src), hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src);
-  return ((uint64_t)hi << 32) | lo;
-}
-__device__ __forceinline__ uint32_t lane_key(uint32_t v, int src) {
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
-}
-__device__ __forceinline__ uint64_t lane_key(uint64_t v, int src) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src);
-  return ((uint64_t)hi << 32) | lo;
-}
-
 __device__ __forceinline__ uint32_t lanes_below_count(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
@@ -231,7 +202,7 @@ __device__ __forceinline__ Key rank_select(Key* scr, uint32_t total, int knn) {
 // ballots, then compaction and ranking. The path for inputs whose cheap
 // thresholds leave more than kCandCap candidates (e.g. many equal scores).
 template <typename Key, typename F>
-__device__ __forceinline__ Key exact_topk(F key_at, int nslots, int knn, Key* scr) {
+__device__ __attribute__((noinline)) Key exact_topk(F key_at, int nslots, int knn, Key* scr) {
   constexpr int BITS = 8 * (int)sizeof(Key);
   const int lane = threadIdx.x & 63;
   const int nv = (nslots + 63) / 64;
@@ -260,49 +231,197 @@ __device__ __forceinline__ Key exact_topk(F key_at, int nslots, int knn, Key* sc
 }
 
 // ---------------------------------------------------------------------------
-// LDS layout (host and device agree through score_lds_layout).
+// Score-tile layout. A row holds the n order keys of one (token, half); the
+// scores of the columns c = j * G + g (j < slots) form group g and sit next
+// to each other, at positions g * slots + ((j + rho) mod slots), where
+// slots = min(8, n / 128) (a power of two, at least 1), G = n / slots, and
+// rho = 2 * ((row >> 2) & 3) mod slots spreads the four rows an MFMA
+// epilogue store writes at once over different LDS banks.
 // ---------------------------------------------------------------------------
+struct TileMap {
+  int slots, lslots, G;
+};
+__host__ __device__ inline TileMap tile_map(int n) {
+  TileMap m;
+  m.lslots = 0;
+  while (m.lslots < 3 && (128 << m.lslots) <= n) ++m.lslots;
+  if (n < 128) m.lslots = 0;
+  m.slots = 1 << m.lslots;
+  m.G = n >> m.lslots;
+  return m;
+}
+__device__ __forceinline__ int tile_rho(const TileMap& m, int row) { return (2 * ((row >> 2) & 3)) & (m.slots - 1); }
+__device__ __forceinline__ int tile_pos(const TileMap& m, int row, int col) {
+  const int j = col / m.G, g = col - j * m.G;
+  return g * m.slots + ((j + tile_rho(m, row)) & (m.slots - 1));
+}
+__device__ __forceinline__ int tile_col(const TileMap& m, int row, int pos) {
+  const int g = pos >> m.lslots, q = pos & (m.slots - 1);
+  return ((q - tile_rho(m, row)) & (m.slots - 1)) * m.G + g;
+}
+
+// ---------------------------------------------------------------------------
+// LDS layout (host and device agree through score_lds_layout).
+//   S: score tile [TM][n] of order keys; after the second half's selection it
+//      holds the first half's lists [TM][KL] and the cartesian results [TM][KL].
+//   R: query stage [TM][half] in phase A; per-row candidate buffers [TM][CAP]
+//      and top-knn lists [TM][KL] in phases B and C.
+// ---------------------------------------------------------------------------
+constexpr int kMaxPairs = 280;  // candidate pairs (a+1)(b+1) <= knn for knn = 64
+
+// The candidate pairs of the cartesian step for every knn <= 64: slot s of
+// knn is ab[off[knn] + s] = a | b << 8, in a-major order, b ascending, over
+// the pairs (a+1)(b+1) <= knn (so slot order is the flat a * knn + b order).
+constexpr int pair_count(int knn) {
+  int c = 0;
+  for (int a = 0; a < knn; ++a) c += knn / (a + 1);
+  return c;
+}
+constexpr int pair_table_size() {
+  int c = 0;
+  for (int k = 1; k <= 64; ++k) c += pair_count(k);
+  return c;
+}
+struct PairTable {
+  int off[66];
+  uint16_t ab[pair_table_size()];
+};
+constexpr PairTable make_pair_table() {
+  PairTable t{};
+  int o = 0;
+  for (int k = 1; k <= 64; ++k) {
+    t.off[k] = o;
+    for (int a = 0; a < k; ++a)
+      for (int b = 0; b < k / (a + 1); ++b) t.ab[o++] = (uint16_t)(a | (b << 8));
+  }
+  t.off[65] = o;
+  return t;
+}
+__constant__ PairTable kPairTable = make_pair_table();
 struct ScoreLds {
-  int s_bytes;     // score tile [TM][n] of order keys
-  int r_bytes;     // shared region: query stage in phase A, else the three below
-  int gmax_bytes;  // [TM][G] uint16 coarse keys of the group maxima
-  int scr_bytes;   // per wave: kCandCap selection keys
-  int list_bytes;  // per wave: n / kChunk uint16 chunk ids
-  int total;
+  int s_bytes, r_bytes, cap, cstride, kl, cand_off, list_off, total;
 };
 
-__host__ __device__ inline int score_groups(int n) { return n < 128 ? n : 128; }
+// Largest n_keys a TM-token tile serves: the tile fits the LDS, and a lane of
+// the selection holds at most 64 words of its row.
+__host__ __device__ constexpr int score_max_n(int TM, int esz) {
+  return (kMaxLds / (TM * esz) < kMaxN ? kMaxLds / (TM * esz) : kMaxN) < 64 * (kThreads / TM) * (4 / esz)
+             ? (kMaxLds / (TM * esz) < kMaxN ? kMaxLds / (TM * esz) : kMaxN) & ~63
+             : 64 * (kThreads / TM) * (4 / esz);
+}
 
-__host__ __device__ inline ScoreLds score_lds_layout(int TM, int n, int half, int esz, int key_bytes) {
+__host__ __device__ inline int score_cap(int knn, int lpr) {
+  int c = 2 * knn;
+  const int fb = kCandCap * lpr / 64;  // a wave's candidate buffers double as its fallback scratch
+  c = c > fb ? c : fb;
+  return (c + 3) & ~3;
+}
+
+__host__ __device__ inline ScoreLds score_lds_layout(int TM, int n, int half, int knn, int esz, int key_bytes) {
   ScoreLds L;
-  L.s_bytes = ((TM * n * esz) + 15) & ~15;
-  L.gmax_bytes = ((TM * score_groups(n) * 2) + 15) & ~15;
-  L.scr_bytes = kCandCap * key_bytes;
-  L.list_bytes = (((n / kChunk) * 2) + 15) & ~15;
+  const int lpr = kThreads / TM;
+  L.cap = score_cap(knn, lpr);
+  L.cstride = L.cap + 4;  // 4 zero keys after the last candidate
+  L.kl = (knn + 3) & ~3;
+  const int tile = TM * n * esz;
+  const int c_bytes = 2 * TM * L.kl * key_bytes;
+  L.s_bytes = ((tile > c_bytes ? tile : c_bytes) + 15) & ~15;
   const int q_bytes = TM * half * (esz == 2 ? 2 : 4);
-  const int sel_bytes = L.gmax_bytes + kWaves * (L.scr_bytes + L.list_bytes);
-  L.r_bytes = q_bytes > sel_bytes ? q_bytes : sel_bytes;
+  L.cand_off = 0;
+  L.list_off = TM * L.cstride * key_bytes;
+  const int sel_bytes = L.list_off + TM * L.kl * key_bytes;
+  L.r_bytes = ((q_bytes > sel_bytes ? q_bytes : sel_bytes) + 15) & ~15;
   L.total = L.s_bytes + L.r_bytes;
   return L;
 }
 
-// Largest power of two (<= 8) dividing `chunks`, minus one: the XOR mask of
-// the query-stage chunk swizzle (stays inside the row).
-__host__ __device__ inline int chunk_swizzle_mask(int chunks) {
-  int m = 1;
-  while (m < 8 && chunks % (2 * m) == 0) m *= 2;
-  return m - 1;
+// ---------------------------------------------------------------------------
+// Lane groups: LPR consecutive lanes (8, 16 or 32, aligned) own one row.
+// Sums and scans over a group with DPP.
+// ---------------------------------------------------------------------------
+template <int LPR>
+__device__ __forceinline__ uint32_t group_sum(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  x += (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  if (LPR >= 8) x += (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xF, 0xF, false);   // row_half_mirror
+  if (LPR >= 16) x += (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xF, 0xF, false);  // row_mirror
+  if (LPR >= 32) x += (uint32_t)__shfl_xor((int)x, 16);
+  return x;
+}
+// inclusive prefix sum over the group (sub = lane index inside the group)
+template <int LPR>
+__device__ __forceinline__ uint32_t group_scan(uint32_t x, int sub) {
+  uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += sub >= 1 ? y : 0u;
+  y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += sub >= 2 ? y : 0u;
+  if (LPR >= 8) {
+    y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += sub >= 4 ? y : 0u;
+  }
+  if (LPR >= 16) {
+    y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    x += sub >= 8 ? y : 0u;
+  }
+  if (LPR >= 32) {  // add the first 16 lanes' total (their last lane's prefix)
+    y = (uint32_t)__shfl((int)x, (int)(threadIdx.x & 32) + 15);
+    x += sub >= 16 ? y : 0u;
+  }
+  return x;
 }
 
-// Column swizzle of the score tile: the 4 rows an MFMA store writes at once
-// (rows 4g + e, g = 0..3) land in different LDS banks. It permutes 16-score
-// blocks inside 64-score blocks, so 8-score chunks stay contiguous.
-__device__ __forceinline__ int s_phys(int row, int col) { return col ^ (((row >> 2) & 3) << 4); }
+// Whether fewer than knn of the group's values v[0, NV) (all lanes) reach
+// trial. Values of B <= 16 bits are counted without compares: v - trial
+// wraps to a set top bit exactly when v < trial.
+template <int LPR, int NV, int B>
+__device__ __forceinline__ bool group_count_ge_below(const uint32_t* v, uint32_t trial, int knn) {
+  uint32_t c = 0;
+  if (B <= 16) {
+    uint32_t below = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) below += (v[i] - trial) >> 31;
+    c = (uint32_t)NV - below;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) c += v[i] >= trial ? 1u : 0u;
+  }
+  return group_sum<LPR>(c) < (uint32_t)knn;
+}
+
+// Best-first top-knn of the C (knn <= C <= LPR * MAXM) unique keys cand[0, C)
+// of one row, by its lane group: each lane counts, for its keys
+// cand[sub + LPR i], the keys above them, and emit(rank, key) is called for
+// the ranks below knn. cand[C, C + 4) must read as 0 (below every key).
+template <typename Key, int LPR, int MAXM, typename F>
+__device__ __forceinline__ void group_rank(const Key* cand, uint32_t C, int knn, int sub, F emit) {
+  Key mine[MAXM];
+  uint32_t rk[MAXM];
+#pragma unroll
+  for (int i = 0; i < MAXM; ++i) {
+    const uint32_t j = (uint32_t)(sub + LPR * i);
+    mine[i] = j < C ? cand[j] : (Key)0;
+    rk[i] = 0;
+  }
+  constexpr int PER16 = 16 / (int)sizeof(Key);
+  uint4 q = *(const uint4*)cand;  // 16 bytes ahead of their use
+  for (uint32_t j = 0; j < C; j += PER16) {
+    const uint4 qn = *(const uint4*)(cand + (j + PER16 < C ? j + PER16 : j));
+    const Key* kq = (const Key*)&q;
+#pragma unroll
+    for (int u = 0; u < PER16; ++u)
+#pragma unroll
+      for (int i = 0; i < MAXM; ++i) rk[i] += kq[u] > mine[i] ? 1u : 0u;
+    q = qn;
+  }
+#pragma unroll
+  for (int i = 0; i < MAXM; ++i)
+    if (mine[i] != 0 && rk[i] < (uint32_t)knn) emit(rk[i], mine[i]);
+}
 
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
-template <typename TIN, int IDW, int TM>
+template <typename TIN, int IDW, int TM, int KSC>
 __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
     const TIN* __restrict__ Q, const TIN* __restrict__ Kt, int64_t Ntok, int H, int n, int half, int knn,
     TIN* __restrict__ out_scores, int64_t* __restrict__ out_idx, int64_t* __restrict__ out_i1,
@@ -314,149 +433,134 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
   constexpr int CB = 4;        // column tiles per batch
   constexpr int ESZ = (int)sizeof(TIN);
   constexpr int EPC = 16 / ESZ;  // input elements per 16-byte chunk
+  constexpr int LPR = kThreads / TM;  // lanes per row in the selection phases
+  constexpr int RPW = 64 / LPR;       // rows per wave
+  constexpr int EPW = 4 / (int)sizeof(Store);  // score-tile elements per 32-bit word
+  constexpr int MAXG = score_max_n(TM, (int)sizeof(Store)) / LPR / EPW / 4;  // 16-byte chunks of a row per lane
+  constexpr int KBITS = 8 * (int)sizeof(Store);                          // bits of an order key
+  constexpr int MAXM = (2 * 64 > kCandCap * LPR / 64 ? 2 * 64 : kCandCap * LPR / 64) / LPR;  // cap / LPR
+  constexpr int MAXS = (kMaxPairs + LPR - 1) / LPR;  // pair slots per lane
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = (int)(blockIdx.x % (unsigned)H);
   const int64_t t0 = (int64_t)(blockIdx.x / (unsigned)H) * TM;
-  const ScoreLds L = score_lds_layout(TM, n, half, (int)sizeof(Store), (int)sizeof(Key));
+  const ScoreLds L = score_lds_layout(TM, n, half, knn, (int)sizeof(Store), (int)sizeof(Key));
+  const TileMap M = tile_map(n);
   Store* S = (Store*)smem;
   unsigned char* R = smem + L.s_bytes;
-  uint4* QS = (uint4*)R;        // phase A: query stage
-  uint16_t* GM = (uint16_t*)R;  // phases B, C: group maxima
-  Key* scr = (Key*)(R + L.gmax_bytes + w * L.scr_bytes);
-  uint16_t* clist = (uint16_t*)(R + L.gmax_bytes + kWaves * L.scr_bytes + w * L.list_bytes);
+  uint4* QS = (uint4*)R;  // phase A: query stage
+
+  // selection: row r = this lane's group, sub = lane inside the group
+  const int r = threadIdx.x / LPR;
+  const int sub = threadIdx.x & (LPR - 1);
+  Key* cand = (Key*)(R + L.cand_off) + r * L.cstride;
+  Key* list = (Key*)(R + L.list_off) + r * L.kl;
+  Key* l0 = (Key*)smem + r * L.kl;             // phase C: the first half's list, in the free tile,
+  Key* fin = (Key*)smem + (TM + r) * L.kl;     // and the ranked pairs
+  const uint16_t* pairs = kPairTable.ab + kPairTable.off[knn];
+  const int64_t t = t0 + r;
+  const bool live = t < Ntok;
+  const int64_t th = t * H + h;
+  const int64_t orow = th * knn;
 
   const int kdim = 2 * half;
-  const int CH = half / EPC;  // 16-byte chunks per query half row
-  const int cmask = chunk_swizzle_mask(CH);
+  const int CH = half / EPC;  // 16-byte chunks per query half row (4 per k-step)
   const int KS = half / SL::KSTEP;
+  // Query stage layout, in 16-byte chunks: chunk c = 4 j + g of row q (the
+  // g-th quarter of k-step j) sits at (j * TM + q) * 4 + (g ^ ((q >> 2) & 3)),
+  // so the A fragment of a k-step is one lane-invariant offset away from a
+  // per-lane base, and the 8 lanes an LDS cycle serves hit distinct banks.
+  const int qlane = (lane & 15) * 4 + ((lane >> 4) ^ ((lane >> 2) & 3));
+  // key chunk of lane (column lane & 15, quarter lane >> 4) inside a tile row block
+  const int klane = (lane & 15) * CH + (lane >> 4);
   const int ncol = n / 16;
-  const int G = score_groups(n);
-  const int NC = n / kChunk;  // culling chunks per row
+  // this wave's column tiles are w, w + 8, ...; batches of CB of them
+  const int ntw = (ncol - w + kWaves - 1) / kWaves;
+  const int nsteps = ((ntw + CB - 1) / CB) * KS;
 
-  // candidate pairs of the cartesian step: slot s -> (a, b), a-major, (a+1)(b+1) <= knn
-  int pa[kMaxPairSlots], pb[kMaxPairSlots];
-  int npairs = 0;
-#pragma unroll
-  for (int s = 0; s < kMaxPairSlots; ++s) pa[s] = pb[s] = 0;
-  for (int a = 0; a < knn; ++a) {
-    const int cnt = knn / (a + 1);
-#pragma unroll
-    for (int s = 0; s < kMaxPairSlots; ++s) {
-      const int slot = 64 * s + lane;
-      if (slot >= npairs && slot < npairs + cnt) {
-        pa[s] = a;
-        pb[s] = slot - npairs;
-      }
-    }
-    npairs += cnt;
-  }
-  const int NP = (npairs + 63) / 64;
+  const int npairs = kPairTable.off[knn + 1] - kPairTable.off[knn];  // candidate pairs of the cartesian step
 
+  // A tile row is read as 16-byte chunks interleaved over the lane group:
+  // lane sub reads chunks LPR (i ^ x) + sub, i < NG, with x = row & 1 when
+  // LPR = 8 so that the two rows an LDS pass serves use different banks. Each
+  // chunk is one group of the threshold (n / (4 EPW) groups per row).
+  const int NCH = n / (4 * EPW);  // chunks per row
+  const int NG = (NCH + LPR - 1) / LPR;
+  const int cx = (LPR == 8 && NCH % (2 * LPR) == 0) ? (r & 1) : 0;
+
+#pragma unroll 1
   for (int hc = 0; hc < 2; ++hc) {
     const TIN* Kc = Kt + (int64_t)(2 * h + hc) * n * half;
     // ---- A0: stage the query half [TM][half] (zeros past the last token)
     for (int i = threadIdx.x; i < TM * CH; i += kThreads) {
-      const int r = i / CH, c = i - (i / CH) * CH;
-      const int64_t t = t0 + r;
+      const int q = i / CH, c = i - (i / CH) * CH;
+      const int64_t tq = t0 + q;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (t < Ntok) v = ld16(Q + (t * H + h) * kdim + hc * half + c * EPC);
-      QS[r * CH + (c ^ (r & cmask))] = v;
+      if (tq < Ntok) v = ld16(Q + (tq * H + h) * kdim + hc * half + c * EPC);
+      QS[((c >> 2) * TM + q) * 4 + ((c & 3) ^ ((q >> 2) & 3))] = v;
     }
     __syncthreads();
 
-    // ---- A: scores of this wave's column tiles (w, w+8, ...), batches of CB
-    float gmax[RT][4];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) gmax[rt][e] = -__builtin_inff();
+    // ---- A: scores of this wave's column tiles, one step = one k-step of a
+    // batch of CB tiles. The keys of step s + 2 (from L2) are loaded while
+    // step s runs, in a ring of 3 register slots continued across batch
+    // boundaries, so the loads of the next batch overlap the epilogue of the
+    // current one; the queries of a step come from LDS at its start.
     float qn[RT];  // idw: squared norm of query row rt*16 + (lane & 15)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float s = 0.f;
       if (IDW) {
-        const int r = rt * 16 + (lane & 15);
-        for (int j = 0; j < KS; ++j) {
-          const int c = j * 4 + (lane >> 4);
-          s += SL::sumsq(QS[r * CH + (c ^ (r & cmask))]);
-        }
+        for (int j = 0; j < KS; ++j) s += SL::sumsq(QS[(j * TM + rt * 16) * 4 + qlane]);
         s += __shfl_xor(s, 16);
         s += __shfl_xor(s, 32);
       }
       qn[rt] = s;
     }
-    for (int jb = 0;; ++jb) {
-      int tile[CB];
-      bool tv[CB];
-#pragma unroll
-      for (int k = 0; k < CB; ++k) {
-        tile[k] = w + kWaves * (CB * jb + k);
-        tv[k] = tile[k] < ncol;
-      }
-      if (!tv[0]) break;
-      // keys of tiles past the end are read from tile 0 (in range) and their scores dropped
-      const uint4* kb[CB];
-#pragma unroll
-      for (int k = 0; k < CB; ++k)
-        kb[k] = (const uint4*)(Kc + (int64_t)(16 * (tv[k] ? tile[k] : 0) + (lane & 15)) * half) + (lane >> 4);
-      f32x4_t acc[RT][CB];
+    f32x4_t acc[RT][CB];
+    float kn[CB];
+    auto reset = [&]() {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int k = 0; k < CB; ++k) acc[rt][k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      float kn[CB] = {0.f, 0.f, 0.f, 0.f};
-      // k-step ks: 16-byte chunk 4*ks + (lane >> 4) of the query and key rows
-      auto load_b = [&](uint4* b, int ks) {
 #pragma unroll
-        for (int k = 0; k < CB; ++k) b[k] = kb[k][4 * ks];
-      };
-      auto load_a = [&](uint4* a, int ks) {
-        const int c = ks * 4 + (lane >> 4);
+      for (int k = 0; k < CB; ++k) kn[k] = 0.f;
+    };
+    // operands of k-step ks of batch jb (ks may run past the batch into the
+    // next one; steps past the last read step 0's, in range, unused); tiles
+    // past the last one read tile 0 and their scores are dropped
+    const uint4* Kc4 = (const uint4*)Kc;
+    const int nbw = nsteps / KS;
+    auto load_b = [&](uint4* b, int jb, int ks) {
+      if (ks >= KS) ks -= KS, ++jb;
+      if (jb >= nbw) jb = 0, ks = 0;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const int r = rt * 16 + (lane & 15);
-          a[rt] = QS[r * CH + (c ^ (r & cmask))];
-        }
-      };
-      auto step = [&](const uint4* a, const uint4* b) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-          for (int k = 0; k < CB; ++k) SL::mma(a[rt], b[k], acc[rt][k]);
-        if (IDW) {
-#pragma unroll
-          for (int k = 0; k < CB; ++k) kn[k] += SL::sumsq(b[k]);
-        }
-      };
-      // two k-steps per iteration on ping-pong registers: the key loads for
-      // step ks+2 are issued while steps ks+1 runs, with no branch between a
-      // load and its use (the clamped loads past the last step are unused)
-      // (scheduling barriers keep the loads where they are issued: the
-      // scheduler would otherwise sink them next to their use)
-      uint4 b0[CB], b1[CB], a0[RT], a1[RT];
-      load_b(b0, 0);
-      load_b(b1, KS > 1 ? 1 : 0);
-      load_a(a0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      int ks = 0;
-      for (; ks + 1 < KS; ks += 2) {
-        load_a(a1, ks + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        step(a0, b0);
-        __builtin_amdgcn_sched_barrier(0);
-        const int k2 = ks + 2 < KS ? ks + 2 : KS - 1;
-        load_b(b0, k2);
-        load_a(a0, k2);
-        __builtin_amdgcn_sched_barrier(0);
-        step(a1, b1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(b1, ks + 3 < KS ? ks + 3 : KS - 1);
-        __builtin_amdgcn_sched_barrier(0);
+      for (int k = 0; k < CB; ++k) {
+        const int tile = w + kWaves * (CB * jb + k);
+        const int tl = tile < ncol ? tile : 0;
+        b[k] = (Kc4 + (16 * tl * CH + 4 * ks))[klane];
       }
-      if (ks < KS) step(a0, b0);
+    };
+    auto load_a = [&](uint4* a, int ks) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) a[rt] = QS[(ks * TM + rt * 16) * 4 + qlane];
+    };
+    auto mma = [&](const uint4* a, const uint4* b) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int k = 0; k < CB; ++k) SL::mma(a[rt], b[k], acc[rt][k]);
+      if (IDW) {
+#pragma unroll
+        for (int k = 0; k < CB; ++k) kn[k] += SL::sumsq(b[k]);
+      }
+    };
+    // epilogue of batch jb: order keys of the rounded scores into the tile
+    // (lane: rows rt*16 + 4 (lane >> 4) + e, column 16 tile + (lane & 15))
+    auto epilogue = [&](int jb) {
       if (IDW) {
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
@@ -464,155 +568,348 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
           kn[k] += __shfl_xor(kn[k], 32);  // squared norm of key 16*tile + (lane & 15)
         }
       }
-      // epilogue: order keys of the rounded scores into the tile, group maxima
 #pragma unroll
       for (int k = 0; k < CB; ++k) {
-        if (!tv[k]) continue;
-        const int col = 16 * tile[k] + (lane & 15);
+        const int tile = w + kWaves * (CB * jb + k);
+        if (tile >= ncol) continue;
+        // the 4 rows 4g + e of a lane share rho, so one position serves them
+        const int pos = tile_pos(M, 4 * (lane >> 4), 16 * tile + (lane & 15));
+        Store* St = S + 4 * (lane >> 4) * n + pos;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
+          float sc[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int rr = 4 * (lane >> 4) + e;  // row inside the tile
-            const int row = rt * 16 + rr;
             float s = acc[rt][k][e];
             if (IDW) {
-              float d2 = __shfl(qn[rt], rr) + kn[k] - 2.f * s;
+              float d2 = __shfl(qn[rt], 4 * (lane >> 4) + e) + kn[k] - 2.f * s;
               d2 = d2 > 0.f ? d2 : 0.f;
               s = -logf(1e-3f + d2);
             }
-            gmax[rt][e] = s > gmax[rt][e] ? s : gmax[rt][e];
-            S[row * n + s_phys(row, col)] = (Store)SL::okey_of(s);
+            sc[e] = s;
           }
+          if (sizeof(Store) == 2) {
+            // two rows per conversion: order keys of a packed bf16 pair
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+              const uint32_t k2 = okey16x2(pack2_bf16(sc[e] + 0.0f, sc[e + 1] + 0.0f));
+              St[(rt * 16 + e) * n] = (Store)k2;
+              St[(rt * 16 + e + 1) * n] = (Store)(k2 >> 16);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) St[(rt * 16 + e) * n] = (Store)SL::okey_of(sc[e]);
+          }
+        }
+      }
+    };
+    uint4 a[RT], b0[CB], b1[CB], b2[CB];
+    reset();
+    load_b(b0, 0, 0);
+    load_b(b1, 0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // k-step ks of batch jb runs on the ring slot b and loads the step two
+    // ahead into bn
+    auto body = [&](int jb, int ks, const uint4* b, uint4* bn) {
+      load_a(a, ks);
+      load_b(bn, jb, ks + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(a, b);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int jb = 0; jb < nbw; ++jb) {
+      if (KSC > 0) {
+        // compile-time k-steps: one straight run per batch, so the waits
+        // before each step cover only that step's loads
+#pragma unroll
+        for (int ks = 0; ks < KSC; ++ks) {
+          if (ks % 3 == 0)
+            body(jb, ks, b0, b2);
+          else if (ks % 3 == 1)
+            body(jb, ks, b1, b0);
+          else
+            body(jb, ks, b2, b1);
+        }
+      } else {
+        for (int ks = 0; ks < KS; ks += 3) {
+          body(jb, ks, b0, b2);
+          if (ks + 1 < KS) body(jb, ks + 1, b1, b0);
+          if (ks + 2 < KS) body(jb, ks + 2, b2, b1);
+        }
+      }
+      epilogue(jb);
+      reset();
+      // the next batch's first two steps are in flight in the slots after the
+      // last one used: rotate them to b0, b1 (after the epilogue, so the moves
+      // rarely wait for the loads)
+      const int rot = (KSC > 0 ? KSC : KS) % 3;
+      if (rot == 1) {
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+          b0[k] = b1[k];
+          b1[k] = b2[k];
+        }
+      } else if (rot == 2) {
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+          const uint4 x = b0[k];
+          b0[k] = b2[k];
+          b1[k] = x;
         }
       }
     }
     __syncthreads();  // score tile complete; the query stage is free
-    if (16 * w < G) {
+    // the first half's list of this row (parked in the index output), needed in C
+    Key park[(64 + LPR - 1) / LPR];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = rt * 16 + 4 * (lane >> 4) + e;
-          GM[row * G + 16 * w + (lane & 15)] = (uint16_t)SL::coarse(SL::okey_of(gmax[rt][e]));
-        }
+    for (int i = 0; i < (64 + LPR - 1) / LPR; ++i) {
+      const int j = sub + LPR * i;
+      park[i] = (hc == 1 && live && j < knn) ? (Key)out_idx[orow + j] : (Key)0;
     }
-    __syncthreads();
 
-    // ---- B: exact top-knn of each row (and C after the second half)
+    // ---- sub-score outputs (every key), coalesced over the workgroup
     TIN* out_s = hc == 0 ? out_s1 : out_s2;
-    for (int r = w; r < TM; r += kWaves) {
-      const int64_t t = t0 + r;
-      if (t >= Ntok) continue;
-      const int64_t th = t * H + h;
-      const Store* Srow = S + r * n;
-      if (out_s != nullptr) {
-        for (int col = lane; col < n; col += 64) SL::put(out_s, th * n + col, Srow[s_phys(r, col)]);
-      }
-      // T0: knn-th largest group maximum
-      const uint32_t gk0 = GM[r * G + lane];
-      const uint32_t gk1 = G > 64 ? GM[r * G + 64 + lane] : 0u;
-      uint32_t T0 = 0;
-      for (int bit = 15; bit >= 0; --bit) {
-        const uint32_t trial = T0 | (1u << bit);
-        uint32_t c = (uint32_t)__popcll(__ballot(gk0 >= trial));
-        if (G > 64) c += (uint32_t)__popcll(__ballot(gk1 >= trial));
-        if (c >= (uint32_t)knn) T0 = trial;
-      }
-      // chunks whose maximum reaches T0
-      uint32_t nact = 0;
-      for (int c = lane; c - lane < NC; c += 64) {
-        const bool act = c < NC && SL::chunk_max(Srow + s_phys(r, kChunk * c)) >= T0;
-        const uint64_t m = __ballot(act);
-        if (act) clist[nact + lanes_below_count(m)] = (uint16_t)c;
-        nact += (uint32_t)__popcll(m);
-      }
-      __builtin_amdgcn_wave_barrier();
-      // their scores >= T0, 64 per ballot
-      uint32_t total = 0;
-      for (uint32_t base = 0; base < nact * kChunk; base += 64) {
-        const uint32_t slot = base + lane;
-        bool cand = false;
-        Key key = 0;
-        if (slot < nact * kChunk) {
-          const int col = kChunk * clist[slot / kChunk] + (int)(slot % kChunk);
-          const uint32_t ok = Srow[s_phys(r, col)];
-          cand = SL::coarse(ok) >= T0;
-          key = SL::make(ok, (uint32_t)col);
-        }
-        wave_append(cand, key, scr, total);
-      }
-      __builtin_amdgcn_wave_barrier();
-      Key best;
-      if (total <= (uint32_t)kCandCap) {
-        best = rank_select(scr, total, knn);
-      } else {
-        best = exact_topk<Key>([&](int col) { return SL::make(Srow[s_phys(r, col)], (uint32_t)col); }, n, knn, scr);
-      }
-      const int64_t orow = th * knn;
-      if (hc == 0) {
-        // park the first half's list in the index output until the cartesian step
-        if (lane < knn) out_idx[orow + lane] = (int64_t)best;
-        if (out_i1 != nullptr && lane < knn) out_i1[orow + lane] = (int64_t)SL::key_idx(best);
-        continue;
-      }
-      if (out_i2 != nullptr && lane < knn) out_i2[orow + lane] = (int64_t)SL::key_idx(best);
-
-      // ---- C: cartesian top-knn of this token
-      const Key l0 = lane < knn ? (Key)out_idx[orow + lane] : (Key)0;
-      const Key l1 = best;
-      // lower bound of the knn-th pair value: the knn pairs (a, 0) and the knn pairs (0, b)
-      const float v0 = SL::value(SL::key_okey(lane_key(l0, 0)));
-      const float w0 = SL::value(SL::key_okey(lane_key(l1, 0)));
-      const uint32_t ta = SL::okey_of(SL::value(SL::key_okey(lane_key(l0, knn - 1))) + w0);
-      const uint32_t tb = SL::okey_of(v0 + SL::value(SL::key_okey(lane_key(l1, knn - 1))));
-      const uint32_t Tc = ta > tb ? ta : tb;
-      Key keys[kMaxPairSlots];
-      uint32_t ctotal = 0;
-#pragma unroll
-      for (int s = 0; s < kMaxPairSlots; ++s) {
-        keys[s] = 0;
-        if (s < NP) {
-          const Key k0 = shfl_key(l0, pa[s]);
-          const Key k1 = shfl_key(l1, pb[s]);
-          const uint32_t ok = SL::okey_of(SL::value(SL::key_okey(k0)) + SL::value(SL::key_okey(k1)));
-          const bool valid = 64 * s + lane < npairs;
-          if (valid) keys[s] = SL::make(ok, (uint32_t)(pa[s] * knn + pb[s]));
-          wave_append(valid && ok >= Tc, keys[s], scr, ctotal);
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      Key top;
-      if (ctotal <= (uint32_t)kCandCap) {
-        top = rank_select(scr, ctotal, knn);
-      } else {
-        top = exact_topk<Key>(
-            [&](int slot) {
-              Key k = 0;
-#pragma unroll
-              for (int s = 0; s < kMaxPairSlots; ++s)
-                if (slot >> 6 == s) k = keys[s];
-              return k;
-            },
-            64 * NP, knn, scr);
-      }
-      const uint32_t flat = SL::key_idx(top);
-      int a = (int)(flat / (uint32_t)knn);
-      int b = (int)(flat - (uint32_t)a * (uint32_t)knn);
-      a = a < 63 ? a : 63;
-      b = b < 63 ? b : 63;
-      const uint32_t i0 = SL::key_idx(shfl_key(l0, a));
-      const uint32_t i1 = SL::key_idx(shfl_key(l1, b));
-      if (lane < knn) {
-        SL::put(out_scores, orow + lane, SL::key_okey(top));
-        out_idx[orow + lane] = (int64_t)i0 * n + (int64_t)i1;
+    if (out_s != nullptr) {
+      for (int i = threadIdx.x; i < TM * n; i += kThreads) {
+        const int q = i / n, col = i - (i / n) * n;
+        if (t0 + q < Ntok) SL::put(out_s, ((t0 + q) * H + h) * n + col, S[q * n + tile_pos(M, q, col)]);
       }
     }
-    __syncthreads();  // before the next half overwrites the score tile and the shared region
+
+    // ---- B: top-knn of row r by its lane group.
+    // T0 = the knn-th largest group maximum is a lower bound of the knn-th
+    // largest score (knn disjoint groups each hold a score >= T0), so the
+    // top-knn are among the scores >= T0; they are compacted into cand and
+    // ranked. More than cap of them (e.g. many equal scores) leave the row to
+    // the exact search of its wave below.
+    // chunk i of this lane (zeros past the row)
+    const uint32_t* Sw = (const uint32_t*)(S + r * n);
+    auto chunk_of = [&](int i) { return LPR * (i ^ cx) + sub; };
+    auto load_chunk = [&](int i) -> uint4 {
+      const int c = chunk_of(i);
+      return c < NCH ? *(const uint4*)(Sw + 4 * c) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto word_max = [&](uint32_t x) -> uint32_t {
+      if (EPW == 2) {
+        const uint32_t lo = x & 0xFFFFu, hi = x >> 16;
+        return lo > hi ? lo : hi;
+      }
+      return x;
+    };
+    uint32_t gm[MAXG];
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      const uint4 v = g < NG ? load_chunk(g) : make_uint4(0u, 0u, 0u, 0u);
+      uint32_t m = word_max(v.x);
+      m = word_max(v.y) > m ? word_max(v.y) : m;
+      m = word_max(v.z) > m ? word_max(v.z) : m;
+      gm[g] = word_max(v.w) > m ? word_max(v.w) : m;
+    }
+    uint32_t T0 = 0;
+    for (int bit = KBITS - 1; bit >= 0; --bit) {
+      const uint32_t trial = T0 | (1u << bit);
+      if (!group_count_ge_below<LPR, MAXG, KBITS>(gm, trial, knn)) T0 = trial;
+    }
+    // candidates: elements >= T0, in the chunks whose maximum reaches it
+    // (T0 >= 1 when any exist: chunks past the row are 0)
+    const uint32_t T0e = T0 > 0u ? T0 : 1u;
+    uint32_t act = 0;
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) act |= (gm[g] >= T0e ? 1u : 0u) << g;
+    uint32_t cnt = 0;
+    for (uint32_t m = act; m != 0; m &= m - 1) {
+      const uint4 v = load_chunk(__builtin_ctz(m));
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4 * EPW; ++j) {
+        const uint32_t x = EPW == 2 ? ((vw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu) : vw[j];
+        cnt += x >= T0e ? 1u : 0u;
+      }
+    }
+    const uint32_t incl = group_scan<LPR>(cnt, sub);
+    const uint32_t total = group_sum<LPR>(cnt);
+    const bool overflow = total > (uint32_t)L.cap;
+    if (!overflow) {
+      uint32_t p = incl - cnt;
+      // column of element j of chunk c: c * (E / slots) + off[j] when a chunk
+      // of E elements spans whole groups of slots positions
+      constexpr int E = 4 * EPW;
+      const bool whole = M.slots <= E;
+      int off[E];
+#pragma unroll
+      for (int j = 0; j < E; ++j) off[j] = tile_col(M, r, j);
+      const int cstep = whole ? (E >> M.lslots) : 0;
+      for (uint32_t m = act; m != 0; m &= m - 1) {
+        const int g = __builtin_ctz(m);
+        const uint4 v = load_chunk(g);
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+        const int c = chunk_of(g);
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+          const uint32_t x = EPW == 2 ? ((vw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu) : vw[j];
+          if (x >= T0e) {
+            const int col = whole ? c * cstep + off[j] : tile_col(M, r, c * E + j);
+            cand[p++] = SL::make(x, (uint32_t)col);
+          }
+        }
+      }
+      if (sub == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) cand[total + u] = (Key)0;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    auto to_list = [&](uint32_t rank, Key k) { list[rank] = k; };
+    if (!overflow) {
+      if (L.cap <= 8 * LPR)
+        group_rank<Key, LPR, 8>(cand, total, knn, sub, to_list);
+      else
+        group_rank<Key, LPR, MAXM>(cand, total, knn, sub, to_list);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // exact search for the rows of this wave that overflowed, one at a time;
+    // the wave's candidate buffers are its scratch
+    Key* wscr = (Key*)(R + L.cand_off) + (w * RPW) * L.cstride;
+    {
+      const uint64_t ov = __ballot(overflow);
+      for (int rr = 0; rr < RPW; ++rr) {
+        if (!((ov >> (rr * LPR)) & 1ull)) continue;
+        const int row = w * RPW + rr;
+        const Store* Srow = S + row * n;
+        const Key best = exact_topk<Key>(
+            [&](int col) { return SL::make(Srow[tile_pos(M, row, col)], (uint32_t)col); }, n, knn, wscr);
+        if (lane < knn) ((Key*)(R + L.list_off) + row * L.kl)[lane] = best;
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (hc == 0) {
+      // park the first half's list in the index output until the cartesian step
+      if (live) {
+        for (int j = sub; j < knn; j += LPR) {
+          const Key k = list[j];
+          out_idx[orow + j] = (int64_t)k;
+          if (out_i1 != nullptr) out_i1[orow + j] = (int64_t)SL::key_idx(k);
+        }
+      }
+      __syncthreads();  // before the next half overwrites the tile and the shared region
+      continue;
+    }
+    if (live && out_i2 != nullptr) {
+      for (int j = sub; j < knn; j += LPR) out_i2[orow + j] = (int64_t)SL::key_idx(list[j]);
+    }
+    __syncthreads();  // every row selected: the tile is free for the first half's lists and the pair table
+
+    // ---- C: cartesian top-knn of token r by its lane group, over the pairs
+    // (a+1)(b+1) <= knn (every other pair is preceded, in (value, flat index)
+    // order, by at least knn of them): T = the knn-th largest pair value, by
+    // a bit search between a lower bound and the best pair, then the pairs
+    // >= T are ranked.
+#pragma unroll
+    for (int i = 0; i < (64 + LPR - 1) / LPR; ++i) {
+      const int j = sub + LPR * i;
+      if (j < knn) l0[j] = park[i];
+    }
+    __builtin_amdgcn_wave_barrier();  // the first half's list of a row is written and read by its own lanes
+    // value (order key) of pair slot s; candidates are keyed by the slot,
+    // whose order is the flat a * knn + b order
+    auto pair_okey = [&](const Key* l0r, const Key* l1r, int s) -> uint32_t {
+      const uint32_t ab = pairs[s];
+      return SL::okey_of(SL::value(SL::key_okey(l0r[ab & 0xFFu])) + SL::value(SL::key_okey(l1r[ab >> 8])));
+    };
+    // the knn-th pair value lies between the knn-th of the pairs (a, 0) or
+    // (0, b) and the best pair; bits above their highest difference are shared
+    uint32_t Tlo, Thi;
+    {
+      const float v0 = SL::value(SL::key_okey(l0[0]));
+      const float w0 = SL::value(SL::key_okey(list[0]));
+      const uint32_t ta = SL::okey_of(SL::value(SL::key_okey(l0[knn - 1])) + w0);
+      const uint32_t tb = SL::okey_of(v0 + SL::value(SL::key_okey(list[knn - 1])));
+      Tlo = ta > tb ? ta : tb;
+      Thi = SL::okey_of(v0 + w0);
+    }
+    // pair values of this lane's slots sub + LPR i (0 past the last), the
+    // threshold T, and the compaction of the pairs >= T; NS = slots per lane
+    auto cartesian = [&](auto ns_tag, uint32_t& ctotal_out) -> bool {
+      constexpr int NS = decltype(ns_tag)::value;
+      uint32_t cv[NS];
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int s = sub + LPR * i;
+        cv[i] = s < npairs ? pair_okey(l0, list, s) : 0u;
+      }
+      const uint32_t d = Tlo ^ Thi;
+      const int hb = d == 0 ? -1 : 31 - __builtin_clz(d);
+      uint32_t T = hb < 0 ? Tlo : (Thi & ~((2u << hb) - 1u));
+      for (int bit = hb; bit >= 0; --bit) {
+        const uint32_t trial = T | (1u << bit);
+        if (!group_count_ge_below<LPR, NS, KBITS>(cv, trial, knn)) T = trial;
+      }
+      T = T > 0u ? T : 1u;
+      uint32_t ccnt = 0;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) ccnt += cv[i] >= T ? 1u : 0u;
+      const uint32_t cincl = group_scan<LPR>(ccnt, sub);
+      const uint32_t ctotal = group_sum<LPR>(ccnt);
+      ctotal_out = ctotal;
+      const bool ov = ctotal > (uint32_t)L.cap;
+      if (!ov) {
+        uint32_t p = cincl - ccnt;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          if (cv[i] >= T) cand[p++] = SL::make(cv[i], (uint32_t)(sub + LPR * i));
+        if (sub == 0) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) cand[ctotal + u] = (Key)0;
+        }
+      }
+      return ov;
+    };
+    uint32_t ctotal = 0;
+    bool coverflow;
+    if (npairs <= LPR * ((pair_count(16) + LPR - 1) / LPR))
+      coverflow = cartesian(std::integral_constant<int, (pair_count(16) + LPR - 1) / LPR>(), ctotal);
+    else if (npairs <= LPR * ((pair_count(32) + LPR - 1) / LPR))
+      coverflow = cartesian(std::integral_constant<int, (pair_count(32) + LPR - 1) / LPR>(), ctotal);
+    else
+      coverflow = cartesian(std::integral_constant<int, MAXS>(), ctotal);
+    __builtin_amdgcn_wave_barrier();
+    auto to_fin = [&](uint32_t rank, Key k) { fin[rank] = k; };
+    if (!coverflow) {
+      if (L.cap <= 8 * LPR)
+        group_rank<Key, LPR, 8>(cand, ctotal, knn, sub, to_fin);
+      else
+        group_rank<Key, LPR, MAXM>(cand, ctotal, knn, sub, to_fin);
+    }
+    __builtin_amdgcn_wave_barrier();
+    {
+      const uint64_t ov = __ballot(coverflow);
+      for (int rr = 0; rr < RPW; ++rr) {
+        if (!((ov >> (rr * LPR)) & 1ull)) continue;
+        const int row = w * RPW + rr;
+        const Key* l0r = (const Key*)smem + row * L.kl;
+        const Key* l1r = (const Key*)(R + L.list_off) + row * L.kl;
+        const Key top = exact_topk<Key>(
+            [&](int s) -> Key { return s < npairs ? SL::make(pair_okey(l0r, l1r, s), (uint32_t)s) : (Key)0; },
+            npairs, knn, wscr);
+        if (lane < knn) ((Key*)smem + (TM + row) * L.kl)[lane] = top;
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // outputs: the pair's rounded sum and slot id i_0[a] * n + i_1[b]
+    if (live) {
+      for (int j = sub; j < knn; j += LPR) {
+        const Key k = fin[j];
+        const uint32_t ab = pairs[SL::key_idx(k)];
+        SL::put(out_scores, orow + j, SL::key_okey(k));
+        out_idx[orow + j] = (int64_t)SL::key_idx(l0[ab & 0xFFu]) * n + (int64_t)SL::key_idx(list[ab >> 8]);
+      }
+    }
   }
 }
 
-template <typename TIN, int IDW, int TM>
+template <typename TIN, int IDW, int TM, int KSC>
 static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
                            size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
                            int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
@@ -624,17 +921,39 @@ static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H,
   if (e != hipSuccess) return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: hipGetDevice failed: %s", hipGetErrorString(e));
   const uint64_t bit = 1ull << (dev & 63);
   if (!(lds_enabled.load(std::memory_order_relaxed) & bit)) {
-    e = hipFuncSetAttribute((const void*)pkm_score_topk_kernel<TIN, IDW, TM>,
+    e = hipFuncSetAttribute((const void*)pkm_score_topk_kernel<TIN, IDW, TM, KSC>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
     if (e != hipSuccess)
       return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
     lds_enabled.fetch_or(bit, std::memory_order_relaxed);
   }
   const int64_t blocks = ((Ntok + TM - 1) / TM) * H;
-  hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
+  hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM, KSC>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
                      (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
                      out_i2, (TIN*)out_s1, (TIN*)out_s2);
   return PKM_OK;
+}
+
+// Kernel variant for (TM, k-steps per half): the k-step counts of the common
+// half key dims (128, 256, 512 elements) are compile-time.
+template <typename TIN, int IDW, int TM>
+static int launch_score_ks(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
+                           size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
+                           int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
+  switch (half / Sel<TIN>::KSTEP) {
+    case 4:
+      return launch_score_tm<TIN, IDW, TM, 4>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+                                              out_i1, out_i2, out_s1, out_s2, st);
+    case 8:
+      return launch_score_tm<TIN, IDW, TM, 8>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+                                              out_i1, out_i2, out_s1, out_s2, st);
+    case 16:
+      return launch_score_tm<TIN, IDW, TM, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+                                               out_i1, out_i2, out_s1, out_s2, st);
+    default:
+      return launch_score_tm<TIN, IDW, TM, 0>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+                                              out_i1, out_i2, out_s1, out_s2, st);
+  }
 }
 
 template <typename TIN, int IDW>
@@ -643,13 +962,13 @@ static int launch_score(int TM, const void* q, const void* keys, int64_t Ntok, i
                         int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
   switch (TM) {
     case 64:
-      return launch_score_tm<TIN, IDW, 64>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+      return launch_score_ks<TIN, IDW, 64>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
                                            out_i2, out_s1, out_s2, st);
     case 32:
-      return launch_score_tm<TIN, IDW, 32>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+      return launch_score_ks<TIN, IDW, 32>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
                                            out_i2, out_s1, out_s2, st);
     default:
-      return launch_score_tm<TIN, IDW, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+      return launch_score_ks<TIN, IDW, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
                                            out_i2, out_s1, out_s2, st);
   }
 }
@@ -689,8 +1008,10 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
     return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: device query failed: %s", hipGetErrorString(e));
   if (lds_max > kMaxLds) lds_max = kMaxLds;
   int TM = 64;
-  while (TM > 16 && score_lds_layout(TM, (int)n_keys, (int)half, esz, key_bytes).total > lds_max) TM /= 2;
-  const int lds = score_lds_layout(TM, (int)n_keys, (int)half, esz, key_bytes).total;
+  while (TM > 16 && (score_lds_layout(TM, (int)n_keys, (int)half, (int)knn, esz, key_bytes).total > lds_max ||
+                     n_keys > score_max_n(TM, esz)))
+    TM /= 2;
+  const int lds = score_lds_layout(TM, (int)n_keys, (int)half, (int)knn, esz, key_bytes).total;
   PKM_REQUIRE(lds <= lds_max, PKM_ERR_UNSUPPORTED,
               "pkm_score_topk: n_keys %lld / half %lld need %d bytes of LDS, the device allows %d", (long long)n_keys,
               (long long)half, lds, lds_max);
