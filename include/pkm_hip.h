@@ -160,6 +160,37 @@ int pkm_score_grad_dense(const int64_t* indices, const void* d_scores, int dtype
                          void* d_sub_dense, void* stream);
 
 /*
+ * RMS normalisation of the query rows, forward (dtype F32 or BF16 for x,
+ * weight and y alike; x, weight, y 16-byte aligned, dim a multiple of 4 / 8):
+ *   rstd[i]  = rsqrt(mean_j x[i, j]^2 + eps)                       float32 [rows]
+ *   y[i, j]  = dtype(weight[j] * dtype(x[i, j] * rstd[i]))          [rows, dim]
+ *
+ * Replaces Qwen3RMSNorm.forward of the query network (pkm/memory.py:311,
+ * 341-349; transformers' Qwen3RMSNorm: float32 cast, pow, mean, rsqrt, mul,
+ * cast back, weight mul).
+ */
+int pkm_rmsnorm_fwd(const void* x, const void* weight, int64_t rows, int64_t dim, int dtype, float eps, void* y,
+                    float* rstd, void* stream);
+
+/* Workspace bytes pkm_rmsnorm_bwd needs for these sizes. */
+size_t pkm_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dim);
+
+/*
+ * Backward of pkm_rmsnorm_fwd, the gradients autograd forms through the
+ * reference's op sequence (rstd from the forward):
+ *   g[i, j]       = dtype(dy[i, j] * weight[j])
+ *   s[i]          = sum_j g[i, j] * x[i, j]                         float32
+ *   dx[i, j]      = dtype(g[i, j] * rstd[i] + x[i, j] * (2 / dim) * (-0.5 * s[i] * rstd[i]^3))
+ *   dweight[j]    = dtype(sum_i dtype(dy[i, j] * dtype(x[i, j] * rstd[i])))   float32 sum
+ * dweight is a deterministic reduction (fixed order over 64-row blocks).
+ * workspace: device buffer of at least pkm_rmsnorm_bwd_workspace_size() bytes.
+ *
+ * Replaces the autograd backward of Qwen3RMSNorm.forward (pkm/memory.py:311).
+ */
+int pkm_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const float* rstd, int64_t rows, int64_t dim,
+                    int dtype, void* dx, void* dweight, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Counts indices outside [0, num_rows) into *count_out (a device int64),
  * which the call overwrites. No counterpart in the reference (its Triton
  * kernels do no bounds check; its CPU path raises from F.embedding_bag,

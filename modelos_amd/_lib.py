@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import c_char_p, c_int, c_int64, c_size_t, c_void_p
+from ctypes import c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (must be imported before the HIP library is opened)
@@ -65,6 +65,20 @@ SIGNATURES = {
             c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, knn
             c_void_p, c_void_p,  # d_sub_scores1, d_sub_scores2
             c_void_p, c_void_p,  # d_sub_dense, stream
+        ],
+    ),
+    "pkm_rmsnorm_fwd": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int, c_float, c_void_p, c_void_p, c_void_p],
+    ),
+    "pkm_rmsnorm_bwd_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "pkm_rmsnorm_bwd": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_void_p,  # dy, x, weight, rstd
+            c_int64, c_int64, c_int,  # rows, dim, dtype
+            c_void_p, c_void_p,  # dx, dweight
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),
 }
@@ -153,6 +167,8 @@ _SIZE_ARGS = {
     "pkm_eb_bwd": (1, 2),
     "pkm_eb_bwd2": (1, 2),
     "pkm_score_topk": (2, 3, 4, 5),  # num_tokens, heads, n_keys, half
+    "pkm_rmsnorm_fwd": (2, 3),  # rows, dim
+    "pkm_rmsnorm_bwd": (4, 5),
 }
 
 

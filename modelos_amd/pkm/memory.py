@@ -28,6 +28,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from ..product_keys import product_key_topk
+from ..rmsnorm import QueryRMSNorm
 from .colwise_embedding_bag import xFormerEmbeddingBag
 
 logger = getLogger()
@@ -235,9 +236,8 @@ class QueryMLP(nn.Module):
         if batchnorm:
             self.norm = nn.BatchNorm1d(sizes[-1], affine=True, eps=1e-6, momentum=0.1)
         elif rmsnorm:
-            from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
-
-            self.norm = Qwen3RMSNorm(sizes[-1], eps=1e-6)
+            # Qwen3RMSNorm (memory.py:311) on the fused HIP kernels
+            self.norm = QueryRMSNorm(sizes[-1], eps=1e-6)
         else:
             self.norm = None
 
