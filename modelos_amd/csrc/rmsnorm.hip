@@ -18,7 +18,8 @@
 // 1 KB access), so x is read once by the forward and x, dy once by the dx
 // pass. dw is a column reduction over all rows: blocks of 256 threads, one
 // 16-byte column vector per thread, sum RB rows each into float32 partials
-// [N / RB, D], which a second pass adds in row-block order (deterministic).
+// [N / RB, D], which a second pass adds in a fixed order (deterministic).
+// Rows too long for registers (more than 8 vectors per lane) are read twice.
 #include "pkm_common.h"
 
 namespace pkm {
@@ -198,17 +199,38 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_dw_partial_kernel(const T* __
   for (int e = 0; e < EPV; e += 4) *(float4*)(pr + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
 }
 
+// dw[j] = sum over the row blocks b (in order) of part[b, j]: 64 columns per
+// block, the partials split over 4 thread slices (each summing a contiguous
+// range of blocks, loads kept in flight), the slices added in order.
 template <typename T>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_dw_reduce_kernel(const float* __restrict__ part, int64_t nrb,
                                                                     int D, T* __restrict__ dw) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= D) return;
+  __shared__ float ps[4][64];
+  const int jl = threadIdx.x & 63, sl = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + jl;
+  const int64_t per = (nrb + 3) / 4;
+  const int64_t b0 = sl * per, b1 = b0 + per < nrb ? b0 + per : nrb;
   float s = 0.f;
-  for (int64_t b = 0; b < nrb; ++b) s += part[b * D + j];
-  if (sizeof(T) == 4)
-    ((float*)dw)[j] = s;
-  else
-    ((uint16_t*)dw)[j] = (uint16_t)f32_to_bf16_bits(s);
+  if (j < D) {
+    int64_t b = b0;
+    for (; b + 8 <= b1; b += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[(b + u) * D + j];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; b < b1; ++b) s += part[b * D + j];
+  }
+  ps[sl][jl] = s;
+  __syncthreads();
+  if (sl == 0 && j < D) {
+    const float t = ((ps[0][jl] + ps[1][jl]) + ps[2][jl]) + ps[3][jl];
+    if (sizeof(T) == 4)
+      ((float*)dw)[j] = t;
+    else
+      ((uint16_t*)dw)[j] = (uint16_t)f32_to_bf16_bits(t);
+  }
 }
 
 }  // namespace pkm
@@ -271,7 +293,7 @@ extern "C" int pkm_rmsnorm_bwd(const void* dy, const void* x, const void* weight
   hipStream_t st = (hipStream_t)stream;
   const int D = (int)dim;
   if (rows == 0) {  // dweight = 0 (a reduction over no partials)
-    const dim3 rgrid((unsigned)((D + 255) / 256));
+    const dim3 rgrid((unsigned)((D + 63) / 64));
     if (dtype == PKM_DTYPE_BF16)
       hipLaunchKernelGGL((rmsnorm_bwd_dw_reduce_kernel<bf16_t>), rgrid, dim3(256), 0, st, (const float*)nullptr,
                          (int64_t)0, D, (bf16_t*)dweight);
@@ -293,7 +315,7 @@ extern "C" int pkm_rmsnorm_bwd(const void* dy, const void* x, const void* weight
               (long long)rows);
   const dim3 grid((unsigned)((rows + 3) / 4));
   const dim3 pgrid((unsigned)((nv + 255) / 256), (unsigned)nrb);
-  const dim3 rgrid((unsigned)((D + 255) / 256));
+  const dim3 rgrid((unsigned)((D + 63) / 64));
   float* part = (float*)workspace;
   if (dtype == PKM_DTYPE_BF16) {
     if (nv <= 64 * 8)
