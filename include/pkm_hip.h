@@ -159,6 +159,32 @@ int pkm_score_grad_dense(const int64_t* indices, const void* d_scores, int dtype
                          const void* d_sub_scores1, const void* d_sub_scores2,
                          void* d_sub_dense, void* stream);
 
+/* Workspace bytes pkm_score_grad_sparse needs for these sizes (0 when unsupported). */
+size_t pkm_score_grad_sparse_workspace_size(int64_t num_tokens, int64_t heads, int64_t n_keys,
+                                            int64_t half, int64_t knn);
+
+/*
+ * Gradients of the selected dot-product scores w.r.t. query and keys without
+ * the dense sub-score gradient: with dS_c the matrix pkm_score_grad_dense
+ * writes (no d_sub_scores),
+ *   d_query[t, h, c*half + e] = sum_i dS_c[h, t, i] * keys[(2h + c) n_keys + i, e]
+ *   d_keys[(2h + c) n_keys + i, e] = sum_t dS_c[h, t, i] * query[t, h, c*half + e]
+ * on MFMA (float32 accumulation; d_keys summed over fixed token splits in
+ * order, so the result is deterministic), rounded once to bfloat16.
+ *   query: [num_tokens, heads, 2*half], keys: [2*heads*n_keys, half] (16-byte aligned),
+ *   indices, d_scores: [num_tokens, heads, knn].
+ *   d_query / d_keys: same shapes as query / keys, fully written; NULL skips one.
+ * dtype BF16 only. Limits: n_keys a multiple of 128 up to 65535, half a multiple of 16
+ * up to 256, knn <= 64. Ids outside [0, n_keys^2) are ignored.
+ *
+ * Replaces the autograd backward of einsum + topk + gather + expand-add in
+ * HashingMemory.get_indices (pkm/memory.py:257-285), score_type DOT.
+ */
+int pkm_score_grad_sparse(const int64_t* indices, const void* d_scores, int dtype,
+                          int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t half, int64_t knn,
+                          const void* query, const void* keys, void* d_query, void* d_keys,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * RMS normalisation of the query rows, forward (dtype F32 or BF16 for x,
  * weight and y alike; x, weight, y 16-byte aligned, dim a multiple of 4 / 8):

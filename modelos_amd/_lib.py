@@ -67,6 +67,16 @@ SIGNATURES = {
             c_void_p, c_void_p,  # d_sub_dense, stream
         ],
     ),
+    "pkm_score_grad_sparse_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "pkm_score_grad_sparse": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_int,  # indices, d_scores, dtype
+            c_int64, c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, half, knn
+            c_void_p, c_void_p, c_void_p, c_void_p,  # query, keys, d_query, d_keys
+            c_void_p, c_size_t, c_void_p,  # workspace, workspace_bytes, stream
+        ],
+    ),
     "pkm_rmsnorm_fwd": (
         c_int,
         [c_void_p, c_void_p, c_int64, c_int64, c_int, c_float, c_void_p, c_void_p, c_void_p],

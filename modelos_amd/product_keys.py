@@ -4,8 +4,11 @@
 stream. `product_key_topk` wraps it in autograd:
 
   * the returned top-knn scores, and the optional full sub-score matrices
-    s_1, s_2 (fast-weight PKM), are differentiable w.r.t. query and keys. The
-    backward scatters the selected scores' gradient into dense sub-score
+    s_1, s_2 (fast-weight PKM), are differentiable w.r.t. query and keys.
+    For bfloat16 dot scores without sub-score gradients the backward is one
+    call (pkm_score_grad_sparse): the nonzeros of each sub-score gradient row
+    are listed and dq = dS @ K, dK = dS^T @ q run on MFMA from those lists.
+    Otherwise it scatters the selected scores' gradient into dense sub-score
     gradients (pkm_score_grad_dense, deterministic, dense upstream gradients
     of s_1, s_2 added) and takes dq = dS @ K and dK = dS^T @ q as batched
     GEMMs per (head, half), as autograd does for the reference's einsum.
@@ -110,6 +113,36 @@ def score_grad_dense(indices: torch.Tensor, d_scores: torch.Tensor, heads: int, 
     return dS
 
 
+def score_grad_sparse(query: torch.Tensor, keys: torch.Tensor, indices: torch.Tensor, d_scores: torch.Tensor,
+                      heads: int, need_query: bool = True, need_keys: bool = True):
+    """Gradients (d_query [tokens, heads, k_dim], d_keys like keys; None where
+    not needed) of the selected dot-product scores, from the sparse rows of
+    the sub-score gradient on MFMA (pkm_score_grad_sparse): bfloat16 only.
+    Returns None when these sizes are outside the kernel's limits."""
+    dev = _require_device(query, keys, indices, d_scores)
+    half = keys.shape[1]
+    n = keys.shape[0] // (2 * heads)
+    NH, knn = indices.shape
+    N = NH // heads
+    if query.dtype != torch.bfloat16 or keys.dtype != torch.bfloat16:
+        return None
+    ws_bytes = int(_lib.load().pkm_score_grad_sparse_workspace_size(N, heads, n, half, knn))
+    if ws_bytes == 0:
+        return None
+    query = _aligned(query)
+    keys = _aligned(keys)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    dq = torch.empty((N, heads, 2 * half), dtype=query.dtype, device=dev) if need_query else None
+    dk = torch.empty_like(keys) if need_keys else None
+    _lib.call(
+        "pkm_score_grad_sparse",
+        _lib.ptr(indices.contiguous()), _lib.ptr(d_scores.to(query.dtype).contiguous()), _lib.dtype_code(query),
+        N, heads, n, half, knn, _lib.ptr(query), _lib.ptr(keys), _lib.ptr(dq), _lib.ptr(dk),
+        _lib.ptr(ws), ws_bytes, _lib.stream_of(dev),
+    )
+    return dq, dk
+
+
 def _grads_from_dense(query, keys, dS, heads, n, score_type):
     """dq [tokens, heads, k_dim] and dkeys [2*heads*n, half] from the dense
     sub-score gradient dS [heads, 2, tokens, n] with one pair of batched GEMMs
@@ -157,8 +190,15 @@ class ProductKeyTopK(torch.autograd.Function):
         d_s2 = rest[3] if ctx.sub_outputs else None
         if d_scores is None:
             d_scores = torch.zeros(indices.shape, dtype=query.dtype, device=query.device)
-        dS = score_grad_dense(indices, d_scores.to(query.dtype), heads, n, d_s1, d_s2)
-        dq, dk = _grads_from_dense(_aligned(query), _aligned(keys), dS, heads, n, ctx.score_type)
+        need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        grads = None
+        if ctx.score_type == "dot" and d_s1 is None and d_s2 is None:
+            grads = score_grad_sparse(query, keys, indices, d_scores, heads, need_q, need_k)
+        if grads is not None:
+            dq, dk = grads
+        else:
+            dS = score_grad_dense(indices, d_scores.to(query.dtype), heads, n, d_s1, d_s2)
+            dq, dk = _grads_from_dense(_aligned(query), _aligned(keys), dS, heads, n, ctx.score_type)
         d_query = dq.to(query.dtype).reshape(ctx.query_shape) if ctx.needs_input_grad[0] else None
         d_keys = dk.to(keys.dtype) if ctx.needs_input_grad[1] else None
         return d_query, d_keys, None, None, None, None
@@ -176,4 +216,4 @@ def product_key_topk(
     return ProductKeyTopK.apply(query, keys, heads, knn, score_type, sub_outputs)
 
 
-__all__ = ["score_topk", "product_key_topk", "ProductKeyTopK", "score_grad_dense", "SCORE_TYPES"]
+__all__ = ["score_topk", "product_key_topk", "ProductKeyTopK", "score_grad_dense", "score_grad_sparse", "SCORE_TYPES"]
