@@ -169,11 +169,13 @@ size_t pkm_score_grad_sparse_workspace_size(int64_t num_tokens, int64_t heads, i
  * writes (no d_sub_scores),
  *   d_query[t, h, c*half + e] = sum_i dS_c[h, t, i] * keys[(2h + c) n_keys + i, e]
  *   d_keys[(2h + c) n_keys + i, e] = sum_t dS_c[h, t, i] * query[t, h, c*half + e]
- * on MFMA (float32 accumulation; d_keys summed over fixed token splits in
- * order, so the result is deterministic), rounded once to bfloat16.
- *   query: [num_tokens, heads, 2*half], keys: [2*heads*n_keys, half] (16-byte aligned),
+ * d_query from the nonzeros of each dS row (a gather of key rows, float32 in
+ * order of first occurrence), d_keys on MFMA (float32, summed over fixed
+ * token splits in order); both deterministic, rounded once to bfloat16.
+ *   query: [num_tokens, heads, 2*half], keys: [2*heads*n_keys, half],
  *   indices, d_scores: [num_tokens, heads, knn].
  *   d_query / d_keys: same shapes as query / keys, fully written; NULL skips one.
+ *   query, keys, d_query, d_keys 16-byte aligned.
  * dtype BF16 only. Limits: n_keys a multiple of 128 up to 65535, half a multiple of 16
  * up to 256, knn <= 64. Ids outside [0, n_keys^2) are ignored.
  *

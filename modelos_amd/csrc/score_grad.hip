@@ -134,223 +134,402 @@ __device__ __forceinline__ void sg_mma(const uint4& a, const uint4& b, sg_f32x4_
 constexpr uint32_t kNoEntry = 0xFFFFFFFFu;  // unused list slot
 constexpr int kSgRows = 128;                // output rows per workgroup (tokens for dq, keys for dk)
 constexpr int kSgChunk = 64;                // reduction chunk (keys for dq, tokens for dk)
-constexpr int kSgLd = kSgChunk + 8;         // LDS row pitch in bf16 (16-byte pad: distinct banks per row)
+constexpr int kSgPitch = kSgChunk;          // bf16 per LDS tile row: 8 slots of 16 bytes
 constexpr int kSgMaxHalf = 256;             // dims per half: 4 waves x 64
 constexpr int kSgThreads = 512;             // 8 waves: 2 (rows, 64 each) x 4 (dims, 64 each)
+constexpr int kSgA = kSgRows * kSgPitch;    // bf16 per dS tile (16 KB)
+constexpr int kSgB = kSgMaxHalf * kSgPitch; // bf16 per operand tile (32 KB)
+constexpr int kListThreads = 256;
 
-// Per (t, h, c): slot j holds (sub-key << 16) | bf16(sum of d over the pairs
-// j' with the same sub-key, float32 in j' order) for the first such j, else
-// kNoEntry: the nonzeros of dS_c[t, :] (the dense kernel's values).
-__global__ __launch_bounds__(64 * kGradWaves) void score_grad_lists_kernel(const int64_t* __restrict__ idx,
-                                                                           const bf16_t* __restrict__ d, int64_t NH,
-                                                                           int n, int knn,
-                                                                           uint32_t* __restrict__ lists) {
-  const int lane = threadIdx.x & 63;
-  const int64_t th = (int64_t)blockIdx.x * kGradWaves + (threadIdx.x >> 6);
-  if (th >= NH) return;
-  int a = -1, b = -1;
+// Offset of (row, col) in a [rows][64] bf16 LDS tile whose 16-byte slot s of
+// row r is stored at slot s ^ (r & 7): eight consecutive rows read at one
+// column slot cover all banks once.
+__device__ __forceinline__ int sg_swz(int row, int col) {
+  return row * kSgPitch + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+}
+
+// Workgroup order that keeps consecutive logical workgroups on one XCD
+// (workgroups are dealt to the 8 XCDs round robin): logical g runs on XCD
+// g / (count / 8) when the count is a multiple of 8.
+__device__ __forceinline__ int sg_logical_block() {
+  const int L = blockIdx.x, cnt = gridDim.x;
+  return (cnt & 7) == 0 ? (L & 7) * (cnt >> 3) + (L >> 3) : L;
+}
+
+// Per (t, h, c): the distinct sub-keys of the row's pairs, in order of first
+// occurrence, as (sub-key << 16) | bf16(sum of d over the pairs with that
+// sub-key, float32 in j order), then kNoEntry up to knn: the nonzeros of
+// dS_c[t, :] (the dense kernel's values). A group of G lanes takes one
+// (t, h); each lane compares its pair with the group's G pairs from LDS
+// (16-byte broadcast reads), and a ballot places the first occurrences.
+template <int G>
+__global__ __launch_bounds__(kListThreads) void score_grad_lists_kernel(const int64_t* __restrict__ idx,
+                                                                        const bf16_t* __restrict__ d, int64_t NH,
+                                                                        int n, int knn,
+                                                                        uint32_t* __restrict__ lists) {
+  __shared__ __align__(16) uint32_t s_pk[kListThreads];
+  __shared__ __align__(16) float s_d[kListThreads];
+  const int tid = threadIdx.x, jl = tid % G, gb = tid - jl;
+  const int64_t th = (int64_t)blockIdx.x * (kListThreads / G) + tid / G;
+  uint32_t pk = kNoEntry;
   float dv = 0.f;
-  if (lane < knn) {
-    const int64_t id = idx[th * knn + lane];
-    if (id >= 0 && id < (int64_t)n * n) {
-      a = (int)(id / n);
-      b = (int)(id - (int64_t)a * n);
-      dv = bf16_to_f32(d[th * knn + lane].x);
+  if (th < NH && jl < knn) {
+    const int64_t id = idx[th * knn + jl];
+    if (id >= 0 && id < (int64_t)n * n) {  // n <= 65535: the id fits 32 bits
+      const uint32_t u = (uint32_t)id, a = u / (uint32_t)n;
+      pk = (a << 16) | (u - a * (uint32_t)n);
+      dv = bf16_to_f32(d[th * knn + jl].x);
     }
   }
+  s_pk[tid] = pk;
+  s_d[tid] = dv;
+  __syncthreads();
+  const uint32_t ua = pk >> 16, ub = pk & 0xFFFFu;  // 0xFFFF (no sub-key) for an unused slot
   float s0 = 0.f, s1 = 0.f;
   bool first0 = true, first1 = true;
-  for (int j = 0; j < knn; ++j) {
-    const int aj = __builtin_amdgcn_readlane(a, j);
-    const int bj = __builtin_amdgcn_readlane(b, j);
-    const float dj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), j));
-    if (aj == a) {
-      s0 += dj;
-      if (j < lane) first0 = false;
-    }
-    if (bj == b) {
-      s1 += dj;
-      if (j < lane) first1 = false;
+#pragma unroll
+  for (int j0 = 0; j0 < G; j0 += 4) {
+    const uint4 kq = *(const uint4*)&s_pk[gb + j0];
+    const float4 dq = *(const float4*)&s_d[gb + j0];
+    const uint32_t kk[4] = {kq.x, kq.y, kq.z, kq.w};
+    const float dd[4] = {dq.x, dq.y, dq.z, dq.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool m0 = (kk[e] >> 16) == ua, m1 = (kk[e] & 0xFFFFu) == ub;
+      s0 = m0 ? s0 + dd[e] : s0;
+      s1 = m1 ? s1 + dd[e] : s1;
+      if (j0 + e < jl) {
+        first0 = first0 && !m0;
+        first1 = first1 && !m1;
+      }
     }
   }
-  if (lane < knn) {
-    lists[(th * 2 + 0) * knn + lane] = (a >= 0 && first0) ? (((uint32_t)a << 16) | f32_to_bf16_bits(s0)) : kNoEntry;
-    lists[(th * 2 + 1) * knn + lane] = (b >= 0 && first1) ? (((uint32_t)b << 16) | f32_to_bf16_bits(s1)) : kNoEntry;
+  const bool valid = pk != kNoEntry;
+  const bool put0 = valid && first0, put1 = valid && first1;
+  // this group's lanes of the wave-wide ballots; slot = first occurrences before this lane
+  const int gw = (tid & 63) - jl;  // the group's first lane in the wave
+  const uint64_t gmask = G == 64 ? ~0ull : ((1ull << G) - 1);
+  const uint64_t below = (1ull << jl) - 1;
+  const uint64_t b0 = (__ballot(put0) >> gw) & gmask, b1 = (__ballot(put1) >> gw) & gmask;
+  if (th < NH) {
+    uint32_t* row0 = lists + (th * 2 + 0) * knn;
+    uint32_t* row1 = row0 + knn;
+    if (put0) row0[__popcll(b0 & below)] = (ua << 16) | f32_to_bf16_bits(s0);
+    if (put1) row1[__popcll(b1 & below)] = (ub << 16) | f32_to_bf16_bits(s1);
+    if (jl < knn && jl >= __popcll(b0)) row0[jl] = kNoEntry;
+    if (jl < knn && jl >= __popcll(b1)) row1[jl] = kNoEntry;
   }
 }
 
-// Kt[hc][dim][key] = keys[hc * n + key][dim] (32 x 32 tiles through LDS).
-__global__ __launch_bounds__(256) void keys_transpose_kernel(const bf16_t* __restrict__ keys, int n, int half,
-                                                             bf16_t* __restrict__ Kt) {
-  __shared__ uint16_t tile[32][33];
-  const int hc = blockIdx.z;
-  const int k0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-  const bf16_t* src = keys + (int64_t)hc * n * half;
-  bf16_t* dst = Kt + (int64_t)hc * half * n;
-  for (int r = ty; r < 32; r += 8) {
-    const int key = k0 + r, dim = d0 + tx;
-    tile[r][tx] = (key < n && dim < half) ? src[(int64_t)key * half + dim].x : (uint16_t)0;
+// Lists and dq in one pass for knn <= 32. One-wave workgroups, each looping
+// over the tokens t = wi, wi + per_head, ... of one head h, with the next
+// row's pairs loaded while the current row is processed. Per row (t, h):
+// lane j of each half-wave takes pair j; lanes 0-31 build the list of
+// sub-key half c = 0, lanes 32-63 that of c = 1 (same values and order as
+// score_grad_lists_kernel), into LDS and the global lists; then half-wave c
+// gathers dq[t, h, c*half + 8 j .. + 8] = sum over its list, in order, of
+// v * keys[(2h + c) n + key][...] (float32, rounded once), 16 key rows in
+// flight. The workgroups of one head stay on one XCD (its key slices in L2).
+// v * k is formed by v_dot2 of (k_lo, k_hi) with (v, 0) or (0, v): exact
+// bf16 products added to the float32 sum with one rounding, as an FMA.
+constexpr int kRowBatch = 16;
+__global__ __launch_bounds__(64) void score_grad_rows_kernel(const int64_t* __restrict__ idx,
+                                                             const bf16_t* __restrict__ d,
+                                                             const bf16_t* __restrict__ keys, int64_t Ntok, int H,
+                                                             int n, int half, int knn, int per_head,
+                                                             uint32_t* __restrict__ lists, bf16_t* __restrict__ dq) {
+  __shared__ __align__(16) uint32_t s_key[2][32];
+  __shared__ __align__(16) float s_d[32];
+  __shared__ __align__(16) uint32_t s_list[2][32];
+  const int g = sg_logical_block();
+  const int h = g / per_head, wi = g - h * per_head;
+  const int lane = threadIdx.x, c = lane >> 5, j = lane & 31;
+  const bool pair = j < knn;
+  // key rows of head h (both halves) from one wave-uniform base; 32-bit byte offsets
+  const char* Kh = (const char*)(keys + (int64_t)2 * h * n * half);
+  const uint32_t row_bytes = (uint32_t)half * 2, lane_off = (uint32_t)c * n * row_bytes + 16u * j;
+  const bool dims = 8 * j < half;
+  int64_t id = -1;
+  uint32_t draw = 0;
+  if (wi < Ntok && pair) {
+    const int64_t th = (int64_t)wi * H + h;
+    id = idx[th * knn + j];
+    draw = d[th * knn + j].x;
   }
-  __syncthreads();
-  for (int r = ty; r < 32; r += 8) {
-    const int dim = d0 + r, key = k0 + tx;
-    if (dim < half && key < n) dst[(int64_t)dim * n + key].x = tile[tx][r];
+  for (int64_t t = wi; t < Ntok; t += per_head) {
+    const int64_t th = t * H + h;
+    uint32_t my = 0xFFFFFFFFu;  // this lane's sub-key of half c (none: matches no sub-key)
+    float dv = 0.f;
+    if (pair && id >= 0 && id < (int64_t)n * n) {  // n <= 65535: the id fits 32 bits
+      const uint32_t u = (uint32_t)id, a = u / (uint32_t)n;
+      my = c ? u - a * (uint32_t)n : a;
+      dv = bf16_to_f32(draw);
+    }
+    // the next row's pairs, in flight during this row
+    const int64_t tn = t + per_head;
+    id = -1;
+    if (tn < Ntok && pair) {
+      const int64_t thn = tn * H + h;
+      id = idx[thn * knn + j];
+      draw = d[thn * knn + j].x;
+    }
+    s_key[c][j] = my;
+    if (c == 0) s_d[j] = dv;
+    __syncthreads();
+    float sum = 0.f;  // starts at +0 and never becomes -0: adding +0 on a mismatch keeps it
+    bool first = true;
+#pragma unroll
+    for (int j0 = 0; j0 < 32; j0 += 4) {
+      const uint4 kq = *(const uint4*)&s_key[c][j0];
+      const float4 dq4 = *(const float4*)&s_d[j0];
+      const uint32_t kk[4] = {kq.x, kq.y, kq.z, kq.w};
+      const float dd[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool m = kk[e] == my;
+        sum += m ? dd[e] : 0.f;
+        if (j0 + e < j) first = first && !m;
+      }
+    }
+    const bool put = my != 0xFFFFFFFFu && first;
+    const uint32_t bits = (uint32_t)(__ballot(put) >> (32 * c));
+    const int cnt = __popc(bits);
+    const int pos = __popc(bits & ((1u << j) - 1));
+    const uint32_t entry = (my << 16) | f32_to_bf16_bits(sum);
+    if (put) s_list[c][pos] = entry;
+    uint32_t* L = lists + (th * 2 + c) * knn;
+    if (put) L[pos] = entry;
+    if (pair && j >= cnt) L[j] = kNoEntry;
+    __syncthreads();
+    if (dims) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int b0 = 0; b0 < cnt; b0 += kRowBatch) {
+        uint32_t e[kRowBatch];
+        uint4 kv[kRowBatch];
+#pragma unroll
+        for (int q = 0; q < kRowBatch; q += 4) {
+          const uint4 eq = *(const uint4*)&s_list[c][b0 + q];
+          e[q] = eq.x;
+          e[q + 1] = eq.y;
+          e[q + 2] = eq.z;
+          e[q + 3] = eq.w;
+        }
+#pragma unroll
+        for (int q = 0; q < kRowBatch; ++q) {
+          kv[q] = make_uint4(0u, 0u, 0u, 0u);
+          if (b0 + q < cnt) kv[q] = *(const uint4*)(Kh + (lane_off + (e[q] >> 16) * row_bytes));
+        }
+#pragma unroll
+        for (int q = 0; q < kRowBatch; ++q) {
+          if (b0 + q < cnt) {
+            const bf16x2_t vlo = __builtin_bit_cast(bf16x2_t, e[q] & 0xFFFFu);  // (v, 0)
+            const bf16x2_t vhi = __builtin_bit_cast(bf16x2_t, e[q] << 16);      // (0, v)
+            const uint32_t x[4] = {kv[q].x, kv[q].y, kv[q].z, kv[q].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const bf16x2_t kx = __builtin_bit_cast(bf16x2_t, x[i]);
+              acc[2 * i] = __builtin_amdgcn_fdot2_f32_bf16(kx, vlo, acc[2 * i], false);
+              acc[2 * i + 1] = __builtin_amdgcn_fdot2_f32_bf16(kx, vhi, acc[2 * i + 1], false);
+            }
+          }
+        }
+      }
+      *(uint4*)(dq + (th * 2 + c) * half + 8 * j) =
+          make_uint4(pack2_bf16(acc[0], acc[1]), pack2_bf16(acc[2], acc[3]), pack2_bf16(acc[4], acc[5]),
+                     pack2_bf16(acc[6], acc[7]));
+    }
   }
 }
 
 // MFMA over one staged chunk: wave (wm, wd) accumulates rows [64 wm, +64) x
-// dims [64 wd, +64) from A [rows][chunk] and B [dims][chunk] (both [.][kSgLd]).
+// dims [64 wd, +64) from A [rows][chunk] and B [dims][chunk] (swizzled tiles).
+// FULL: half == kSgMaxHalf (every wave's dims exist).
+template <bool FULL>
 __device__ __forceinline__ void sg_chunk_mma(const uint16_t* As, const uint16_t* Bs, int wm, int wd, int lane,
                                              int half, sg_f32x4_t (&acc)[4][4]) {
-  const int r = lane & 15, kq = 8 * (lane >> 4);
+  const int r = lane & 15;
+  uint4 a[2][4], b[2][4];
 #pragma unroll
   for (int ks = 0; ks < kSgChunk / 32; ++ks) {
-    uint4 a[4], b[4];
+    const int so = (((4 * ks + (lane >> 4)) ^ r) & 7) << 3;  // row & 7 == r & 7 for every tile row below
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) a[mt] = *(const uint4*)(As + (64 * wm + 16 * mt + r) * kSgLd + 32 * ks + kq);
+    for (int mt = 0; mt < 4; ++mt) a[ks][mt] = *(const uint4*)(As + (64 * wm + 16 * mt + r) * kSgPitch + so);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) b[nt] = *(const uint4*)(Bs + (64 * wd + 16 * nt + r) * kSgLd + 32 * ks + kq);
+    for (int nt = 0; nt < 4; ++nt) b[ks][nt] = *(const uint4*)(Bs + (64 * wd + 16 * nt + r) * kSgPitch + so);
+  }
+#pragma unroll
+  for (int ks = 0; ks < kSgChunk / 32; ++ks) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      if (64 * wd + 16 * nt < half) {
+      if (FULL || 64 * wd + 16 * nt < half) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) sg_mma(a[mt], b[nt], acc[mt][nt]);
+        for (int mt = 0; mt < 4; ++mt) sg_mma(a[ks][mt], b[ks][nt], acc[mt][nt]);
       }
     }
   }
 }
 
-__device__ __forceinline__ void sg_zero(uint16_t* p, int elems) {
-  for (int i = threadIdx.x; i < elems / 8; i += kSgThreads) *(uint4*)(p + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+__device__ __forceinline__ void sg_zero(uint16_t* p) {
+#pragma unroll
+  for (int i = threadIdx.x; i < kSgA / 8; i += kSgThreads) *(uint4*)(p + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// dq[t, h, c*half + dim] = sum_key dS_c[t, key] * K_c[key, dim]:
-// workgroup = 128 tokens of one (h, c); chunks of 64 keys.
-template <int EPT>  // list entries per thread (knn <= 4 * EPT)
-__global__ __launch_bounds__(kSgThreads) void score_dq_kernel(const uint32_t* __restrict__ lists,
-                                                              const bf16_t* __restrict__ Kt, int64_t Ntok, int H,
-                                                              int n, int half, int knn, bf16_t* __restrict__ dq) {
-  __shared__ __align__(16) uint16_t As[kSgRows * kSgLd];     // [token][key of the chunk]
-  __shared__ __align__(16) uint16_t Bs[kSgMaxHalf * kSgLd];  // [dim][key of the chunk]
-  const int hc = blockIdx.y, h = hc >> 1, c = hc & 1;
-  const int64_t t0 = (int64_t)blockIdx.x * kSgRows;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w & 1, wd = w >> 1;
-  // this thread's list entries: token tl = tid / 4, slots (tid % 4) + 4 s
-  const int tl = tid >> 2;
-  const int64_t t = t0 + tl;
-  uint32_t ent[EPT];
+// dq[t, h, c*half + e] = sum over the list of (t, h, c), in list order, of
+// v * keys[(2h + c) n + key][e] (float32, rounded once): the row of dS_c @ K_c
+// from its nonzeros. One wave per (t, h, c) (the list is wave-uniform: scalar
+// loads, uniform early exit at the first empty slot), 4 dims per lane;
+// workgroups of one (h, c) stay on one XCD so its key slice stays in that L2.
+constexpr int kDqWaves = 4;
+__global__ __launch_bounds__(64 * kDqWaves) void score_dq_gather_kernel(const uint32_t* __restrict__ lists,
+                                                                        const bf16_t* __restrict__ keys,
+                                                                        int64_t Ntok, int H, int n, int half, int knn,
+                                                                        int tok_blocks, bf16_t* __restrict__ dq) {
+  const int g = sg_logical_block();
+  const int hc = g / tok_blocks, h = hc >> 1, c = hc & 1;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)(g - hc * tok_blocks) * kDqWaves + w;
+  if (t >= Ntok) return;
+  const bool active = 4 * lane < half;
+  const uint32_t* L = lists + ((t * H + h) * 2 + c) * knn;
+  const bf16_t* Kc = keys + (int64_t)hc * n * half + 4 * lane;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < knn; j0 += 8) {
+    uint32_t e[8];
 #pragma unroll
-  for (int s = 0; s < EPT; ++s) {
-    const int j = (tid & 3) + 4 * s;
-    ent[s] = (t < Ntok && j < knn) ? lists[((t * H + h) * 2 + c) * knn + j] : kNoEntry;
-  }
-  const bf16_t* Kc = Kt + (int64_t)hc * half * n;
-  sg_f32x4_t acc[4][4];
+    for (int jj = 0; jj < 8; ++jj) e[jj] = j0 + jj < knn ? L[j0 + jj] : kNoEntry;
+    if (e[0] == kNoEntry) break;  // entries are packed at the front
+    uint2 kv[8];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = sg_f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < n; k0 += kSgChunk) {
-    sg_zero(As, kSgRows * kSgLd);
-    // B: Kt[dim][k0 .. k0 + 64) for dim < half (8 x 16 bytes per dim)
-    for (int i = tid; i < half * (kSgChunk / 8); i += kSgThreads) {
-      const int dim = i >> 3, q8 = i & 7;
-      *(uint4*)(Bs + dim * kSgLd + 8 * q8) = *(const uint4*)(Kc + (int64_t)dim * n + k0 + 8 * q8);
+    for (int jj = 0; jj < 8; ++jj) {
+      kv[jj] = make_uint2(0u, 0u);
+      if (e[jj] != kNoEntry && active) kv[jj] = *(const uint2*)(Kc + (int64_t)(e[jj] >> 16) * half);
     }
-    __syncthreads();
 #pragma unroll
-    for (int s = 0; s < EPT; ++s) {
-      const uint32_t e = ent[s];
-      const int key = (int)(e >> 16) - k0;
-      if (e != kNoEntry && key >= 0 && key < kSgChunk) As[tl * kSgLd + key] = (uint16_t)(e & 0xFFFFu);
-    }
-    __syncthreads();
-    sg_chunk_mma(As, Bs, wm, wd, lane, half, acc);
-    __syncthreads();
-  }
-  // acc[mt][nt][e]: token 64 wm + 16 mt + 4 (lane / 16) + e, dim 64 wd + 16 nt + lane % 16
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t tt = t0 + 64 * wm + 16 * mt + 4 * (lane >> 4) + e;
-      if (tt >= Ntok) continue;
-      bf16_t* row = dq + (tt * H + h) * 2 * half + (int64_t)c * half;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int dim = 64 * wd + 16 * nt + (lane & 15);
-        if (dim < half) row[dim].x = (uint16_t)f32_to_bf16_bits(acc[mt][nt][e]);
+    for (int jj = 0; jj < 8; ++jj) {
+      if (e[jj] != kNoEntry) {
+        const float v = bf16_to_f32((uint16_t)(e[jj] & 0xFFFFu));
+        acc[0] = fmaf(v, bf16_to_f32((uint16_t)(kv[jj].x & 0xFFFFu)), acc[0]);
+        acc[1] = fmaf(v, bf16_to_f32((uint16_t)(kv[jj].x >> 16)), acc[1]);
+        acc[2] = fmaf(v, bf16_to_f32((uint16_t)(kv[jj].y & 0xFFFFu)), acc[2]);
+        acc[3] = fmaf(v, bf16_to_f32((uint16_t)(kv[jj].y >> 16)), acc[3]);
       }
     }
   }
+  if (active)
+    *(uint2*)(dq + (t * H + h) * 2 * half + (int64_t)c * half + 4 * lane) =
+        make_uint2(pack2_bf16(acc[0], acc[1]), pack2_bf16(acc[2], acc[3]));
 }
 
-// Partial dK_c[key, dim] = sum over tokens of the split of dS_c[t, key] q_c[t, dim]:
-// workgroup = 128 keys of one (h, c) and one token split; chunks of 64 tokens.
-template <int EPT>  // list entries per thread and chunk (knn <= 8 * EPT)
+// Partial dK_c[key, dim] = sum over the split's tokens of dS_c[t, key] q_c[t, dim]:
+// workgroup = 128 keys of one (h, c) and one token split; chunks of 64 tokens,
+// buffered as in score_dq_kernel (lists and query rows loaded a chunk ahead).
+template <int EPT, bool FULL>  // list entries per thread and chunk (knn <= 8 * EPT); FULL: half == kSgMaxHalf
 __global__ __launch_bounds__(kSgThreads) void score_dk_kernel(const uint32_t* __restrict__ lists,
                                                               const bf16_t* __restrict__ Q, int64_t Ntok, int H,
                                                               int n, int half, int knn, int64_t tok_split,
-                                                              float* __restrict__ part) {
-  __shared__ __align__(16) uint16_t As[kSgRows * kSgLd];     // [key][token of the chunk]
-  __shared__ __align__(16) uint16_t Bs[kSgMaxHalf * kSgLd];  // [dim][token of the chunk]
-  const int hc = blockIdx.y, h = hc >> 1, c = hc & 1;
-  const int kb = blockIdx.x * kSgRows;
-  const int64_t ts = (int64_t)blockIdx.z * tok_split;
+                                                              int kblocks, float* __restrict__ part) {
+  __shared__ __align__(16) uint16_t As[3 * kSgA];  // [key][token of the chunk]
+  __shared__ __align__(16) uint16_t Bs[2 * kSgB];  // [dim][token of the chunk]
+  const int g = sg_logical_block();
+  const int kbi = g % kblocks, rest = g / kblocks;
+  const int HC = 2 * H;
+  const int hc = rest % HC, split = rest / HC, h = hc >> 1, c = hc & 1;
+  const int kb = kbi * kSgRows;
+  const int64_t ts = (int64_t)split * tok_split;
   const int64_t te = ts + tok_split < Ntok ? ts + tok_split : Ntok;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wd = w >> 1;
+  const int kdim = 2 * half;
+  // list entries of a chunk: token tl = tid / 8, slots (tid % 8) + 8 s
+  const int tl = tid >> 3;
+  uint32_t ent[EPT];
+  auto load_e = [&](int64_t tc) {
+    const int64_t t = tc + tl;
+#pragma unroll
+    for (int s = 0; s < EPT; ++s) {
+      const int j = (tid & 7) + 8 * s;
+      ent[s] = (t < te && j < knn) ? lists[((t * H + h) * 2 + c) * knn + j] : kNoEntry;
+    }
+  };
+  auto scatter = [&](uint16_t* A) {
+#pragma unroll
+    for (int s = 0; s < EPT; ++s) {
+      const uint32_t e = ent[s];
+      const int key = (int)(e >> 16) - kb;
+      if (e != kNoEntry && (unsigned)key < (unsigned)kSgRows) A[sg_swz(key, tl)] = (uint16_t)(e & 0xFFFFu);
+    }
+  };
+  // query staging, transposed to [dim][token]: item i = (token pair i % 32, 8-dim group i / 32)
+  constexpr int BPT = (kSgChunk / 2) * (kSgMaxHalf / 8) / kSgThreads;
+  uint4 qa[BPT], qb[BPT];
+  auto load_b = [&](int64_t tc) {
+#pragma unroll
+    for (int r = 0; r < BPT; ++r) {
+      const int i = tid + r * kSgThreads, p = i & (kSgChunk / 2 - 1), dg = i / (kSgChunk / 2);
+      const int64_t ta = tc + 2 * p, tb = ta + 1;
+      qa[r] = qb[r] = make_uint4(0u, 0u, 0u, 0u);
+      if (FULL || 8 * dg < half) {
+        if (ta < te) qa[r] = *(const uint4*)(Q + (ta * H + h) * kdim + c * half + 8 * dg);
+        if (tb < te) qb[r] = *(const uint4*)(Q + (tb * H + h) * kdim + c * half + 8 * dg);
+      }
+    }
+  };
+  auto store_b = [&](uint16_t* B) {
+#pragma unroll
+    for (int r = 0; r < BPT; ++r) {
+      const int i = tid + r * kSgThreads, p = i & (kSgChunk / 2 - 1), dg = i / (kSgChunk / 2);
+      if (FULL || 8 * dg < half) {
+        const uint32_t xa[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w}, xb[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int dim = 8 * dg + 2 * e;
+          *(uint32_t*)(B + sg_swz(dim, 2 * p)) = (xa[e] & 0xFFFFu) | (xb[e] << 16);
+          *(uint32_t*)(B + sg_swz(dim + 1, 2 * p)) = (xa[e] >> 16) | (xb[e] & 0xFFFF0000u);
+        }
+      }
+    }
+  };
   sg_f32x4_t acc[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = sg_f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int kdim = 2 * half;
-  for (int64_t tc = ts; tc < te; tc += kSgChunk) {
-    sg_zero(As, kSgRows * kSgLd);
-    // B: q_c[t][dim] transposed to [dim][t]; a thread packs tokens 2p, 2p + 1 of 8 dims
-    for (int i = tid; i < (kSgChunk / 2) * (half / 8); i += kSgThreads) {
-      const int p = i & (kSgChunk / 2 - 1), dg = i / (kSgChunk / 2);
-      const int64_t ta = tc + 2 * p, tb = ta + 1;
-      uint4 va = make_uint4(0u, 0u, 0u, 0u), vb = va;
-      if (ta < te) va = *(const uint4*)(Q + (ta * H + h) * kdim + c * half + 8 * dg);
-      if (tb < te) vb = *(const uint4*)(Q + (tb * H + h) * kdim + c * half + 8 * dg);
-      const uint32_t xa[4] = {va.x, va.y, va.z, va.w}, xb[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        *(uint32_t*)(Bs + (8 * dg + 2 * e) * kSgLd + 2 * p) = (xa[e] & 0xFFFFu) | (xb[e] << 16);
-        *(uint32_t*)(Bs + (8 * dg + 2 * e + 1) * kSgLd + 2 * p) = (xa[e] >> 16) | (xb[e] & 0xFFFF0000u);
-      }
+  const int nch = (int)((te - ts + kSgChunk - 1) / kSgChunk);
+  sg_zero(As);
+  sg_zero(As + kSgA);
+  load_e(ts);
+  load_b(ts);
+  __syncthreads();
+  scatter(As);
+  store_b(Bs);
+  if (nch > 1) {
+    load_e(ts + kSgChunk);
+    load_b(ts + kSgChunk);
+  }
+  __syncthreads();
+  int ia = 0;
+  for (int i = 0; i < nch; ++i) {
+    const int ia1 = ia == 2 ? 0 : ia + 1, ia2 = ia1 == 2 ? 0 : ia1 + 1;
+    sg_zero(As + ia2 * kSgA);
+    if (i + 1 < nch) {
+      scatter(As + ia1 * kSgA);
+      store_b(Bs + ((i + 1) & 1) * kSgB);
     }
-    __syncthreads();
-    // A: this chunk's entries with a key in the block; token tl = tid / 8, slots (tid % 8) + 8 s
-    {
-      const int tl = tid >> 3;
-      const int64_t t = tc + tl;
-#pragma unroll
-      for (int s = 0; s < EPT; ++s) {
-        const int j = (tid & 7) + 8 * s;
-        if (t < te && j < knn) {
-          const uint32_t e = lists[((t * H + h) * 2 + c) * knn + j];
-          const int key = (int)(e >> 16) - kb;
-          if (e != kNoEntry && key >= 0 && key < kSgRows) As[key * kSgLd + tl] = (uint16_t)(e & 0xFFFFu);
-        }
-      }
+    if (i + 2 < nch) {
+      load_e(ts + (int64_t)(i + 2) * kSgChunk);
+      load_b(ts + (int64_t)(i + 2) * kSgChunk);
     }
+    sg_chunk_mma<FULL>(As + ia * kSgA, Bs + (i & 1) * kSgB, wm, wd, lane, half, acc);
     __syncthreads();
-    sg_chunk_mma(As, Bs, wm, wd, lane, half, acc);
-    __syncthreads();
+    ia = ia1;
   }
   // acc[mt][nt][e]: key kb + 64 wm + 16 mt + 4 (lane / 16) + e, dim 64 wd + 16 nt + lane % 16
-  float* P = part + ((int64_t)blockIdx.z * gridDim.y + hc) * n * half;
+  float* P = part + ((int64_t)split * HC + hc) * n * half;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int key = kb + 64 * wm + 16 * mt + 4 * (lane >> 4) + e;
-      if (key >= n) continue;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const int dim = 64 * wd + 16 * nt + (lane & 15);
@@ -373,7 +552,7 @@ __global__ void score_dk_reduce_kernel(const float* __restrict__ part, int64_t t
 struct SparseGradPlan {
   int splits;
   int64_t tok_split;
-  size_t lists, kt, part, total;
+  size_t lists, part, total;
 };
 
 static SparseGradPlan sparse_grad_plan(int64_t N, int64_t H, int64_t n, int64_t half, int64_t knn) {
@@ -392,8 +571,6 @@ static SparseGradPlan sparse_grad_plan(int64_t N, int64_t H, int64_t n, int64_t 
   size_t off = 0;
   p.lists = off;
   off += a256((size_t)N * H * 2 * knn * 4);
-  p.kt = off;
-  off += a256((size_t)2 * H * n * half * 2);
   p.part = off;
   off += a256((size_t)p.splits * 2 * H * n * half * 4);
   p.total = off;
@@ -469,40 +646,44 @@ extern "C" int pkm_score_grad_sparse(const int64_t* indices, const void* d_score
   PKM_REQUIRE(workspace != nullptr && workspace_bytes >= pl.total && (uintptr_t)workspace % 256 == 0,
               PKM_ERR_WORKSPACE, "pkm_score_grad_sparse: workspace of %zu bytes given, %zu needed (256-byte aligned)",
               workspace_bytes, pl.total);
-  PKM_REQUIRE((uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
-              "pkm_score_grad_sparse: query and keys must be 16-byte aligned");
+  PKM_REQUIRE((uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0 && (uintptr_t)d_query % 16 == 0 &&
+                  (uintptr_t)d_keys % 16 == 0,
+              PKM_ERR_INVALID_ARGUMENT, "pkm_score_grad_sparse: query, keys, d_query, d_keys must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   uint32_t* lists = (uint32_t*)(ws + pl.lists);
   const int64_t NH = num_tokens * heads;
-  hipLaunchKernelGGL(score_grad_lists_kernel, dim3((unsigned)((NH + kGradWaves - 1) / kGradWaves)),
-                     dim3(64 * kGradWaves), 0, st, indices, (const bf16_t*)d_scores, NH, (int)n_keys, (int)knn, lists);
-  const unsigned tb = (unsigned)((num_tokens + kSgRows - 1) / kSgRows);
-  if (d_query != nullptr) {
-    bf16_t* Kt = (bf16_t*)(ws + pl.kt);
-    hipLaunchKernelGGL(keys_transpose_kernel, dim3((unsigned)(n_keys / 32), (unsigned)((half + 31) / 32),
-                                                   (unsigned)(2 * heads)),
-                       dim3(256), 0, st, (const bf16_t*)keys, (int)n_keys, (int)half, Kt);
+  if (d_query != nullptr && knn <= 32) {  // lists and dq in one pass
+    // about 16 waves per CU on 256 CUs, split evenly over the heads
+    int per_head = (int)((4096 + heads - 1) / heads);
+    if ((int64_t)per_head > num_tokens) per_head = (int)num_tokens;
+    hipLaunchKernelGGL(score_grad_rows_kernel, dim3((unsigned)(per_head * heads)), dim3(64), 0, st, indices,
+                       (const bf16_t*)d_scores, (const bf16_t*)keys, num_tokens, (int)heads, (int)n_keys, (int)half,
+                       (int)knn, per_head, lists, (bf16_t*)d_query);
+  } else {
     if (knn <= 32)
-      hipLaunchKernelGGL(score_dq_kernel<8>, dim3(tb, (unsigned)(2 * heads)), dim3(kSgThreads), 0, st,
-                         (const uint32_t*)lists, (const bf16_t*)Kt, num_tokens, (int)heads, (int)n_keys, (int)half,
-                         (int)knn, (bf16_t*)d_query);
+      hipLaunchKernelGGL(score_grad_lists_kernel<32>,
+                         dim3((unsigned)((NH + kListThreads / 32 - 1) / (kListThreads / 32))), dim3(kListThreads), 0,
+                         st, indices, (const bf16_t*)d_scores, NH, (int)n_keys, (int)knn, lists);
     else
-      hipLaunchKernelGGL(score_dq_kernel<16>, dim3(tb, (unsigned)(2 * heads)), dim3(kSgThreads), 0, st,
-                         (const uint32_t*)lists, (const bf16_t*)Kt, num_tokens, (int)heads, (int)n_keys, (int)half,
-                         (int)knn, (bf16_t*)d_query);
+      hipLaunchKernelGGL(score_grad_lists_kernel<64>,
+                         dim3((unsigned)((NH + kListThreads / 64 - 1) / (kListThreads / 64))), dim3(kListThreads), 0,
+                         st, indices, (const bf16_t*)d_scores, NH, (int)n_keys, (int)knn, lists);
+    if (d_query != nullptr) {
+      const int tok_blocks = (int)((num_tokens + kDqWaves - 1) / kDqWaves);
+      hipLaunchKernelGGL(score_dq_gather_kernel, dim3((unsigned)(tok_blocks * 2 * heads)), dim3(64 * kDqWaves), 0, st,
+                         (const uint32_t*)lists, (const bf16_t*)keys, num_tokens, (int)heads, (int)n_keys, (int)half,
+                         (int)knn, tok_blocks, (bf16_t*)d_query);
+    }
   }
   if (d_keys != nullptr) {
     float* part = (float*)(ws + pl.part);
-    const dim3 grid((unsigned)(n_keys / kSgRows), (unsigned)(2 * heads), (unsigned)pl.splits);
-    if (knn <= 32)
-      hipLaunchKernelGGL(score_dk_kernel<4>, grid, dim3(kSgThreads), 0, st, (const uint32_t*)lists,
-                         (const bf16_t*)query, num_tokens, (int)heads, (int)n_keys, (int)half, (int)knn, pl.tok_split,
-                         part);
-    else
-      hipLaunchKernelGGL(score_dk_kernel<8>, grid, dim3(kSgThreads), 0, st, (const uint32_t*)lists,
-                         (const bf16_t*)query, num_tokens, (int)heads, (int)n_keys, (int)half, (int)knn, pl.tok_split,
-                         part);
+    const int kblocks = (int)(n_keys / kSgRows);
+    const dim3 grid((unsigned)(kblocks * 2 * heads * pl.splits));
+    auto dk_kernel = knn <= 32 ? (half == kSgMaxHalf ? score_dk_kernel<4, true> : score_dk_kernel<4, false>)
+                               : (half == kSgMaxHalf ? score_dk_kernel<8, true> : score_dk_kernel<8, false>);
+    hipLaunchKernelGGL(dk_kernel, grid, dim3(kSgThreads), 0, st, (const uint32_t*)lists, (const bf16_t*)query,
+                       num_tokens, (int)heads, (int)n_keys, (int)half, (int)knn, pl.tok_split, kblocks, part);
     hipLaunchKernelGGL(score_dk_reduce_kernel, dim3(reduce_blocks), dim3(256), 0, st, (const float*)part, total,
                        pl.splits, (bf16_t*)d_keys);
   }
