@@ -177,6 +177,7 @@ _SIZE_ARGS = {
     "pkm_eb_bwd": (1, 2),
     "pkm_eb_bwd2": (1, 2),
     "pkm_score_topk": (2, 3, 4, 5),  # num_tokens, heads, n_keys, half
+    "pkm_score_grad_sparse": (3, 4, 5, 6),  # num_tokens, heads, n_keys, half
     "pkm_rmsnorm_fwd": (2, 3),  # rows, dim
     "pkm_rmsnorm_bwd": (4, 5),
 }

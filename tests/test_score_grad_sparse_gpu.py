@@ -28,6 +28,7 @@ SHAPES = [
     (129, 3, 128, 48, 7),  # half not a multiple of 64 (partial wave tiles), odd knn
     (1, 1, 128, 16, 1),  # one token, knn 1, smallest half
     (700, 8, 1024, 256, 32),  # the PKM layer's head shape
+    (40, 1, 8448, 16, 8),  # key rows too many for the LDS slice: direct gather
 ]
 
 
