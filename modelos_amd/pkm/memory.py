@@ -31,6 +31,57 @@ from ..product_keys import product_key_topk
 from ..rmsnorm import QueryRMSNorm
 from .colwise_embedding_bag import xFormerEmbeddingBag
 
+
+def _weight_grad_splits(rows: int, out_features: int, in_features: int) -> int:
+    """Row splits for the weight gradient g^T x of a Linear over `rows`
+    inputs: enough that (256 x 256 output tiles) x splits covers the GPU's 256
+    CUs, each split at least 2048 rows."""
+    tiles = max(1, (out_features // 256) * (in_features // 256))
+    s = 1
+    while s * 2 * tiles <= 256 and rows % (s * 2) == 0 and rows // (s * 2) >= 2048:
+        s *= 2
+    return s
+
+
+class _Linear(torch.autograd.Function):
+    """F.linear with the same gradients as nn.Linear's autograd, the weight
+    gradient g^T x of a 2-D bf16/fp16 input on the GPU formed as a split-K
+    batched product (float32 partials, summed in split order, rounded once):
+    the plain product has only (out/256)(in/256) output tiles for K = rows."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return F.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, weight = ctx.saved_tensors
+        g = g.contiguous()
+        gx = gw = gb = None
+        if ctx.needs_input_grad[0]:
+            gx = g @ weight
+        if ctx.needs_input_grad[1]:
+            rows, (out_f, in_f) = x.shape[0], weight.shape
+            s = 1
+            if g.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and x.is_contiguous():
+                s = _weight_grad_splits(rows, out_f, in_f)
+            if s > 1:
+                part = torch.bmm(g.view(s, rows // s, out_f).transpose(1, 2), x.view(s, rows // s, in_f),
+                                 out_dtype=torch.float32)
+                gw = part.sum(0).to(weight.dtype)
+            else:
+                gw = g.t() @ x
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            gb = g.sum(0)
+        return gx, gw, gb
+
+
+def _linear(layer: nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    """layer(x) for a 2-D x, through _Linear."""
+    return _Linear.apply(x, layer.weight, layer.bias)
+
 logger = getLogger()
 
 
@@ -196,9 +247,9 @@ class HashingMemory(nn.Module):
         if not self.use_peer_variant:
             output = self.values(indices, scores)  # [bs, v_dim]
             if self.v_proj and not self.swilu_proj:
-                output = self.value_proj(output)
+                output = _linear(self.value_proj, output)
             if self.swilu_proj:
-                output = self.value_proj(output * F.silu(self.swilu_projection(input)))
+                output = _linear(self.value_proj, output * F.silu(_linear(self.swilu_projection, input)))
         else:
             # PEER variant (memory.py:231-237): per-slot expert vectors
             u = self.values_u(indices)  # [bs, heads * knn, v_dim]
@@ -256,7 +307,9 @@ class QueryMLP(nn.Module):
         assert input.shape[-1] == self.input_dim
         input = input.contiguous().view(-1, self.input_dim) if input.dim() > 2 else input
         bs = len(input)
-        query = self.query_mlps(input)
+        query = input
+        for layer in self.query_mlps:
+            query = _linear(layer, query) if isinstance(layer, nn.Linear) else layer(query)
         if self.norm is not None:
             query = self.norm(query)
         assert query.shape == (bs, self.heads * self.k_dim)

@@ -1,0 +1,54 @@
+"""The layer's Linear wrapper: same forward and gradients as nn.Linear's
+autograd; on the GPU the bf16 weight gradient is a split-K product with
+float32 partials (checked against float64 at the bf16 tolerance)."""
+from __future__ import annotations
+
+import pytest
+import torch
+from torch import nn
+
+from modelos_amd.pkm.memory import _linear, _weight_grad_splits
+from tests.helpers import REL_TOL, assert_rel_close, gen
+
+
+def _grads(layer, x, g, fn):
+    layer.zero_grad(set_to_none=True)
+    xx = x.clone().requires_grad_(True)
+    y = fn(layer, xx)
+    y.backward(g)
+    return y.detach(), xx.grad, layer.weight.grad, layer.bias.grad
+
+
+def test_matches_nn_linear_cpu_fp32():
+    torch.manual_seed(0)
+    layer = nn.Linear(64, 48)
+    x = torch.randn((300, 64), generator=gen(1))
+    g = torch.randn((300, 48), generator=gen(2))
+    a = _grads(layer, x, g, lambda m, v: m(v))
+    b = _grads(layer, x, g, _linear)
+    for u, v in zip(a, b):
+        assert torch.allclose(u, v, rtol=1e-6, atol=1e-6)
+
+
+def test_split_heuristic():
+    assert _weight_grad_splits(16384, 1024, 1024) == 8
+    assert _weight_grad_splits(16384, 4096, 1024) == 4
+    assert _weight_grad_splits(4096, 1024, 1024) == 2
+    assert _weight_grad_splits(3000, 1024, 1024) == 1  # below 2 x 2048 rows
+    assert _weight_grad_splits(16384 + 2, 1024, 1024) == 2  # rows must divide evenly
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,in_f,out_f", [(16384, 1024, 1024), (16384, 1024, 4096), (8192, 256, 512)])
+def test_split_k_weight_grad_gpu(device, rows, in_f, out_f):
+    torch.manual_seed(0)
+    layer = nn.Linear(in_f, out_f).to(device).to(torch.bfloat16)
+    x = torch.randn((rows, in_f), device=device).to(torch.bfloat16)
+    g = torch.randn((rows, out_f), device=device).to(torch.bfloat16)
+    y, gx, gw, gb = _grads(layer, x, g, _linear)
+    y0, gx0, gw0, gb0 = _grads(layer, x, g, lambda m, v: m(v))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0) and torch.equal(gx, gx0)  # same products as nn.Linear
+    assert torch.equal(gb, gb0)
+    e_gw = g.double().t() @ x.double()
+    assert_rel_close(gw, e_gw, REL_TOL[torch.bfloat16], "grad_weight")
