@@ -539,6 +539,136 @@ __global__ __launch_bounds__(kSgThreads) void score_dk_kernel(const uint32_t* __
   }
 }
 
+// Wide dK tiles: workgroup = 512 keys x 128 dims of one (h, c) and one token
+// split, 16 waves of 64 x 64, chunks of 32 tokens (one MFMA k-step). Query
+// rows are read by 2 workgroups and lists by 4 (a 128 x 256 tile reads them
+// 8 times). LDS tiles are [rows][32] bf16 (64-byte rows, four 16-byte slots;
+// slot s of row r stored at s ^ ((r >> 1) & 3): 8 consecutive rows read at
+// one slot cover all banks once); dS tiles triple-buffered, query tiles
+// double-buffered, one barrier per chunk.
+constexpr int kWkKeys = 512;
+constexpr int kWkDims = 128;
+constexpr int kWkChunk = 32;
+constexpr int kWkThreads = 1024;
+constexpr int kWkA = kWkKeys * kWkChunk;  // bf16 per dS tile (32 KB)
+constexpr int kWkB = kWkDims * kWkChunk;  // bf16 per query tile (8 KB)
+
+__device__ __forceinline__ int wk_swz(int row, int col) {
+  return row * kWkChunk + ((((col >> 3) ^ (row >> 1)) & 3) << 3) + (col & 7);
+}
+
+template <int EPT>  // list entries per thread and chunk (knn <= EPT)
+__global__ __launch_bounds__(kWkThreads) void score_dk_wide_kernel(const uint32_t* __restrict__ lists,
+                                                                   const bf16_t* __restrict__ Q, int64_t Ntok,
+                                                                   int H, int n, int half, int knn,
+                                                                   int64_t tok_split, int kblocks, int dblocks,
+                                                                   float* __restrict__ part) {
+  __shared__ __align__(16) uint16_t As[3 * kWkA];  // [key][token of the chunk]
+  __shared__ __align__(16) uint16_t Bs[2 * kWkB];  // [dim][token of the chunk]
+  const int g = sg_logical_block();
+  const int dbi = g % dblocks, r1 = g / dblocks;
+  const int kbi = r1 % kblocks, r2 = r1 / kblocks;
+  const int HC = 2 * H;
+  const int hc = r2 % HC, split = r2 / HC, h = hc >> 1, c = hc & 1;
+  const int kb = kbi * kWkKeys, db = dbi * kWkDims;
+  const int64_t ts = (int64_t)split * tok_split;
+  const int64_t te = ts + tok_split < Ntok ? ts + tok_split : Ntok;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 7, wd = w >> 3;  // 8 key tiles x 2 dim tiles of 64
+  const int kdim = 2 * half;
+  // lists: token tid / 32 of the chunk, slots tid % 32 (+ 32 s)
+  const int tl = tid >> 5;
+  // query items: 16 token pairs x 16 groups of 8 dims, threads 0..255
+  const bool qthread = tid < (kWkChunk / 2) * (kWkDims / 8);
+  const int qp = tid & (kWkChunk / 2 - 1), qg = (tid >> 4) & (kWkDims / 8 - 1);
+  struct Stage {
+    uint32_t ent[EPT];
+    uint4 qa, qb;
+  };
+  auto load = [&](Stage& S, int64_t tc) {
+    const int64_t t = tc + tl;
+#pragma unroll
+    for (int s = 0; s < EPT; ++s) {
+      const int j = (tid & 31) + 32 * s;
+      S.ent[s] = (t < te && j < knn) ? lists[((t * H + h) * 2 + c) * knn + j] : kNoEntry;
+    }
+    S.qa = S.qb = make_uint4(0u, 0u, 0u, 0u);
+    if (qthread) {
+      const int64_t ta = tc + 2 * qp, tb = ta + 1;
+      if (ta < te) S.qa = *(const uint4*)(Q + (ta * H + h) * kdim + c * half + db + 8 * qg);
+      if (tb < te) S.qb = *(const uint4*)(Q + (tb * H + h) * kdim + c * half + db + 8 * qg);
+    }
+  };
+  auto put = [&](const Stage& S, uint16_t* A, uint16_t* B) {
+#pragma unroll
+    for (int s = 0; s < EPT; ++s) {
+      const uint32_t e = S.ent[s];
+      const int key = (int)(e >> 16) - kb;
+      if (e != kNoEntry && (unsigned)key < (unsigned)kWkKeys) A[wk_swz(key, tl)] = (uint16_t)(e & 0xFFFFu);
+    }
+    if (qthread) {
+      const uint32_t xa[4] = {S.qa.x, S.qa.y, S.qa.z, S.qa.w}, xb[4] = {S.qb.x, S.qb.y, S.qb.z, S.qb.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int dim = 8 * qg + 2 * e;
+        *(uint32_t*)(B + wk_swz(dim, 2 * qp)) = (xa[e] & 0xFFFFu) | (xb[e] << 16);
+        *(uint32_t*)(B + wk_swz(dim + 1, 2 * qp)) = (xa[e] >> 16) | (xb[e] & 0xFFFF0000u);
+      }
+    }
+  };
+  auto zero = [&](uint16_t* A) {
+#pragma unroll
+    for (int i = tid; i < kWkA / 8; i += kWkThreads) *(uint4*)(A + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+  };
+  sg_f32x4_t acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = sg_f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const uint16_t* A, const uint16_t* B) {
+    const int r = lane & 15, q = lane >> 4;
+    uint4 a[4], b[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) a[mt] = *(const uint4*)(A + wk_swz(64 * wm + 16 * mt + r, 8 * q));
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) b[nt] = *(const uint4*)(B + wk_swz(64 * wd + 16 * nt + r, 8 * q));
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) sg_mma(a[mt], b[nt], acc[mt][nt]);
+  };
+  const int nch = (int)((te - ts + kWkChunk - 1) / kWkChunk);
+  Stage st;
+  zero(As);
+  zero(As + kWkA);
+  load(st, ts);
+  __syncthreads();
+  put(st, As, Bs);
+  if (nch > 1) load(st, ts + kWkChunk);
+  __syncthreads();
+  int ia = 0;
+  for (int i = 0; i < nch; ++i) {
+    const int ia1 = ia == 2 ? 0 : ia + 1, ia2 = ia1 == 2 ? 0 : ia1 + 1;
+    zero(As + ia2 * kWkA);  // chunk i-1's tile, multiplied before the last barrier
+    if (i + 1 < nch) put(st, As + ia1 * kWkA, Bs + ((i + 1) & 1) * kWkB);
+    if (i + 2 < nch) load(st, ts + (int64_t)(i + 2) * kWkChunk);
+    mma(As + ia * kWkA, Bs + (i & 1) * kWkB);
+    __syncthreads();
+    ia = ia1;
+  }
+  // acc[mt][nt][e]: key kb + 64 wm + 16 mt + 4 (lane / 16) + e, dim db + 64 wd + 16 nt + lane % 16
+  float* P = part + ((int64_t)split * HC + hc) * n * half;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int key = kb + 64 * wm + 16 * mt + 4 * (lane >> 4) + e;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) P[(int64_t)key * half + db + 64 * wd + 16 * nt + (lane & 15)] = acc[mt][nt][e];
+    }
+  }
+}
+
 // dK[i] = bf16(sum over splits, in order, of the partials); i over 2H * n * half.
 __global__ void score_dk_reduce_kernel(const float* __restrict__ part, int64_t total, int splits,
                                        bf16_t* __restrict__ dk) {
@@ -550,21 +680,28 @@ __global__ void score_dk_reduce_kernel(const float* __restrict__ part, int64_t t
 }
 
 struct SparseGradPlan {
+  bool wide;  // score_dk_wide_kernel (512 x 128 tiles, 32-token chunks)
   int splits;
   int64_t tok_split;
   size_t lists, part, total;
 };
 
+static bool dk_wide_fits(int64_t n, int64_t half) { return n % kWkKeys == 0 && half % kWkDims == 0; }
+
 static SparseGradPlan sparse_grad_plan(int64_t N, int64_t H, int64_t n, int64_t half, int64_t knn) {
   SparseGradPlan p;
   if (N < 1) N = 1;  // sizes for no tokens: the smallest plan (d_keys is only cleared then)
-  // token splits of dK: enough workgroups for the GPU (>= 512), chunks of 64 per split
-  const int64_t wg = (n / kSgRows) * 2 * H;
-  int64_t sp = (512 + wg - 1) / wg;
-  const int64_t max_sp = (N + kSgChunk - 1) / kSgChunk;
+  p.wide = dk_wide_fits(n, half);
+  // token splits of dK: enough workgroups for the GPU (256 of the wide tiles,
+  // one per CU; 512 of the 128 x 256 tiles), whole chunks per split
+  const int64_t chunk = p.wide ? kWkChunk : kSgChunk;
+  const int64_t wg = p.wide ? (n / kWkKeys) * (half / kWkDims) * 2 * H : (n / kSgRows) * 2 * H;
+  const int64_t target = p.wide ? 256 : 512;
+  int64_t sp = (target + wg - 1) / wg;
+  const int64_t max_sp = (N + chunk - 1) / chunk;
   if (sp > max_sp) sp = max_sp;
   if (sp < 1) sp = 1;
-  p.tok_split = ((N + sp - 1) / sp + kSgChunk - 1) / kSgChunk * kSgChunk;
+  p.tok_split = ((N + sp - 1) / sp + chunk - 1) / chunk * chunk;
   p.splits = (int)((N + p.tok_split - 1) / p.tok_split);
   if (p.splits < 1) p.splits = 1;
   auto a256 = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -678,12 +815,21 @@ extern "C" int pkm_score_grad_sparse(const int64_t* indices, const void* d_score
   }
   if (d_keys != nullptr) {
     float* part = (float*)(ws + pl.part);
-    const int kblocks = (int)(n_keys / kSgRows);
-    const dim3 grid((unsigned)(kblocks * 2 * heads * pl.splits));
-    auto dk_kernel = knn <= 32 ? (half == kSgMaxHalf ? score_dk_kernel<4, true> : score_dk_kernel<4, false>)
-                               : (half == kSgMaxHalf ? score_dk_kernel<8, true> : score_dk_kernel<8, false>);
-    hipLaunchKernelGGL(dk_kernel, grid, dim3(kSgThreads), 0, st, (const uint32_t*)lists, (const bf16_t*)query,
-                       num_tokens, (int)heads, (int)n_keys, (int)half, (int)knn, pl.tok_split, kblocks, part);
+    if (pl.wide) {
+      const int kblocks = (int)(n_keys / kWkKeys), dblocks = (int)(half / kWkDims);
+      const dim3 grid((unsigned)(kblocks * dblocks * 2 * heads * pl.splits));
+      auto dk_kernel = knn <= 32 ? score_dk_wide_kernel<1> : score_dk_wide_kernel<2>;
+      hipLaunchKernelGGL(dk_kernel, grid, dim3(kWkThreads), 0, st, (const uint32_t*)lists, (const bf16_t*)query,
+                         num_tokens, (int)heads, (int)n_keys, (int)half, (int)knn, pl.tok_split, kblocks, dblocks,
+                         part);
+    } else {
+      const int kblocks = (int)(n_keys / kSgRows);
+      const dim3 grid((unsigned)(kblocks * 2 * heads * pl.splits));
+      auto dk_kernel = knn <= 32 ? (half == kSgMaxHalf ? score_dk_kernel<4, true> : score_dk_kernel<4, false>)
+                                 : (half == kSgMaxHalf ? score_dk_kernel<8, true> : score_dk_kernel<8, false>);
+      hipLaunchKernelGGL(dk_kernel, grid, dim3(kSgThreads), 0, st, (const uint32_t*)lists, (const bf16_t*)query,
+                         num_tokens, (int)heads, (int)n_keys, (int)half, (int)knn, pl.tok_split, kblocks, part);
+    }
     hipLaunchKernelGGL(score_dk_reduce_kernel, dim3(reduce_blocks), dim3(256), 0, st, (const float*)part, total,
                        pl.splits, (bf16_t*)d_keys);
   }

@@ -27,7 +27,8 @@ SHAPES = [
     (300, 2, 256, 256, 64),  # knn 64, several token splits of d_keys
     (129, 3, 128, 48, 7),  # half not a multiple of 64 (partial wave tiles), odd knn
     (1, 1, 128, 16, 1),  # one token, knn 1, smallest half
-    (700, 8, 1024, 256, 32),  # the PKM layer's head shape
+    (700, 8, 1024, 256, 32),  # the PKM layer's head shape (512 x 128 dK tiles)
+    (150, 2, 512, 128, 64),  # 512 x 128 dK tiles with knn 64, one dim block, ragged chunk
     (40, 1, 8448, 16, 8),  # key rows too many for the LDS slice: direct gather
 ]
 
