@@ -237,8 +237,10 @@ def run_layer(args, dev):
            "nonzero lists + fused dq gather, dK on MFMA + ordered split reduction (several kernels)")
     add_ms("pkm_rmsnorm_fwd (query)", "pkm_rmsnorm_fwd", "query RMSNorm forward")
     add_ms("pkm_rmsnorm_bwd (query)", "pkm_rmsnorm_bwd", "query RMSNorm backward + ordered weight-gradient reduction")
+    add_ms("pkm_swilu_fwd (value gate)", "pkm_swilu_fwd", "e * silu(s) of the value output")
+    add_ms("pkm_swilu_bwd (value gate)", "pkm_swilu_bwd", "gradients of the value gate")
     hip_ms = sum(v["ms"] * v["calls_per_step"] for v in kernels.values())
-    kernels["other (query/swilu/value GEMMs, softmax, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
+    kernels["other (query/swilu/value GEMMs, bias sums, softmax, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
 
     single = {kk: v for kk, v in kernels.items() if "bound" in v and "note" not in v}
     dom_name, dom = max(single.items(), key=lambda kv: kv[1]["ms"])

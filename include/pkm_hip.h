@@ -200,6 +200,24 @@ int pkm_score_grad_sparse(const int64_t* indices, const void* d_scores, int dtyp
 int pkm_rmsnorm_fwd(const void* x, const void* weight, int64_t rows, int64_t dim, int dtype, float eps, void* y,
                     float* rstd, void* stream);
 
+/*
+ * SwiLU gating of the value output (dtype F32 or BF16 for every tensor;
+ * all 16-byte aligned, n elements each):
+ *   a[i] = dtype(s[i] / (1 + exp(-s[i])))      h[i] = dtype(e[i] * a[i])
+ * Replaces `output * F.silu(swilu_projection(input))` in HashingMemory.forward
+ * (pkm/memory.py:229), float32 math and the same rounding points.
+ */
+int pkm_swilu_fwd(const void* e, const void* s, int64_t n, int dtype, void* h, void* stream);
+
+/*
+ * Backward of pkm_swilu_fwd, the gradients autograd forms through the product
+ * and F.silu (pkm/memory.py:229):
+ *   de[i] = dtype(dh[i] * a[i])        dm[i] = dtype(dh[i] * e[i])
+ *   ds[i] = dtype(dm[i] * sig * (1 + s[i] * (1 - sig))),  sig = 1 / (1 + exp(-s[i]))
+ */
+int pkm_swilu_bwd(const void* dh, const void* e, const void* s, int64_t n, int dtype, void* de, void* ds,
+                  void* stream);
+
 /* Workspace bytes pkm_rmsnorm_bwd needs for these sizes. */
 size_t pkm_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dim);
 

@@ -29,6 +29,7 @@ from torch.nn import functional as F
 
 from ..product_keys import product_key_topk
 from ..rmsnorm import QueryRMSNorm
+from ..swilu import swilu_gate
 from .colwise_embedding_bag import xFormerEmbeddingBag
 
 
@@ -249,7 +250,7 @@ class HashingMemory(nn.Module):
             if self.v_proj and not self.swilu_proj:
                 output = _linear(self.value_proj, output)
             if self.swilu_proj:
-                output = _linear(self.value_proj, output * F.silu(_linear(self.swilu_projection, input)))
+                output = _linear(self.value_proj, swilu_gate(output, _linear(self.swilu_projection, input)))
         else:
             # PEER variant (memory.py:231-237): per-slot expert vectors
             u = self.values_u(indices)  # [bs, heads * knn, v_dim]
