@@ -199,6 +199,101 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_dw_partial_kernel(const T* __
   for (int e = 0; e < EPV; e += 4) *(float4*)(pr + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
 }
 
+// Backward, dx and the dw partials in one pass (rows of at most 64 * 8 vectors):
+// a wave takes kFusedRB consecutive rows, one at a time with the next row's x
+// and dy in flight, writes dx as rmsnorm_bwd_dx_kernel does and adds
+// T(dy * T(x * r)) of its lane columns into float32 partials in row order,
+// stored as row block `wave` of part (the partial kernel's sums, over blocks
+// of kFusedRB rows).
+// ---------------------------------------------------------------------------
+constexpr int kFusedRB = 16;
+
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_fused_kernel(const T* __restrict__ dy, const T* __restrict__ x,
+                                                                const T* __restrict__ w, const float* __restrict__ rs,
+                                                                int64_t N, int D, T* __restrict__ dx,
+                                                                float* __restrict__ part) {
+  constexpr int EPV = VecTraits<T>::EPV;
+  constexpr int HV = 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r0 = wave * kFusedRB;
+  if (r0 >= N) return;
+  const int64_t r1 = r0 + kFusedRB < N ? r0 + kFusedRB : N;
+  const int NV = D / EPV;
+  uint4 wp[HV];
+  float pacc[HV][EPV];
+#pragma unroll
+  for (int i = 0; i < HV; ++i) {
+    const int c = lane + 64 * i;
+    wp[i] = c < NV ? ld16(w + c * EPV) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) pacc[i][e] = 0.f;
+  }
+  uint4 xa[HV], da[HV], xb[HV], db[HV];
+  auto load = [&](int64_t row, uint4 (&xv)[HV], uint4 (&dv)[HV]) {
+#pragma unroll
+    for (int i = 0; i < HV; ++i) {
+      const int c = lane + 64 * i;
+      xv[i] = dv[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (c < NV) {
+        xv[i] = ld16(x + row * D + c * EPV);
+        dv[i] = ld16(dy + row * D + c * EPV);
+      }
+    }
+  };
+  auto process = [&](int64_t row, const uint4 (&xv)[HV], const uint4 (&dv)[HV]) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < HV; ++i) {
+      float fx[EPV], fd[EPV], fw[EPV];
+      VecTraits<T>::unpack(xv[i], fx);
+      VecTraits<T>::unpack(dv[i], fd);
+      VecTraits<T>::unpack(wp[i], fw);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s = __builtin_fmaf(NormIO<T>::round(fd[e] * fw[e]), fx[e], s);
+    }
+    s = wave_sum(s);
+    const float r = rs[row];
+    const float dvar = -0.5f * s * (r * r * r);  // d loss / d (mean x^2 + eps)
+    const float k = dvar * (1.0f / (float)D) * 2.0f;
+    T* dxr = dx + row * D;
+#pragma unroll
+    for (int i = 0; i < HV; ++i) {
+      const int c = lane + 64 * i;
+      float fx[EPV], fd[EPV], fw[EPV], o[EPV];
+      VecTraits<T>::unpack(xv[i], fx);
+      VecTraits<T>::unpack(dv[i], fd);
+      VecTraits<T>::unpack(wp[i], fw);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        o[e] = NormIO<T>::round(fd[e] * fw[e]) * r + fx[e] * k;
+        pacc[i][e] += NormIO<T>::round(fd[e] * NormIO<T>::round(fx[e] * r));
+      }
+      if (c < NV) *(uint4*)(dxr + c * EPV) = VecTraits<T>::pack(o);
+    }
+  };
+  load(r0, xa, da);
+  for (int64_t row = r0; row < r1; row += 2) {
+    if (row + 1 < r1) load(row + 1, xb, db);
+    process(row, xa, da);
+    if (row + 1 < r1) {
+      if (row + 2 < r1) load(row + 2, xa, da);
+      process(row + 1, xb, db);
+    }
+  }
+  float* pr = part + wave * D;
+#pragma unroll
+  for (int i = 0; i < HV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < NV) {
+#pragma unroll
+      for (int e = 0; e < EPV; e += 4)
+        *(float4*)(pr + c * EPV + e) = make_float4(pacc[i][e], pacc[i][e + 1], pacc[i][e + 2], pacc[i][e + 3]);
+    }
+  }
+}
+
 // dw[j] = sum over the row blocks b (in order) of part[b, j]: 64 columns per
 // block, the partials split over 4 thread slices (each summing a contiguous
 // range of blocks, loads kept in flight), the slices added in order.
@@ -281,7 +376,7 @@ extern "C" int pkm_rmsnorm_fwd(const void* x, const void* weight, int64_t rows, 
 
 extern "C" size_t pkm_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dim) {
   if (rows <= 0 || dim <= 0) return 0;
-  return (size_t)((rows + kNormRB - 1) / kNormRB) * (size_t)dim * sizeof(float);
+  return (size_t)((rows + kFusedRB - 1) / kFusedRB) * (size_t)dim * sizeof(float);
 }
 
 extern "C" int pkm_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const float* rstd, int64_t rows,
@@ -317,24 +412,30 @@ extern "C" int pkm_rmsnorm_bwd(const void* dy, const void* x, const void* weight
   const dim3 pgrid((unsigned)((nv + 255) / 256), (unsigned)nrb);
   const dim3 rgrid((unsigned)((D + 63) / 64));
   float* part = (float*)workspace;
-  if (dtype == PKM_DTYPE_BF16) {
-    if (nv <= 64 * 8)
-      hipLaunchKernelGGL((rmsnorm_bwd_dx_kernel<bf16_t, 8>), grid, dim3(256), 0, st, (const bf16_t*)dy,
-                         (const bf16_t*)x, (const bf16_t*)weight, rstd, rows, D, (bf16_t*)dx);
-    else
-      hipLaunchKernelGGL((rmsnorm_bwd_dx_kernel<bf16_t, 0>), grid, dim3(256), 0, st, (const bf16_t*)dy,
-                         (const bf16_t*)x, (const bf16_t*)weight, rstd, rows, D, (bf16_t*)dx);
+  if (nv <= 64 * 8) {  // dx and the dw partials in one pass, kFusedRB rows per partial
+    const int64_t fnrb = (rows + kFusedRB - 1) / kFusedRB;
+    const dim3 fgrid((unsigned)((fnrb + 3) / 4));
+    if (dtype == PKM_DTYPE_BF16) {
+      hipLaunchKernelGGL((rmsnorm_bwd_fused_kernel<bf16_t>), fgrid, dim3(256), 0, st, (const bf16_t*)dy,
+                         (const bf16_t*)x, (const bf16_t*)weight, rstd, rows, D, (bf16_t*)dx, part);
+      hipLaunchKernelGGL((rmsnorm_bwd_dw_reduce_kernel<bf16_t>), rgrid, dim3(256), 0, st, (const float*)part, fnrb,
+                         D, (bf16_t*)dweight);
+    } else {
+      hipLaunchKernelGGL((rmsnorm_bwd_fused_kernel<float>), fgrid, dim3(256), 0, st, (const float*)dy,
+                         (const float*)x, (const float*)weight, rstd, rows, D, (float*)dx, part);
+      hipLaunchKernelGGL((rmsnorm_bwd_dw_reduce_kernel<float>), rgrid, dim3(256), 0, st, (const float*)part, fnrb, D,
+                         (float*)dweight);
+    }
+  } else if (dtype == PKM_DTYPE_BF16) {
+    hipLaunchKernelGGL((rmsnorm_bwd_dx_kernel<bf16_t, 0>), grid, dim3(256), 0, st, (const bf16_t*)dy,
+                       (const bf16_t*)x, (const bf16_t*)weight, rstd, rows, D, (bf16_t*)dx);
     hipLaunchKernelGGL((rmsnorm_bwd_dw_partial_kernel<bf16_t>), pgrid, dim3(256), 0, st, (const bf16_t*)dy,
                        (const bf16_t*)x, rstd, rows, D, part);
     hipLaunchKernelGGL((rmsnorm_bwd_dw_reduce_kernel<bf16_t>), rgrid, dim3(256), 0, st, (const float*)part, nrb, D,
                        (bf16_t*)dweight);
   } else {
-    if (nv <= 64 * 8)
-      hipLaunchKernelGGL((rmsnorm_bwd_dx_kernel<float, 8>), grid, dim3(256), 0, st, (const float*)dy,
-                         (const float*)x, (const float*)weight, rstd, rows, D, (float*)dx);
-    else
-      hipLaunchKernelGGL((rmsnorm_bwd_dx_kernel<float, 0>), grid, dim3(256), 0, st, (const float*)dy,
-                         (const float*)x, (const float*)weight, rstd, rows, D, (float*)dx);
+    hipLaunchKernelGGL((rmsnorm_bwd_dx_kernel<float, 0>), grid, dim3(256), 0, st, (const float*)dy,
+                       (const float*)x, (const float*)weight, rstd, rows, D, (float*)dx);
     hipLaunchKernelGGL((rmsnorm_bwd_dw_partial_kernel<float>), pgrid, dim3(256), 0, st, (const float*)dy,
                        (const float*)x, rstd, rows, D, part);
     hipLaunchKernelGGL((rmsnorm_bwd_dw_reduce_kernel<float>), rgrid, dim3(256), 0, st, (const float*)part, nrb, D,
