@@ -200,6 +200,20 @@ int pkm_score_grad_sparse(const int64_t* indices, const void* d_scores, int dtyp
 int pkm_rmsnorm_fwd(const void* x, const void* weight, int64_t rows, int64_t dim, int dtype, float eps, void* y,
                     float* rstd, void* stream);
 
+/* Workspace bytes pkm_column_sum needs for these sizes. */
+size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);
+
+/*
+ * Column sums of a row-major [rows, cols] matrix (dtype F32 or BF16; x and the
+ * workspace 16-byte aligned, cols a multiple of 4 / 8):
+ *   out[j] = dtype(sum_i x[i, j])   float32, over fixed row blocks in order
+ * (deterministic). Replaces g.sum(0), the bias gradient autograd forms for the
+ * Linear layers of HashingMemory and its query network (pkm/memory.py:147-149,
+ * 305).
+ */
+int pkm_column_sum(const void* x, int64_t rows, int64_t cols, int dtype, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /*
  * SwiLU gating of the value output (dtype F32 or BF16 for every tensor;
  * all 16-byte aligned, n elements each):

@@ -27,6 +27,8 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from .. import _lib
+from ..embedding_bag import _aligned
 from ..product_keys import product_key_topk
 from ..rmsnorm import QueryRMSNorm
 from ..swilu import swilu_gate
@@ -75,8 +77,25 @@ class _Linear(torch.autograd.Function):
             else:
                 gw = g.t() @ x
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            gb = g.sum(0)
+            gb = _column_sum(g)
         return gx, gw, gb
+
+
+def _column_sum(g: torch.Tensor) -> torch.Tensor:
+    """g.sum(0) of a 2-D gradient: on the GPU for float32 / bfloat16 rows of
+    whole 16-byte vectors (pkm_column_sum: float32 sums over fixed row blocks,
+    deterministic), else torch's sum."""
+    if not (g.is_cuda and g.dim() == 2 and g.dtype in (torch.float32, torch.bfloat16)
+            and g.shape[1] % (16 // g.element_size()) == 0 and g.shape[1] > 0):
+        return g.sum(0)
+    g = _aligned(g)
+    rows, cols = g.shape
+    out = torch.empty(cols, dtype=g.dtype, device=g.device)
+    ws_bytes = int(_lib.load().pkm_column_sum_workspace_size(rows, cols))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=g.device)
+    _lib.call("pkm_column_sum", _lib.ptr(g), rows, cols, _lib.dtype_code(g), _lib.ptr(out), _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(g.device))
+    return out
 
 
 def _linear(layer: nn.Linear, x: torch.Tensor) -> torch.Tensor:
