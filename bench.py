@@ -240,8 +240,10 @@ def run_layer(args, dev):
     add_ms("pkm_swilu_fwd (value gate)", "pkm_swilu_fwd", "e * silu(s) of the value output")
     add_ms("pkm_swilu_bwd (value gate)", "pkm_swilu_bwd", "gradients of the value gate")
     add_ms("pkm_column_sum (Linear bias gradients)", "pkm_column_sum", "per call; one call per Linear")
+    add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
+    add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
     hip_ms = sum(v["ms"] * v["calls_per_step"] for v in kernels.values())
-    kernels["other (query/swilu/value GEMMs, softmax, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
+    kernels["other (query/swilu/value GEMMs, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
 
     single = {kk: v for kk, v in kernels.items() if "bound" in v and "note" not in v}
     dom_name, dom = max(single.items(), key=lambda kv: kv[1]["ms"])

@@ -200,6 +200,22 @@ int pkm_score_grad_sparse(const int64_t* indices, const void* d_scores, int dtyp
 int pkm_rmsnorm_fwd(const void* x, const void* weight, int64_t rows, int64_t dim, int dtype, float eps, void* y,
                     float* rstd, void* stream);
 
+/*
+ * Softmax of the selected scores over each row of cols <= 64 entries (dtype
+ * F32 or BF16 for x, y, dy, dx alike; float32 math, sums in column order):
+ *   y[i, j] = dtype(exp(x[i, j] - max_k x[i, k]) / sum_k exp(x[i, k] - max_k x[i, k]))
+ * Replaces `F.softmax(scores.float(), dim=-1).type_as(scores)` in
+ * HashingMemory.forward (pkm/memory.py:218).
+ */
+int pkm_softmax_fwd(const void* x, int64_t rows, int64_t cols, int dtype, void* y, void* stream);
+
+/*
+ * Backward of pkm_softmax_fwd through .float(), softmax and .type_as
+ * (pkm/memory.py:218), with the float32 probabilities p recomputed from x:
+ *   dx[i, j] = dtype(p_j * (dy[i, j] - sum_k dy[i, k] * p_k))
+ */
+int pkm_softmax_bwd(const void* dy, const void* x, int64_t rows, int64_t cols, int dtype, void* dx, void* stream);
+
 /* Workspace bytes pkm_column_sum needs for these sizes. */
 size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);
 

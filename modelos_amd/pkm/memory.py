@@ -3,15 +3,17 @@
 HashingMemory keeps the reference's constructor arguments, parameter names
 and shapes (so state dicts load unchanged), reset_parameters, and its forward
 contract x [B, T, C] -> (out [B, T, output_dim], indices [B, T, heads * knn]).
-The two hot steps run on gfx950 HIP kernels:
+On gfx950 HIP kernels:
 
   * get_indices: sub-key scores on MFMA, per-half top-k and the cartesian
-    top-k fused in one kernel (modelos_amd.product_keys), with a sparse
-    backward through the embedding-bag kernels on the key table;
-  * the value read: the weighted embedding bag (xFormerEmbeddingBag).
+    top-k fused in one kernel (modelos_amd.product_keys); the backward works
+    from the nonzeros of the sub-score gradient (dq gathered, dK on MFMA);
+  * the value read: the weighted embedding bag (xFormerEmbeddingBag);
+  * the glue around them: the query RMSNorm, the score softmax, the swilu
+    gate and the Linears' bias gradients, one kernel each way.
 
-The query network, softmax and the swilu/value projections are ordinary
-torch ops around them (GEMMs on the vendor BLAS).
+The Linear products run on the vendor BLAS (their weight gradients as a
+split-K batched product).
 
 Reference: pkm/memory.py:15-28 (ProductKeyArgs), :37-248 (HashingMemory),
 :250-289 (get_indices), :292-349 (QueryMLP).
@@ -29,7 +31,7 @@ from torch.nn import functional as F
 
 from .. import _lib
 from ..embedding_bag import _aligned
-from ..product_keys import product_key_topk
+from ..product_keys import product_key_topk, score_softmax
 from ..rmsnorm import QueryRMSNorm
 from ..swilu import swilu_gate
 from .colwise_embedding_bag import xFormerEmbeddingBag
@@ -260,7 +262,7 @@ class HashingMemory(nn.Module):
             self.last_scores = scores.view(bs, self.heads, knn).detach().cpu().float()
 
         # softmax over each head's knn scores in float32 (memory.py:218)
-        scores = F.softmax(scores.float(), dim=-1).type_as(scores)
+        scores = score_softmax(scores)
         indices = indices.view(bs, self.heads * knn)
         scores = scores.view(bs, self.heads * knn)
 

@@ -174,6 +174,7 @@ class ProductKeyTopK(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query, keys, heads, knn, score_type, sub_outputs):
+        ctx.set_materialize_grads(False)  # no zero tensors for the outputs without a gradient
         outs = score_topk(query, keys, heads, knn, score_type, sub_outputs)
         ctx.heads, ctx.knn, ctx.score_type, ctx.sub_outputs = heads, knn, score_type, sub_outputs
         ctx.n = keys.shape[0] // (2 * heads)
@@ -204,6 +205,40 @@ class ProductKeyTopK(torch.autograd.Function):
         return d_query, d_keys, None, None, None, None
 
 
+class _ScoreSoftmax(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        x2 = _aligned(x)
+        rows, cols = x2.shape
+        y = torch.empty_like(x2)
+        _lib.call("pkm_softmax_fwd", _lib.ptr(x2), rows, cols, _lib.dtype_code(x2), _lib.ptr(y),
+                  _lib.stream_of(x2.device))
+        ctx.save_for_backward(x2)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (x2,) = ctx.saved_tensors
+        rows, cols = x2.shape
+        dy2 = _aligned(dy.to(x2.dtype))
+        dx = torch.empty_like(x2)
+        _lib.call("pkm_softmax_bwd", _lib.ptr(dy2), _lib.ptr(x2), rows, cols, _lib.dtype_code(x2), _lib.ptr(dx),
+                  _lib.stream_of(x2.device))
+        return dx
+
+
+def score_softmax(scores: torch.Tensor) -> torch.Tensor:
+    """F.softmax(scores.float(), dim=-1).type_as(scores) (pkm/memory.py:218)
+    with one kernel each way (pkm_softmax_fwd / pkm_softmax_bwd) for float32
+    or bfloat16 rows of at most 64 scores on the GPU; other cases use that
+    expression."""
+    _require_device(scores)
+    k = scores.shape[-1]
+    if scores.dtype in (torch.float32, torch.bfloat16) and 1 <= k <= 64 and scores.numel() > 0:
+        return _ScoreSoftmax.apply(scores.reshape(-1, k)).view(scores.shape)
+    return torch.softmax(scores.float(), dim=-1).type_as(scores)
+
+
 def product_key_topk(
     query: torch.Tensor,
     keys: torch.Tensor,
@@ -216,4 +251,5 @@ def product_key_topk(
     return ProductKeyTopK.apply(query, keys, heads, knn, score_type, sub_outputs)
 
 
-__all__ = ["score_topk", "product_key_topk", "ProductKeyTopK", "score_grad_dense", "score_grad_sparse", "SCORE_TYPES"]
+__all__ = ["score_topk", "product_key_topk", "ProductKeyTopK", "score_grad_dense", "score_grad_sparse", "score_softmax",
+           "SCORE_TYPES"]
