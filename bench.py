@@ -18,7 +18,7 @@ region), every entry point's time, and the reference's CPU path (op-for-op
 torch CPU restatement: einsum/topk/F.embedding_bag + ATen autograd) timed on
 this host's cores on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload layer|eb] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload layer|eb|fwupdate] [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -396,12 +396,90 @@ def run_eb(args, dev):
     }
 
 
+def run_fwupdate(args, dev):
+    """Fast-weight value update (FwPKM update_fw, values, sgd): 2^18 x 512 float32
+    table (4 heads x 512 keys per half), 8192 tokens x 64 lookups, lr 0.1."""
+    import torch
+
+    from modelos_amd import _lib
+    from modelos_amd.fwpkm.fwpkm import sgd_value_update
+    from oracle import fw_update as ref
+
+    K, D, N, L = 1 << 18, 512, 8192, 4 * 16
+    scale, lr = N * D * 16 * 4, 0.1
+    gen = torch.Generator(device=dev).manual_seed(0)
+    p = (torch.randn((K, D), generator=gen, device=dev) * D**-0.5).float()
+    g = torch.randn((K, D), generator=gen, device=dev) * 1e-6
+    idx = torch.randint(0, K, (N, L), generator=gen, device=dev)
+
+    def step():
+        return sgd_value_update(p, g, idx, scale, lr, 0.0, False)
+
+    def torch_step():
+        return ref.sgd_value_update(p, g, idx, scale, lr, 0.0, False)
+
+    for _ in range(args.warmup):
+        step()
+        torch_step()
+    torch.cuda.synchronize()
+    timer = _lib.CallTimer()
+    t0 = time.perf_counter()
+    with timer:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        torch_step()
+    torch.cuda.synchronize()
+    torch_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    calls = timer.summary()
+    v = sorted(next(c for k, c in calls.items() if k[0] == "pkm_fw_sgd_update"))
+    kern_ms = v[len(v) // 2]
+    work = 4 * K * D * 4 + K * 8  # read values and gradient, write both outputs; the counts
+    achieved = work / (kern_ms * 1e-3) / 1e9
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (kernel {kern_ms:.3f} ms), "
+        f"reference op sequence on the GPU {torch_ms:.3f} ms")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline ...")
+        pc, gc, ic = p.cpu(), g.cpu(), idx.cpu()
+        t, reps = timed_median(lambda: ref.sgd_value_update(pc, gc, ic, scale, lr, 0.0, False), budget_s=10.0)
+        cores = torch.get_num_threads()
+        cpu = {"value": round(K / t, 1), "unit": "rows/s", "cores": cores, "kind": "port",
+               "sample": f"full update ({K} x {D} float32), median of {reps} after 1 warm-up; the reference's "
+               f"ATen op sequence on {cores} threads ({cpu_model()})", "ms_per_step": round(t * 1e3, 1)}
+    return {
+        "metric": "FwPKM fast-weight value update (bincount-normalised SGD) table rows/sec, float32",
+        "value": round(K / (ms_per_step * 1e-3), 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "FwPKM update_fw values step (scale, bincount division, sgd) in one pass",
+                   "num_rows": K, "dim": D, "tokens": N, "lookups_per_token": L},
+        "roofline": {"bound": "hbm", "kernel": "pkm_fw_sgd_update", "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "kernels": {"pkm_fw_sgd_update": {"ms": round(kern_ms, 4), "work": work},
+                    "reference op sequence (torch, same GPU)": {"ms": round(torch_ms, 4)}},
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["layer", "eb"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate"], default="layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
         "--copy-probe-mib", type=int, default=0,
@@ -429,7 +507,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
         log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
-    res = run_layer(args, dev) if args.workload == "layer" else run_eb(args, dev)
+    runs = {"layer": run_layer, "eb": run_eb, "fwupdate": run_fwupdate}
+    res = runs[args.workload](args, dev)
     print(json.dumps(res), flush=True)
 
 

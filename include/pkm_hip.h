@@ -216,6 +216,21 @@ int pkm_softmax_fwd(const void* x, int64_t rows, int64_t cols, int dtype, void* 
  */
 int pkm_softmax_bwd(const void* dy, const void* x, int64_t rows, int64_t cols, int dtype, void* dx, void* stream);
 
+/*
+ * Fast-weight value update of FwPKM in one pass (fwpkm/fwpkm.py:334-365 with
+ * update_fw_param at 266-272; optimizer "sgd"). For rows r < num_rows and
+ * columns j < dim (dtype F32 or BF16 for values, grad and both outputs;
+ * counts int64 [num_rows], the bincount of the step's indices):
+ *   scaled_grad[r, j] = dtype(dtype(grad[r, j] * scale) / dtype(max(counts[r], 1)))
+ *   c                 = grad_clip ? clamp(scaled_grad[r, j], -1, 1) : scaled_grad[r, j]
+ *   new_values[r, j]  = dtype(values - dtype(lr * dtype(c + dtype(weight_decay * values))))
+ * every step rounded to dtype in the reference's order, no fused multiply-add.
+ * values, grad and the outputs 16-byte aligned; dim a multiple of 4 / 8.
+ */
+int pkm_fw_sgd_update(const void* values, const void* grad, const int64_t* counts, int64_t num_rows, int64_t dim,
+                      int dtype, float scale, float lr, float weight_decay, int grad_clip, void* scaled_grad,
+                      void* new_values, void* stream);
+
 /* Workspace bytes pkm_column_sum needs for these sizes. */
 size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);
 

@@ -77,6 +77,14 @@ SIGNATURES = {
             c_void_p, c_size_t, c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "pkm_fw_sgd_update": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int,  # values, grad, counts, num_rows, dim, dtype
+            c_float, c_float, c_float, c_int,  # scale, lr, weight_decay, grad_clip
+            c_void_p, c_void_p, c_void_p,  # scaled_grad, new_values, stream
+        ],
+    ),
     "pkm_softmax_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_softmax_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_column_sum_workspace_size": (c_size_t, [c_int64, c_int64]),
