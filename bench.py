@@ -18,7 +18,7 @@ region), every entry point's time, and the reference's CPU path (op-for-op
 torch CPU restatement: einsum/topk/F.embedding_bag + ATen autograd) timed on
 this host's cores on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload layer|eb|fwupdate] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload layer|eb|fwupdate|fwpkm] [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -474,12 +474,88 @@ def run_fwupdate(args, dev):
     }
 
 
+def run_fwpkm(args, dev):
+    """Fast-weight PKM step at 4 heads x 512 keys per half (2^18 slots), knn 16,
+    value dim 512, 8192 tokens, float32: retrieval, the inner MSE gradient with
+    create_graph, the fused value update (lr 0.1), retrieval from the updated
+    table, and the outer backward through the update (the embedding bag's
+    grad-of-grad). Synthetic indices and weights of that shape."""
+    import torch
+
+    from modelos_amd import _lib
+    from modelos_amd.fwpkm.fwpkm import sgd_value_update
+    from modelos_amd.fwpkm.xformer_embeddingbag_grad_wrapper import xformers_embedding_bag as xeb
+
+    N, H, knn, K, D = 8192, 4, 16, 512 * 512, 512
+    L = H * knn
+    scale, lr = N * D * knn * H, 0.1
+    gen = torch.Generator(device=dev).manual_seed(0)
+    V = (torch.randn((K, D), generator=gen, device=dev) * D**-0.5).requires_grad_(True)
+    idx = torch.randint(0, K, (N, L), generator=gen, device=dev)
+    idx2 = torch.randint(0, K, (N, L), generator=gen, device=dev)
+    psw = torch.softmax(torch.randn((N, L), generator=gen, device=dev), -1).requires_grad_(True)
+    psw2 = torch.softmax(torch.randn((N, L), generator=gen, device=dev), -1).requires_grad_(True)
+    targets = torch.randn((N, D), generator=gen, device=dev)
+    dout = torch.randn((N, D), generator=gen, device=dev)
+
+    def step():
+        V.grad = psw.grad = psw2.grad = None
+        hyp = xeb(idx, V, psw)
+        mem_loss = ((hyp - targets) ** 2).mean(-1).mean() * 0.5
+        (gV,) = torch.autograd.grad(mem_loss, V, create_graph=True)
+        Vn, _ = sgd_value_update(V, gV, idx, scale, lr, 0.0, False)
+        xeb(idx2, Vn, psw2).backward(dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = _lib.CallTimer()
+    t0 = time.perf_counter()
+    with timer:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    calls = timer.summary()
+    kernels = {}
+    for name in ("pkm_eb_fwd", "pkm_eb_bwd", "pkm_eb_bwd2", "pkm_fw_sgd_update"):
+        keys = [k for k in calls if k[0] == name]
+        if keys:
+            tot = sum(sum(calls[k]) for k in keys) / args.steps
+            kernels[name] = {"ms_per_step": round(tot, 4), "calls_per_step": sum(len(calls[k]) for k in keys) // args.steps}
+    b2 = sorted(next(c for k, c in calls.items() if k[0] == "pkm_eb_bwd2"))
+    b2_ms = b2[len(b2) // 2]
+    work = N * L * D * 4 + 2 * N * D * 4 + N * L * (8 + 8)  # g-bar rows, upstream gradient in/out, ids and weights
+    achieved = work / (b2_ms * 1e-3) / 1e9
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; grad-of-grad {b2_ms:.3f} ms")
+    return {
+        "metric": "FwPKM inner update + outer backward (grad-of-grad) tokens/sec, float32",
+        "value": round(N / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (uniform indices, softmax weights, N(0,1) targets and upstream gradient)",
+        "config": {"workload": "fast-weight PKM value retrieval, inner update, outer backward through it",
+                   "tokens": N, "heads": H, "knn": knn, "num_rows": K, "v_dim": D, "lr": lr},
+        "roofline": {"bound": "hbm", "kernel": "pkm_eb_bwd2", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "kernels": kernels,
+        "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate", "fwpkm"], default="layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument(
         "--copy-probe-mib", type=int, default=0,
@@ -507,7 +583,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
         log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
-    runs = {"layer": run_layer, "eb": run_eb, "fwupdate": run_fwupdate}
+    runs = {"layer": run_layer, "eb": run_eb, "fwupdate": run_fwupdate, "fwpkm": run_fwpkm}
     res = runs[args.workload](args, dev)
     print(json.dumps(res), flush=True)
 
