@@ -231,6 +231,19 @@ int pkm_fw_sgd_update(const void* values, const void* grad, const int64_t* count
                       int dtype, float scale, float lr, float weight_decay, int grad_clip, void* scaled_grad,
                       void* new_values, void* stream);
 
+/*
+ * Backward of pkm_fw_sgd_update: the gradients autograd forms for the
+ * reference's p - lr * (clip(gs) + wd * p), gs = grad * scale / count
+ * (fwpkm/fwpkm.py:334-365, 266-272), op by op in dtype:
+ *   x             = dtype(lr * -d_new_values)
+ *   d_values      = dtype(d_new_values + dtype(weight_decay * x))
+ *   d             = (grad_clip ? x * [-1 <= scaled_grad <= 1] : x) (+ d_scaled_grad, when not NULL)
+ *   d_grad        = dtype(dtype(d / dtype(max(counts, 1))) * scale)
+ */
+int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_scaled_grad, const void* scaled_grad,
+                          const int64_t* counts, int64_t num_rows, int64_t dim, int dtype, float scale, float lr,
+                          float weight_decay, int grad_clip, void* d_values, void* d_grad, void* stream);
+
 /* Workspace bytes pkm_column_sum needs for these sizes. */
 size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);
 

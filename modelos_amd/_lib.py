@@ -85,6 +85,15 @@ SIGNATURES = {
             c_void_p, c_void_p, c_void_p,  # scaled_grad, new_values, stream
         ],
     ),
+    "pkm_fw_sgd_update_bwd": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_void_p,  # d_new_values, d_scaled_grad, scaled_grad, counts
+            c_int64, c_int64, c_int,  # num_rows, dim, dtype
+            c_float, c_float, c_float, c_int,  # scale, lr, weight_decay, grad_clip
+            c_void_p, c_void_p, c_void_p,  # d_values, d_grad, stream
+        ],
+    ),
     "pkm_softmax_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_softmax_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_column_sum_workspace_size": (c_size_t, [c_int64, c_int64]),

@@ -104,23 +104,24 @@ class _SgdValueUpdate(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_new, d_gs):
         # the reference's autograd through p - lr * (clamp(g * scale / c) + wd * p), op by op
+        # (pkm_fw_sgd_update_bwd); only the scaled gradient's own gradient: its two ops
         gs, counts = ctx.saved_tensors
-        d_p = d_g = None
-        grad_x = None
-        if d_new is not None:
-            grad_x = ctx.lr * (-d_new)  # d (lr * X), X = gc + wd * p
-            d_p = d_new + ctx.wd * grad_x
-            d_gc = grad_x
-            d_gsv = d_gc * ((gs >= -1.0) & (gs <= 1.0)).to(gs.dtype) if ctx.clip else d_gc
-        else:
-            d_gsv = None
-        if d_gs is not None:
-            d_gsv = d_gs if d_gsv is None else d_gsv + d_gs
-        if d_gsv is not None and ctx.needs_input_grad[1]:
+        if d_new is None:
+            if d_gs is None or not ctx.needs_input_grad[1]:
+                return None, None, None, None, None, None, None
             c = counts.to(gs.dtype)
             c[c == 0] = 1.0
-            d_g = (d_gsv / c.unsqueeze(-1)) * ctx.scale
-        return (d_p if ctx.needs_input_grad[0] else None), d_g, None, None, None, None, None
+            return None, (d_gs / c.unsqueeze(-1)) * ctx.scale, None, None, None, None, None
+        dn = _aligned(d_new.to(gs.dtype))
+        dgi = _aligned(d_gs.to(gs.dtype)) if d_gs is not None else None
+        d_p = torch.empty_like(gs)
+        d_g = torch.empty_like(gs)
+        K, D = gs.shape
+        _lib.call("pkm_fw_sgd_update_bwd", _lib.ptr(dn), _lib.ptr(dgi), _lib.ptr(gs), _lib.ptr(counts), K, D,
+                  _lib.dtype_code(gs), float(ctx.scale), float(ctx.lr), float(ctx.wd), int(bool(ctx.clip)),
+                  _lib.ptr(d_p), _lib.ptr(d_g), _lib.stream_of(gs.device))
+        return (d_p if ctx.needs_input_grad[0] else None), (d_g if ctx.needs_input_grad[1] else None), \
+            None, None, None, None, None
 
 
 def sgd_value_update(p: torch.Tensor, g: torch.Tensor, indices: torch.Tensor, scale: float, lr: float,
