@@ -239,7 +239,8 @@ def run_layer(args, dev):
     add_ms("pkm_rmsnorm_bwd (query)", "pkm_rmsnorm_bwd", "query RMSNorm backward + ordered weight-gradient reduction")
     add_ms("pkm_swilu_fwd (value gate)", "pkm_swilu_fwd", "e * silu(s) of the value output")
     add_ms("pkm_swilu_bwd (value gate)", "pkm_swilu_bwd", "gradients of the value gate")
-    add_ms("pkm_column_sum (Linear bias gradients)", "pkm_column_sum", "per call; one call per Linear")
+    add_ms("pkm_column_sum (Linear bias gradients, split-K sums)", "pkm_column_sum",
+           "per call; per Linear one bias gradient and one sum of the weight gradient's split-K partials")
     add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
     add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
     hip_ms = sum(v["ms"] * v["calls_per_step"] for v in kernels.values())

@@ -248,14 +248,16 @@ int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_scaled_grad, c
 size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);
 
 /*
- * Column sums of a row-major [rows, cols] matrix (dtype F32 or BF16; x and the
- * workspace 16-byte aligned, cols a multiple of 4 / 8):
- *   out[j] = dtype(sum_i x[i, j])   float32, over fixed row blocks in order
- * (deterministic). Replaces g.sum(0), the bias gradient autograd forms for the
- * Linear layers of HashingMemory and its query network (pkm/memory.py:147-149,
- * 305).
+ * Column sums of a row-major [rows, cols] matrix (dtype F32 or BF16; out in
+ * out_dtype F32 or BF16; x and the workspace 16-byte aligned, cols a multiple
+ * of 4 / 8):
+ *   out[j] = out_dtype(sum_i x[i, j])   float32, over fixed row blocks in order
+ * (deterministic; up to 32 rows need no workspace). Replaces g.sum(0), the bias
+ * gradient autograd forms for the Linear layers of HashingMemory and its query
+ * network (pkm/memory.py:147-149, 305), and sums the split-K partials of their
+ * weight gradients.
  */
-int pkm_column_sum(const void* x, int64_t rows, int64_t cols, int dtype, void* out, void* workspace,
+int pkm_column_sum(const void* x, int64_t rows, int64_t cols, int dtype, int out_dtype, void* out, void* workspace,
                    size_t workspace_bytes, void* stream);
 
 /*

@@ -97,7 +97,7 @@ SIGNATURES = {
     "pkm_softmax_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_softmax_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_column_sum_workspace_size": (c_size_t, [c_int64, c_int64]),
-    "pkm_column_sum": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "pkm_column_sum": (c_int, [c_void_p, c_int64, c_int64, c_int, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "pkm_swilu_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_swilu_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
     "pkm_rmsnorm_fwd": (

@@ -15,9 +15,18 @@ namespace pkm {
 
 constexpr int kColRB = 32;  // rows per partial
 
-template <typename T>
+template <typename T, typename TO>
+__device__ __forceinline__ void colsum_store(TO* out, int64_t j, float v) {
+  if (sizeof(TO) == 4)
+    ((float*)out)[j] = v;
+  else
+    ((uint16_t*)out)[j] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+// part == nullptr: the rows form one block and the sums go straight to out
+template <typename T, typename TO>
 __global__ __launch_bounds__(256) void colsum_partial_kernel(const T* __restrict__ x, int64_t rows, int cols,
-                                                             float* __restrict__ part) {
+                                                             float* __restrict__ part, TO* __restrict__ out) {
   constexpr int EPV = VecTraits<T>::EPV;
   const int nv = cols / EPV;
   const int c = blockIdx.x * 256 + threadIdx.x;  // column vector
@@ -46,14 +55,19 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(const T* __restrict
 #pragma unroll
     for (int e = 0; e < EPV; ++e) acc[e] += f[e];
   }
+  if (part == nullptr) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) colsum_store<T, TO>(out, (int64_t)c * EPV + e, acc[e]);
+    return;
+  }
   float* pr = part + (int64_t)blockIdx.y * cols + c * EPV;
 #pragma unroll
   for (int e = 0; e < EPV; e += 4) *(float4*)(pr + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
 }
 
-template <typename T>
+template <typename TO>
 __global__ __launch_bounds__(256) void colsum_reduce_kernel(const float* __restrict__ part, int64_t nb, int cols,
-                                                            T* __restrict__ out) {
+                                                            TO* __restrict__ out) {
   __shared__ float ps[4][64];
   const int jl = threadIdx.x & 63, sl = threadIdx.x >> 6;
   const int j = blockIdx.x * 64 + jl;
@@ -75,10 +89,7 @@ __global__ __launch_bounds__(256) void colsum_reduce_kernel(const float* __restr
   __syncthreads();
   if (sl == 0 && j < cols) {
     const float t = ((ps[0][jl] + ps[1][jl]) + ps[2][jl]) + ps[3][jl];
-    if (sizeof(T) == 4)
-      ((float*)out)[j] = t;
-    else
-      ((uint16_t*)out)[j] = (uint16_t)f32_to_bf16_bits(t);
+    colsum_store<float, TO>(out, j, t);
   }
 }
 
@@ -91,10 +102,12 @@ extern "C" size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols) {
   return (size_t)((rows + kColRB - 1) / kColRB) * (size_t)cols * sizeof(float);
 }
 
-extern "C" int pkm_column_sum(const void* x, int64_t rows, int64_t cols, int dtype, void* out, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+extern "C" int pkm_column_sum(const void* x, int64_t rows, int64_t cols, int dtype, int out_dtype, void* out,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
               "pkm_column_sum: dtype %d not supported (float32, bfloat16 are)", dtype);
+  PKM_REQUIRE(out_dtype == PKM_DTYPE_F32 || out_dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
+              "pkm_column_sum: output dtype %d not supported (float32, bfloat16 are)", out_dtype);
   const int epv = dtype == PKM_DTYPE_BF16 ? 8 : 4;
   PKM_REQUIRE(rows >= 0 && cols >= 1 && cols % epv == 0 && cols < (1 << 30), PKM_ERR_UNSUPPORTED,
               "pkm_column_sum: %lld columns must be a positive multiple of %d", (long long)cols, epv);
@@ -102,26 +115,32 @@ extern "C" int pkm_column_sum(const void* x, int64_t rows, int64_t cols, int dty
   hipStream_t st = (hipStream_t)stream;
   const int C = (int)cols;
   const int64_t nb = (rows + kColRB - 1) / kColRB;
-  const dim3 rgrid((unsigned)((C + 63) / 64));
+  const bool one = nb == 1;  // one block of rows: sums straight to out, no workspace
+  const bool bf_in = dtype == PKM_DTYPE_BF16, bf_out = out_dtype == PKM_DTYPE_BF16;
   if (rows > 0) {
-    PKM_REQUIRE(x != nullptr && workspace != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_column_sum: null pointer");
-    PKM_REQUIRE(((uintptr_t)x | (uintptr_t)workspace) % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
+    PKM_REQUIRE(x != nullptr && (one || workspace != nullptr), PKM_ERR_INVALID_ARGUMENT,
+                "pkm_column_sum: null pointer");
+    PKM_REQUIRE(((uintptr_t)x | (uintptr_t)(one ? nullptr : workspace)) % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
                 "pkm_column_sum: x and workspace must be 16-byte aligned");
-    PKM_REQUIRE(workspace_bytes >= pkm_column_sum_workspace_size(rows, cols), PKM_ERR_WORKSPACE,
+    PKM_REQUIRE(one || workspace_bytes >= pkm_column_sum_workspace_size(rows, cols), PKM_ERR_WORKSPACE,
                 "pkm_column_sum: workspace of %zu bytes, %zu needed", workspace_bytes,
                 pkm_column_sum_workspace_size(rows, cols));
     PKM_REQUIRE(nb < 65536, PKM_ERR_UNSUPPORTED, "pkm_column_sum: %lld rows exceed the partial grid",
                 (long long)rows);
     const dim3 pgrid((unsigned)((C / epv + 255) / 256), (unsigned)nb);
-    if (dtype == PKM_DTYPE_BF16)
-      hipLaunchKernelGGL(colsum_partial_kernel<bf16_t>, pgrid, dim3(256), 0, st, (const bf16_t*)x, rows, C,
-                         (float*)workspace);
-    else
-      hipLaunchKernelGGL(colsum_partial_kernel<float>, pgrid, dim3(256), 0, st, (const float*)x, rows, C,
-                         (float*)workspace);
+    float* part = one ? nullptr : (float*)workspace;
+#define PKM_COLSUM_P(TI, TO) \
+  hipLaunchKernelGGL((colsum_partial_kernel<TI, TO>), pgrid, dim3(256), 0, st, (const TI*)x, rows, C, part, (TO*)out)
+    if (bf_in && bf_out) PKM_COLSUM_P(bf16_t, bf16_t);
+    else if (bf_in) PKM_COLSUM_P(bf16_t, float);
+    else if (bf_out) PKM_COLSUM_P(float, bf16_t);
+    else PKM_COLSUM_P(float, float);
+#undef PKM_COLSUM_P
+    if (one) return pkm_check_launch("pkm_column_sum");
   }
-  // no rows: out = 0 (a sum over no partials)
-  if (dtype == PKM_DTYPE_BF16)
+  // the partials in block order (no rows: out = 0, a sum over no partials)
+  const dim3 rgrid((unsigned)((C + 63) / 64));
+  if (bf_out)
     hipLaunchKernelGGL(colsum_reduce_kernel<bf16_t>, rgrid, dim3(256), 0, st, (const float*)workspace, nb, C,
                        (bf16_t*)out);
   else

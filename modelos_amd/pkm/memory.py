@@ -75,7 +75,7 @@ class _Linear(torch.autograd.Function):
             if s > 1:
                 part = torch.bmm(g.view(s, rows // s, out_f).transpose(1, 2), x.view(s, rows // s, in_f),
                                  out_dtype=torch.float32)
-                gw = part.sum(0).to(weight.dtype)
+                gw = _column_sum(part.view(s, out_f * in_f), weight.dtype).view(out_f, in_f)
             else:
                 gw = g.t() @ x
         if ctx.has_bias and ctx.needs_input_grad[2]:
@@ -83,20 +83,22 @@ class _Linear(torch.autograd.Function):
         return gx, gw, gb
 
 
-def _column_sum(g: torch.Tensor) -> torch.Tensor:
-    """g.sum(0) of a 2-D gradient: on the GPU for float32 / bfloat16 rows of
-    whole 16-byte vectors (pkm_column_sum: float32 sums over fixed row blocks,
-    deterministic), else torch's sum."""
+def _column_sum(g: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """g.sum(0) of a 2-D matrix in out_dtype (default g's): on the GPU for
+    float32 / bfloat16 rows of whole 16-byte vectors (pkm_column_sum: float32
+    sums over fixed row blocks, deterministic), else torch's sum."""
+    out_dtype = out_dtype or g.dtype
     if not (g.is_cuda and g.dim() == 2 and g.dtype in (torch.float32, torch.bfloat16)
+            and out_dtype in (torch.float32, torch.bfloat16)
             and g.shape[1] % (16 // g.element_size()) == 0 and g.shape[1] > 0):
-        return g.sum(0)
+        return g.sum(0).to(out_dtype)
     g = _aligned(g)
     rows, cols = g.shape
-    out = torch.empty(cols, dtype=g.dtype, device=g.device)
+    out = torch.empty(cols, dtype=out_dtype, device=g.device)
     ws_bytes = int(_lib.load().pkm_column_sum_workspace_size(rows, cols))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=g.device)
-    _lib.call("pkm_column_sum", _lib.ptr(g), rows, cols, _lib.dtype_code(g), _lib.ptr(out), _lib.ptr(ws), ws_bytes,
-              _lib.stream_of(g.device))
+    _lib.call("pkm_column_sum", _lib.ptr(g), rows, cols, _lib.dtype_code(g), _lib.DTYPE_CODES[out_dtype],
+              _lib.ptr(out), _lib.ptr(ws), ws_bytes, _lib.stream_of(g.device))
     return out
 
 

@@ -71,6 +71,20 @@ def test_column_sum_gpu(device, dtype, rows, cols):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("rows", [8, 32, 33, 200])
+def test_column_sum_float32_to_bf16(device, rows):
+    """float32 input summed into a bfloat16 output (the split-K partials of a
+    weight gradient): one rounding of the float32 sum."""
+    from modelos_amd.pkm.memory import _column_sum
+
+    g = torch.randn((rows, 4096), generator=gen(4)).to(device)
+    a = _column_sum(g, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert a.dtype == torch.bfloat16
+    assert_rel_close(a, g.double().sum(0), REL_TOL[torch.bfloat16], "column sum")
+
+
+@pytest.mark.gpu
 def test_column_sum_no_rows(device):
     from modelos_amd.pkm.memory import _column_sum
 
