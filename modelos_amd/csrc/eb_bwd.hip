@@ -592,10 +592,10 @@ struct RowMeta {
 template <typename TW, int VPL, int U>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 && U <= 4) ? 5 : ((VPL == 1 || (VPL == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows64_kernel(
     const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TW* __restrict__ g,
-    const uint32_t* __restrict__ offs, const uint4* __restrict__ meta, const float* __restrict__ partials,
+    const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
     const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
     uint32_t dummy_slot) {
-  __shared__ uint4 smeta[4][kMetaChunk];
+  __shared__ uint2 smeta[4][kMetaChunk];
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   const int lane = threadIdx.x & 63;
@@ -619,7 +619,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     my_end = offs[r0 + lane + 1];
   }
 
-  uint4* sm = smeta[wv];
+  uint2* sm = smeta[wv];
   uint32_t cbase = (uint32_t)__builtin_amdgcn_readlane((int)my_beg, 0);
   auto load_chunk = [&](uint32_t start) {
     cbase = start;
@@ -640,9 +640,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     if (M.beg + U > cbase + kMetaChunk) load_chunk(M.beg);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint4 m = sm[M.beg - cbase + u];
-      M.b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)m.y);
-      M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readfirstlane((int)m.z)) : 0.f;
+      const uint2 m = sm[M.beg - cbase + u];
+      M.b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)m.x);
+      M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readfirstlane((int)m.y)) : 0.f;
     }
   };
   auto issue = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
@@ -703,9 +703,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
         float w[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const uint4 m = meta[s + u];
-          const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.y * rowbytes : zb;
-          w[u] = (uint32_t)u < nh ? __uint_as_float(m.z) : 0.f;
+          const uint2 m = meta[s + u];
+          const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * rowbytes : zb;
+          w[u] = (uint32_t)u < nh ? __uint_as_float(m.y) : 0.f;
 #pragma unroll
           for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
         }
@@ -733,31 +733,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   }
 }
 
-// meta[i] = {position, bag, weight as float32 bits, 0} in sorted order;
+// meta[i] = {bag, weight as float32 bits} of sorted occurrence i;
 // entries past the valid count (padding included) are zero.
 __global__ void occ_meta_kernel(const uint32_t* __restrict__ svals, const uint32_t* __restrict__ nvalid,
                                 int64_t n_total, uint32_t L32, const void* __restrict__ psw, int pdt,
-                                uint4* __restrict__ meta) {
+                                uint2* __restrict__ meta) {
   const uint32_t nv = *nvalid;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_total; i += (int64_t)gridDim.x * blockDim.x) {
-    uint4 m = make_uint4(0u, 0u, 0u, 0u);
+    uint2 m = make_uint2(0u, 0u);
     if (i < (int64_t)nv) {
       const uint32_t p = svals[i];
-      m.x = p;
-      m.y = p / L32;
-      m.z = __float_as_uint(psw ? load_scalar(psw, pdt, p) : 1.f);
+      m.x = p / L32;
+      m.y = __float_as_uint(psw ? load_scalar(psw, pdt, p) : 1.f);
     }
     meta[i] = m;
   }
 }
 
 // gpsw[position] <- psw-gradient dots computed in sorted order.
-__global__ void gpsw_scatter_kernel(const uint4* __restrict__ meta, const float* __restrict__ dsorted,
+__global__ void gpsw_scatter_kernel(const uint32_t* __restrict__ svals, const float* __restrict__ dsorted,
                                     const uint32_t* __restrict__ nvalid, int64_t N, void* __restrict__ gpsw, int pdt) {
   const uint32_t nv = *nvalid;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N; i += (int64_t)gridDim.x * blockDim.x) {
     if (i >= (int64_t)nv) break;
-    store_scalar(gpsw, pdt, meta[i].x, dsorted[i]);
+    store_scalar(gpsw, pdt, svals[i], dsorted[i]);
   }
 }
 
@@ -820,7 +819,7 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   // a zero row read by unused prefetch slots and a dummy row written by tail rows
   l.nmeta = N + kMetaChunk + 16;
   l.meta = off;
-  off += align256((size_t)l.nmeta * 16);
+  off += align256((size_t)l.nmeta * 8);
   l.dsorted = off;
   off += align256((size_t)(N + 1) * 4);
   l.zrow = off;
@@ -881,7 +880,7 @@ static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], ui
 
 template <typename TW, int VPL, int U>
 static void launch_rows64(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
-                          const uint4* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
+                          const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                           float* dsorted, uint32_t dummy_slot, hipStream_t st) {
   const unsigned rb = (unsigned)cdiv(K, 4 * 64);
   hipLaunchKernelGGL((eb_bwd_rows64_kernel<TW, VPL, U>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, want_dot,
@@ -898,7 +897,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
   float* partials = (float*)(ws + l.partials);
   const unsigned hb = (unsigned)cdiv(l.nchunks, groups_per_block);
   if constexpr (LPG == 64) {
-    uint4* meta = (uint4*)(ws + l.meta);
+    uint2* meta = (uint2*)(ws + l.meta);
     float* dsorted = (float*)(ws + l.dsorted);
     void* zrow = ws + l.zrow;
     hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(D, 256, 64)), dim3(256), 0, st, (uint32_t*)zrow, 0u, D);
@@ -909,8 +908,8 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
                          pdt, (const TW*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
                          dsorted);
     } else {
-      hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(4 * l.nmeta, 256, 4096)), dim3(256), 0, st,
-                         (uint32_t*)meta, 0u, 4 * l.nmeta);
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * l.nmeta, 256, 4096)), dim3(256), 0, st,
+                         (uint32_t*)meta, 0u, 2 * l.nmeta);
     }
     if (K > 0) {
       const int want_dot = psw != nullptr ? 1 : 0;
@@ -934,7 +933,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       }
     }
     if (N > 0 && psw != nullptr)
-      hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, (const uint4*)meta,
+      hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, svals,
                          (const float*)dsorted, nvalid, N, gpsw, pdt);
   } else {
     if (N > 0)

@@ -31,8 +31,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+// Two floats to a packed bf16 pair in one v_cvt_pk_bf16_f32 (round to
+// nearest even, as f32_to_bf16_bits).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 __device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
@@ -117,7 +121,6 @@ struct VecTraits<f16_t> {
 
 // Float32 dot product of two packed bf16 pairs accumulated into c
 // (v_dot2_f32_bf16: the bf16 products are exact in float32).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
