@@ -38,7 +38,9 @@
 //      preceded, in (value, flat index) order, by at least knn of them. The
 //      knn-th pair value is found by a bit search between the bound given by
 //      the pairs (a, 0) and (0, b) and the best pair, and the pairs reaching
-//      it are ranked.
+//      it are ranked. With bf16 scores (32-bit keys) the two lists are stored
+//      as the low and high words of the index output and C runs as its own
+//      kernel at full occupancy; with float32 scores it follows B in LDS.
 // Workgroups map head-fastest onto the grid, so with 8 heads each XCD (and its
 // L2) serves one head's keys.
 #include <atomic>
@@ -419,6 +421,123 @@ __device__ __forceinline__ void group_rank(const Key* cand, uint32_t C, int knn,
 }
 
 // ---------------------------------------------------------------------------
+// C: cartesian top-knn of one row per lane group, over the pairs
+// (a+1)(b+1) <= knn (every other pair is preceded, in (value, flat index)
+// order, by at least knn of them): T = the knn-th largest pair value, by a bit
+// search between a lower bound and the best pair, then the pairs >= T are
+// ranked. l0r / l1r: the row's two lists (best first), cand: its candidate
+// buffer (cap + 4 keys), finr: the ranked pair-slot keys out. Rows whose
+// candidates overflow cap are redone exactly by their wave, one at a time,
+// with wscr as scratch; rows(rr) gives the (l0, l1, fin) lists of the wave's
+// row rr for that. Rows with active = false select nothing.
+// ---------------------------------------------------------------------------
+template <typename Key>
+struct CartRow {
+  const Key* l0;
+  const Key* l1;
+  Key* fin;
+};
+
+template <typename TIN, int LPR, int MAXM, int MAXS, typename RowsF>
+__device__ __forceinline__ void cartesian_rows(const typename Sel<TIN>::Key* l0r, const typename Sel<TIN>::Key* l1r,
+                                               typename Sel<TIN>::Key* cand, typename Sel<TIN>::Key* finr, int cap,
+                                               int knn, int sub, bool active, typename Sel<TIN>::Key* wscr,
+                                               RowsF rows) {
+  typedef Sel<TIN> SL;
+  typedef typename SL::Key Key;
+  constexpr int KBITS = 8 * (int)sizeof(typename SL::Store);
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const uint16_t* pairs = kPairTable.ab + kPairTable.off[knn];
+  const int npairs = kPairTable.off[knn + 1] - kPairTable.off[knn];
+  // value (order key) of pair slot s; candidates are keyed by the slot,
+  // whose order is the flat a * knn + b order
+  auto pair_okey = [&](const Key* a, const Key* b, int s) -> uint32_t {
+    const uint32_t ab = pairs[s];
+    return SL::okey_of(SL::value(SL::key_okey(a[ab & 0xFFu])) + SL::value(SL::key_okey(b[ab >> 8])));
+  };
+  // the knn-th pair value lies between the knn-th of the pairs (a, 0) or
+  // (0, b) and the best pair; bits above their highest difference are shared
+  uint32_t Tlo, Thi;
+  {
+    const float v0 = SL::value(SL::key_okey(l0r[0]));
+    const float w0 = SL::value(SL::key_okey(l1r[0]));
+    const uint32_t ta = SL::okey_of(SL::value(SL::key_okey(l0r[knn - 1])) + w0);
+    const uint32_t tb = SL::okey_of(v0 + SL::value(SL::key_okey(l1r[knn - 1])));
+    Tlo = ta > tb ? ta : tb;
+    Thi = SL::okey_of(v0 + w0);
+  }
+  // pair values of this lane's slots sub + LPR i (0 past the last), the
+  // threshold T, and the compaction of the pairs >= T; NS = slots per lane
+  auto cartesian = [&](auto ns_tag, uint32_t& ctotal_out) -> bool {
+    constexpr int NS = decltype(ns_tag)::value;
+    uint32_t cv[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int s = sub + LPR * i;
+      cv[i] = s < npairs ? pair_okey(l0r, l1r, s) : 0u;
+    }
+    const uint32_t d = Tlo ^ Thi;
+    const int hb = d == 0 ? -1 : 31 - __builtin_clz(d);
+    uint32_t T = hb < 0 ? Tlo : (Thi & ~((2u << hb) - 1u));
+    for (int bit = hb; bit >= 0; --bit) {
+      const uint32_t trial = T | (1u << bit);
+      if (!group_count_ge_below<LPR, NS, KBITS>(cv, trial, knn)) T = trial;
+    }
+    T = T > 0u ? T : 1u;
+    uint32_t ccnt = 0;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) ccnt += cv[i] >= T ? 1u : 0u;
+    const uint32_t cincl = group_scan<LPR>(ccnt, sub);
+    const uint32_t ctotal = group_sum<LPR>(ccnt);
+    ctotal_out = ctotal;
+    const bool ov = ctotal > (uint32_t)cap;
+    if (!ov) {
+      uint32_t p = cincl - ccnt;
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+        if (cv[i] >= T) cand[p++] = SL::make(cv[i], (uint32_t)(sub + LPR * i));
+      if (sub == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) cand[ctotal + u] = (Key)0;
+      }
+    }
+    return ov;
+  };
+  uint32_t ctotal = 0;
+  bool coverflow;
+  if (npairs <= LPR * ((pair_count(16) + LPR - 1) / LPR))
+    coverflow = cartesian(std::integral_constant<int, (pair_count(16) + LPR - 1) / LPR>(), ctotal);
+  else if (npairs <= LPR * ((pair_count(32) + LPR - 1) / LPR))
+    coverflow = cartesian(std::integral_constant<int, (pair_count(32) + LPR - 1) / LPR>(), ctotal);
+  else
+    coverflow = cartesian(std::integral_constant<int, MAXS>(), ctotal);
+  coverflow = coverflow && active;
+  __builtin_amdgcn_wave_barrier();
+  auto to_fin = [&](uint32_t rank, Key k) { finr[rank] = k; };
+  if (!coverflow && active) {
+    if (cap <= 8 * LPR)
+      group_rank<Key, LPR, 8>(cand, ctotal, knn, sub, to_fin);
+    else
+      group_rank<Key, LPR, MAXM>(cand, ctotal, knn, sub, to_fin);
+  }
+  __builtin_amdgcn_wave_barrier();
+  {
+    const uint64_t ov = __ballot(coverflow);
+    for (int rr = 0; rr < RPW; ++rr) {
+      if (!((ov >> (rr * LPR)) & 1ull)) continue;
+      const CartRow<Key> row = rows(rr);
+      const Key top = exact_topk<Key>(
+          [&](int s) -> Key { return s < npairs ? SL::make(pair_okey(row.l0, row.l1, s), (uint32_t)s) : (Key)0; },
+          npairs, knn, wscr);
+      if (lane < knn) row.fin[lane] = top;
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
 template <typename TIN, int IDW, int TM, int KSC>
@@ -440,6 +559,9 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
   constexpr int KBITS = 8 * (int)sizeof(Store);                          // bits of an order key
   constexpr int MAXM = (2 * 64 > kCandCap * LPR / 64 ? 2 * 64 : kCandCap * LPR / 64) / LPR;  // cap / LPR
   constexpr int MAXS = (kMaxPairs + LPR - 1) / LPR;  // pair slots per lane
+  // 32-bit keys (bf16 scores): both lists fit one index word and the
+  // cartesian step runs as its own kernel (pkm_score_cartesian_kernel)
+  constexpr bool kSplitC = sizeof(Key) == 4;
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -480,7 +602,6 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
   const int ntw = (ncol - w + kWaves - 1) / kWaves;
   const int nsteps = ((ntw + CB - 1) / CB) * KS;
 
-  const int npairs = kPairTable.off[knn + 1] - kPairTable.off[knn];  // candidate pairs of the cartesian step
 
   // A tile row is read as 16-byte chunks interleaved over the lane group:
   // lane sub reads chunks LPR (i ^ x) + sub, i < NG, with x = row & 1 when
@@ -664,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
 #pragma unroll
     for (int i = 0; i < (64 + LPR - 1) / LPR; ++i) {
       const int j = sub + LPR * i;
-      park[i] = (hc == 1 && live && j < knn) ? (Key)out_idx[orow + j] : (Key)0;
+      park[i] = (!kSplitC && hc == 1 && live && j < knn) ? (Key)out_idx[orow + j] : (Key)0;
     }
 
     // ---- sub-score outputs (every key), coalesced over the workgroup
@@ -798,139 +919,139 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
     if (live && out_i2 != nullptr) {
       for (int j = sub; j < knn; j += LPR) out_i2[orow + j] = (int64_t)SL::key_idx(list[j]);
     }
-    __syncthreads();  // every row selected: the tile is free for the first half's lists and the pair table
-
-    // ---- C: cartesian top-knn of token r by its lane group, over the pairs
-    // (a+1)(b+1) <= knn (every other pair is preceded, in (value, flat index)
-    // order, by at least knn of them): T = the knn-th largest pair value, by
-    // a bit search between a lower bound and the best pair, then the pairs
-    // >= T are ranked.
-#pragma unroll
-    for (int i = 0; i < (64 + LPR - 1) / LPR; ++i) {
-      const int j = sub + LPR * i;
-      if (j < knn) l0[j] = park[i];
-    }
-    __builtin_amdgcn_wave_barrier();  // the first half's list of a row is written and read by its own lanes
-    // value (order key) of pair slot s; candidates are keyed by the slot,
-    // whose order is the flat a * knn + b order
-    auto pair_okey = [&](const Key* l0r, const Key* l1r, int s) -> uint32_t {
-      const uint32_t ab = pairs[s];
-      return SL::okey_of(SL::value(SL::key_okey(l0r[ab & 0xFFu])) + SL::value(SL::key_okey(l1r[ab >> 8])));
-    };
-    // the knn-th pair value lies between the knn-th of the pairs (a, 0) or
-    // (0, b) and the best pair; bits above their highest difference are shared
-    uint32_t Tlo, Thi;
-    {
-      const float v0 = SL::value(SL::key_okey(l0[0]));
-      const float w0 = SL::value(SL::key_okey(list[0]));
-      const uint32_t ta = SL::okey_of(SL::value(SL::key_okey(l0[knn - 1])) + w0);
-      const uint32_t tb = SL::okey_of(v0 + SL::value(SL::key_okey(list[knn - 1])));
-      Tlo = ta > tb ? ta : tb;
-      Thi = SL::okey_of(v0 + w0);
-    }
-    // pair values of this lane's slots sub + LPR i (0 past the last), the
-    // threshold T, and the compaction of the pairs >= T; NS = slots per lane
-    auto cartesian = [&](auto ns_tag, uint32_t& ctotal_out) -> bool {
-      constexpr int NS = decltype(ns_tag)::value;
-      uint32_t cv[NS];
-#pragma unroll
-      for (int i = 0; i < NS; ++i) {
-        const int s = sub + LPR * i;
-        cv[i] = s < npairs ? pair_okey(l0, list, s) : 0u;
+    if constexpr (kSplitC) {
+      // 32-bit keys: the second half's list joins the first in the high words
+      // of the index output; the cartesian step runs as its own kernel
+      if (live) {
+        for (int j = sub; j < knn; j += LPR) ((uint32_t*)(out_idx + orow + j))[1] = (uint32_t)list[j];
       }
-      const uint32_t d = Tlo ^ Thi;
-      const int hb = d == 0 ? -1 : 31 - __builtin_clz(d);
-      uint32_t T = hb < 0 ? Tlo : (Thi & ~((2u << hb) - 1u));
-      for (int bit = hb; bit >= 0; --bit) {
-        const uint32_t trial = T | (1u << bit);
-        if (!group_count_ge_below<LPR, NS, KBITS>(cv, trial, knn)) T = trial;
+      continue;
+    } else {
+      __syncthreads();  // every row selected: the tile is free for the first half's lists
+#pragma unroll
+      for (int i = 0; i < (64 + LPR - 1) / LPR; ++i) {
+        const int j = sub + LPR * i;
+        if (j < knn) l0[j] = park[i];
       }
-      T = T > 0u ? T : 1u;
-      uint32_t ccnt = 0;
-#pragma unroll
-      for (int i = 0; i < NS; ++i) ccnt += cv[i] >= T ? 1u : 0u;
-      const uint32_t cincl = group_scan<LPR>(ccnt, sub);
-      const uint32_t ctotal = group_sum<LPR>(ccnt);
-      ctotal_out = ctotal;
-      const bool ov = ctotal > (uint32_t)L.cap;
-      if (!ov) {
-        uint32_t p = cincl - ccnt;
-#pragma unroll
-        for (int i = 0; i < NS; ++i)
-          if (cv[i] >= T) cand[p++] = SL::make(cv[i], (uint32_t)(sub + LPR * i));
-        if (sub == 0) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) cand[ctotal + u] = (Key)0;
-        }
-      }
-      return ov;
-    };
-    uint32_t ctotal = 0;
-    bool coverflow;
-    if (npairs <= LPR * ((pair_count(16) + LPR - 1) / LPR))
-      coverflow = cartesian(std::integral_constant<int, (pair_count(16) + LPR - 1) / LPR>(), ctotal);
-    else if (npairs <= LPR * ((pair_count(32) + LPR - 1) / LPR))
-      coverflow = cartesian(std::integral_constant<int, (pair_count(32) + LPR - 1) / LPR>(), ctotal);
-    else
-      coverflow = cartesian(std::integral_constant<int, MAXS>(), ctotal);
-    __builtin_amdgcn_wave_barrier();
-    auto to_fin = [&](uint32_t rank, Key k) { fin[rank] = k; };
-    if (!coverflow) {
-      if (L.cap <= 8 * LPR)
-        group_rank<Key, LPR, 8>(cand, ctotal, knn, sub, to_fin);
-      else
-        group_rank<Key, LPR, MAXM>(cand, ctotal, knn, sub, to_fin);
-    }
-    __builtin_amdgcn_wave_barrier();
-    {
-      const uint64_t ov = __ballot(coverflow);
-      for (int rr = 0; rr < RPW; ++rr) {
-        if (!((ov >> (rr * LPR)) & 1ull)) continue;
+      __builtin_amdgcn_wave_barrier();  // the first half's list of a row is written and read by its own lanes
+      cartesian_rows<TIN, LPR, MAXM, MAXS>(l0, list, cand, fin, L.cap, knn, sub, true, wscr, [&](int rr) {
         const int row = w * RPW + rr;
-        const Key* l0r = (const Key*)smem + row * L.kl;
-        const Key* l1r = (const Key*)(R + L.list_off) + row * L.kl;
-        const Key top = exact_topk<Key>(
-            [&](int s) -> Key { return s < npairs ? SL::make(pair_okey(l0r, l1r, s), (uint32_t)s) : (Key)0; },
-            npairs, knn, wscr);
-        if (lane < knn) ((Key*)smem + (TM + row) * L.kl)[lane] = top;
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    // outputs: the pair's rounded sum and slot id i_0[a] * n + i_1[b]
-    if (live) {
-      for (int j = sub; j < knn; j += LPR) {
-        const Key k = fin[j];
-        const uint32_t ab = pairs[SL::key_idx(k)];
-        SL::put(out_scores, orow + j, SL::key_okey(k));
-        out_idx[orow + j] = (int64_t)SL::key_idx(l0[ab & 0xFFu]) * n + (int64_t)SL::key_idx(list[ab >> 8]);
+        return CartRow<Key>{(const Key*)smem + row * L.kl, (const Key*)(R + L.list_off) + row * L.kl,
+                            (Key*)smem + (TM + row) * L.kl};
+      });
+      // outputs: the pair's rounded sum and slot id i_0[a] * n + i_1[b]
+      if (live) {
+        for (int j = sub; j < knn; j += LPR) {
+          const Key k = fin[j];
+          const uint32_t ab = pairs[SL::key_idx(k)];
+          SL::put(out_scores, orow + j, SL::key_okey(k));
+          out_idx[orow + j] = (int64_t)SL::key_idx(l0[ab & 0xFFu]) * n + (int64_t)SL::key_idx(list[ab >> 8]);
+        }
       }
     }
   }
+}
+
+
+// C as its own kernel for 32-bit keys: the lists of row i (token, head) are
+// the low (first half) and high (second half) words of out_idx[i * knn + j];
+// the scores and slot ids replace them. A lane group of LPR lanes per row,
+// kThreads / LPR rows per workgroup.
+template <typename TIN, int LPR>
+__global__ __launch_bounds__(kThreads) void pkm_score_cartesian_kernel(int64_t rows, int n, int knn,
+                                                                      TIN* __restrict__ out_scores,
+                                                                      int64_t* __restrict__ out_idx) {
+  typedef Sel<TIN> SL;
+  typedef typename SL::Key Key;
+  static_assert(sizeof(Key) == 4, "two lists per index word");
+  constexpr int RPB = kThreads / LPR;
+  constexpr int RPW = 64 / LPR;
+  constexpr int MAXM = (2 * 64 > kCandCap * LPR / 64 ? 2 * 64 : kCandCap * LPR / 64) / LPR;
+  constexpr int MAXS = (kMaxPairs + LPR - 1) / LPR;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int cap = score_cap(knn, LPR);
+  const int cstride = cap + 4;
+  const int kl = (knn + 3) & ~3;
+  Key* lists = (Key*)smem;               // [RPB][2][kl]
+  Key* fins = lists + RPB * 2 * kl;      // [RPB][kl]
+  Key* cands = fins + RPB * kl;          // [RPB][cstride]
+  const int r = threadIdx.x / LPR;
+  const int sub = threadIdx.x & (LPR - 1);
+  const int w = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * RPB + r;
+  const bool live = row < rows;
+  const int64_t orow = row * knn;
+  Key* l0 = lists + 2 * r * kl;
+  Key* l1 = l0 + kl;
+  Key* fin = fins + r * kl;
+  for (int j = sub; j < knn; j += LPR) {
+    const uint64_t v = live ? (uint64_t)out_idx[orow + j] : 0ull;
+    l0[j] = (Key)(uint32_t)v;
+    l1[j] = (Key)(uint32_t)(v >> 32);
+  }
+  __builtin_amdgcn_wave_barrier();  // a row's lists are written and read by its own lanes
+  cartesian_rows<TIN, LPR, MAXM, MAXS>(l0, l1, cands + r * cstride, fin, cap, knn, sub, live,
+                                       cands + (w * RPW) * cstride, [&](int rr) {
+                                         const int rw = w * RPW + rr;
+                                         return CartRow<Key>{lists + 2 * rw * kl, lists + (2 * rw + 1) * kl,
+                                                             fins + rw * kl};
+                                       });
+  if (live) {
+    const uint16_t* pairs = kPairTable.ab + kPairTable.off[knn];
+    for (int j = sub; j < knn; j += LPR) {
+      const Key k = fin[j];
+      const uint32_t ab = pairs[SL::key_idx(k)];
+      SL::put(out_scores, orow + j, SL::key_okey(k));
+      out_idx[orow + j] = (int64_t)SL::key_idx(l0[ab & 0xFFu]) * n + (int64_t)SL::key_idx(l1[ab >> 8]);
+    }
+  }
+}
+
+constexpr int kCartLpr = 8;  // lanes per row of the cartesian kernel
+__host__ inline size_t cartesian_lds_bytes(int knn) {
+  const int kl = (knn + 3) & ~3;
+  return (size_t)(kThreads / kCartLpr) * (size_t)(3 * kl + score_cap(knn, kCartLpr) + 4) * 4;
+}
+
+// Dynamic LDS above 64 KiB is enabled once per device and kernel (idempotent,
+// so a race between threads only repeats the call).
+static int enable_lds(const void* fn, int bytes, std::atomic<uint64_t>& done, const char* what) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return pkm_set_error(PKM_ERR_HIP, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(done.load(std::memory_order_relaxed) & bit)) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess)
+      return pkm_set_error(PKM_ERR_HIP, "%s: hipFuncSetAttribute failed: %s", what, hipGetErrorString(e));
+    done.fetch_or(bit, std::memory_order_relaxed);
+  }
+  return PKM_OK;
 }
 
 template <typename TIN, int IDW, int TM, int KSC>
 static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
                            size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
                            int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
-  // Dynamic LDS above 64 KiB is enabled once per device (idempotent, so a
-  // race between threads only repeats the call).
   static std::atomic<uint64_t> lds_enabled{0};
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: hipGetDevice failed: %s", hipGetErrorString(e));
-  const uint64_t bit = 1ull << (dev & 63);
-  if (!(lds_enabled.load(std::memory_order_relaxed) & bit)) {
-    e = hipFuncSetAttribute((const void*)pkm_score_topk_kernel<TIN, IDW, TM, KSC>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
-    if (e != hipSuccess)
-      return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
-    lds_enabled.fetch_or(bit, std::memory_order_relaxed);
-  }
+  int rc = enable_lds((const void*)pkm_score_topk_kernel<TIN, IDW, TM, KSC>, lds_max, lds_enabled, "pkm_score_topk");
+  if (rc != PKM_OK) return rc;
   const int64_t blocks = ((Ntok + TM - 1) / TM) * H;
   hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM, KSC>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
                      (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
                      out_i2, (TIN*)out_s1, (TIN*)out_s2);
+  if constexpr (sizeof(typename Sel<TIN>::Key) == 4) {
+    // the cartesian step of the packed lists
+    static std::atomic<uint64_t> cart_lds_enabled{0};
+    const size_t cl = cartesian_lds_bytes(knn);
+    rc = enable_lds((const void*)pkm_score_cartesian_kernel<TIN, kCartLpr>, (int)cl, cart_lds_enabled,
+                    "pkm_score_topk");
+    if (rc != PKM_OK) return rc;
+    const int64_t rows = Ntok * H;
+    const int64_t cblocks = (rows + kThreads / kCartLpr - 1) / (kThreads / kCartLpr);
+    hipLaunchKernelGGL((pkm_score_cartesian_kernel<TIN, kCartLpr>), dim3((unsigned)cblocks), dim3(kThreads), cl, st,
+                       rows, n, knn, (TIN*)out_scores, out_idx);
+  }
   return PKM_OK;
 }
 
