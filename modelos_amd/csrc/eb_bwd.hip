@@ -296,6 +296,10 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restri
   for (int d = threadIdx.x; d < R; d += 256) hist[(int64_t)d * ntiles + blockIdx.x] = h[d];
 }
 
+// Stable scatter of one tile by digit. The tile is first ordered by digit in
+// LDS (per digit in item order), then written out in that order, so each
+// digit's run of the tile goes to consecutive addresses: keys first, then
+// values, through one LDS buffer.
 template <bool FIRST, int BITS>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __restrict__ idx,
                                                             const uint32_t* __restrict__ keys_in,
@@ -305,7 +309,12 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
                                                             int64_t ntiles, uint32_t* __restrict__ keys_out,
                                                             uint32_t* __restrict__ vals_out) {
   constexpr int R = 1 << BITS;
-  __shared__ uint32_t wcnt[4][R];
+  constexpr int DPT = R / 256;  // digits per thread in the digit scan
+  static_assert(R % 256 == 0, "digit count per thread");
+  __shared__ uint32_t wcnt[4][R];        // per-wave digit counts, then their starts inside the tile
+  __shared__ uint32_t gofs[R];           // per digit: global start - start inside the tile
+  __shared__ uint32_t stage[kRadixTile];  // the tile in digit order (keys, then values)
+  __shared__ uint32_t wsum[4];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   for (int d = threadIdx.x; d < R; d += 256) {
@@ -340,24 +349,69 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
     pre[i] = old + rank;
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < R; d += 256) {
-    uint32_t run = ofs[(int64_t)d * ntiles + blockIdx.x];
+  // digit starts inside the tile: exclusive scan over the digits (thread t
+  // owns digits DPT t .. DPT t + DPT - 1) of the tile's digit counts
+  uint32_t tot[DPT], mine = 0;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = threadIdx.x * DPT + j;
+    tot[j] = wcnt[0][d] + wcnt[1][d] + wcnt[2][d] + wcnt[3][d];
+    mine += tot[j];
+  }
+  uint32_t incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_up((int)incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  uint32_t run = incl - mine;
+  for (int i = 0; i < w; ++i) run += wsum[i];
+  const uint32_t nloc = wsum[0] + wsum[1] + wsum[2] + wsum[3];  // valid items of the tile
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = threadIdx.x * DPT + j;
+    gofs[d] = ofs[(int64_t)d * ntiles + blockIdx.x] - run;
+    uint32_t r2 = run;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t t = wcnt[i][d];
-      wcnt[i][d] = run;
-      run += t;
+      wcnt[i][d] = r2;
+      r2 += t;
+    }
+    run += tot[j];
+  }
+  __syncthreads();
+  uint32_t lp[kRadixItems];  // position of item i inside the tile's digit order
+#pragma unroll
+  for (int i = 0; i < kRadixItems; ++i) {
+    lp[i] = wcnt[w][(k[i] >> shift) & (R - 1)] + pre[i];
+    if (validmask & (1u << i)) stage[lp[i]] = k[i];
+  }
+  __syncthreads();
+  // keys out in digit order (consecutive positions of a digit: consecutive
+  // addresses); the destinations are kept for the values
+  uint32_t dst[kRadixItems];
+#pragma unroll
+  for (int i = 0; i < kRadixItems; ++i) {
+    const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
+    dst[i] = 0;
+    if (q < nloc) {
+      const uint32_t key = stage[q];
+      dst[i] = gofs[(key >> shift) & (R - 1)] + q;
+      keys_out[dst[i]] = key;
     }
   }
   __syncthreads();
 #pragma unroll
+  for (int i = 0; i < kRadixItems; ++i)
+    if (validmask & (1u << i)) stage[lp[i]] = v[i];
+  __syncthreads();
+#pragma unroll
   for (int i = 0; i < kRadixItems; ++i) {
-    if (validmask & (1u << i)) {
-      const uint32_t d = (k[i] >> shift) & (R - 1);
-      const uint32_t dst = wcnt[w][d] + pre[i];
-      keys_out[dst] = k[i];
-      vals_out[dst] = v[i];
-    }
+    const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
+    if (q < nloc) vals_out[dst[i]] = stage[q];
   }
 }
 
