@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
     VecTraits<T>::unpack(ld16(w + c * EPV), wv);
 #pragma unroll
     for (int e = 0; e < EPV; ++e) o[e] = wv[e] * NormIO<T>::round(xv[e] * r);
-    *(uint4*)(yr + c * EPV) = VecTraits<T>::pack(o);
+    st16_nt(yr + c * EPV, VecTraits<T>::pack(o));  // streamed out
   };
   if (MAXV > 0) {
 #pragma unroll
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_fused_kernel(const T* __restr
         o[e] = NormIO<T>::round(fd[e] * fw[e]) * r + fx[e] * k;
         pacc[i][e] += NormIO<T>::round(fd[e] * NormIO<T>::round(fx[e] * r));
       }
-      if (c < NV) *(uint4*)(dxr + c * EPV) = VecTraits<T>::pack(o);
+      if (c < NV) st16_nt(dxr + c * EPV, VecTraits<T>::pack(o));
     }
   };
   load(r0, xa, da);
