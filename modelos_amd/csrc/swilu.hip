@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void swilu_fwd_kernel(const T* __restrict__ e,
     VecTraits<T>::unpack(((const uint4*)s)[v], fs);
 #pragma unroll
     for (int k = 0; k < EPV; ++k) fh[k] = sw_fwd<T>(fe[k], fs[k]);
-    ((uint4*)h)[v] = VecTraits<T>::pack(fh);
+    st16_nt((uint4*)h + v, VecTraits<T>::pack(fh));
   }
   const int64_t i = nvec * EPV + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) {
@@ -88,8 +88,8 @@ __global__ __launch_bounds__(256) void swilu_bwd_kernel(const T* __restrict__ dh
     VecTraits<T>::unpack(((const uint4*)s)[v], fs);
 #pragma unroll
     for (int k = 0; k < EPV; ++k) sw_bwd<T>(fdh[k], fe[k], fs[k], fde[k], fds[k]);
-    ((uint4*)de)[v] = VecTraits<T>::pack(fde);
-    ((uint4*)ds)[v] = VecTraits<T>::pack(fds);
+    st16_nt((uint4*)de + v, VecTraits<T>::pack(fde));
+    st16_nt((uint4*)ds + v, VecTraits<T>::pack(fds));
   }
   const int64_t i = nvec * EPV + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) {
