@@ -5,8 +5,9 @@ and shapes (so state dicts load unchanged), reset_parameters, and its forward
 contract x [B, T, C] -> (out [B, T, output_dim], indices [B, T, heads * knn]).
 On gfx950 HIP kernels:
 
-  * get_indices: sub-key scores on MFMA, per-half top-k and the cartesian
-    top-k fused in one kernel (modelos_amd.product_keys); the backward works
+  * get_indices: sub-key scores on MFMA and the per-half top-k in one kernel,
+    the cartesian top-k in a second one for bf16 scores (in the same kernel
+    for float32) (modelos_amd.product_keys); the backward works
     from the nonzeros of the sub-score gradient (dq gathered, dK on MFMA);
   * the value read: the weighted embedding bag (xFormerEmbeddingBag);
   * the glue around them: the query RMSNorm, the score softmax, the swilu
@@ -290,8 +291,9 @@ class HashingMemory(nn.Module):
 
     def get_indices(self, query, knn):
         """(scores, indices) [bs * heads, knn]: the best knn product keys per
-        (token, head), best first (memory.py:250-289). One fused HIP kernel;
-        equal scores are ordered by the smaller sub-key position."""
+        (token, head), best first (memory.py:250-289), from the fused scoring
+        and selection kernels of pkm_score_topk; equal scores are ordered by
+        the smaller sub-key position."""
         assert query.dim() == 2 and query.size(1) == self.k_dim
         return product_key_topk(query, self.keys, self.heads, knn, "dot")
 
