@@ -1042,9 +1042,14 @@ static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H,
                      out_i2, (TIN*)out_s1, (TIN*)out_s2);
   if constexpr (sizeof(typename Sel<TIN>::Key) == 4) {
     // the cartesian step of the packed lists
+    // (the attribute is set once per device: to the device maximum, so that
+    // every knn's layout fits)
     static std::atomic<uint64_t> cart_lds_enabled{0};
     const size_t cl = cartesian_lds_bytes(knn);
-    rc = enable_lds((const void*)pkm_score_cartesian_kernel<TIN, kCartLpr>, (int)cl, cart_lds_enabled,
+    if ((int)cl > lds_max)
+      return pkm_set_error(PKM_ERR_UNSUPPORTED, "pkm_score_topk: knn %d needs %zu bytes of LDS for the cartesian step",
+                           knn, cl);
+    rc = enable_lds((const void*)pkm_score_cartesian_kernel<TIN, kCartLpr>, lds_max, cart_lds_enabled,
                     "pkm_score_topk");
     if (rc != PKM_OK) return rc;
     const int64_t rows = Ntok * H;

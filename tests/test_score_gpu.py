@@ -255,3 +255,15 @@ def test_fwpkm_drop_in(device, score_type):
     kv = k.view(m.heads, 2, m.subsize, m.k_dim // 2)[:, 0].contiguous().to(device)
     dense = m.compute_qk_scores(q[:, :, : m.k_dim // 2].contiguous().to(device), kv)
     assert_rel_close(dense.cpu(), e_s1, 1e-4, "compute_qk_scores")
+
+
+def test_bf16_knn_growing_in_one_process(device):
+    """The cartesian step's LDS grows with knn (83 KB at knn 64): a small knn
+    followed by knn 64 in the same process must both run (the kernel's LDS
+    limit is raised once, to the device maximum) and match the oracle."""
+    N, H, n, half = 24, 2, 1024, 128
+    q, k = _int_inputs(N, H, n, half, torch.bfloat16, seed=61)
+    for knn in (4, 64):
+        scores, idx, _, _, _, _ = _run(q, k, H, knn, "dot", device)
+        e_scores, e_idx, _, _, _, _ = ref.get_indices(q, k, H, knn)
+        assert torch.equal(idx, e_idx.reshape(N * H, knn)) and torch.equal(scores, e_scores.reshape(N * H, knn)), knn
