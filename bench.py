@@ -54,6 +54,16 @@ def eb_algorithmic_bytes(B, L, K, D, U, s_w=2, s_p=2, s_g=2):
     return fwd, bwd
 
 
+def eb_rows_algorithmic_bytes(B, L, K, D, U, s_w=2, s_g=2):
+    """Algorithmic HBM bytes of the backward's row-reduction kernel (after the
+    sort): each distinct row of W once (U*D*s_w), the dense weight-gradient
+    write (K*D*s_w), the upstream gradient once (B*D*s_g), 8 bytes of sorted
+    occurrence metadata per lookup (N*8), the row offsets ((K+1)*4) and the
+    float32 psw-gradients in sorted order (N*4)."""
+    N = B * L
+    return U * D * s_w + K * D * s_w + B * D * s_g + N * 8 + (K + 1) * 4 + N * 4
+
+
 def score_flops(tokens, heads, n_keys, k_dim):
     """Sub-key scoring: 2 * tokens * heads * 2 halves * n_keys * k_dim/2."""
     return 2 * tokens * heads * 2 * n_keys * (k_dim // 2)
@@ -183,18 +193,23 @@ def run_layer(args, dev):
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     timer = _lib.CallTimer()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    with timer:
-        for i in range(args.steps):
-            ev[i][0].record()
-            step()
-            ev[i][1].record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    ktimer = _lib.KernelTimer()  # single kernels of multi-kernel entry points
+    with ktimer:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with timer:
+            for i in range(args.steps):
+                ev[i][0].record()
+                step()
+                ev[i][1].record()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     step_ms = sorted(a.elapsed_time(b) for a, b in ev)[args.steps // 2]
     calls = timer.summary()
+    for kname in ktimer.KERNELS:
+        if ktimer.ms(kname):
+            calls[("kernel", kname)] = ktimer.ms(kname)
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (median event time {step_ms:.3f} ms)")
 
     L = H * knn
@@ -219,11 +234,15 @@ def run_layer(args, dev):
         if note:
             kernels[name]["note"] = note
 
+    add("pkm_score_topk_kernel (scoring + per-half top-k)", ("kernel", "score_topk"), score_flops(tokens, H, n, k),
+        "TFLOP/s", MFMA_BF16_PEAK_TFLOPS, "mfma")
     add("pkm_score_topk", ("pkm_score_topk", (tokens, H, n, k // 2)), score_flops(tokens, H, n, k), "TFLOP/s",
-        MFMA_BF16_PEAK_TFLOPS, "mfma")
+        MFMA_BF16_PEAK_TFLOPS, "mfma", "entry point: scoring + per-half top-k kernel, then the cartesian kernel")
     add("pkm_eb_fwd (values)", ("pkm_eb_fwd", (n * n, D)), a_fwd, "GB/s", HBM_PEAK_GBS, "hbm")
+    add("eb_bwd_rows64_kernel (values backward, row reduction)", ("kernel", "eb_bwd_rows"),
+        eb_rows_algorithmic_bytes(tokens, L, n * n, D, U), "GB/s", HBM_PEAK_GBS, "hbm")
     add("pkm_eb_bwd (values)", ("pkm_eb_bwd", (n * n, D)), a_bwd, "GB/s", HBM_PEAK_GBS, "hbm",
-        "sort + reduction sequence (several kernels)")
+        "entry point: sort + row reduction + psw-gradient scatter (several kernels)")
 
     def add_ms(name, entry, note):
         """Every call of one entry point, whatever its sizes."""
@@ -243,7 +262,12 @@ def run_layer(args, dev):
            "per call; per Linear one bias gradient and one sum of the weight gradient's split-K partials")
     add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
     add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
-    hip_ms = sum(v["ms"] * v["calls_per_step"] for v in kernels.values())
+    # single kernels timed inside an entry point are part of that entry's time
+    inner = ("pkm_score_topk_kernel (scoring + per-half top-k)", "eb_bwd_rows64_kernel (values backward, row reduction)")
+    for kk in inner:
+        if kk in kernels:
+            kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd (values)"
+    hip_ms = sum(v["ms"] * v["calls_per_step"] for kk, v in kernels.items() if kk not in inner)
     kernels["other (query/swilu/value GEMMs, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
 
     single = {kk: v for kk, v in kernels.items() if "bound" in v and "note" not in v}
@@ -343,33 +367,42 @@ def run_eb(args, dev):
         step()
     torch.cuda.synchronize()
     timer = _lib.CallTimer()
-    t0 = time.perf_counter()
-    with timer:
-        for _ in range(args.steps):
-            step()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ktimer = _lib.KernelTimer()  # the row-reduction kernel inside the backward entry point
+    with ktimer:
+        t0 = time.perf_counter()
+        with timer:
+            for _ in range(args.steps):
+                step()
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
     calls = timer.summary()
+    calls["rows"] = ktimer.ms("eb_bwd_rows")
 
     def med(key):
         v = sorted(calls[key])
         return v[len(v) // 2]
 
-    fwd_ms, bwd_ms = med(("pkm_eb_fwd", (K, D))), med(("pkm_eb_bwd", (K, D)))
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms)")
+    fwd_ms, bwd_ms, rows_ms = med(("pkm_eb_fwd", (K, D))), med(("pkm_eb_bwd", (K, D))), med("rows")
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms, "
+        f"row kernel {rows_ms:.3f} ms)")
     a_fwd, a_bwd = eb_algorithmic_bytes(B, L, K, D, U)
     kernels = {
         "pkm_eb_fwd (values)": {"ms": round(fwd_ms, 4), "work": a_fwd},
+        "eb_bwd_rows64_kernel (values backward, row reduction)": {
+            "ms": round(rows_ms, 4), "work": eb_rows_algorithmic_bytes(B, L, K, D, U),
+            "part_of": "pkm_eb_bwd (values)"},
         "pkm_eb_bwd (values)": {"ms": round(bwd_ms, 4), "work": a_bwd,
-                                "note": "sort + reduction sequence (several kernels)"},
+                                "note": "entry point: sort + row reduction + psw-gradient scatter (several kernels)"},
     }
     for v in kernels.values():
         v["achieved"] = round(v["work"] / (v["ms"] * 1e-3) / 1e9, 2)
         v["unit"] = "GB/s"
         v["frac"] = round(v["achieved"] / HBM_PEAK_GBS, 4)
-    dom = kernels["pkm_eb_fwd (values)"]
-    roofline = {"bound": "hbm", "kernel": "pkm_eb_fwd (values)", "achieved": dom["achieved"], "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": dom["frac"], "traffic": load_traffic().get("eb:pkm_eb_fwd (values)")}
+    dom_name = max(("pkm_eb_fwd (values)", "eb_bwd_rows64_kernel (values backward, row reduction)"),
+                   key=lambda kk: kernels[kk]["ms"])
+    dom = kernels[dom_name]
+    roofline = {"bound": "hbm", "kernel": dom_name, "achieved": dom["achieved"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": dom["frac"], "traffic": load_traffic().get("eb:" + dom_name)}
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")

@@ -306,6 +306,28 @@ int pkm_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const flo
 int pkm_count_invalid_indices(const int64_t* indices, int64_t n, int64_t num_rows,
                               int64_t* count_out, void* stream);
 
+/*
+ * Kernel timing for measurement tools. No counterpart in the reference (it
+ * has no FFI); it lets a benchmark time one kernel of a multi-kernel entry
+ * point on the stream the kernel runs on.
+ * pkm_kernel_timing_begin() turns timing on for the process (every thread:
+ * backward passes launch from the autograd engine's thread) and drops earlier
+ * records. While it is on, these launches are bracketed by a pair of HIP
+ * events recorded on the call's stream (at most 4096 records):
+ *   "eb_fwd"       the gather kernel of pkm_eb_fwd;
+ *   "eb_bwd2"      the kernel of pkm_eb_bwd2;
+ *   "eb_bwd_rows"  the row-reduction kernel of pkm_eb_bwd (after its sort);
+ *   "score_topk"   the scoring + per-half top-k kernel of pkm_score_topk
+ *                  (not its cartesian kernel).
+ * pkm_kernel_timing_read() waits for the records named `kernel` and writes the
+ * milliseconds of the first `cap` of them, in call order, to ms_out; *count_out
+ * gets their number. pkm_kernel_timing_end() turns timing off and releases the
+ * records. Timing is for measurement: each record creates two events.
+ */
+int pkm_kernel_timing_begin(void);
+int pkm_kernel_timing_read(const char* kernel, float* ms_out, int64_t cap, int64_t* count_out);
+int pkm_kernel_timing_end(void);
+
 #ifdef __cplusplus
 }
 #endif

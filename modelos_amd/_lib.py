@@ -104,6 +104,9 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_void_p, c_int64, c_int64, c_int, c_float, c_void_p, c_void_p, c_void_p],
     ),
+    "pkm_kernel_timing_begin": (c_int, []),
+    "pkm_kernel_timing_read": (c_int, [c_char_p, c_void_p, c_int64, c_void_p]),
+    "pkm_kernel_timing_end": (c_int, []),
     "pkm_rmsnorm_bwd_workspace_size": (c_size_t, [c_int64, c_int64]),
     "pkm_rmsnorm_bwd": (
         c_int,
@@ -191,6 +194,45 @@ class CallTimer:
         for key, a, b in self.events:
             out.setdefault(key, []).append(a.elapsed_time(b))
         return out
+
+
+class KernelTimer:
+    """Times single kernels inside multi-kernel entry points with the
+    library's own event pairs, recorded on the stream each kernel runs on
+    (pkm_kernel_timing_*; process-wide, so backward passes on the autograd
+    thread are timed too). Use as a context manager; on exit it synchronises,
+    keeps the durations and turns timing off. `ms(kernel)` returns the
+    durations of one kernel name in call order."""
+
+    KERNELS = ("eb_fwd", "eb_bwd2", "eb_bwd_rows", "score_topk")
+
+    def __init__(self):
+        self.records: dict = {}
+
+    def __enter__(self):
+        call("pkm_kernel_timing_begin")
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        try:
+            for kernel in self.KERNELS:
+                count = c_int64(0)
+                name = kernel.encode()
+                status = lib.pkm_kernel_timing_read(name, None, 0, ctypes.byref(count))
+                buf = (c_float * max(count.value, 1))()
+                if status == 0 and count.value:
+                    status = lib.pkm_kernel_timing_read(name, buf, count.value, ctypes.byref(count))
+                if status != 0:
+                    raise PkmError("pkm_kernel_timing_read", status,
+                                   lib.pkm_last_error_string().decode(errors="replace"))
+                self.records[kernel] = list(buf)[: count.value]
+        finally:
+            lib.pkm_kernel_timing_end()
+        return False
+
+    def ms(self, kernel: str) -> list:
+        return self.records.get(kernel, [])
 
 
 _timer: CallTimer | None = None

@@ -937,6 +937,7 @@ static void launch_rows64(const void* W, int64_t K, int64_t D, int want_dot, con
                           const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                           float* dsorted, uint32_t dummy_slot, hipStream_t st) {
   const unsigned rb = (unsigned)cdiv(K, 4 * 64);
+  KernelSpan span("eb_bwd_rows", st);
   hipLaunchKernelGGL((eb_bwd_rows64_kernel<TW, VPL, U>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, want_dot,
                      (const TW*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW, dsorted,
                      dummy_slot);
@@ -998,6 +999,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     const int rows_per_group = 4;
     const int64_t groups = cdiv(K, rows_per_group);
     const unsigned rb = (unsigned)cdiv(groups, groups_per_block);
+    KernelSpan span("eb_bwd_rows", st);
     hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, LPG, VPL>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, psw, pdt,
                        (const TW*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW,
                        gpsw);

@@ -198,6 +198,7 @@ static void launch_fwd(const void* W, int64_t K, int64_t D, const int64_t* idx, 
   const int64_t tasks = B * S;
   const int64_t per_block = 4 * GPW;
   const unsigned blocks = (unsigned)((tasks + per_block - 1) / per_block);
+  KernelSpan span(DOT ? "eb_bwd2" : "eb_fwd", stream);
   hipLaunchKernelGGL((eb_fwd_kernel<TW, LPG, VPL, DOT>), dim3(blocks), dim3(256), 0, stream, (const TW*)W, K, D,
                      idx, psw, pdt, B, L, S, (TW*)out, (const TW*)g, dot_out, ddt);
 }

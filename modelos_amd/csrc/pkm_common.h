@@ -239,6 +239,21 @@ bool choose_group_cfg(int64_t D, int epv, bool single_slice, GroupCfg* c);
 int pkm_set_error(int code, const char* fmt, ...);
 int pkm_check_launch(const char* what);
 
+// Kernel timing for measurement tools (pkm_kernel_timing_begin / _read /
+// _end, defined in capi.hip): while timing is on (process-wide), a
+// KernelSpan records a HIP event on its stream when it is constructed and
+// another when it goes out of scope, so the pair brackets the launches made in
+// its scope. Off (the default), it does nothing.
+struct KernelSpan {
+  KernelSpan(const char* name, hipStream_t st);
+  ~KernelSpan();
+  KernelSpan(const KernelSpan&) = delete;
+  KernelSpan& operator=(const KernelSpan&) = delete;
+  long slot;            // record index, -1 when timing is off
+  uint64_t generation;  // of the record set the slot belongs to
+  hipStream_t stream;
+};
+
 #define PKM_REQUIRE(cond, code, ...)             \
   do {                                           \
     if (!(cond)) return pkm_set_error((code), __VA_ARGS__); \

@@ -1037,9 +1037,12 @@ static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H,
   int rc = enable_lds((const void*)pkm_score_topk_kernel<TIN, IDW, TM, KSC>, lds_max, lds_enabled, "pkm_score_topk");
   if (rc != PKM_OK) return rc;
   const int64_t blocks = ((Ntok + TM - 1) / TM) * H;
-  hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM, KSC>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
-                     (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
-                     out_i2, (TIN*)out_s1, (TIN*)out_s2);
+  {
+    KernelSpan span("score_topk", st);
+    hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM, KSC>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
+                       (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
+                       out_i2, (TIN*)out_s1, (TIN*)out_s2);
+  }
   if constexpr (sizeof(typename Sel<TIN>::Key) == 4) {
     // the cartesian step of the packed lists
     // (the attribute is set once per device: to the device maximum, so that
