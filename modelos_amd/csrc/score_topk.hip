@@ -615,12 +615,34 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
   for (int hc = 0; hc < 2; ++hc) {
     const TIN* Kc = Kt + (int64_t)(2 * h + hc) * n * half;
     // ---- A0: stage the query half [TM][half] (zeros past the last token)
-    for (int i = threadIdx.x; i < TM * CH; i += kThreads) {
-      const int q = i / CH, c = i - (i / CH) * CH;
-      const int64_t tq = t0 + q;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (tq < Ntok) v = ld16(Q + (tq * H + h) * kdim + hc * half + c * EPC);
-      QS[((c >> 2) * TM + q) * 4 + ((c & 3) ^ ((q >> 2) & 3))] = v;
+    if constexpr (KSC > 0 && (TM * 4 * KSC) % kThreads == 0) {
+      // compile-time trip count (CH = 4 KSC chunks per row): every load is
+      // in flight before the first store
+      constexpr int CHC = 4 * KSC;
+      constexpr int NI = TM * CHC / kThreads;
+      uint4 v[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int i = (int)threadIdx.x + j * kThreads;
+        const int q = i / CHC, c = i % CHC;
+        const int64_t tq = t0 + q;
+        v[j] = make_uint4(0u, 0u, 0u, 0u);
+        if (tq < Ntok) v[j] = ld16(Q + (tq * H + h) * kdim + hc * half + c * EPC);
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int i = (int)threadIdx.x + j * kThreads;
+        const int q = i / CHC, c = i % CHC;
+        QS[((c >> 2) * TM + q) * 4 + ((c & 3) ^ ((q >> 2) & 3))] = v[j];
+      }
+    } else {
+      for (int i = threadIdx.x; i < TM * CH; i += kThreads) {
+        const int q = i / CH, c = i - (i / CH) * CH;
+        const int64_t tq = t0 + q;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (tq < Ntok) v = ld16(Q + (tq * H + h) * kdim + hc * half + c * EPC);
+        QS[((c >> 2) * TM + q) * 4 + ((c & 3) ^ ((q >> 2) & 3))] = v;
+      }
     }
     __syncthreads();
 
