@@ -1006,10 +1006,23 @@ __global__ __launch_bounds__(kThreads) void pkm_score_cartesian_kernel(int64_t r
   Key* l0 = lists + 2 * r * kl;
   Key* l1 = l0 + kl;
   Key* fin = fins + r * kl;
-  for (int j = sub; j < knn; j += LPR) {
-    const uint64_t v = live ? (uint64_t)out_idx[orow + j] : 0ull;
-    l0[j] = (Key)(uint32_t)v;
-    l1[j] = (Key)(uint32_t)(v >> 32);
+  {
+    // every load (knn <= 64) is in flight before the first store
+    constexpr int MAXJ = (64 + LPR - 1) / LPR;
+    uint64_t v[MAXJ];
+#pragma unroll
+    for (int i = 0; i < MAXJ; ++i) {
+      const int j = sub + LPR * i;
+      v[i] = (live && j < knn) ? (uint64_t)out_idx[orow + j] : 0ull;
+    }
+#pragma unroll
+    for (int i = 0; i < MAXJ; ++i) {
+      const int j = sub + LPR * i;
+      if (j < knn) {
+        l0[j] = (Key)(uint32_t)v[i];
+        l1[j] = (Key)(uint32_t)(v[i] >> 32);
+      }
+    }
   }
   __builtin_amdgcn_wave_barrier();  // a row's lists are written and read by its own lanes
   cartesian_rows<TIN, LPR, MAXM, MAXS>(l0, l1, cands + r * cstride, fin, cap, knn, sub, live,
