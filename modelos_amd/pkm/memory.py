@@ -32,7 +32,7 @@ from torch.nn import functional as F
 
 from .. import _lib
 from ..embedding_bag import _aligned
-from ..product_keys import product_key_topk, score_softmax
+from ..product_keys import check_supported, product_key_topk, score_softmax
 from ..rmsnorm import QueryRMSNorm
 from ..swilu import swilu_gate
 from .colwise_embedding_bag import xFormerEmbeddingBag
@@ -53,21 +53,34 @@ class _Linear(torch.autograd.Function):
     """F.linear with the same gradients as nn.Linear's autograd, the weight
     gradient g^T x of a 2-D bf16/fp16 input on the GPU formed as a split-K
     batched product (float32 partials, summed in split order, rounded once):
-    the plain product has only (out/256)(in/256) output tiles for K = rows."""
+    the plain product has only (out/256)(in/256) output tiles for K = rows.
+
+    Under torch.autocast the operands are cast to the autocast dtype as
+    autocast casts F.linear's, the products run in that dtype, and each
+    gradient is returned in its own input's dtype (fp32 master weights get
+    fp32 gradients), as nn.Linear's autograd does."""
 
     @staticmethod
     def forward(ctx, x, weight, bias):
+        ctx.dtypes = (x.dtype, weight.dtype, bias.dtype if bias is not None else None)
+        dev = x.device.type
+        if torch.is_autocast_enabled(dev):
+            dt = torch.get_autocast_dtype(dev)
+            x, weight = x.to(dt), weight.to(dt)
+            bias = bias.to(dt) if bias is not None else None
         ctx.save_for_backward(x, weight)
         ctx.has_bias = bias is not None
-        return F.linear(x, weight, bias)
+        with torch.autocast(dev, enabled=False):
+            return F.linear(x, weight, bias)
 
     @staticmethod
     def backward(ctx, g):
         x, weight = ctx.saved_tensors
-        g = g.contiguous()
+        x_dt, w_dt, b_dt = ctx.dtypes
+        g = g.to(x.dtype).contiguous()
         gx = gw = gb = None
         if ctx.needs_input_grad[0]:
-            gx = g @ weight
+            gx = (g @ weight).to(x_dt)
         if ctx.needs_input_grad[1]:
             rows, (out_f, in_f) = x.shape[0], weight.shape
             s = 1
@@ -79,8 +92,9 @@ class _Linear(torch.autograd.Function):
                 gw = _column_sum(part.view(s, out_f * in_f), weight.dtype).view(out_f, in_f)
             else:
                 gw = g.t() @ x
+            gw = gw.to(w_dt)
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            gb = _column_sum(g)
+            gb = _column_sum(g).to(b_dt)
         return gx, gw, gb
 
 
@@ -175,6 +189,8 @@ class HashingMemory(nn.Module):
                 "estimations in the BatchNorm layer."
             )
         assert not (mem_query_batchnorm and mem_query_rmsnorm), "Cannot use both batchnorm and rmsnorm"
+        value_width = None if peer_variant else (mem_v_dim if mem_v_dim > 0 else output_dim)
+        check_supported(mem_n_keys, mem_k_dim, mem_knn, value_width, "HashingMemory")
         super().__init__()
         self.use_peer_variant = peer_variant
         self.input_dim = input_dim
@@ -283,10 +299,9 @@ class HashingMemory(nn.Module):
             v = self.values_v(indices)
             output = torch.bmm(x.unsqueeze(1), v).squeeze(1)
 
-        output = F.dropout(output, p=self.value_dropout, training=self.training)
-        output = output.view(B, T, self.v_dim)
+        output = F.dropout(output, p=self.value_dropout, training=self.training)  # [bs, output width]
         if self.gating:
-            output = F.sigmoid(self.gating(input)).view(B, T, 1) * output
+            output = F.sigmoid(_linear(self.gating, input)) * output
         return output.view(B, T, -1), indices.view(B, T, -1)
 
     def get_indices(self, query, knn):

@@ -1,7 +1,8 @@
 """Writes golden vectors of the reference's HashingMemory (pkm/memory.py) on the CPU.
 
 Run in a checkout that has the reference at REFERENCE (default
-/root/reference):  python tests/golden/make_pkm_layer_golden.py
+/root/reference):  python tests/golden/make_pkm_layer_golden.py [case ...]
+(all cases when none is named)
 
 The reference module is imported only here, on the CPU, to pin the one
 thing no closed form covers: the composition of its forward (query network,
@@ -33,6 +34,9 @@ CASES = {
     # BatchNorm query in train mode, 4 heads (the CPU parity configuration's choices, smaller)
     "batchnorm": dict(input_dim=48, output_dim=32, mem_k_dim=128, mem_heads=4, mem_knn=16, mem_n_keys=64,
                       mem_query_rmsnorm=False, mem_query_batchnorm=True),
+    # a value width different from the output width (the model's pkm_v_dim 512 vs hidden 1024, smaller)
+    "vdim": dict(input_dim=64, output_dim=32, mem_k_dim=64, mem_heads=2, mem_knn=8, mem_n_keys=64, mem_v_dim=16,
+                 mem_query_rmsnorm=True, mem_query_batchnorm=False),
 }
 BATCH, SEQ = 2, 12
 
@@ -45,7 +49,9 @@ def main():
     sys.path.insert(0, REFERENCE)
     from pkm.memory import HashingMemory  # noqa: E402  (reference, CPU only)
 
-    for name, kw in CASES.items():
+    names = sys.argv[1:] or list(CASES)
+    for name in names:
+        kw = CASES[name]
         torch.manual_seed(0)
         mem = HashingMemory(**kw)
         g = torch.Generator().manual_seed(1234)
@@ -86,7 +92,8 @@ def main():
                 rec["grad." + pname] = p.grad.clone()
         rec["sha256.x"] = torch.tensor(list(bytes.fromhex(sha(rec["x"]))), dtype=torch.uint8)
         rec["config"] = torch.tensor([kw["input_dim"], kw["output_dim"], kw["mem_k_dim"], kw["mem_heads"],
-                                      kw["mem_knn"], kw["mem_n_keys"], int(kw["mem_query_batchnorm"])])
+                                      kw["mem_knn"], kw["mem_n_keys"], int(kw["mem_query_batchnorm"]),
+                                      kw.get("mem_v_dim", -1)])
         path = OUT / f"pkm_layer_{name}.pt"
         torch.save(rec, path)
         print(f"wrote {path} ({path.stat().st_size} bytes)")

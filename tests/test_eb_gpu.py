@@ -318,8 +318,10 @@ def test_backward_large_gradient_parity(B, L, K, D, dtype, device):
     idx = _hot_indices(B, L, K, seed=32 + D)
     gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
     eW, ep = ref.eb_backward(idx, W, p, g)
-    assert_rel_close(gW, eW, REL_TOL[dtype], "grad_weight")
-    assert_rel_close(gp, ep, REL_TOL[dtype], "grad_psw")
+    # hot rows sum thousands of terms: elementwise against the sums of |terms|
+    cW, cp = ref.eb_backward(idx, W.abs(), p.abs(), g.abs())
+    assert_rel_close(gW, eW, REL_TOL[dtype], "grad_weight", cond=cW)
+    assert_rel_close(gp, ep, REL_TOL[dtype], "grad_psw", cond=cp)
     assert (gp.cpu()[idx < 0] == 0).all()
     gW2, gp2 = eb.eb_backward(*_dev(idx, W, p, g, device=device))
     assert torch.equal(gW, gW2) and torch.equal(gp, gp2)

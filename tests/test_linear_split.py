@@ -90,3 +90,27 @@ def test_column_sum_no_rows(device):
 
     g = torch.zeros((0, 64), device=device, dtype=torch.bfloat16)
     assert not bool(_column_sum(g).any())
+
+
+def test_matches_nn_linear_under_autocast_cpu():
+    """fp32 master weights under autocast(bf16): the product runs in bf16 and
+    every gradient comes back in its input's dtype, exactly as nn.Linear's."""
+    torch.manual_seed(0)
+    layer = nn.Linear(64, 48)
+    x = torch.randn((40, 64), generator=gen(3))
+    g = torch.randn((40, 48), generator=gen(4))
+
+    def run(fn):
+        layer.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            y = fn(layer, xx)
+        y.float().backward(g)
+        return y.detach(), xx.grad, layer.weight.grad, layer.bias.grad
+
+    a = run(lambda m, v: m(v))
+    b = run(_linear)
+    assert b[0].dtype == torch.bfloat16
+    assert [t.dtype for t in b[1:]] == [torch.float32] * 3
+    for u, v in zip(a, b):
+        assert u.dtype == v.dtype and torch.equal(u, v)
