@@ -89,6 +89,26 @@ int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dty
                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * pkm_eb_bwd without a workspace argument: the same kernels and results
+ * (bit-identical outputs), with their workspace in a fixed scratch array of
+ * 64 MiB that the library holds on each GPU it runs on until the process ends.
+ * It allocates nothing (no hipMalloc / hipFree, no allocating library call).
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Limits:
+ *   - sizes whose pkm_eb_bwd_workspace_size() exceeds 64 MiB are rejected with
+ *     PKM_ERR_WORKSPACE (e.g. a 2^18 x 1024 table with 8192 x 64 lookups
+ *     needs 31.5 MiB, a 2^20 x 1024 table with 2048 x 256 lookups 34.5 MiB);
+ *   - the device current on the calling thread must be the stream's device;
+ *   - every call on a GPU shares that GPU's array: calls that overlap on one
+ *     GPU (other streams, other threads) race, so serialise them.
+ */
+int pkm_eb_bwd_noalloc(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                       const int64_t* indices, const void* psw, int psw_dtype,
+                       const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
+                       void* grad_weight, void* grad_psw, void* stream);
+
+/*
  * Double backward of the embedding bag: the VJP of
  *   grad_weight = EBbwd(indices, a, grad_out)
  * with respect to grad_out and a, given gbar = dLoss/d(grad_weight):

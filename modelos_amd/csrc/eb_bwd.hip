@@ -34,6 +34,8 @@
 // HBM traffic: W is read once per distinct row, gW written once per row, the
 // upstream gradient g (B x D, tens of MB) is re-read per occurrence from
 // L2 / Infinity Cache.
+#include <mutex>
+
 #include "pkm_common.h"
 
 namespace pkm {
@@ -1134,4 +1136,69 @@ extern "C" int pkm_count_invalid_indices(const int64_t* indices, int64_t n, int6
     hipLaunchKernelGGL(count_invalid_kernel, dim3(grid_for(n, 256, 4096)), dim3(256), 0, st, indices, n, num_rows,
                        (unsigned long long*)count_out);
   return pkm_check_launch("pkm_count_invalid_indices");
+}
+
+// ---------------------------------------------------------------------------
+// pkm_eb_bwd_noalloc: pkm_eb_bwd on a fixed scratch array instead of a
+// caller-provided workspace, for callers that cannot allocate.
+// ---------------------------------------------------------------------------
+namespace pkm {
+
+constexpr size_t kNoallocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxScratchDevices = 64;
+
+// One copy per GPU the library runs on, held until the process ends. Host
+// code never passes `scratch` itself to a kernel (on the host the name is only
+// a stand-in for the symbol): it uses the per-device address that
+// hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the calling thread's current device, looked
+// up once per device (with that device current) and kept.
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  PKM_REQUIRE(e == hipSuccess, PKM_ERR_HIP, "pkm_eb_bwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  PKM_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd_noalloc: device %d beyond the %d this library keeps scratch addresses for", dev,
+              kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    PKM_REQUIRE(e == hipSuccess && p != nullptr, PKM_ERR_HIP,
+                "pkm_eb_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PKM_OK;
+}
+
+}  // namespace pkm
+
+extern "C" int pkm_eb_bwd_noalloc(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                                  const int64_t* indices, const void* psw, int psw_dtype, const void* grad_out,
+                                  int grad_dtype, int64_t bags, int64_t bag_size, void* grad_weight, void* grad_psw,
+                                  void* stream) {
+  PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd_noalloc: bad sizes num_rows=%lld dim=%lld bags=%lld bag_size=%lld", (long long)num_rows,
+              (long long)dim, (long long)bags, (long long)bag_size);
+  PKM_REQUIRE(bags * bag_size < ((int64_t)1 << 31) && num_rows < ((int64_t)1 << 31) - 1, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd_noalloc: bags*bag_size=%lld must be < 2^31 and num_rows=%lld < 2^31-1",
+              (long long)(bags * bag_size), (long long)num_rows);
+  const size_t need = bwd_layout(num_rows, dim, bags * bag_size).total;
+  PKM_REQUIRE(need <= kNoallocScratchBytes, PKM_ERR_WORKSPACE,
+              "pkm_eb_bwd_noalloc: these sizes (num_rows=%lld dim=%lld bags=%lld bag_size=%lld) need %zu bytes of "
+              "scratch, more than the fixed %zu bytes; use pkm_eb_bwd with a workspace",
+              (long long)num_rows, (long long)dim, (long long)bags, (long long)bag_size, need,
+              kNoallocScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != PKM_OK) return rc;
+  return pkm_eb_bwd(weight, num_rows, dim, weight_dtype, indices, psw, psw_dtype, grad_out, grad_dtype, bags,
+                    bag_size, grad_weight, grad_psw, ws, kNoallocScratchBytes, stream);
 }
