@@ -1,38 +1,57 @@
-"""Drop-in product-key retrieval for the reference's fast-weight PKM
-(fwpkm/fwpkm.py:853-934).
+"""Drop-in for the reference's fwpkm/fwpkm.py: the fast-weight product-key memory.
 
-FastWeightProductKeyMemory reads the attributes heads, k_dim, topk, subsize
-and qk_score_type ("dot_product" or "idw") in compute_qk_scores/get_indices.
-ProductKeyIndexMixin provides both methods with the reference's signatures
-and return values on the fused HIP kernel (scores, per-half top-k, cartesian
-top-k in one launch), differentiable w.r.t. query and keys, including the
-full sub-score matrices the address loss uses (fwpkm.py:117-147, 250-253).
-A class using it replaces the two methods, e.g.
+FastWeightProductKeyMemory keeps the reference's constructor arguments,
+parameter names and shapes (`keys` [2 * heads * n_subkeys, k_dim / 2],
+`values` [n_subkeys^2, v_dim]), its methods and their return conventions
+(fwpkm.py:22-934), so modeling code calls it unchanged. The in-context
+update runs on gfx950 HIP kernels:
 
-    class FastWeightProductKeyMemory(ProductKeyIndexMixin, reference.FastWeightProductKeyMemory): ...
+  * get_indices: sub-key scores (dot product or idw), per-half top-k and the
+    cartesian top-k in one fused kernel, which also writes the full sub-score
+    matrices the marginal-entropy address loss reads; differentiable w.r.t.
+    query and keys, including through those matrices (product_keys);
+  * score_transform: the softmax over heads x top-k on one kernel each way;
+  * retrieve_values: the weighted bag over the fast values (forward gather,
+    deterministic first-order backward, and the fused double backward the
+    outer loss takes through the inner gradient step);
+  * update_fw: the values' SGD step (sample-count scaling, division by the
+    slot access counts, optional clipping, weight decay) in one pass over the
+    table, differentiable for the outer loss.
 
-FusedValueUpdateMixin.update_fw is the reference's update_fw (fwpkm.py:274-367)
-with the values' step (gradient scaling by the sample count, division by the
-bincount of the indices, optional clipping, SGD with weight decay) in one
-kernel pass over the [size, v_dim] table instead of about a dozen elementwise
-passes; it stays differentiable for the outer loss (create_graph).
+The losses (mean squared error, marginal entropy of the sub-key addressing)
+and the chunk loop are torch code around these kernels, with the reference's
+semantics, including its quirks: the output of a chunk is read before that
+chunk's update; the streaming path normalises the update with the forward
+chunk's indices and counts samples as B * chunk length; addr_loss=None with
+mem_grad_to_values_only=True fails in the keys' update (fwpkm.py:266-272,
+298-318).
 
-The rest of the module (value retrieval through
-modelos_amd.fwpkm.xformer_embeddingbag_grad_wrapper) is ordinary torch code
-around these drop-ins.
+There is no CPU path: the kernels raise on CPU tensors.
 """
 from __future__ import annotations
 
-from collections import OrderedDict
+from collections import OrderedDict, defaultdict
+from logging import getLogger
+import math
 from typing import Optional
 
 import torch
+from torch import nn
+from torch.nn import functional as F
 
 from .. import _lib
 from ..embedding_bag import _aligned, _require_device
-from ..product_keys import product_key_topk
+from ..product_keys import check_supported, product_key_topk, score_softmax
+from .xformer_embeddingbag_grad_wrapper import xformers_embedding_bag
+
+logger = getLogger()
 
 SCORE_TYPES = {"dot_product": "dot", "idw": "idw"}
+
+
+def l2norm(x: torch.FloatTensor, dim: int = -1, eps: float = 1e-6):
+    """x / sqrt(sum(x^2) + eps) along `dim` (fwpkm.py:16-19; the FLA library's l2norm)."""
+    return x * torch.rsqrt((x * x).sum(dim=dim, keepdim=True) + eps)
 
 
 def _score_type(name: str) -> str:
@@ -70,17 +89,6 @@ def compute_qk_scores(q: torch.Tensor, k: torch.Tensor, qk_score_type: str = "do
         return dots.permute(1, 0, 2)
     d2 = (qh * qh).sum(-1, keepdim=True) + (k * k).sum(-1)[:, None, :] - 2.0 * dots
     return (-torch.log(1e-3 + d2.clamp_min(0.0))).permute(1, 0, 2)
-
-
-class ProductKeyIndexMixin:
-    """compute_qk_scores / get_indices of FastWeightProductKeyMemory on the
-    HIP kernels (needs self.heads, self.k_dim, self.topk, self.qk_score_type)."""
-
-    def compute_qk_scores(self, q, k):
-        return compute_qk_scores(q, k, self.qk_score_type)
-
-    def get_indices(self, query, keys):
-        return get_indices(query, keys, self.heads, self.k_dim, self.topk, self.qk_score_type)
 
 
 class _SgdValueUpdate(torch.autograd.Function):
@@ -139,31 +147,196 @@ def sgd_value_update(p: torch.Tensor, g: torch.Tensor, indices: torch.Tensor, sc
     return _SgdValueUpdate.apply(p, g, counts, scale, lr, weight_decay, grad_clip)
 
 
-class FusedValueUpdateMixin:
-    """update_fw of FastWeightProductKeyMemory (fwpkm.py:274-367) with the
-    values' step on pkm_fw_sgd_update; the gradients are formed as the
-    reference forms them, and every other parameter takes the reference's
-    update_fw_param."""
+def _chunks(T: int, first: int, size: int):
+    """[(start, end)]: the first chunk ends at min(first, T), the rest are
+    `size` long (the last one shorter)."""
+    first = min(first, T)
+    bounds = [(0, first)]
+    bounds += [(s, min(s + size, T)) for s in range(first, T, size)]
+    return bounds
+
+
+def _sl(t: Optional[torch.Tensor], a: int, b: int) -> Optional[torch.Tensor]:
+    return t[:, a:b].contiguous() if t is not None else None
+
+
+class FastWeightProductKeyMemory(nn.Module):
+    """Fast-weight product-key memory (fwpkm/fwpkm.py:22-934): product-key
+    retrieval over `keys` / `values` that are updated in context, chunk by
+    chunk, by one SGD step on a memorisation loss (and an addressing loss on
+    the keys); the outer loss differentiates through those steps."""
+
+    def __init__(
+        self,
+        mem_k_dim=512,
+        mem_v_dim=512,
+        mem_heads=1,
+        mem_topk=8,
+        mem_n_subkeys=512,
+        lookahead=1,
+        qk_score_type="idw",
+        score_nonlinear="softmax",
+        score_temperature=1.0,
+        optimizer_type="sgd",
+        learning_rate=1.0,
+        weight_decay=0.0,
+        loss_type="mse",
+        mem_grad_to_values_only=True,
+        grad_clip=False,
+        addr_loss="me",
+        addr_loss_weight=1.0,
+        fp32_fw=True,
+    ):
+        assert mem_k_dim >= 2
+        assert mem_k_dim % 2 == 0
+        check_supported(mem_n_subkeys, mem_k_dim, mem_topk, mem_v_dim, "FastWeightProductKeyMemory")
+        super().__init__()
+        self.subsize = mem_n_subkeys
+        self.size = mem_n_subkeys**2
+        self.k_dim = mem_k_dim
+        self.v_dim = mem_v_dim
+        self.heads = mem_heads
+        self.topk = mem_topk
+        self.lookahead = lookahead
+        self.qk_score_type = qk_score_type
+        self.score_nonlinear = score_nonlinear
+        self.score_temperature = score_temperature
+        self.optimizer_type = optimizer_type
+        self.learning_rate = learning_rate
+        self.weight_decay = weight_decay
+        self.loss_type = loss_type
+        self.mem_grad_to_values_only = mem_grad_to_values_only
+        self.grad_clip = grad_clip
+        self.addr_loss = addr_loss
+        self.addr_loss_weight = addr_loss_weight
+        self.fp32_fw = fp32_fw
+        # slot observation log (write_ob_log), off unless ob_mode is set
+        self.ob_mode = None
+        self.ob_idx2log = defaultdict(list)
+        # key (h, c, i) is row (2h + c) * subsize + i; value slot i1 * subsize + i2
+        self.keys = nn.Parameter(torch.zeros(2 * self.heads * self.subsize, self.k_dim // 2))
+        self.values = nn.Parameter(torch.zeros(self.size, self.v_dim))
+
+    def reset_parameters(self):
+        """fwpkm.py:90-95: keys U(+-1/sqrt(k_dim)), values N(0, v_dim^-1/2)."""
+        bound = 1 / math.sqrt(self.k_dim)
+        nn.init.uniform_(self.keys, a=-bound, b=bound)
+        nn.init.normal_(self.values, mean=0, std=self.v_dim**-0.5)
+
+    def get_fw_named_params(self):
+        """The fast weights an update chain starts from (float32 copies with
+        fp32_fw; for float32 parameters, the parameters themselves)."""
+        return OrderedDict((n, p.float() if self.fp32_fw else p) for n, p in self.named_parameters())
+
+    # ---- retrieval ------------------------------------------------------------------------
+
+    def compute_qk_scores(self, q, k):
+        return compute_qk_scores(q, k, self.qk_score_type)
+
+    def get_indices(self, query: torch.Tensor, keys: torch.Tensor):
+        """(scores, indices, topk_indices1, topk_indices2 [BT, heads, topk],
+        scores1, scores2 [BT, heads, subsize]) (fwpkm.py:871-934)."""
+        return get_indices(query, keys, self.heads, self.k_dim, self.topk, self.qk_score_type)
+
+    def score_transform(self, scores):
+        """softmax / silu / relu of scores / temperature over the last dim
+        (heads x topk jointly), in the scores' dtype (fwpkm.py:105-115)."""
+        scores = scores / self.score_temperature
+        if self.score_nonlinear == "softmax":
+            return score_softmax(scores)
+        if self.score_nonlinear == "silu":
+            return F.silu(scores).type_as(scores)
+        if self.score_nonlinear == "relu":
+            return F.relu(scores).type_as(scores)
+        raise NotImplementedError(f"Non-linear {self.score_nonlinear} not implemented for scores.")
+
+    def retrieve_values(self, query: torch.Tensor, fw_named_params: OrderedDict):
+        """query [B, T, heads * k_dim] -> dict of the retrieved values
+        [B * T, v_dim] (key "retireved_values", spelled as the reference
+        spells it), the top-k scores, their transform, the indices, the
+        per-half indices and the full sub-score matrices (fwpkm.py:149-198)."""
+        B, T = query.shape[:2]
+        scores, indices, i1, i2, s1, s2 = self.get_indices(query.view(B * T, self.heads, self.k_dim),
+                                                           fw_named_params["keys"])
+        normed = self.score_transform(scores.view(B * T, self.heads * self.topk))
+        vals = xformers_embedding_bag(indices=indices.view(B * T, self.heads * self.topk),
+                                      weight=fw_named_params["values"], per_sample_weights=normed)
+        return {
+            "retireved_values": vals,
+            "scores": scores,
+            "normed_scores": normed,
+            "indices": indices,
+            "sub_indices1": i1,
+            "sub_indices2": i2,
+            "all_sub_scores1": s1,
+            "all_sub_scores2": s2,
+        }
+
+    # ---- losses -----------------------------------------------------------------------------
+
+    def compute_marginal_entropy(self, M, epsilon=1e-8):
+        """Entropy of the batch-mean softmax over each row's top-k logits of M
+        [N, K] (the rest masked to -inf) (fwpkm.py:117-147)."""
+        if self.addr_loss_weight == 0.0:
+            return torch.tensor(0.0, device=M.device, dtype=M.dtype)
+        kth = torch.topk(M, self.topk, dim=1)[0][:, -1:]
+        masked = torch.where(M >= kth, M, torch.full_like(M, float("-inf")))
+        p_bar = F.softmax(masked.float(), dim=1).mean(dim=0)
+        return (-(p_bar * torch.log(p_bar + epsilon)).sum()).to(M.dtype)
+
+    def compute_mem_loss(self, hyp_values, ref_values, loss_mask=None, loss_weights=None):
+        """Per-example mean squared error [BT], times the optional mask and
+        weights (fwpkm.py:200-231)."""
+        if self.loss_type != "mse":
+            raise NotImplementedError(f"Loss type {self.loss_type} not implemented.")
+        losses = F.mse_loss(hyp_values, ref_values, reduction="none").mean(dim=-1)
+        if loss_mask is not None:
+            losses = losses * loss_mask
+        if loss_weights is not None:
+            losses = losses * loss_weights
+        return losses
+
+    def compute_addr_loss(self, sub_indices1, sub_indices2, all_sub_scores1, all_sub_scores2):
+        """-(marginal entropy of each half's addressing), weighted, or None
+        (fwpkm.py:233-264)."""
+        if self.addr_loss is None:
+            return None
+        if self.addr_loss != "me":
+            raise NotImplementedError(f"Addressing loss {self.addr_loss} not implemented.")
+        h1 = self.compute_marginal_entropy(all_sub_scores1.view(-1, self.subsize))
+        h2 = self.compute_marginal_entropy(all_sub_scores2.view(-1, self.subsize))
+        return self.addr_loss_weight * (-1.0 * h1 + -1.0 * h2)
+
+    # ---- inner update -----------------------------------------------------------------------
+
+    def update_fw_param(self, p, g, lr, wd):
+        if self.optimizer_type != "sgd":
+            raise NotImplementedError(f"Optimizer {self.optimizer_type} not implemented.")
+        return p - lr * (g + wd * p)
 
     def update_fw(self, fw_named_params: OrderedDict, num_samples: int, indices: torch.Tensor,
                   mem_loss: torch.Tensor, addr_loss: Optional[torch.Tensor] = None):
+        """One SGD step of the fast weights on 0.5 * mem_loss (+ addr_loss)
+        (fwpkm.py:274-367). Returns (updated params, unclipped gradients with
+        the values' one scaled). The values' step runs as one kernel pass
+        (sgd_value_update); create_graph follows self.training."""
         mem_loss = mem_loss * 0.5
         names = list(fw_named_params.keys())
+        params = list(fw_named_params.values())
         if self.mem_grad_to_values_only:
             if addr_loss is not None:
-                addr_grads = torch.autograd.grad(addr_loss, fw_named_params.values(), create_graph=self.training,
-                                                 allow_unused=True)
+                addr_grads = torch.autograd.grad(addr_loss, params, create_graph=self.training, allow_unused=True)
             else:
-                addr_grads = [None] * len(fw_named_params)
-            mem_grads = torch.autograd.grad(mem_loss, fw_named_params["values"], create_graph=self.training)
-            grads = [mem_grads[0] if n == "values" else addr_grads[i] for i, n in enumerate(names)]
+                addr_grads = [None] * len(params)
+            (g_values,) = torch.autograd.grad(mem_loss, fw_named_params["values"], create_graph=self.training)
+            grads = [g_values if n == "values" else addr_grads[i] for i, n in enumerate(names)]
         else:
             loss = mem_loss if addr_loss is None else mem_loss + addr_loss
-            grads = list(torch.autograd.grad(loss, tuple(fw_named_params.values()), create_graph=self.training))
-        fused = self.optimizer_type == "sgd"
+            grads = list(torch.autograd.grad(loss, params, create_graph=self.training))
         scale = num_samples * self.v_dim * self.topk * self.heads
+        fused = self.optimizer_type == "sgd"
         scaled, updated = [], []
-        for n, p, g in zip(names, fw_named_params.values(), grads):
+        for n, p, g in zip(names, params, grads):
             if n == "values" and fused and g is not None:
                 new_p, g_scaled = sgd_value_update(p, g, indices, scale, self.learning_rate, self.weight_decay,
                                                    self.grad_clip)
@@ -171,11 +344,210 @@ class FusedValueUpdateMixin:
                 updated.append(new_p)
                 continue
             if n == "values":
-                g = g * scale
-                binc = torch.bincount(indices.view(-1), minlength=self.size).to(g.dtype)
-                binc[binc == 0] = 1.0
-                g = g / binc.unsqueeze(-1)
+                counts = torch.bincount(indices.view(-1), minlength=self.size).to(g.dtype)
+                counts[counts == 0] = 1.0
+                g = (g * scale) / counts.unsqueeze(-1)
             scaled.append(g)
-            gc = torch.clamp(g, min=-1.0, max=1.0) if self.grad_clip else g
-            updated.append(self.update_fw_param(p, gc, self.learning_rate, self.weight_decay))
+            step = torch.clamp(g, min=-1.0, max=1.0) if self.grad_clip else g
+            updated.append(self.update_fw_param(p, step, self.learning_rate, self.weight_decay))
         return OrderedDict(zip(names, updated)), scaled
+
+    def write_ob_log(self, token_ids, indices, scores):
+        """Appends, per slot read, (query token, value token, up to 10 tokens
+        of context either side of the value token, score) to ob_idx2log
+        (fwpkm.py:369-393). token_ids [B, T]; indices, scores [B, T, heads * topk]."""
+        assert self.ob_mode
+        B, T = token_ids.shape
+        ids = token_ids.tolist()
+        la = self.lookahead
+        for b in range(B):
+            for t in range(T - la):
+                v = t + la
+                entry_ctx = (ids[b][t], ids[b][v], ids[b][max(0, v - 10):v], ids[b][v + 1:min(T, v + 10)])
+                for j in range(self.heads * self.topk):
+                    self.ob_idx2log[indices[b, t, j].item()].append(entry_ctx + (scores[b, t, j].item(),))
+
+    def _update_targets(self, hyp, ref, gates, mask):
+        """The (hyp, ref, weights, mask) the update fits: the last `lookahead`
+        hypotheses (and their weights / mask) drop out, the targets shift by
+        `lookahead` (fwpkm.py:464-486, 684-701)."""
+        la = self.lookahead
+        stop = None if la == 0 else -la
+        return (hyp[:, :stop].contiguous(), ref[:, la:].contiguous(),
+                gates[:, :stop].contiguous() if gates is not None else None,
+                mask[:, :stop].contiguous() if mask is not None else None)
+
+    def _losses(self, hyp, ref, weights, mask, retrieval):
+        D = hyp.size(-1)
+        mem_losses = self.compute_mem_loss(
+            hyp_values=hyp.view(-1, D),
+            ref_values=ref.view(-1, ref.size(-1)),
+            loss_mask=mask.view(-1) if mask is not None else None,
+            loss_weights=weights.view(-1) if weights is not None else None,
+        )
+        addr_loss = self.compute_addr_loss(retrieval["sub_indices1"], retrieval["sub_indices2"],
+                                           retrieval["all_sub_scores1"], retrieval["all_sub_scores2"])
+        return mem_losses, addr_loss
+
+    def _store_fast_weights(self, fw_named_params):
+        with torch.no_grad():
+            for n, p in self.named_parameters():
+                if n in fw_named_params:
+                    p.data.copy_(fw_named_params[n].data.to(p.dtype))
+
+    # ---- chunked forward --------------------------------------------------------------------
+
+    def forward_wo_past(self, q, ref_v, chunk_size, gates=None, loss_mask=None, token_ids=None):
+        """Training / prefill: split T into chunks; each chunk reads the
+        memory, then fits it with one update step whose result the next chunk
+        reads; the outer graph runs through every step (fwpkm.py:395-558)."""
+        B, T = q.shape[:2]
+        input_dtype = q.dtype
+        if self.fp32_fw:
+            q, ref_v = q.float(), ref_v.float()
+        outputs, indices, scores, losses, addr_losses, step_grads = [], [], [], [], [], []
+        with torch.enable_grad():
+            params = self.get_fw_named_params()
+            n_params = len(params)
+            for start, end in _chunks(T, chunk_size, chunk_size):
+                cT = end - start
+                cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
+                r = self.retrieve_values(q[:, start:end, :].contiguous(), params)
+                hyp = r["retireved_values"].view(B, cT, -1)
+                # the chunk's output is read before its own update
+                outputs.append(hyp)
+                indices.append(r["indices"].view(B, cT, -1))
+                scores.append(r["normed_scores"].view(B, cT, -1))
+                u_hyp, u_ref, u_w, u_mask = self._update_targets(hyp, ref_v[:, start:end, :].contiguous(), cgates,
+                                                                 cmask)
+                mem_losses, addr_loss = self._losses(u_hyp, u_ref, u_w, u_mask, r)
+                num_samples = (u_mask > 0).sum().item() if u_mask is not None else B * cT
+                params, grads = self.update_fw(params, num_samples, r["indices"], mem_losses.mean(), addr_loss)
+                if self.ob_mode:
+                    self.write_ob_log(token_ids=cids.view(B, cT), indices=r["indices"].view(B, cT, -1),
+                                      scores=cgates.view(B, cT, -1))
+                step_grads.append([g.detach() for g in grads])
+                losses.append(mem_losses.view(B, -1).detach())
+                if self.addr_loss is not None:
+                    addr_losses.append(addr_loss.detach())
+        with torch.no_grad():
+            grad_norms = [torch.stack([g[i].norm() for g in step_grads]).mean() for i in range(n_params)]
+        self._store_fast_weights(params)
+        return {
+            "output": torch.cat(outputs, dim=1).to(input_dtype),
+            "indices": torch.cat(indices, dim=1).view(B, T, self.heads, self.topk),
+            "scores": torch.cat(scores, dim=1).view(B, T, self.heads, self.topk),
+            "losses": torch.cat(losses, dim=1),
+            "addr_loss": torch.stack(addr_losses).mean() if self.addr_loss is not None else None,
+            "grad_norms": grad_norms,
+            "past_key_values": None,
+        }
+
+    def forward_w_past(self, q, ref_v, gates, chunk_size, loss_mask=None, past_key_values=None, token_ids=None):
+        """Streaming (generation): tokens queue up with the unprocessed tail
+        of earlier calls (past_key_values = (q, hyp_v, ref_v, gates, mask,
+        ids) queues); the memory is fitted on a queue once it holds a chunk
+        (fwpkm.py:560-820)."""
+        B, T = q.shape[:2]
+        input_dtype = q.dtype
+        if self.fp32_fw:
+            q, ref_v = q.float(), ref_v.float()
+        dev, dt = ref_v.device, ref_v.dtype
+
+        def empty(width=None, dtype=dt):
+            return torch.zeros((B, 0) if width is None else (B, 0, width), device=dev, dtype=dtype)
+
+        qq, hq, rq = empty(q.size(-1)), empty(ref_v.size(-1)), empty(ref_v.size(-1))
+        gq = empty() if gates is not None else None
+        mq = empty() if loss_mask is not None else None
+        iq = empty(dtype=torch.long) if token_ids is not None else None
+        if past_key_values is not None:
+            p_q, p_h, p_r, p_g, p_m, p_i = past_key_values
+            if p_h is not None:
+                assert p_h.size(1) < chunk_size + self.lookahead, (
+                    f"Past key values length {p_h.size(1)} longer than "
+                    f"chunk size + lookahead ({chunk_size} + {self.lookahead})."
+                )
+                qq, hq, rq = torch.cat([p_q, qq], 1), torch.cat([p_h, hq], 1), torch.cat([p_r, rq], 1)
+                gq = torch.cat([p_g, gq], 1) if gates is not None else None
+                mq = torch.cat([p_m, mq], 1) if loss_mask is not None else None
+                iq = torch.cat([p_i, iq], 1) if token_ids is not None else None
+
+        la = self.lookahead
+        stop = None if la == 0 else -la
+        updated = False
+        params = self.get_fw_named_params()
+        outputs, indices, scores, losses, addr_losses = [], [], [], [], []
+        for start, end in _chunks(T, chunk_size + la - rq.size(1), chunk_size):
+            cT = end - start
+            cq = q[:, start:end, :].contiguous()
+            cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
+            r = self.retrieve_values(cq, params)
+            hyp = r["retireved_values"].view(B, cT, -1)
+            chunk_indices = r["indices"]
+            outputs.append(hyp)
+            indices.append(chunk_indices.view(B, cT, -1))
+            scores.append(r["normed_scores"].view(B, cT, -1))
+            qq, hq, rq = torch.cat([qq, cq], 1), torch.cat([hq, hyp], 1), torch.cat([rq, ref_v[:, start:end]], 1)
+            gq = torch.cat([gq, cgates], 1) if gates is not None else None
+            mq = torch.cat([mq, cmask], 1) if loss_mask is not None else None
+            iq = torch.cat([iq, cids], 1) if token_ids is not None else None
+            if past_key_values and hq.size(1) < chunk_size:
+                continue  # not a chunk's worth of signal yet
+            updated = True
+            with torch.enable_grad():
+                params = {n: p.detach().requires_grad_(True) for n, p in params.items()}
+                ru = self.retrieve_values(qq[:, :stop].contiguous(), params)
+                u_w = gq[:, :stop].contiguous() if gq is not None else None
+                u_mask = mq[:, :stop].contiguous() if mq is not None else None
+                mem_losses, addr_loss = self._losses(ru["retireved_values"], rq[:, la:].contiguous(), u_w, u_mask,
+                                                     ru)
+                # as the reference: samples counted as B * chunk length, slots from the forward chunk
+                num_samples = (u_mask > 0).sum().item() if u_mask is not None else B * cT
+                params, _ = self.update_fw(params, num_samples, chunk_indices, mem_losses.mean(), addr_loss)
+                if self.ob_mode:
+                    pad = torch.zeros(iq.size(0), la, self.heads * self.topk, device=iq.device)
+                    n_u = iq.size(1) - la
+                    self.write_ob_log(
+                        token_ids=iq,
+                        indices=torch.cat([ru["indices"].view(B, n_u, -1), pad.to(ru["indices"].dtype)], 1),
+                        scores=torch.cat([ru["scores"].view(B, n_u, -1), pad.to(ru["scores"].dtype)], 1),
+                    )
+            if la == 0:
+                qq, hq, rq = empty(q.size(-1)), empty(ref_v.size(-1)), empty(ref_v.size(-1))
+                gq = empty() if gates is not None else None
+                mq = empty() if loss_mask is not None else None
+                iq = empty(dtype=torch.long)
+            else:
+                qq, hq, rq = qq[:, -la:].contiguous(), hq[:, -la:].contiguous(), rq[:, -la:].contiguous()
+                gq = gq[:, -la:].contiguous() if gates is not None else None
+                mq = mq[:, -la:].contiguous() if u_mask is not None else None
+                # (the reference slices the id queue unconditionally and fails without token ids)
+                iq = iq[:, -la:].contiguous() if iq is not None else None
+            losses.append(mem_losses.view(B, -1).detach())
+            if self.addr_loss is not None:
+                addr_losses.append(addr_loss.detach())
+        if updated:
+            self._store_fast_weights(params)
+        return {
+            "output": torch.cat(outputs, dim=1).to(input_dtype),
+            "indices": torch.cat(indices, dim=1).view(B, T, self.heads, self.topk),
+            "scores": torch.cat(scores, dim=1).view(B, T, self.heads, self.topk),
+            "losses": torch.cat(losses, dim=1) if updated else None,
+            "addr_loss": torch.stack(addr_losses).mean() if (updated and self.addr_loss is not None) else None,
+            "grad_norms": None,
+            "past_key_values": (qq, hq, rq, gq, mq, iq),
+        }
+
+    @torch.compiler.disable(recursive=True)
+    def forward(self, q, ref_v, gates, chunk_size, loss_mask=None, past_key_values=None, token_ids=None):
+        """Dict of output [B, T, v_dim], indices / scores [B, T, heads, topk],
+        losses, addr_loss, grad_norms, past_key_values (fwpkm.py:822-851)."""
+        if past_key_values is None:
+            return self.forward_wo_past(q=q, ref_v=ref_v, gates=gates, chunk_size=chunk_size, loss_mask=loss_mask,
+                                        token_ids=token_ids)
+        return self.forward_w_past(q=q, ref_v=ref_v, gates=gates, chunk_size=chunk_size, loss_mask=loss_mask,
+                                   past_key_values=past_key_values, token_ids=token_ids)
+
+
+__all__ = ["FastWeightProductKeyMemory", "l2norm", "get_indices", "compute_qk_scores", "sgd_value_update"]

@@ -171,11 +171,48 @@ def score_grad_sparse(query: torch.Tensor, keys: torch.Tensor, indices: torch.Te
     return dq, dk
 
 
-def _grads_from_dense(query, keys, dS, heads, n, score_type):
+class _DenseScoreGrad(torch.autograd.Function):
+    """score_grad_dense as an autograd node (a scatter-add of the selected
+    scores' gradient plus the dense sub-score gradients), so that a backward
+    taken with create_graph (the fast-weight inner step) stays
+    differentiable. Its VJP is the matching gather."""
+
+    @staticmethod
+    def forward(ctx, indices, d_scores, d_sub1, d_sub2, heads, n_keys):
+        ctx.save_for_backward(indices)
+        ctx.heads, ctx.n = heads, n_keys
+        ctx.has_sub = (d_sub1 is not None, d_sub2 is not None)
+        return score_grad_dense(indices, d_scores, heads, n_keys, d_sub1, d_sub2)
+
+    @staticmethod
+    def backward(ctx, g):
+        (indices,) = ctx.saved_tensors
+        H, n = ctx.heads, ctx.n
+        NH, knn = indices.shape
+        N = NH // H
+        idx = indices.view(N, H, knn)
+        g0 = g[:, 0].permute(1, 0, 2)  # [N, H, n]
+        g1 = g[:, 1].permute(1, 0, 2)
+        d_scores = (g0.gather(2, idx // n) + g1.gather(2, idx % n)).reshape(NH, knn)
+        return (None, d_scores, g0 if ctx.has_sub[0] else None, g1 if ctx.has_sub[1] else None, None, None)
+
+
+def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
     """dq [tokens, heads, k_dim] and dkeys [2*heads*n, half] from the dense
     sub-score gradient dS [heads, 2, tokens, n] with one pair of batched GEMMs
     per (head, half) — the products autograd forms for the reference's einsum
-    (dot) or cdist (idw) on the full score matrices."""
+    (dot) or cdist (idw) on the full score matrices. Torch ops: differentiable
+    when the backward runs with create_graph.
+
+    Which key values the products read follows the reference's saved tensors
+    (the fast-weight module stores updated weights into the key table in
+    place after its forward, fwpkm.py:540-545, so a table saved by reference
+    is read as it is at backward time): the einsum (dot) saves the key table
+    itself; cdist with use_mm_for_euclid_dist (idw) on the table's
+    strided half view works on a copy made at forward time, so every value
+    it reads, first and second order, is the forward-time one. `keys_fwd` is
+    that copy (idw); under create_graph it carries the table's own autograd
+    identity."""
     half = keys.shape[1]
     N = dS.shape[2]
     Kh = keys.reshape(heads * 2, n, half)
@@ -185,14 +222,20 @@ def _grads_from_dense(query, keys, dS, heads, n, score_type):
         dqh = torch.bmm(D, Kh)  # [2H, N, half]
         dk = torch.bmm(D.transpose(1, 2), qh)  # [2H, n, half]
     else:
-        # s = -log(1e-3 + max(d2, 0)), d2 = |q|^2 + |k|^2 - 2<q,k>:
-        #   ds/dq = 2 u (k - q), ds/dk = 2 u (q - k), u = 1 / (1e-3 + d2) (0 where d2 < 0)
+        # s = -log(1e-3 + d^2), d^2 = |q|^2 + |k|^2 - 2<q,k> (0 where not positive):
+        #   ds/dq = 2 u (k - q), ds/dk = 2 u (q - k), u = 1 / (1e-3 + d^2)
         q32, k32 = qh.float(), Kh.float()
-        dots = torch.bmm(q32, k32.transpose(1, 2).contiguous())
-        d2 = (q32 * q32).sum(-1)[:, :, None] + (k32 * k32).sum(-1)[:, None, :] - 2.0 * dots
-        U = torch.where(d2 >= 0, D.float() / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
-        dqh = 2.0 * (torch.bmm(U, k32) - q32 * U.sum(-1, keepdim=True))
-        dk = 2.0 * (torch.bmm(U.transpose(1, 2).contiguous(), q32) - k32 * U.sum(1)[:, :, None])
+        kf = k32
+        if keys_fwd is not None:
+            # the forward-time values; under create_graph differentiable as the table itself
+            kf = keys_fwd.reshape(heads * 2, n, half).float()
+            if torch.is_grad_enabled():
+                kf = kf + (k32 - k32.detach())
+        dots = torch.bmm(q32, kf.transpose(1, 2).contiguous())
+        d2 = (q32 * q32).sum(-1)[:, :, None] + (kf * kf).sum(-1)[:, None, :] - 2.0 * dots
+        U = torch.where(d2 > 0, D.float() / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
+        dqh = 2.0 * (torch.bmm(U, kf) - q32 * U.sum(-1, keepdim=True))
+        dk = 2.0 * (torch.bmm(U.transpose(1, 2).contiguous(), q32) - kf * U.sum(1)[:, :, None])
     dq = dqh.view(heads, 2, N, half).permute(2, 0, 1, 3).reshape(N, heads, 2 * half)
     return dq, dk.reshape(keys.shape)
 
@@ -207,13 +250,16 @@ class ProductKeyTopK(torch.autograd.Function):
         ctx.heads, ctx.knn, ctx.score_type, ctx.sub_outputs = heads, knn, score_type, sub_outputs
         ctx.n = keys.shape[0] // (2 * heads)
         ctx.query_shape = query.shape
-        ctx.save_for_backward(query, keys, outs[1])
+        # idw: the key values the distances were taken at (see _grads_from_dense)
+        saved = (query, keys, outs[1]) + ((keys.detach().clone(),) if score_type == "idw" else ())
+        ctx.save_for_backward(*saved)
         ctx.mark_non_differentiable(*(outs[1:4] if sub_outputs else outs[1:2]))
         return outs
 
     @staticmethod
     def backward(ctx, d_scores, d_indices, *rest):
-        query, keys, indices = ctx.saved_tensors
+        query, keys, indices = ctx.saved_tensors[:3]
+        keys_fwd = ctx.saved_tensors[3] if ctx.score_type == "idw" else None
         heads, n = ctx.heads, ctx.n
         d_s1 = rest[2] if ctx.sub_outputs else None
         d_s2 = rest[3] if ctx.sub_outputs else None
@@ -221,13 +267,16 @@ class ProductKeyTopK(torch.autograd.Function):
             d_scores = torch.zeros(indices.shape, dtype=query.dtype, device=query.device)
         need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         grads = None
-        if ctx.score_type == "dot" and d_s1 is None and d_s2 is None:
+        # the sparse kernel's gradients are not differentiable: a create_graph backward takes the dense path
+        if ctx.score_type == "dot" and d_s1 is None and d_s2 is None and not torch.is_grad_enabled():
             grads = score_grad_sparse(query, keys, indices, d_scores, heads, need_q, need_k)
         if grads is not None:
             dq, dk = grads
         else:
-            dS = score_grad_dense(indices, d_scores.to(query.dtype), heads, n, d_s1, d_s2)
-            dq, dk = _grads_from_dense(_aligned(query), _aligned(keys), dS, heads, n, ctx.score_type)
+            d_s1 = d_s1.to(query.dtype) if d_s1 is not None else None
+            d_s2 = d_s2.to(query.dtype) if d_s2 is not None else None
+            dS = _DenseScoreGrad.apply(indices, d_scores.to(query.dtype), d_s1, d_s2, heads, n)
+            dq, dk = _grads_from_dense(query, keys, dS, heads, n, ctx.score_type, keys_fwd)
         d_query = dq.to(query.dtype).reshape(ctx.query_shape) if ctx.needs_input_grad[0] else None
         d_keys = dk.to(keys.dtype) if ctx.needs_input_grad[1] else None
         return d_query, d_keys, None, None, None, None
@@ -247,6 +296,12 @@ class _ScoreSoftmax(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         (x2,) = ctx.saved_tensors
+        if torch.is_grad_enabled():
+            # a create_graph backward (the fast-weight inner step): the same float32 expression in
+            # torch ops, so that it is differentiable in turn
+            p = torch.softmax(x2.float(), dim=-1)
+            dyf = dy.float()
+            return (p * (dyf - (dyf * p).sum(-1, keepdim=True))).to(x2.dtype)
         rows, cols = x2.shape
         dy2 = _aligned(dy.to(x2.dtype))
         dx = torch.empty_like(x2)

@@ -64,3 +64,17 @@ def assert_rel_close(actual: torch.Tensor, expected: torch.Tensor, rel: float, w
             f"got {a.reshape(-1)[i].item()!r} expected {e.reshape(-1)[i].item()!r} "
             f"(max abs err {err.max().item():.3e}, scale {scale:.3e}, rel {rel})"
         )
+
+
+def assert_norm_close(actual: torch.Tensor, expected: torch.Tensor, rel: float, what: str = ""):
+    """Normwise relative error in the 2-norm, ||a - e|| <= rel * ||e||: for
+    long chains of rounded stages whose outputs are sums with heavy
+    cancellation, where single elements can carry the input rounding of many
+    terms beyond their own size."""
+    a = actual.detach().to("cpu", torch.float64)
+    e = expected.detach().to("cpu", torch.float64)
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    err = (a - e).norm().item()
+    ref = e.norm().item()
+    assert err <= rel * ref, f"{what}: ||a - e|| = {err:.3e} > {rel} * ||e|| = {rel * ref:.3e}"
+

@@ -2,7 +2,7 @@
 oracle.fw_update, which applies the reference's ATen ops in the same dtype on
 the CPU: every step rounds to the dtype in the same order, so the results are
 bit-exact. Its autograd (create_graph updates) is checked against torch's
-autograd of the reference expression, and FusedValueUpdateMixin.update_fw
+autograd of the reference expression, and FastWeightProductKeyMemory.update_fw
 against the oracle end to end."""
 from __future__ import annotations
 
@@ -11,7 +11,7 @@ from collections import OrderedDict
 import pytest
 import torch
 
-from modelos_amd.fwpkm.fwpkm import FusedValueUpdateMixin, sgd_value_update
+from modelos_amd.fwpkm.fwpkm import sgd_value_update
 from oracle import fw_update as ref
 from tests.helpers import REL_TOL, assert_rel_close, gen
 
@@ -82,24 +82,20 @@ def test_autograd_matches_reference_expression(device, clip):
     assert_rel_close(got[1], exp[1], REL_TOL[torch.float32], "d grad")
 
 
-class _FwStub(FusedValueUpdateMixin):
-    """The attributes update_fw reads (fwpkm.py:274-367), and update_fw_param (266-272)."""
+def _fw_module(clip):
+    """A FastWeightProductKeyMemory whose update_fw (fwpkm.py:274-367) is
+    called directly: 2 heads, top-8, value dim 64, 2^12 slots."""
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
 
-    def __init__(self, clip):
-        self.mem_grad_to_values_only = True
-        self.training = False
-        self.optimizer_type = "sgd"
-        self.v_dim, self.topk, self.heads, self.size = 64, 8, 2, 300
-        self.learning_rate, self.weight_decay, self.grad_clip = 0.5, 0.01, clip
-
-    def update_fw_param(self, p, g, lr, wd):
-        return p - lr * (g + wd * p)
+    m = FastWeightProductKeyMemory(mem_k_dim=32, mem_v_dim=64, mem_heads=2, mem_topk=8, mem_n_subkeys=64,
+                                   learning_rate=0.5, weight_decay=0.01, grad_clip=clip)
+    return m.eval()
 
 
 @pytest.mark.parametrize("clip", [False, True], ids=["plain", "clip"])
 def test_update_fw_end_to_end(device, clip):
     g = gen(9)
-    V = torch.randn((300, 64), generator=g).to(device).requires_grad_(True)
+    V = torch.randn((4096, 64), generator=g).to(device).requires_grad_(True)
     Kp = torch.randn((10, 4), generator=g).to(device).requires_grad_(True)
     idx = torch.randint(0, 250, (12, 16), generator=g).to(device)
     w = torch.randn((12, 16), generator=g).to(device)
@@ -110,7 +106,7 @@ def test_update_fw_end_to_end(device, clip):
     # oracle: the same gradients (taken first: update_fw frees the graph), then the reference's steps
     gv = torch.autograd.grad(0.5 * mem_loss, V, retain_graph=True)[0]
     gk = torch.autograd.grad(addr_loss, Kp, retain_graph=True)[0]
-    mod = _FwStub(clip)
+    mod = _fw_module(clip)
     params = OrderedDict([("keys", Kp), ("values", V)])
     upd, grads = mod.update_fw(params, 12, idx, mem_loss, addr_loss)
     e_v, e_gv = ref.sgd_value_update(V.detach().cpu(), gv.cpu(), idx.cpu(), 12 * 64 * 8 * 2, 0.5, 0.01, clip)

@@ -1,0 +1,237 @@
+"""FastWeightProductKeyMemory on the HIP kernels (GPU).
+
+  * float32 against the reference's own outputs (tests/golden/fwpkm_*.pt,
+    written by fwpkm/fwpkm.py on the CPU): the chunked forward with the inner
+    updates and every outer gradient through them, and three streaming calls
+    carrying the queues; 1e-5 relative, indices exact;
+  * bfloat16 (fp32_fw off, the whole chain in bf16) against the float64
+    oracle (oracle/fwpkm.py) evaluated at the kernel's selections, 2e-2
+    normwise (a bf16 chain of a dozen rounded stages);
+  * the fast-weight workload's full shape (x [8, 1024, 1024] as 4 heads x 256,
+    512 keys per half, knn 16, value dim 1024, chunks of 512, lookahead 0,
+    lr 0.1, "me" address loss), float32 and bfloat16: the outer gradients are
+    finite and bitwise reproducible, and sampled tokens' retrieved values and
+    sampled rows of the updated table match float64 recomputations from the
+    kernel's own selections.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import fwpkm as ofw
+from tests.helpers import assert_norm_close, assert_rel_close, gen
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def load(case):
+    return torch.load(GOLDEN / f"fwpkm_{case}.pt", weights_only=True)
+
+
+def module(kwargs, keys, values, device, dtype=torch.float32):
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
+
+    mem = FastWeightProductKeyMemory(**kwargs).to(device=device, dtype=dtype)
+    with torch.no_grad():
+        mem.keys.copy_(keys)
+        mem.values.copy_(values)
+    return mem.train()
+
+
+def _dev(x, device):
+    return x.to(device) if x is not None else None
+
+
+@pytest.mark.parametrize("case", ["idw_la0", "dot_la1"])
+def test_chunked_matches_reference_golden(case, device):
+    rec = load(case)
+    (call,) = rec["calls"]
+    c = call["inputs"]
+    mem = module(rec["kwargs"], rec["param.keys"], rec["param.values"], device)
+    q = c["q"].to(device).requires_grad_(True)
+    ref_v = c["ref_v"].to(device).requires_grad_(True)
+    gates = c["gates"].to(device).requires_grad_(True) if "gates" in c else None
+    out = mem(q=q, ref_v=ref_v, gates=gates, chunk_size=rec["chunk_size"], loss_mask=_dev(c.get("loss_mask"), device),
+              past_key_values=None, token_ids=c["token_ids"].to(device))
+    assert torch.equal(out["indices"].cpu(), call["indices"])
+    for k in ("output", "scores", "losses", "addr_loss"):
+        assert_rel_close(out[k], call[k], 1e-5, k)
+    for a, e in zip(out["grad_norms"], call["grad_norms"]):
+        assert_rel_close(a, e, 1e-5, "grad_norm")
+    assert_rel_close(mem.keys, call["final.keys"], 1e-5, "final keys")
+    assert_rel_close(mem.values, call["final.values"], 1e-5, "final values")
+    out["output"].backward(c["dout"].to(device))
+    assert_rel_close(q.grad, call["grad.q"], 1e-5, "dq")
+    assert_rel_close(ref_v.grad, call["grad.ref_v"], 1e-5, "dref_v")
+    assert_rel_close(mem.keys.grad, call["grad.keys"], 1e-5, "dkeys")
+    assert_rel_close(mem.values.grad, call["grad.values"], 1e-5, "dvalues")
+    if gates is not None:
+        assert_rel_close(gates.grad, call["grad.gates"], 1e-5, "dgates")
+
+
+def test_streaming_matches_reference_golden(device):
+    rec = load("stream")
+    mem = module(rec["kwargs"], rec["param.keys"], rec["param.values"], device)
+    past = (None,) * 6
+    for n, call in enumerate(rec["calls"]):
+        c = call["inputs"]
+        with torch.no_grad():
+            out = mem(q=c["q"].to(device), ref_v=c["ref_v"].to(device), gates=_dev(c.get("gates"), device),
+                      chunk_size=rec["chunk_size"], loss_mask=_dev(c.get("loss_mask"), device),
+                      past_key_values=past, token_ids=c["token_ids"].to(device))
+        assert torch.equal(out["indices"].cpu(), call["indices"]), n
+        assert_rel_close(out["output"], call["output"], 1e-5, f"call {n} output")
+        assert_rel_close(out["scores"], call["scores"], 1e-5, f"call {n} scores")
+        assert (out["losses"] is None) == (call["losses"] is None)
+        if call["losses"] is not None:
+            assert_rel_close(out["losses"], call["losses"], 1e-5, f"call {n} losses")
+            assert_rel_close(out["addr_loss"], call["addr_loss"], 1e-5, f"call {n} addr_loss")
+        for a, e in zip(out["past_key_values"], call["queues"]):
+            assert (a is None) == (e is None)
+            if e is not None:
+                assert a.shape == e.shape
+                assert_rel_close(a, e, 1e-5, f"call {n} queue")
+        assert_rel_close(mem.keys, call["final.keys"], 1e-5, f"call {n} keys")
+        assert_rel_close(mem.values, call["final.values"], 1e-5, f"call {n} values")
+        past = out["past_key_values"]
+
+
+def _record_selections(mem, scores=None):
+    """Wraps mem.get_indices to keep the indices of every retrieval, in call
+    order (and, into `scores`, the sub-score matrices)."""
+    seen = []
+    orig = mem.get_indices
+
+    def recording(query, keys):
+        out = orig(query, keys)
+        seen.append(out[1].detach().cpu())
+        if scores is not None:
+            scores.append((out[4].detach().cpu(), out[5].detach().cpu()))
+        return out
+
+    mem.get_indices = recording
+    return seen
+
+
+@pytest.mark.parametrize("score_type", ["idw", "dot_product"])
+def test_bf16_chain_vs_fp64_oracle(score_type, device):
+    kw = dict(mem_k_dim=256, mem_v_dim=256, mem_heads=4, mem_topk=16, mem_n_subkeys=512, lookahead=0,
+              qk_score_type=score_type, learning_rate=0.1, fp32_fw=False)
+    g = gen(71)
+    keys = ((torch.rand((2 * 4 * 512, 128), generator=g) * 2 - 1) / 16).to(torch.bfloat16)
+    values = (torch.randn((512 * 512, 256), generator=g) / 16).to(torch.bfloat16)
+    B, T, chunk = 2, 256, 128
+    q = (torch.randn((B, T, 4 * 256), generator=g) * 0.25).to(torch.bfloat16)
+    ref_v = torch.randn((B, T, 256), generator=g).to(torch.bfloat16)
+    dout = torch.randn((B, T, 256), generator=g).to(torch.bfloat16)
+
+    mem = module(kw, keys, values, device, torch.bfloat16)
+    sub = []
+    sel = _record_selections(mem, sub)
+    qd, rd = q.to(device).requires_grad_(True), ref_v.to(device).requires_grad_(True)
+    out = mem(q=qd, ref_v=rd, gates=None, chunk_size=chunk)
+    out["output"].backward(dout.to(device))
+    torch.cuda.synchronize()
+
+    cfg = ofw.FwConfig.from_module_kwargs(kw)
+    k64 = keys.double().requires_grad_(True)
+    v64 = values.double().requires_grad_(True)
+    q64, r64 = q.double().requires_grad_(True), ref_v.double().requires_grad_(True)
+    # the oracle keeps the kernel's selections and its address-loss masks (bf16 scores tie at the threshold)
+    e = ofw.forward_wo_past(q64, r64, k64, v64, cfg, chunk, selections=sel, sel_scores=sub)
+    e["output"].backward(dout.double())
+    tol = 2e-2
+    assert_rel_close(out["output"], e["output"], tol, "output", elem_frac=None)
+    assert_rel_close(out["losses"], e["losses"], tol, "losses", elem_frac=None)
+    assert_rel_close(mem.values, e["final"]["values"], tol, "final values", elem_frac=None)
+    assert_rel_close(qd.grad, q64.grad, tol, "dq", elem_frac=None)
+    assert_rel_close(rd.grad, r64.grad, tol, "dref_v", elem_frac=None)
+    assert_rel_close(mem.values.grad, v64.grad, tol, "dvalues", elem_frac=None)
+    # a key's gradient sums every token's 2 u (q - k) with heavy cancellation; the bf16 sub-score
+    # gradient (the reference's bf16 autograd rounds it too) moves single entries by a few % of the
+    # maximum: 2-norm relative error here
+    assert_norm_close(mem.keys.grad, k64.grad, tol, "dkeys")
+
+
+FULL = dict(mem_k_dim=256, mem_v_dim=1024, mem_heads=4, mem_topk=16, mem_n_subkeys=512, lookahead=0,
+            qk_score_type="idw", learning_rate=0.1, addr_loss="me")
+
+
+def _full_inputs(dtype):
+    g = gen(5)
+    x = torch.randn((8, 1024, 1024), generator=g)
+    target = torch.randn((8, 1024, 1024), generator=g)
+    return x.to(dtype), target.to(dtype)
+
+
+def _full_step(mem, x, target, ref_v):
+    """Two chunks of 512; the outer loss is the MSE of the second chunk's
+    output (which reads the table after one update) against `target`."""
+    x = x.clone().requires_grad_(True)
+    out = mem(q=x, ref_v=ref_v, gates=None, chunk_size=512)
+    loss = torch.nn.functional.mse_loss(out["output"][:, 512:].float(), target[:, 512:].float())
+    loss.backward()
+    return out, x.grad
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_full_shape_fast_weight_step(dtype, device):
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
+
+    x, target = _full_inputs(dtype)
+    xd, td = x.to(device), target.to(device)
+    ref_v = td  # the memorisation targets
+    torch.manual_seed(0)
+    base = FastWeightProductKeyMemory(**FULL, fp32_fw=dtype == torch.float32)
+    base.reset_parameters()
+    k0, v0 = base.keys.detach().clone(), base.values.detach().clone()
+    runs = []
+    for _ in range(2):
+        mem = module(dict(FULL, fp32_fw=dtype == torch.float32), k0, v0, device, dtype)
+        sel = _record_selections(mem)
+        out, dx = _full_step(mem, xd, td, ref_v)
+        torch.cuda.synchronize()
+        runs.append((out, dx, mem.keys.grad.clone(), mem.values.grad.clone(), mem.values.detach().clone(), sel))
+    (o1, dx1, dk1, dv1, vf1, sel1), (o2, dx2, dk2, dv2, vf2, _) = runs
+    # bitwise reproducible, finite
+    for a, b, name in ((o1["output"], o2["output"], "output"), (dx1, dx2, "dx"), (dk1, dk2, "dkeys"),
+                       (dv1, dv2, "dvalues"), (vf1, vf2, "updated values")):
+        assert torch.equal(a, b), f"{name} differs between identical runs"
+        assert torch.isfinite(a).all(), f"{name} not finite"
+    assert o1["indices"].shape == (8, 1024, 4, 16)
+    idx = o1["indices"].cpu()
+    assert int(idx.min()) >= 0 and int(idx.max()) < 512 * 512
+    # sampled tokens of chunk 1: retrieved values = sum_j w_j V0[idx_j] in float64
+    w = o1["scores"].cpu().double()
+    V0 = v0 if dtype == torch.float32 else v0.to(dtype)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for b in (0, 7):
+        for t in (0, 37, 300, 511):
+            e = (V0[idx[b, t].reshape(-1)].double() * w[b, t].reshape(-1, 1)).sum(0)
+            assert_rel_close(o1["output"][b, t].cpu(), e, tol, f"retrieved value b={b} t={t}")
+    # sampled rows of the table after both chunks' updates: per chunk c,
+    # gV_c[r] = sum over chunk-c lookups of r of w * dL/dhyp, dL/dhyp = (hyp - ref) / (tokens * v_dim),
+    # scaled by tokens * v_dim * topk * heads / count_c(r); SGD with lr 0.1
+    out_all = o1["output"].cpu().double()
+    rows = idx[:, :512].reshape(-1)[torch.tensor([0, 1000, 20000, 100000])].tolist()
+    expected = {r: V0[r].double().clone() for r in rows}
+    for c in range(2):
+        sl = slice(512 * c, 512 * (c + 1))
+        hyp = out_all[:, sl].reshape(-1, 1024)
+        dh = (hyp - target[:, sl].double().reshape(-1, 1024)) / (hyp.shape[0] * 1024)
+        ic = idx[:, sl].reshape(-1, 64)
+        wc = w[:, sl].reshape(-1, 64)
+        for r in rows:
+            bags, slots = (ic == r).nonzero(as_tuple=True)
+            if bags.numel() == 0:
+                continue
+            gv = (wc[bags, slots, None] * dh[bags]).sum(0)
+            expected[r] = expected[r] - 0.1 * gv * (4096 * 1024 * 16 * 4 / bags.numel())
+    for r in rows:
+        assert_rel_close(vf1[r].cpu(), expected[r], 1e-4 if dtype == torch.float32 else 2e-2, f"updated row {r}",
+                         elem_frac=None)

@@ -134,8 +134,8 @@ def test_layer_bf16_vs_oracle(device):
     tol = REL_TOL[torch.bfloat16]
     sel = idx.cpu().view(-1, 32)
     for ref_dtype, frac in ((torch.bfloat16, 0.1), (torch.float64, None)):
-        P = {n: p.detach().cpu().to(ref_dtype).requires_grad_(True) for n, p in mem.named_parameters()}
-        xr = x.to(ref_dtype).requires_grad_(True)
+        P = {n: p.detach().cpu().to(ref_dtype).clone().requires_grad_(True) for n, p in mem.named_parameters()}
+        xr = x.detach().to(ref_dtype).clone().requires_grad_(True)
         e_out, _ = pkm_layer.hashing_memory_forward(xr, P, 8, 32, idx=sel)
         e_out.backward(dout.to(ref_dtype))
         assert_rel_close(out.cpu(), e_out, tol, f"out vs {ref_dtype}", elem_frac=frac)

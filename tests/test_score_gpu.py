@@ -236,12 +236,10 @@ def test_fwpkm_drop_in(device, score_type):
     """fwpkm get_indices / compute_qk_scores drop-ins (fwpkm/fwpkm.py:853-934):
     the 6-tuple's shapes, the selection bit-exact from the returned
     sub-scores, and compute_qk_scores within tolerance of the oracle."""
-    from modelos_amd.fwpkm.fwpkm import ProductKeyIndexMixin
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
 
-    class Mem(ProductKeyIndexMixin):
-        heads, k_dim, topk, subsize, qk_score_type = 4, 256, 16, 512, score_type
-
-    m = Mem()
+    m = FastWeightProductKeyMemory(mem_k_dim=256, mem_v_dim=16, mem_heads=4, mem_topk=16, mem_n_subkeys=512,
+                                   qk_score_type=score_type)
     BT = 50
     q, k = _random_inputs(BT, m.heads, m.subsize, m.k_dim // 2, torch.float32, seed=22)
     scores, idx, i1, i2, s1, s2 = m.get_indices(q.to(device), k.to(device))
