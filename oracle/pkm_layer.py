@@ -81,12 +81,14 @@ def get_indices_torch(query: torch.Tensor, keys: torch.Tensor, heads: int, knn: 
 
 def hashing_memory_forward(x: torch.Tensor, P: Dict[str, torch.Tensor], heads: int, knn: int,
                            batchnorm: bool = False, idx: torch.Tensor | None = None,
-                           reference_ops: bool = False):
+                           reference_ops: bool = False, bag_idx: torch.Tensor | None = None):
     """(out [B, T, out_dim], indices [B, T, H*knn]) of HashingMemory.forward
     with swilu projection and no gating (the layer's defaults). `idx` forces
     the selection (to evaluate the layer at another implementation's ids);
     reference_ops selects with the reference's einsum/topk sequence instead of
-    the stable-tie oracle (the CPU baseline)."""
+    the stable-tie oracle (the CPU baseline). `bag_idx` [N*H, knn], when
+    given, addresses P["values.weight"] instead of idx (a compact table of
+    just the rows idx reads)."""
     B, T, C = x.shape
     X = x.reshape(-1, C)
     N = X.shape[0]
@@ -98,7 +100,7 @@ def hashing_memory_forward(x: torch.Tensor, P: Dict[str, torch.Tensor], heads: i
     else:
         scores, idx = get_indices_differentiable(q.reshape(N * heads, k_dim), P["keys"], heads, knn, idx)
     p = F.softmax(scores.float(), dim=-1).type_as(scores)
-    E = F.embedding_bag(idx.reshape(N, heads * knn), P["values.weight"],
+    E = F.embedding_bag((idx if bag_idx is None else bag_idx).reshape(N, heads * knn), P["values.weight"],
                         per_sample_weights=p.reshape(N, heads * knn), mode="sum")
     gate = F.silu(F.linear(X, P["swilu_projection.weight"], P["swilu_projection.bias"]))
     out = F.linear(E * gate, P["value_proj.weight"], P["value_proj.bias"])
