@@ -18,7 +18,15 @@ region), every entry point's time, and the reference's CPU path (op-for-op
 torch CPU restatement: einsum/topk/F.embedding_bag + ATen autograd) timed on
 this host's cores on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--workload layer|eb|fwupdate|fwpkm] [--no-cpu-baseline]
+The default run also reports, under extra keys, the standalone embedding bag
+("eb_standalone"), the fast-weight PKM layer in float32 and bfloat16
+("fwpkm"), the CPU parity configuration's forward ("cpu_parity_config"),
+each with its CPU baseline, and the layer step after a 512 MB cache flush
+("cache_flush"). "--workload model" times a Qwen3-0.6B-shaped decoder train
+step with two PKM layers.
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
+                       [--workload layer|eb|fwupdate|fwpkm|model] [--no-cpu-baseline] [--no-extras]
 """
 from __future__ import annotations
 
@@ -70,6 +78,16 @@ def score_flops(tokens, heads, n_keys, k_dim):
 
 
 def cpu_model():
+    """The host CPU's model name as lscpu prints it (/proc/cpuinfo if lscpu is absent)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -82,14 +100,18 @@ def cpu_model():
 def load_traffic():
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE,
     WRITE_SIZE, scaled by a copy-kernel calibration), committed under
-    profiles/; None if absent."""
+    profiles/ (not measured in this run: the counters need a profiler run of
+    their own); each entry is returned with the tree it was profiled on."""
     p = ROOT / "profiles" / "hbm_traffic.json"
     if not p.exists():
         return {}
     try:
-        return json.loads(p.read_text())
+        d = json.loads(p.read_text())
     except ValueError:
         return {}
+    when = d.get("_profiled_at", "see profiles/hbm_traffic.md")
+    return {k: {"bytes": v, "source": "profiles/hbm_traffic.json", "profiled_at": when}
+            for k, v in d.items() if not k.startswith("_")}
 
 
 def timed_median(fn, budget_s=25.0, max_repeats=3):
@@ -154,7 +176,7 @@ def cpu_baseline_layer(mem, x, dout, budget_s=25.0):
         "kind": "port",
         "sample": f"{tokens} of the {total} tokens (same bf16 parameters and inputs), full 2^20 x 1024 value "
         f"table, fwd+bwd; median of {reps} after 1 warm-up; torch CPU ops of the reference's path on {cores} "
-        f"threads ({cpu_model()})",
+        f"threads ({cpu_model()}, lscpu model name)",
         "ms_per_step": round(t * 1e3, 1),
     }
 
@@ -275,8 +297,24 @@ def run_layer(args, dev):
     traffic = load_traffic().get(dom_name)
     roofline = {
         "bound": dom["bound"], "kernel": dom_name, "achieved": dom["achieved"], "peak": dom["peak"],
-        "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,
+        "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic["bytes"] if traffic else None,
+        "traffic_profiled_at": traffic["profiled_at"] if traffic else None,
     }
+
+    # the same step with a 512 MB write between steps (caches hold none of the previous step's data)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    fl_ms = []
+    for i in range(args.steps):
+        flush.fill_(i & 0xFF)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        step()
+        b.record()
+        fl_ms.append((a, b))
+    torch.cuda.synchronize()
+    flushed_ms = sorted(a.elapsed_time(b) for a, b in fl_ms)[args.steps // 2]
+    del flush
+    log(f"with a 512 MB cache flush between steps: {flushed_ms:.3f} ms/step (median event time)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -304,6 +342,9 @@ def run_layer(args, dev):
         },
         "roofline": roofline,
         "kernels": kernels,
+        "cache_flush": {"ms_per_step": round(flushed_ms, 4), "ms_per_step_no_flush": round(step_ms, 4),
+                        "note": "median HIP-event time of a step run right after a 512 MB write; "
+                                "ms_per_step_no_flush: the same median for back-to-back steps"},
         "cpu_baseline": cpu,
     }
 
@@ -508,79 +549,234 @@ def run_fwupdate(args, dev):
     }
 
 
-def run_fwpkm(args, dev):
-    """Fast-weight PKM step at 4 heads x 512 keys per half (2^18 slots), knn 16,
-    value dim 512, 8192 tokens, float32: retrieval, the inner MSE gradient with
-    create_graph, the fused value update (lr 0.1), retrieval from the updated
-    table, and the outer backward through the update (the embedding bag's
-    grad-of-grad). Synthetic indices and weights of that shape."""
+FWPKM = dict(mem_k_dim=256, mem_v_dim=1024, mem_heads=4, mem_topk=16, mem_n_subkeys=512, lookahead=0,
+             qk_score_type="idw", learning_rate=0.1, addr_loss="me")
+
+
+def cpu_baseline_fwpkm(mem, x, target, budget_s=25.0):
+    """The reference's fast-weight chain as torch CPU ops (oracle.fwpkm, pinned
+    to the reference's own outputs): one sequence of 1024 tokens (two chunks
+    of 512, the second reading the updated table), full 2^18 x 1024 float32
+    table, outer backward."""
+    import torch
+
+    from oracle import fwpkm as ofw
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = ofw.FwConfig.from_module_kwargs(dict(FWPKM, fp32_fw=True))
+    k0 = mem.keys.detach().float().cpu()
+    v0 = mem.values.detach().float().cpu()
+    xs, ts = x[:1].float().cpu(), target[:1].float().cpu()
+
+    def step():
+        keys, values = k0.clone().requires_grad_(True), v0.clone().requires_grad_(True)
+        q = xs.clone().requires_grad_(True)
+        out = ofw.forward_wo_past(q, ts, keys, values, cfg, 512)
+        torch.nn.functional.mse_loss(out["output"][:, 512:], ts[:, 512:]).backward()
+
+    t, reps = timed_median(step, budget_s=budget_s, max_repeats=2)
+    return {"value": round(1024 / t, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"1 of the 8 sequences (1024 tokens, 2 chunks), full 2^18 x 1024 float32 table, inner update "
+            f"+ outer backward; median of {reps} after 1 warm-up; torch CPU ops of the reference's chain "
+            f"(oracle.fwpkm) on {cores} threads ({cpu_model()})", "ms_per_step": round(t * 1e3, 1)}
+
+
+def run_fwpkm(args, dev, with_cpu=None):
+    """Fast-weight PKM layer step (the drop-in FastWeightProductKeyMemory):
+    x [8, 1024, 1024] as queries (4 heads x 256), targets ~ N(0,1), 512 keys
+    per half (2^18 slots), knn 16, value dim 1024, chunks of 512 (the second
+    chunk reads the table after one inner SGD step, lr 0.1, "me" address loss),
+    outer loss the MSE of the second chunk's output: forward with the inner
+    update, then the outer backward through it (the embedding bag's
+    grad-of-grad). float32 (fp32_fw) and bfloat16 (fp32_fw off)."""
     import torch
 
     from modelos_amd import _lib
-    from modelos_amd.fwpkm.fwpkm import sgd_value_update
-    from modelos_amd.fwpkm.xformer_embeddingbag_grad_wrapper import xformers_embedding_bag as xeb
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
 
-    N, H, knn, K, D = 8192, 4, 16, 512 * 512, 512
-    L = H * knn
-    scale, lr = N * D * knn * H, 0.1
+    with_cpu = (not args.no_cpu_baseline) if with_cpu is None else with_cpu
+    results = {}
     gen = torch.Generator(device=dev).manual_seed(0)
-    V = (torch.randn((K, D), generator=gen, device=dev) * D**-0.5).requires_grad_(True)
-    idx = torch.randint(0, K, (N, L), generator=gen, device=dev)
-    idx2 = torch.randint(0, K, (N, L), generator=gen, device=dev)
-    psw = torch.softmax(torch.randn((N, L), generator=gen, device=dev), -1).requires_grad_(True)
-    psw2 = torch.softmax(torch.randn((N, L), generator=gen, device=dev), -1).requires_grad_(True)
-    targets = torch.randn((N, D), generator=gen, device=dev)
-    dout = torch.randn((N, D), generator=gen, device=dev)
+    x32 = torch.randn((8, 1024, 1024), generator=gen, device=dev)
+    t32 = torch.randn((8, 1024, 1024), generator=gen, device=dev)
+    for dtype in (torch.float32, torch.bfloat16):
+        torch.manual_seed(0)
+        mem = FastWeightProductKeyMemory(**FWPKM, fp32_fw=dtype == torch.float32).to(dev)
+        mem.reset_parameters()
+        mem = mem.to(dtype).train()
+        x, target = x32.to(dtype), t32.to(dtype)
+
+        def step():
+            mem.zero_grad(set_to_none=True)
+            xx = x.detach().requires_grad_(True)
+            out = mem(q=xx, ref_v=target, gates=None, chunk_size=512)
+            torch.nn.functional.mse_loss(out["output"][:, 512:].float(), target[:, 512:].float()).backward()
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        timer = _lib.CallTimer()
+        t0 = time.perf_counter()
+        with timer:
+            for _ in range(args.steps):
+                step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        calls = timer.summary()
+        kern = {}
+        for name in ("pkm_score_topk", "pkm_eb_fwd", "pkm_eb_bwd", "pkm_eb_bwd2", "pkm_fw_sgd_update"):
+            keys = [k for k in calls if k[0] == name]
+            if keys:
+                kern[name] = {"ms_per_step": round(sum(sum(calls[k]) for k in keys) / args.steps, 4),
+                              "calls_per_step": sum(len(calls[k]) for k in keys) // args.steps}
+        tag = "f32" if dtype == torch.float32 else "bf16"
+        log(f"fwpkm {tag}: {ms:.3f} ms/step")
+        results[tag] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(8192 / (ms * 1e-3), 1), "kernels": kern}
+        if with_cpu and dtype == torch.float32:
+            log("timing the fast-weight CPU baseline ...")
+            results["cpu_baseline"] = cpu_baseline_fwpkm(mem, x, target)
+        del mem
+    return {
+        "workload": "fast-weight PKM step (FastWeightProductKeyMemory.forward_wo_past, 2 chunks of 512 per "
+                    "sequence, inner update + outer backward), 8 x 1024 tokens, 4 heads x 512 keys/half, knn 16, "
+                    "v_dim 1024, idw scores, lr 0.1",
+        **results,
+    }
+
+
+def run_fwpkm_workload(args, dev):
+    r = run_fwpkm(args, dev)
+    f32 = r["f32"]
+    return {
+        "metric": "FwPKM layer step (inner update + outer backward) tokens/sec, float32",
+        "value": f32["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": f32["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (N(0,1) queries and targets, reset_parameters init)",
+        "config": {"workload": r["workload"], "tokens": 8192},
+        "fwpkm": r, "cpu_baseline": r.get("cpu_baseline"),
+    }
+
+
+def cpu_parity_config(args, dev, budget_s=20.0):
+    """The CPU parity configuration: one PKM layer forward, float32, x [4, 512,
+    1024], 4 heads x 256 keys per half (65,536 slots), k_dim 512, knn 32, value
+    dim 1024, BatchNorm query: the reference's op sequence on the CPU
+    (oracle.pkm_layer, reference_ops) and the drop-in module on the GPU."""
+    import torch
+
+    from modelos_amd.pkm.memory import HashingMemory
+    from oracle import pkm_layer
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    torch.manual_seed(0)
+    mem = HashingMemory(input_dim=1024, output_dim=1024, mem_k_dim=512, mem_heads=4, mem_knn=32, mem_n_keys=256,
+                        mem_query_batchnorm=True, mem_query_rmsnorm=False)
+    mem.reset_parameters()
+    g = torch.Generator().manual_seed(0)
+    with torch.no_grad():
+        mem.keys.copy_((torch.rand(mem.keys.shape, generator=g) * 2 - 1) / 16)
+        mem.values.weight.copy_(torch.randn(mem.values.weight.shape, generator=g) * 1024**-0.5)
+    x = torch.randn((4, 512, 1024), generator=g)
+    P = {n: p.detach() for n, p in mem.named_parameters()}
+
+    def cpu_step():
+        with torch.no_grad():
+            pkm_layer.hashing_memory_forward(x, P, 4, 32, batchnorm=True, reference_ops=True)
+
+    t_cpu, reps = timed_median(cpu_step, budget_s=budget_s)
+    memd = mem.to(dev).train()
+    xd = x.to(dev)
+    with torch.no_grad():
+        for _ in range(3):
+            memd(xd)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            memd(xd)
+        torch.cuda.synchronize()
+    t_gpu = (time.perf_counter() - t0) / args.steps
+    return {
+        "workload": "PKM layer forward, float32, x [4, 512, 1024], 4 heads x 256 keys/half, k_dim 512, knn 32, "
+                    "v_dim 1024, BatchNorm query",
+        "gpu_ms": round(t_gpu * 1e3, 4), "gpu_tokens_per_s": round(2048 / t_gpu, 1),
+        "cpu_baseline": {"value": round(2048 / t_cpu, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+                         "sample": f"the whole forward (2048 tokens), median of {reps} after 1 warm-up; torch CPU "
+                         f"ops of the reference's path on {cores} threads ({cpu_model()})",
+                         "ms_per_step": round(t_cpu * 1e3, 1)},
+    }
+
+
+# ---------------------------------------------------------------------------
+# Model step: a Qwen3-0.6B-shaped decoder with PKM layers
+# ---------------------------------------------------------------------------
+def run_model(args, dev):
+    """A Qwen3-0.6B-shaped decoder (hidden 1024, 28 layers, 16 query / 8 KV
+    heads, head_dim 128, MLP 3072, vocab 151936; transformers' Qwen3 modules,
+    random init) whose layers 8 and 20 replace the MLP with the drop-in
+    HashingMemory (8 heads, 1024 keys per half, knn 32, value dim 1024, as
+    modeling_qwen3pkm.py:319-329 and :700-707 wire it): one train step
+    (forward, causal-LM loss, backward) on 8 x 2048 uniform token ids, bf16."""
+    import torch
+    from torch import nn
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    from modelos_amd.pkm.memory import HashingMemory
+
+    class PkmBlock(nn.Module):
+        """The decoder layer's feed-forward slot: hidden_states, _ = self.pkm(hidden_states)."""
+
+        def __init__(self, mem):
+            super().__init__()
+            self.pkm = mem
+
+        def forward(self, h):
+            out, _ = self.pkm(h)
+            return out
+
+    cfg = Qwen3Config(hidden_size=1024, num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
+                      head_dim=128, intermediate_size=3072, vocab_size=151936, max_position_embeddings=4096,
+                      tie_word_embeddings=True, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen3ForCausalLM(cfg)
+        for i in (8, 20):
+            mem = HashingMemory(input_dim=1024, output_dim=1024, mem_k_dim=512, mem_v_dim=1024, mem_heads=8,
+                                mem_knn=32, mem_n_keys=1024, mem_share_values=False, mem_query_rmsnorm=True)
+            mem.reset_parameters()
+            model.model.layers[i].mlp = PkmBlock(mem)
+    model = model.to(torch.bfloat16).train()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    ids = torch.randint(0, cfg.vocab_size, (8, 2048), generator=gen, device=dev)
+    n_params = sum(p.numel() for p in model.parameters())
+    log(f"model ready: {n_params / 1e6:.1f} M parameters, PKM at layers 8 and 20")
 
     def step():
-        V.grad = psw.grad = psw2.grad = None
-        hyp = xeb(idx, V, psw)
-        mem_loss = ((hyp - targets) ** 2).mean(-1).mean() * 0.5
-        (gV,) = torch.autograd.grad(mem_loss, V, create_graph=True)
-        Vn, _ = sgd_value_update(V, gV, idx, scale, lr, 0.0, False)
-        xeb(idx2, Vn, psw2).backward(dout)
+        model.zero_grad(set_to_none=True)
+        out = model(input_ids=ids, labels=ids)
+        out.loss.backward()
+        return out.loss.detach()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    timer = _lib.CallTimer()
     t0 = time.perf_counter()
-    with timer:
-        for _ in range(args.steps):
-            step()
+    for _ in range(args.steps):
+        loss = step()
     torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    calls = timer.summary()
-    kernels = {}
-    for name in ("pkm_eb_fwd", "pkm_eb_bwd", "pkm_eb_bwd2", "pkm_fw_sgd_update"):
-        keys = [k for k in calls if k[0] == name]
-        if keys:
-            tot = sum(sum(calls[k]) for k in keys) / args.steps
-            kernels[name] = {"ms_per_step": round(tot, 4), "calls_per_step": sum(len(calls[k]) for k in keys) // args.steps}
-    b2 = sorted(next(c for k, c in calls.items() if k[0] == "pkm_eb_bwd2"))
-    b2_ms = b2[len(b2) // 2]
-    work = N * L * D * 4 + 2 * N * D * 4 + N * L * (8 + 8)  # g-bar rows, upstream gradient in/out, ids and weights
-    achieved = work / (b2_ms * 1e-3) / 1e9
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; grad-of-grad {b2_ms:.3f} ms")
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"model step: {ms:.2f} ms, loss {float(loss):.3f}")
     return {
-        "metric": "FwPKM inner update + outer backward (grad-of-grad) tokens/sec, float32",
-        "value": round(N / (ms_per_step * 1e-3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (uniform indices, softmax weights, N(0,1) targets and upstream gradient)",
-        "config": {"workload": "fast-weight PKM value retrieval, inner update, outer backward through it",
-                   "tokens": N, "heads": H, "knn": knn, "num_rows": K, "v_dim": D, "lr": lr},
-        "roofline": {"bound": "hbm", "kernel": "pkm_eb_bwd2", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
-        "kernels": kernels,
-        "cpu_baseline": None,
+        "metric": "Qwen3-0.6B-shaped decoder with 2 PKM layers, train step tokens/sec, bf16",
+        "value": round(16384 / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (uniform token ids, random init)",
+        "config": {"workload": "Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads, MLP 3072, vocab "
+                               "151936), FFN of layers 8 and 20 replaced by PKM (8 heads, 2^20 slots, knn 32, "
+                               "v_dim 1024); forward + causal-LM loss + backward, no optimizer",
+                   "batch": 8, "seq_len": 2048, "parameters": n_params},
+        "roofline": None, "cpu_baseline": None,
     }
 
 
@@ -589,8 +785,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate", "fwpkm"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate", "fwpkm", "model"], default="layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="layer workload: skip the extra measurements (standalone embedding bag, fast-weight "
+                    "layer, the CPU parity configuration)")
     ap.add_argument(
         "--copy-probe-mib", type=int, default=0,
         help="run one plain elementwise copy (torch.neg, fp32) of this many MiB first; "
@@ -617,8 +816,23 @@ def main():
         torch.cuda.synchronize()
         del src, dst
         log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
-    runs = {"layer": run_layer, "eb": run_eb, "fwupdate": run_fwupdate, "fwpkm": run_fwpkm}
+    runs = {"layer": run_layer, "eb": run_eb, "fwupdate": run_fwupdate, "fwpkm": run_fwpkm_workload,
+            "model": run_model}
     res = runs[args.workload](args, dev)
+    if args.workload == "layer" and not args.no_extras:
+        # the other benchmark configurations, reported beside the headline (not part of `value`)
+        torch.cuda.empty_cache()
+        log("extra: standalone embedding bag ...")
+        eb = run_eb(args, dev)
+        res["eb_standalone"] = {k: eb[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline",
+                                                    "kernels", "cpu_baseline")}
+        torch.cuda.empty_cache()
+        log("extra: fast-weight PKM layer ...")
+        res["fwpkm"] = run_fwpkm(args, dev)
+        torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            log("extra: CPU parity configuration ...")
+            res["cpu_parity_config"] = cpu_parity_config(args, dev)
     print(json.dumps(res), flush=True)
 
 
