@@ -45,6 +45,7 @@
 // L2) serves one head's keys.
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "pkm_common.h"
 
@@ -1042,6 +1043,429 @@ __global__ __launch_bounds__(kThreads) void pkm_score_cartesian_kernel(int64_t r
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming scoring: bfloat16 dot scores, knn <= 32, half key dim 128 or 256.
+//
+// One workgroup (4 waves, one per SIMD) owns 256 tokens of one (head, half).
+// The keys of the half stream through LDS in blocks of 64 (double-buffered,
+// direct global->LDS loads, every key read once per workgroup). A wave
+// multiplies them with its 64 tokens' query halves, held in accumulation
+// registers, on 32x32x16 bf16 MFMA: A = 32 keys from LDS (read four steps
+// ahead), B = 32 tokens, and the wave's two token sets share every A
+// fragment. v_permlane32_swap then gives each lane the scores of one token:
+// lane l owns token l of the wave for the whole stream, and a block's 64
+// scores of a lane are 32 words of two bf16.
+//
+// Selection per lane, exact, on the unique keys
+// (order key of the bf16 score << 16) | (0xFFFF - key index):
+//   * T: the best 32 keys merged so far, sorted, in registers; theta =
+//     T[knn - 1] (0 while fewer than knn are merged).
+//   * Every score whose bf16 value can reach theta is appended to the lane's
+//     LDS slots, branch-free (the slot is written, the count moves on a
+//     pass). The test is one float compare of the raw word
+//     (bf16 bits << 16) | (0xFFFF - index) against tau, the smallest raw word
+//     of theta's value (NaN while theta = 0, which nothing is below): a raw
+//     word is a float within its bf16 value's rounding interval, so every key
+//     >= theta passes, and some equal-valued keys below theta too. A block's
+//     appends run between the MFMAs of the next block.
+//   * After each block the workgroup merges if any of its lanes holds 28
+//     slots (all waves at once, at the block's barrier): up to two chunks of
+//     32 slots become keys (-0 counted as +0), are sorted by Batcher's
+//     odd-even merge sort (191 compare-exchanges), and the best 32 of T and
+//     a chunk, max(T[i], C[31 - i]), are sorted by a bitonic half-cleaner
+//     cascade.
+// T[0 .. knn) is the half's list, stored (through an LDS transpose, two
+// tokens' rows per store) as the low (first half) or high (second half) word
+// of the index output, for the cartesian kernel below.
+// ---------------------------------------------------------------------------
+namespace stream {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTok = 64 * kWaves;  // tokens per workgroup
+constexpr int kKB = 64;            // keys per staged block
+constexpr int kBuf = 92;           // appended-score slots per token
+constexpr int kNet = 32;           // length of the sorted list
+
+struct CeNet {
+  int n;
+  uint8_t a[192], b[192];
+};
+// Batcher's odd-even merge sort on N elements.
+constexpr CeNet oem_net(int N) {
+  CeNet t{};
+  for (int p = 1; p < N; p <<= 1)
+    for (int k = p; k >= 1; k >>= 1)
+      for (int j = k % p; j + k < N; j += 2 * k)
+        for (int i = 0; i < k && i + j + k < N; ++i)
+          if ((i + j) / (2 * p) == (i + j + k) / (2 * p)) {
+            t.a[t.n] = (uint8_t)(i + j);
+            t.b[t.n] = (uint8_t)(i + j + k);
+            ++t.n;
+          }
+  return t;
+}
+// Half-cleaner cascade: sorts a bitonic sequence of N elements.
+constexpr CeNet clean_net(int N) {
+  CeNet t{};
+  for (int j = N / 2; j >= 1; j >>= 1)
+    for (int i = 0; i < N; ++i)
+      if (!(i & j)) {
+        t.a[t.n] = (uint8_t)i;
+        t.b[t.n] = (uint8_t)(i + j);
+        ++t.n;
+      }
+  return t;
+}
+constexpr CeNet kSort32 = oem_net(32);
+constexpr CeNet kClean32 = clean_net(32);
+static_assert(kSort32.n == 191 && kClean32.n == 80, "network sizes");
+
+__device__ __forceinline__ void ce_desc(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+// (positions as template arguments: register indices fixed at compile time)
+template <int A, int B>
+__device__ __forceinline__ void ce_at(uint32_t (&x)[32]) {
+  ce_desc(x[A], x[B]);
+}
+template <size_t... I>
+__device__ __forceinline__ void sort32_desc(uint32_t (&x)[32], std::index_sequence<I...>) {
+  (ce_at<kSort32.a[I], kSort32.b[I]>(x), ...);
+}
+template <size_t... I>
+__device__ __forceinline__ void clean32_desc(uint32_t (&x)[32], std::index_sequence<I...>) {
+  (ce_at<kClean32.a[I], kClean32.b[I]>(x), ...);
+}
+
+// Key of a raw slot word (bf16 bits << 16 | inverted index); -0 counts as +0.
+__device__ __forceinline__ uint32_t raw_key(uint32_t r) {
+  const uint32_t sgn = (uint32_t)((int32_t)r >> 31);
+  uint32_t k = r ^ ((sgn & 0x7FFF0000u) | 0x80000000u);
+  k += ((k >> 16) == 0x7FFFu) ? 0x10000u : 0u;  // okey16(-0) = 0x7FFF, directly below okey16(+0)
+  return k;
+}
+// The smallest raw word (as a float) whose bf16 value is that of key th; NaN
+// for th = 0, so that every score passes.
+__device__ __forceinline__ float raw_floor(uint32_t th) {
+  const uint32_t ok = th >> 16;
+  uint32_t b = okey16_inv(ok);
+  if (ok == 0x8000u) b = 0x8000u;  // +0 stands for the -0 slots too
+  return __uint_as_float((b << 16) | ((b & 0x8000u) ? 0xFFFFu : 0u));
+}
+// a pair of bf16 scores with -0 written as +0
+__device__ __forceinline__ uint32_t canon_pair(uint32_t p) {
+  if ((p & 0xFFFFu) == 0x8000u) p &= 0xFFFF0000u;
+  if ((p >> 16) == 0x8000u) p &= 0xFFFFu;
+  return p;
+}
+
+// Merge slots [J0, J0 + 32) (those below cnt) into T.
+template <int J0>
+__device__ __forceinline__ void merge_chunk(uint32_t (&T)[kNet], const uint32_t* buf, uint32_t cnt) {
+  uint32_t C[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const uint32_t r = buf[(J0 + j) * kThreads];
+    C[j] = (uint32_t)(J0 + j) < cnt ? raw_key(r) : 0u;
+  }
+  sort32_desc(C, std::make_index_sequence<191>{});
+#pragma unroll
+  for (int j = 0; j < 32; ++j) T[j] = T[j] > C[31 - j] ? T[j] : C[31 - j];
+  clean32_desc(T, std::make_index_sequence<80>{});
+}
+// tau of theta = T[knn - 1], the smallest of T[0 .. knn) (T is sorted; a
+// minimum rather than an indexed pick keeps T in registers)
+__device__ __forceinline__ float tau_of(const uint32_t (&T)[kNet], int knn) {
+  uint32_t th = T[0];
+#pragma unroll
+  for (int j = 1; j < kNet; ++j) {
+    const uint32_t v = j < knn ? T[j] : 0xFFFFFFFFu;
+    th = th < v ? th : v;
+  }
+  return raw_floor(th);
+}
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Slot budget. Merges are decided once per 64-key block for the whole
+// workgroup. At the start of a block every lane holds at most kTrigger - 1
+// unmerged slots (a merge takes slots [0, 64) and leaves max(cnt - 64, 0)),
+// and a block appends at most 64, so kTrigger + 63 slots suffice; the merge
+// moves slots [64, kBuf) to the front.
+constexpr int kTrigger = 28;
+static_assert(kTrigger + 63 <= kBuf && kBuf - 64 >= kTrigger - 1, "slot budget");
+
+// A block's 64 scores of a lane are 32 words of two bf16: word w = 16 kt + 2 j
+// + v holds keys word_key(w) and word_key(w) + 1 of the block (tile kt,
+// elements 2j and 2j + 1 of the MFMA output, swap half v).
+__host__ __device__ constexpr int word_key(int w) {
+  return 32 * (w >> 4) + 8 * ((w >> 2) & 3) + 4 * (w & 1) + 2 * ((w >> 1) & 1);
+}
+
+// Append the two scores of word p (keys key, key + 1) that can reach theta.
+__device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* buf, uint32_t& cnt, float tau,
+                                            uint32_t hi_mask) {
+  const uint32_t r0 = (p << 16) | (0xFFFFu - key);
+  const uint32_t r1 = (p & hi_mask) | (0xFFFEu - key);
+  buf[cnt * kThreads] = r0;
+  cnt += !(__uint_as_float(r0) < tau);
+  buf[cnt * kThreads] = r1;
+  cnt += !(__uint_as_float(r1) < tau);
+}
+
+// Words 16 KT + 2 J + {0, 1} from elements 2J, 2J + 1 of the token-set
+// accumulators A0, A1: the swap gives lane l token l's scores (element e of
+// A0 for swap half 0, of A1 for half 1).
+#define PKM_STREAM_WORDS(A0, A1, KT, J)                                                                      \
+  {                                                                                                          \
+    const auto s0_ = __builtin_amdgcn_permlane32_swap(__float_as_uint((A0)[2 * (J)]),                        \
+                                                      __float_as_uint((A1)[2 * (J)]), false, false);         \
+    const auto s1_ = __builtin_amdgcn_permlane32_swap(__float_as_uint((A0)[2 * (J) + 1]),                    \
+                                                      __float_as_uint((A1)[2 * (J) + 1]), false, false);     \
+    P[16 * (KT) + 2 * (J)] = pack2_bf16(__uint_as_float(s0_[0]), __uint_as_float(s1_[0]));                   \
+    P[16 * (KT) + 2 * (J) + 1] = pack2_bf16(__uint_as_float(s0_[1]), __uint_as_float(s1_[1]));               \
+  }
+
+// global_load_lds_dwordx4: lane i's 16 bytes at src go to LDS at dst + 16 i
+// (dst wave-uniform). Issued as inline assembly, so that the compiler's
+// waitcnt tracking does not treat every later LDS read as dependent on it
+// (which turns its lgkmcnt waits into lgkmcnt(0)); the caller waits with
+// s_waitcnt vmcnt(0) before the barrier that publishes the data.
+// The LDS offset of dst is the low word of its flat address; M0 (reserved to
+// the compiler) is restored after the load has read it.
+__device__ __forceinline__ void dma16(const void* src, unsigned char* dst) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)dst);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(m0v)
+      : "memory");
+}
+
+// Key block B (64 rows of HALF bf16) into the LDS block at byte pointer DST by
+// direct global->LDS loads: load j of wave w fills the 16-byte chunks
+// (w LOADS + j) 64 + lane of the block, and chunk slot q of row r holds the
+// row's chunk q ^ (r & 15), so that the rows an LDS read serves hit distinct
+// banks.
+#define PKM_STREAM_STAGE(B, DST)                                                                       \
+  {                                                                                                   \
+    const int b_ = (B);                                                                               \
+    unsigned char* d_ = (DST);                                                                        \
+    _Pragma("unroll") for (int l_ = 0; l_ < LOADS; ++l_) {                                            \
+      const int p_ = (w * LOADS + l_) * 64 + lane;                                                    \
+      const int r_ = p_ / CPR, q_ = p_ % CPR;                                                         \
+      const uint16_t* src_ = kb + (int64_t)(b_ * kKB + r_) * HALF + (q_ ^ (r_ & 15)) * 8;            \
+      dma16(src_, d_ + (w * LOADS + l_) * 1024);                                                      \
+    }                                                                                                 \
+  }
+
+// Q [Ntok, H, 2 HALF], Kt [2 H n, HALF] (bf16 bits); lists: out_idx as 32-bit
+// words; out_i1/out_i2 [Ntok, H, knn]; with SUB, out_s1/out_s2 [Ntok, H, n]
+// as pairs of bf16.
+template <int KS, bool SUB>
+__global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kt, int64_t Ntok, int H, int n, int knn,
+    uint32_t* __restrict__ lists, int64_t* __restrict__ out_i1, int64_t* __restrict__ out_i2,
+    uint32_t* __restrict__ out_s1, uint32_t* __restrict__ out_s2) {
+  constexpr int HALF = 16 * KS;
+  constexpr int CPR = HALF / 8;               // 16-byte chunks per key row
+  constexpr int BLK = kKB * HALF * 2;         // bytes per staged block
+  constexpr int LOADS = BLK / 1024 / kWaves;  // 1 KB global->LDS loads per wave per block
+  constexpr int STEPS = 2 * KS;               // MFMA steps per block: tile 0's k-steps, then tile 1's
+  constexpr int WPS = 32 / STEPS;             // words appended per step
+  constexpr int LOOK = 4;                     // A fragments read this many steps ahead
+  static_assert(LOADS * 1024 * kWaves == BLK && CPR >= 16 && WPS * STEPS == 32, "block layout");
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* kst = smem;                                  // [2][kKB][CPR] 16-byte chunks
+  uint32_t* buf = (uint32_t*)(smem + 2 * BLK) + threadIdx.x;  // slot j at buf[j * kThreads]
+  uint32_t* flags = (uint32_t*)(smem + 2 * BLK) + kBuf * kThreads;  // [2][kWaves]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H2 = 2 * H;
+  // (half, head) fastest, head fastest of all: workgroups go round-robin to
+  // the 8 XCDs, so with H a multiple of 8 an XCD's L2 serves fixed heads,
+  // both halves (whose lists share the output's cache lines)
+  const int hc = (int)(blockIdx.x % (unsigned)H2);
+  const int64_t tile = blockIdx.x / (unsigned)H2;
+  const int h = hc % H, c = hc / H;
+  const int hk = 2 * h + c;                 // key rows (2h + c) n .. of this head-half
+  const int64_t tw = tile * kTok + 64 * w;  // first token of this wave
+
+  // B fragments: token set u is tokens tw + 32 u + lane % 32; k = 16 s + 8 (lane / 32)
+  u32x4_t bq[2][KS];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t t = tw + 32 * u + (lane & 31);
+    const uint16_t* qr = Q + ((t < Ntok ? t : 0) * H + h) * (2 * HALF) + c * HALF + 8 * (lane >> 5);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bq[u][s] = *(const u32x4_t*)(qr + 16 * s);
+    if (t >= Ntok) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) bq[u][s] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  // the B fragments live in accumulation registers (MFMA reads them there),
+  // leaving the arch VGPRs to the selection and the A fragments
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" : "+a"(bq[u][s]));
+  // byte offset of A chunk 2 s + lane / 32 in the lane's (swizzled) row, s < 8;
+  // s >= 8 adds 256 (the row's second 16 chunks)
+  int aoff[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) aoff[s] = ((2 * s + (lane >> 5)) ^ (lane & 15)) * 16;
+
+  const uint16_t* kb = Kt + (int64_t)hk * n * HALF;
+  const int nb = n / kKB;
+
+  uint32_t T[kNet];
+#pragma unroll
+  for (int i = 0; i < kNet; ++i) T[i] = 0u;
+  uint32_t P[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) P[i] = 0u;
+  uint32_t cnt = 0;
+  // +inf while P holds no scores (its zero words stay below it), NaN (every
+  // score passes) from the first block's words until the first merge
+  float tau = __uint_as_float(0x7F800000u);
+  const int64_t tok = tw + lane;  // this lane's token once the scores are swapped
+  const bool live = tok < Ntok;
+  uint32_t* srow = nullptr;
+  if constexpr (SUB) {
+    uint32_t* out_s = c == 0 ? out_s1 : out_s2;
+    srow = out_s + (live ? tok * H + h : 0) * (n / 2);
+  }
+  // 0xFFFF0000 in a register: v_and_or_b32 takes it beside the scalar index
+  uint32_t hi_mask = 0xFFFF0000u;
+  asm volatile("" : "+v"(hi_mask));
+
+  PKM_STREAM_STAGE(0, kst);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Iteration j < nb: the MFMAs of block j interleaved with the appends of
+  // block j - 1's words (P), which are replaced by block j's as its tiles
+  // complete; block j + 1 is staged meanwhile. Iteration nb appends block
+  // nb - 1's words. After each iteration the workgroup merges if any of its
+  // lanes holds kTrigger slots (the waves decide together at the barrier, so
+  // that they merge at the same time); after the last, each wave merges until
+  // its slots are empty.
+#pragma unroll 1
+  for (int j = 0; j <= nb; ++j) {
+    if (j < nb) {
+      const unsigned char* kcur = kst + (j & 1) * BLK;
+      if (j + 1 < nb) {
+        PKM_STREAM_STAGE(j + 1, kst + ((j + 1) & 1) * BLK);
+      }
+      const uint32_t kprev = (uint32_t)(j - 1) * kKB;  // key base of the words being appended
+      const unsigned char* ar = kcur + (lane & 31) * (CPR * 16);
+      f32x16_t X[2][2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) X[kt][u] = f32x16_t{};
+      u32x4_t A[STEPS];
+#pragma unroll
+      for (int t = 0; t < LOOK; ++t)
+        A[t] = *(const u32x4_t*)(ar + (t / KS) * 32 * CPR * 16 + aoff[(t % KS) & 7] + ((t % KS) >> 3) * 256);
+#pragma unroll
+      for (int t = 0; t < STEPS; ++t) {
+        const int kt = t / KS, st = t % KS;
+        if (t + LOOK < STEPS) {
+          const int t2 = t + LOOK;
+          A[t2] = *(const u32x4_t*)(ar + (t2 / KS) * 32 * CPR * 16 + aoff[(t2 % KS) & 7] + ((t2 % KS) >> 3) * 256);
+        }
+        X[kt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, A[t]),
+                                                           __builtin_bit_cast(bf16x8_t, bq[0][st]), X[kt][0], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < WPS; ++q)
+          append_pair(P[t * WPS + q], kprev + word_key(t * WPS + q), buf, cnt, tau, hi_mask);
+        X[kt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, A[t]),
+                                                           __builtin_bit_cast(bf16x8_t, bq[1][st]), X[kt][1], 0, 0, 0);
+        if (t >= KS) {
+          // tile 0 is complete: its words replace the appended ones
+#pragma unroll
+          for (int jj = ((t - KS) * 8) / KS; jj < ((t - KS + 1) * 8) / KS; ++jj) PKM_STREAM_WORDS(X[0][0], X[0][1], 0, jj);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) PKM_STREAM_WORDS(X[1][0], X[1][1], 1, jj);
+      if constexpr (SUB) {
+        if (live) {
+#pragma unroll
+          for (int q = 0; q < 32; ++q) srow[(j * kKB + word_key(q)) >> 1] = canon_pair(P[q]);
+        }
+      }
+      if (j == 0) tau = __uint_as_float(0xFFFFFFFFu);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 32; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, cnt, tau, hi_mask);
+    }
+    bool need;
+    if (j < nb) {
+      const bool mine = __builtin_amdgcn_ballot_w64(cnt >= (uint32_t)kTrigger) != 0;
+      if (lane == 0) flags[(j & 1) * kWaves + w] = mine ? 1u : 0u;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      uint32_t any = 0;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) any |= flags[(j & 1) * kWaves + v];
+      need = any != 0;
+    } else {
+      need = __builtin_amdgcn_ballot_w64(cnt > 0u) != 0;
+    }
+    while (need) {
+      merge_chunk<0>(T, buf, cnt);
+      if (__builtin_amdgcn_ballot_w64(cnt > 32u) != 0) merge_chunk<32>(T, buf, cnt);
+#pragma unroll
+      for (int q = 0; q < kBuf - 64; ++q) buf[q * kThreads] = buf[(64 + q) * kThreads];
+      cnt = cnt > 64u ? cnt - 64u : 0u;
+      tau = tau_of(T, knn);
+      need = j == nb && __builtin_amdgcn_ballot_w64(cnt > 0u) != 0;
+    }
+  }
+
+  // Outputs through a [64][33] word tile per wave (LDS is idle once every wave
+  // has merged), so that a store covers two tokens' contiguous rows: lane i
+  // writes word i % 32 of token 2 m + i / 32 of the wave.
+  __syncthreads();
+  uint32_t* tp = (uint32_t*)smem + w * (64 * 33);
+#pragma unroll
+  for (int q = 0; q < kNet; ++q) tp[lane * 33 + q] = T[q];
+  __builtin_amdgcn_wave_barrier();
+  int64_t* oi = c == 0 ? out_i1 : out_i2;
+  const int q = lane & 31;
+#pragma unroll 4
+  for (int m = 0; m < 32; ++m) {
+    const int tl = 2 * m + (lane >> 5);
+    const int64_t t = tw + tl;
+    const uint32_t k = tp[tl * 33 + q];
+    if (t < Ntok && q < knn) {
+      lists[(t * H + h) * (2 * (int64_t)knn) + 2 * q + c] = k;
+      if (oi != nullptr) oi[(t * H + h) * knn + q] = (int64_t)(0xFFFFu - (k & 0xFFFFu));
+    }
+  }
+}
+#undef PKM_STREAM_STAGE
+#undef PKM_STREAM_WORDS
+
+__host__ inline size_t lds_bytes(int half) {
+  return (size_t)2 * kKB * half * 2 + (size_t)kBuf * kThreads * 4 + 2 * kWaves * 4;
+}
+
+}  // namespace stream
+
 constexpr int kCartLpr = 8;  // lanes per row of the cartesian kernel
 __host__ inline size_t cartesian_lds_bytes(int knn) {
   const int kl = (knn + 3) & ~3;
@@ -1064,6 +1488,28 @@ static int enable_lds(const void* fn, int bytes, std::atomic<uint64_t>& done, co
   return PKM_OK;
 }
 
+// The cartesian step of the packed lists (32-bit keys: bf16 scores). The LDS
+// attribute is set once per device, to the device maximum, so that every
+// knn's layout fits.
+template <typename TIN>
+static int launch_cartesian(int64_t Ntok, int H, int n, int knn, int lds_max, void* out_scores, int64_t* out_idx,
+                            hipStream_t st) {
+  static_assert(sizeof(typename Sel<TIN>::Key) == 4, "packed lists need 32-bit keys");
+  static std::atomic<uint64_t> cart_lds_enabled{0};
+  const size_t cl = cartesian_lds_bytes(knn);
+  if ((int)cl > lds_max)
+    return pkm_set_error(PKM_ERR_UNSUPPORTED, "pkm_score_topk: knn %d needs %zu bytes of LDS for the cartesian step",
+                         knn, cl);
+  const int rc = enable_lds((const void*)pkm_score_cartesian_kernel<TIN, kCartLpr>, lds_max, cart_lds_enabled,
+                            "pkm_score_topk");
+  if (rc != PKM_OK) return rc;
+  const int64_t rows = Ntok * H;
+  const int64_t cblocks = (rows + kThreads / kCartLpr - 1) / (kThreads / kCartLpr);
+  hipLaunchKernelGGL((pkm_score_cartesian_kernel<TIN, kCartLpr>), dim3((unsigned)cblocks), dim3(kThreads), cl, st,
+                     rows, n, knn, (TIN*)out_scores, out_idx);
+  return PKM_OK;
+}
+
 template <typename TIN, int IDW, int TM, int KSC>
 static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
                            size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
@@ -1078,24 +1524,26 @@ static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H,
                        (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
                        out_i2, (TIN*)out_s1, (TIN*)out_s2);
   }
-  if constexpr (sizeof(typename Sel<TIN>::Key) == 4) {
-    // the cartesian step of the packed lists
-    // (the attribute is set once per device: to the device maximum, so that
-    // every knn's layout fits)
-    static std::atomic<uint64_t> cart_lds_enabled{0};
-    const size_t cl = cartesian_lds_bytes(knn);
-    if ((int)cl > lds_max)
-      return pkm_set_error(PKM_ERR_UNSUPPORTED, "pkm_score_topk: knn %d needs %zu bytes of LDS for the cartesian step",
-                           knn, cl);
-    rc = enable_lds((const void*)pkm_score_cartesian_kernel<TIN, kCartLpr>, lds_max, cart_lds_enabled,
-                    "pkm_score_topk");
-    if (rc != PKM_OK) return rc;
-    const int64_t rows = Ntok * H;
-    const int64_t cblocks = (rows + kThreads / kCartLpr - 1) / (kThreads / kCartLpr);
-    hipLaunchKernelGGL((pkm_score_cartesian_kernel<TIN, kCartLpr>), dim3((unsigned)cblocks), dim3(kThreads), cl, st,
-                       rows, n, knn, (TIN*)out_scores, out_idx);
-  }
+  if constexpr (sizeof(typename Sel<TIN>::Key) == 4) return launch_cartesian<TIN>(Ntok, H, n, knn, lds_max, out_scores, out_idx, st);
   return PKM_OK;
+}
+
+// The streaming kernel (bf16 dot, knn <= 32), then the cartesian step.
+template <int KS, bool SUB>
+static int launch_stream(const void* q, const void* keys, int64_t Ntok, int H, int n, int knn, int lds_max,
+                         void* out_scores, int64_t* out_idx, int64_t* out_i1, int64_t* out_i2, void* out_s1,
+                         void* out_s2, hipStream_t st) {
+  static std::atomic<uint64_t> lds_enabled{0};
+  int rc = enable_lds((const void*)stream::pkm_score_stream_kernel<KS, SUB>, lds_max, lds_enabled, "pkm_score_topk");
+  if (rc != PKM_OK) return rc;
+  const int64_t blocks = ((Ntok + stream::kTok - 1) / stream::kTok) * 2 * H;
+  {
+    KernelSpan span("score_topk", st);
+    hipLaunchKernelGGL((stream::pkm_score_stream_kernel<KS, SUB>), dim3((unsigned)blocks), dim3(stream::kThreads),
+                       stream::lds_bytes(16 * KS), st, (const uint16_t*)q, (const uint16_t*)keys, Ntok, H, n, knn,
+                       (uint32_t*)out_idx, out_i1, out_i2, (uint32_t*)out_s1, (uint32_t*)out_s2);
+  }
+  return launch_cartesian<bf16_t>(Ntok, H, n, knn, lds_max, out_scores, out_idx, st);
 }
 
 // Kernel variant for (TM, k-steps per half): the k-step counts of the common
@@ -1171,6 +1619,19 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
   if (e != hipSuccess)
     return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: device query failed: %s", hipGetErrorString(e));
   if (lds_max > kMaxLds) lds_max = kMaxLds;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == PKM_DTYPE_BF16 && score_type == PKM_SCORE_DOT && knn <= stream::kNet && (half == 128 || half == 256) &&
+      (int)stream::lds_bytes((int)half) <= lds_max) {
+    const int64_t blocks = ((num_tokens + stream::kTok - 1) / stream::kTok) * 2 * heads;
+    PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: grid too large");
+    const bool sub = out_sub_scores1 != nullptr || out_sub_scores2 != nullptr;
+    auto* launch = half == 256 ? (sub ? launch_stream<16, true> : launch_stream<16, false>)
+                               : (sub ? launch_stream<8, true> : launch_stream<8, false>);
+    const int rc = launch(query, keys, num_tokens, (int)heads, (int)n_keys, (int)knn, lds_max, out_scores, out_indices,
+                          out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, st);
+    if (rc != PKM_OK) return rc;
+    return pkm_check_launch("pkm_score_topk");
+  }
   int TM = 64;
   while (TM > 16 && (score_lds_layout(TM, (int)n_keys, (int)half, (int)knn, esz, key_bytes).total > lds_max ||
                      n_keys > score_max_n(TM, esz)))
@@ -1181,7 +1642,6 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
               (long long)half, lds, lds_max);
   const int64_t blocks = ((num_tokens + TM - 1) / TM) * heads;
   PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: grid too large");
-  hipStream_t st = (hipStream_t)stream;
   int rc;
   const int H = (int)heads, n = (int)n_keys, hf = (int)half, k = (int)knn;
   if (dtype == PKM_DTYPE_BF16) {
