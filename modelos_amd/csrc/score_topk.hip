@@ -1140,19 +1140,23 @@ __device__ __forceinline__ void clean32_desc(uint32_t (&x)[32], std::index_seque
   (ce_at<kClean32.a[I], kClean32.b[I]>(x), ...);
 }
 
-// Key of a raw slot word (bf16 bits << 16 | inverted index); -0 counts as +0.
+// Inside the kernel keys use the order key okz(b) = b + 0x8000 for b >= 0 and
+// 0x10000 - b for negative b (okey16 + 1), under which -0 and +0 are both
+// 0x8000 and every other value keeps its order; 0 is no value's key. The lists
+// leave the kernel in okey16 form (okz - 1 below 0x8000).
+// Key of a raw slot word (bf16 bits << 16 | inverted index).
 __device__ __forceinline__ uint32_t raw_key(uint32_t r) {
   const uint32_t sgn = (uint32_t)((int32_t)r >> 31);
-  uint32_t k = r ^ ((sgn & 0x7FFF0000u) | 0x80000000u);
-  k += ((k >> 16) == 0x7FFFu) ? 0x10000u : 0u;  // okey16(-0) = 0x7FFF, directly below okey16(+0)
-  return k;
+  return (r ^ ((sgn & 0x7FFF0000u) | 0x80000000u)) + ((r >> 31) << 16);
 }
+__device__ __forceinline__ uint32_t key_to_okey16(uint32_t k) { return k - (k < 0x80000000u ? 0x10000u : 0u); }
 // The smallest raw word (as a float) whose bf16 value is that of key th; NaN
 // for th = 0, so that every score passes.
 __device__ __forceinline__ float raw_floor(uint32_t th) {
   const uint32_t ok = th >> 16;
-  uint32_t b = okey16_inv(ok);
-  if (ok == 0x8000u) b = 0x8000u;  // +0 stands for the -0 slots too
+  if (ok == 0u) return __uint_as_float(0xFFFFFFFFu);
+  // okz inverse; +0 (0x8000) stands for the -0 slots too, so it takes -0's bits
+  const uint32_t b = ok > 0x8000u ? ok - 0x8000u : 0x10000u - ok;
   return __uint_as_float((b << 16) | ((b & 0x8000u) ? 0xFFFFu : 0u));
 }
 // a pair of bf16 scores with -0 written as +0
@@ -1206,15 +1210,16 @@ __host__ __device__ constexpr int word_key(int w) {
   return 32 * (w >> 4) + 8 * ((w >> 2) & 3) + 4 * (w & 1) + 2 * ((w >> 1) & 1);
 }
 
-// Append the two scores of word p (keys key, key + 1) that can reach theta.
-__device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* buf, uint32_t& cnt, float tau,
+// Append the two scores of word p (keys key, key + 1) that can reach theta;
+// cb is the lane's slot count times the slot stride (kThreads words).
+__device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* buf, uint32_t& cb, float tau,
                                             uint32_t hi_mask) {
   const uint32_t r0 = (p << 16) | (0xFFFFu - key);
   const uint32_t r1 = (p & hi_mask) | (0xFFFEu - key);
-  buf[cnt * kThreads] = r0;
-  cnt += !(__uint_as_float(r0) < tau);
-  buf[cnt * kThreads] = r1;
-  cnt += !(__uint_as_float(r1) < tau);
+  *(uint32_t*)((unsigned char*)buf + cb) = r0;
+  cb += !(__uint_as_float(r0) < tau) ? kThreads * 4u : 0u;
+  *(uint32_t*)((unsigned char*)buf + cb) = r1;
+  cb += !(__uint_as_float(r1) < tau) ? kThreads * 4u : 0u;
 }
 
 // Words 16 KT + 2 J + {0, 1} from elements 2J, 2J + 1 of the token-set
@@ -1334,7 +1339,8 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   uint32_t P[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) P[i] = 0u;
-  uint32_t cnt = 0;
+  uint32_t cb = 0;  // slot count x slot stride in bytes
+  constexpr uint32_t SB = kThreads * 4u;
   // +inf while P holds no scores (its zero words stay below it), NaN (every
   // score passes) from the first block's words until the first merge
   float tau = __uint_as_float(0x7F800000u);
@@ -1389,7 +1395,7 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
                                                            __builtin_bit_cast(bf16x8_t, bq[0][st]), X[kt][0], 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < WPS; ++q)
-          append_pair(P[t * WPS + q], kprev + word_key(t * WPS + q), buf, cnt, tau, hi_mask);
+          append_pair(P[t * WPS + q], kprev + word_key(t * WPS + q), buf, cb, tau, hi_mask);
         X[kt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, A[t]),
                                                            __builtin_bit_cast(bf16x8_t, bq[1][st]), X[kt][1], 0, 0, 0);
         if (t >= KS) {
@@ -1410,11 +1416,11 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
       if (j == 0) tau = __uint_as_float(0xFFFFFFFFu);
     } else {
 #pragma unroll
-      for (int q = 0; q < 32; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, cnt, tau, hi_mask);
+      for (int q = 0; q < 32; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, cb, tau, hi_mask);
     }
     bool need;
     if (j < nb) {
-      const bool mine = __builtin_amdgcn_ballot_w64(cnt >= (uint32_t)kTrigger) != 0;
+      const bool mine = __builtin_amdgcn_ballot_w64(cb >= kTrigger * SB) != 0;
       if (lane == 0) flags[(j & 1) * kWaves + w] = mine ? 1u : 0u;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -1423,16 +1429,17 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
       for (int v = 0; v < kWaves; ++v) any |= flags[(j & 1) * kWaves + v];
       need = any != 0;
     } else {
-      need = __builtin_amdgcn_ballot_w64(cnt > 0u) != 0;
+      need = __builtin_amdgcn_ballot_w64(cb > 0u) != 0;
     }
     while (need) {
+      const uint32_t cnt = cb / SB;
       merge_chunk<0>(T, buf, cnt);
       if (__builtin_amdgcn_ballot_w64(cnt > 32u) != 0) merge_chunk<32>(T, buf, cnt);
 #pragma unroll
       for (int q = 0; q < kBuf - 64; ++q) buf[q * kThreads] = buf[(64 + q) * kThreads];
-      cnt = cnt > 64u ? cnt - 64u : 0u;
+      cb = cnt > 64u ? cb - 64u * SB : 0u;
       tau = tau_of(T, knn);
-      need = j == nb && __builtin_amdgcn_ballot_w64(cnt > 0u) != 0;
+      need = j == nb && __builtin_amdgcn_ballot_w64(cb > 0u) != 0;
     }
   }
 
@@ -1442,7 +1449,7 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   __syncthreads();
   uint32_t* tp = (uint32_t*)smem + w * (64 * 33);
 #pragma unroll
-  for (int q = 0; q < kNet; ++q) tp[lane * 33 + q] = T[q];
+  for (int q = 0; q < kNet; ++q) tp[lane * 33 + q] = key_to_okey16(T[q]);
   __builtin_amdgcn_wave_barrier();
   int64_t* oi = c == 0 ? out_i1 : out_i2;
   const int q = lane & 31;
