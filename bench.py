@@ -83,9 +83,18 @@ def cpu_model():
 
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = {}
         for line in out.splitlines():
-            if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields.setdefault(k.strip(), v.strip())
+        name = fields.get("Model name")
+        if name:
+            if not any(ch.isdigit() for ch in name):
+                # a generic name (virtualised hosts): add lscpu's family / model / stepping numbers
+                ids = ", ".join(f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if k in fields)
+                name = f"{name} ({ids})" if ids else name
+            return name
     except (OSError, subprocess.SubprocessError):
         pass
     try:
@@ -176,7 +185,7 @@ def cpu_baseline_layer(mem, x, dout, budget_s=25.0):
         "kind": "port",
         "sample": f"{tokens} of the {total} tokens (same bf16 parameters and inputs), full 2^20 x 1024 value "
         f"table, fwd+bwd; median of {reps} after 1 warm-up; torch CPU ops of the reference's path on {cores} "
-        f"threads ({cpu_model()}, lscpu model name)",
+        f"threads ({cpu_model()})",
         "ms_per_step": round(t * 1e3, 1),
     }
 
@@ -256,7 +265,7 @@ def run_layer(args, dev):
         if note:
             kernels[name]["note"] = note
 
-    add("pkm_score_topk_kernel (scoring + per-half top-k)", ("kernel", "score_topk"), score_flops(tokens, H, n, k),
+    add("pkm_score_stream_kernel (scoring + per-half top-k)", ("kernel", "score_topk"), score_flops(tokens, H, n, k),
         "TFLOP/s", MFMA_BF16_PEAK_TFLOPS, "mfma")
     add("pkm_score_topk", ("pkm_score_topk", (tokens, H, n, k // 2)), score_flops(tokens, H, n, k), "TFLOP/s",
         MFMA_BF16_PEAK_TFLOPS, "mfma", "entry point: scoring + per-half top-k kernel, then the cartesian kernel")
@@ -285,7 +294,7 @@ def run_layer(args, dev):
     add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
     add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
     # single kernels timed inside an entry point are part of that entry's time
-    inner = ("pkm_score_topk_kernel (scoring + per-half top-k)", "eb_bwd_rows64_kernel (values backward, row reduction)")
+    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "eb_bwd_rows64_kernel (values backward, row reduction)")
     for kk in inner:
         if kk in kernels:
             kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd (values)"

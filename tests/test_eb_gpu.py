@@ -186,6 +186,41 @@ def test_double_backward_parity(B, L, K, D, dtype, with_a, device):
         assert d_a is None
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_backward_float32_gradient_into_half_table(dtype, device):
+    """A float32 upstream gradient into a 16-bit table: the library rounds the
+    gradient to the table dtype before its float32 reduction, where the
+    reference reads it in float32 (pkm/xformer_embeddingbag.py:322). Against
+    the oracle on the float32 gradient (the reference's result), within the
+    table dtype's tolerance."""
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K, D = 48, 32, 700, 512
+    W, idx, p, _ = eb_inputs(B, L, K, D, dtype, seed=77, psw_dtype=torch.float32, with_grad=False)
+    g = torch.randn((B, D), generator=torch.Generator().manual_seed(78))
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    assert gW.dtype == dtype and gp.dtype == torch.float32
+    assert_rel_close(gW, eW, REL_TOL[dtype], f"grad_weight {dtype} <- float32 gradient")
+    assert_rel_close(gp, ep, REL_TOL[dtype], f"grad_psw {dtype} <- float32 gradient")
+
+
+def test_double_backward_table_gradient_dtype_differs(device):
+    """g_bar (the gradient of the table gradient) in bfloat16 with a float32
+    upstream gradient: g_bar is widened to float32 (exact) and the result is
+    the reference's to float32 tolerance."""
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K, D = 40, 24, 600, 256
+    _, idx, a, g = eb_inputs(B, L, K, D, torch.float32, seed=79)
+    gbar = torch.randn((K, D), generator=torch.Generator().manual_seed(80)).to(torch.bfloat16)
+    d_g, d_a = eb.eb_double_backward(*_dev(idx, a, g, gbar, device=device))
+    e_g, e_a = ref.eb_double_backward(idx, a, g, gbar.float())
+    assert d_g.dtype == torch.float32
+    assert_rel_close(d_g, e_g, REL_TOL[torch.float32], "d_grad_output")
+    assert_rel_close(d_a, e_a, REL_TOL[torch.float32], "d_a")
+
+
 def test_autograd_dropin_pkm(device):
     from modelos_amd.pkm.xformer_embeddingbag import xformers_embedding_bag
 
