@@ -12,11 +12,12 @@ forward + backward (gradients of x and every parameter; no optimizer step).
 bf16: 16384 bags x 128 lookups into a 2^20 x 1024 table, softmax per-sample
 weights, N(0,1) upstream gradient (drop-in xformers_embedding_bag).
 
-Prints one JSON line: whole-job tokens/s, the roofline of the dominant HIP
-kernel (algorithmic bytes or flops / its HIP-event time inside the timed
-region), every entry point's time, and the reference's CPU path (op-for-op
-torch CPU restatement: einsum/topk/F.embedding_bag + ATen autograd) timed on
-this host's cores on a bounded sample of the same workload.
+Prints one JSON line: whole-job tokens/s (K steps timed with nothing but the
+work on the stream), the roofline of the dominant HIP kernel (algorithmic
+bytes or flops / its HIP-event time, from a second, instrumented pass of the
+same K steps), every entry point's time (same pass), and the reference's CPU
+path (op-for-op torch CPU restatement: einsum/topk/F.embedding_bag + ATen
+autograd) timed on this host's cores on a bounded sample of the same workload.
 
 The default run also reports, under extra keys, the standalone embedding bag
 ("eb_standalone"), the fast-weight PKM layer in float32 and bfloat16
@@ -123,6 +124,45 @@ def load_traffic():
             for k, v in d.items() if not k.startswith("_")}
 
 
+def timed_steps(step, steps, kernel_timer=True):
+    """Times `steps` calls of `step` with nothing else on the stream (the
+    headline: wall clock between two synchronizations, and the median of
+    per-step event pairs), then runs the same number of steps again with the
+    library's call timer (event pair around every entry point) and, when
+    asked, its kernel timer (event pairs around single kernels inside entry
+    points) for the per-kernel breakdown. The instrumented pass is not part of
+    the headline: its event records add host work to every call.
+    Returns (wall ms per step, median event ms, call records, kernel timer)."""
+    import torch
+
+    from modelos_amd import _lib
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        step()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms = sorted(a.elapsed_time(b) for a, b in ev)[steps // 2]
+
+    timer = _lib.CallTimer()
+    ktimer = _lib.KernelTimer()
+    if kernel_timer:
+        ktimer.__enter__()
+    try:
+        with timer:
+            for _ in range(steps):
+                step()
+        torch.cuda.synchronize()
+    finally:
+        if kernel_timer:
+            ktimer.__exit__(None, None, None)
+    return ms_per_step, step_ms, timer.summary(), ktimer
+
+
 def timed_median(fn, budget_s=25.0, max_repeats=3):
     """1 warm-up, then up to max_repeats timed calls within the budget; median seconds."""
     t0 = time.perf_counter()
@@ -222,22 +262,9 @@ def run_layer(args, dev):
     U = int(torch.unique(idx).numel())
     log(f"warmup done ({args.warmup} steps); distinct value rows U={U}")
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    timer = _lib.CallTimer()
-    ktimer = _lib.KernelTimer()  # single kernels of multi-kernel entry points
-    with ktimer:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        with timer:
-            for i in range(args.steps):
-                ev[i][0].record()
-                step()
-                ev[i][1].record()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    step_ms = sorted(a.elapsed_time(b) for a, b in ev)[args.steps // 2]
-    calls = timer.summary()
+    # headline steps bare, then the same number instrumented (per-call and
+    # single-kernel event pairs) for the breakdown
+    ms_per_step, step_ms, calls, ktimer = timed_steps(step, args.steps)
     for kname in ktimer.KERNELS:
         if ktimer.ms(kname):
             calls[("kernel", kname)] = ktimer.ms(kname)
@@ -416,17 +443,8 @@ def run_eb(args, dev):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    timer = _lib.CallTimer()
-    ktimer = _lib.KernelTimer()  # the row-reduction kernel inside the backward entry point
-    with ktimer:
-        t0 = time.perf_counter()
-        with timer:
-            for _ in range(args.steps):
-                step()
-        torch.cuda.synchronize()
-        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    calls = timer.summary()
-    calls["rows"] = ktimer.ms("eb_bwd_rows")
+    ms_per_step, _, calls, ktimer = timed_steps(step, args.steps)
+    calls["rows"] = ktimer.ms("eb_bwd_rows")  # the row-reduction kernel inside the backward entry point
 
     def med(key):
         v = sorted(calls[key])
@@ -506,19 +524,12 @@ def run_fwupdate(args, dev):
         step()
         torch_step()
     torch.cuda.synchronize()
-    timer = _lib.CallTimer()
-    t0 = time.perf_counter()
-    with timer:
-        for _ in range(args.steps):
-            step()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_per_step, _, calls, _ = timed_steps(step, args.steps, kernel_timer=False)
     t1 = time.perf_counter()
     for _ in range(args.steps):
         torch_step()
     torch.cuda.synchronize()
     torch_ms = (time.perf_counter() - t1) * 1e3 / args.steps
-    calls = timer.summary()
     v = sorted(next(c for k, c in calls.items() if k[0] == "pkm_fw_sgd_update"))
     kern_ms = v[len(v) // 2]
     work = 4 * K * D * 4 + K * 8  # read values and gradient, write both outputs; the counts
@@ -625,14 +636,7 @@ def run_fwpkm(args, dev, with_cpu=None):
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
-        timer = _lib.CallTimer()
-        t0 = time.perf_counter()
-        with timer:
-            for _ in range(args.steps):
-                step()
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        calls = timer.summary()
+        ms, _, calls, _ = timed_steps(step, args.steps, kernel_timer=False)
         kern = {}
         for name in ("pkm_score_topk", "pkm_eb_fwd", "pkm_eb_bwd", "pkm_eb_bwd2", "pkm_fw_sgd_update"):
             keys = [k for k in calls if k[0] == name]
