@@ -633,6 +633,30 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
 // scattered by position afterwards.
 constexpr int kMetaChunk = 256;  // per-wave LDS window of occurrence metadata (entries)
 
+// Sums of 8 per-lane partials over the 64 lanes of a wave, one butterfly for
+// all 8 (18 lane operations instead of 8 full-wave reductions): lane l gets the
+// total of slot 4 b5 + 2 b4 + b3 (bits 5, 4, 3 of l). Exchanges: the 32-lane
+// halves (v_permlane32_swap), lane ^ 16, lane ^ 8 (DPP row_ror:8), then the 8
+// lanes of a group. Fixed order, so the sums are deterministic.
+__device__ __forceinline__ float reduce8_slots(const float (&d)[8], int lane) {
+  float e[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // lanes 0-31: d[j] of lanes l and l + 32; lanes 32-63: d[j + 4] of lanes l - 32 and l
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(d[j]), __float_as_uint(d[j + 4]), false, false);
+    e[j] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+  const bool b4 = (lane & 16) != 0;
+  float f[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) f[j] = (b4 ? e[j + 2] : e[j]) + __shfl_xor(b4 ? e[j] : e[j + 2], 16);
+  const bool b3 = (lane & 8) != 0;
+  const float send = b3 ? f[0] : f[1];
+  const float t = (b3 ? f[1] : f[0]) +
+                  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xF, 0xF, false));
+  return group_sum<8>(t);
+}
+
 template <int VPL, int U>
 struct RowData {
   uint4 wraw[VPL];
@@ -733,22 +757,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     }
     float mydot = 0.f;
     if (want_dot) {
+      if constexpr (U == 8) {
+        mydot = reduce8_slots(d, lane);  // the total of slot dot_slot (slots >= nh hold 0)
+      } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if ((uint32_t)u < nh) {
-          const float t = group_sum<64>(d[u]);
-          mydot = lane == u ? t : mydot;
+        for (int u = 0; u < U; ++u) {
+          if ((uint32_t)u < nh) {
+            const float t = group_sum<64>(d[u]);
+            mydot = lane == u ? t : mydot;
+          }
         }
       }
     }
     return mydot;
   };
+  // the slot whose dot this lane returns, and whether it stores it (one lane per slot)
+  const int dot_slot = U == 8 ? 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1) : lane;
+  const bool dot_store = U == 8 ? (lane & 7) == 0 : true;
   auto process = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
     float mydot = accumulate(R, M.w, M.nh, acc);
-    if (want_dot) dsorted[(uint32_t)lane < M.nh ? M.beg + lane : dummy_slot] = mydot;
+    if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
     const uint32_t cnt = M.end - M.beg;
     if (cnt > (uint32_t)kHeavyT) {
       add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
@@ -766,7 +797,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
           for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
         }
         mydot = accumulate(R, w, nh, acc);
-        if (want_dot) dsorted[(uint32_t)lane < nh ? s + lane : dummy_slot] = mydot;
+        if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nh ? s + dot_slot : dummy_slot] = mydot;
       }
     }
     char* orow = (r0 + i < K) ? (char*)gW + (uint64_t)(r0 + i) * rowbytes : (char*)dummy_row;
