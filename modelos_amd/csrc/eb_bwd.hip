@@ -17,9 +17,8 @@
 //              row's occurrences end up in increasing position order: the
 //              float32 sums below have a fixed order, independent of the launch
 //              (no float atomics anywhere).
-//  2. offsets: row r starts at the first sorted position whose key is >= r:
-//              run starts scatter their position, a suffix-min scan fills the
-//              untouched rows.
+//  2. offsets: row r starts at the first sorted position whose key is >= r
+//              (a binary search per row).
 //  3. heavy:   rows with more than T occurrences are cut into fixed chunks of
 //              T sorted occurrences; each chunk writes a float32 partial sum
 //              (2 slots per chunk: the row running in from the previous chunk
@@ -65,8 +64,8 @@ __global__ void count_invalid_kernel(const int64_t* __restrict__ idx, int64_t n,
 __global__ void zero_i64_kernel(unsigned long long* p) { *p = 0; }
 
 // ---------------------------------------------------------------------------
-// Device-wide scans of uint32 (tiles of 4096 = 256 threads x 16):
-//   exclusive prefix sum (radix digit offsets), inclusive suffix min (row offsets).
+// Device-wide exclusive prefix sum of uint32 (tiles of 4096 = 256 threads x
+// 16): the radix digit offsets.
 // ---------------------------------------------------------------------------
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
@@ -94,33 +93,6 @@ __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* to
   __syncthreads();
   *total = tot;
   return pre + x - v;
-}
-
-// Exclusive suffix min across a 256-thread block (threads with a larger index
-// are to the right); *total gets the block min.
-__device__ __forceinline__ uint32_t block_exclusive_suffix_min(uint32_t v, uint32_t* total, uint32_t* lds4) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_down(x, o);
-    if (lane + o < 64) x = x < y ? x : y;
-  }
-  if (lane == 0) lds4[w] = x;
-  __syncthreads();
-  uint32_t right = 0xFFFFFFFFu, tot = 0xFFFFFFFFu;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t t = lds4[i];
-    if (i > w) right = right < t ? right : t;
-    tot = tot < t ? tot : t;
-  }
-  __syncthreads();
-  uint32_t in_wave = __shfl_down(x, 1);
-  if (lane == 63) in_wave = 0xFFFFFFFFu;
-  *total = tot;
-  return in_wave < right ? in_wave : right;
 }
 
 __global__ __launch_bounds__(256) void scan_reduce_kernel(const uint32_t* __restrict__ in, int64_t n,
@@ -184,79 +156,19 @@ __global__ __launch_bounds__(256) void scan_apply_kernel(uint32_t* __restrict__ 
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) data[n] = parts[blockIdx.x] + tot;
 }
 
-__global__ __launch_bounds__(256) void smin_reduce_kernel(const uint32_t* __restrict__ in, int64_t n,
-                                                          uint32_t* __restrict__ parts) {
-  __shared__ uint32_t lds4[4];
-  const int64_t base = (int64_t)blockIdx.x * kScanTile;
-  uint32_t m = 0xFFFFFFFFu;
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const int64_t p = base + (int64_t)i * kScanThreads + threadIdx.x;
-    const uint32_t x = p < n ? in[p] : 0xFFFFFFFFu;
-    m = m < x ? m : x;
-  }
-  uint32_t tot;
-  block_exclusive_suffix_min(m, &tot, lds4);
-  if (threadIdx.x == 0) parts[blockIdx.x] = tot;
-}
-
-// Single block: exclusive suffix min of the per-tile mins, in place.
-__global__ __launch_bounds__(256) void smin_parts_kernel(uint32_t* __restrict__ parts, int64_t nparts) {
-  __shared__ uint32_t lds4[4];
-  uint32_t carry = 0xFFFFFFFFu;
-  const int64_t nchunks = (nparts + kScanTile - 1) / kScanTile;
-  for (int64_t ch = nchunks - 1; ch >= 0; --ch) {
-    const int64_t p0 = ch * kScanTile + (int64_t)threadIdx.x * kScanItems;
-    uint32_t v[kScanItems];
-    uint32_t m = 0xFFFFFFFFu;
-#pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
-      v[i] = (p0 + i < nparts) ? parts[p0 + i] : 0xFFFFFFFFu;
-      m = m < v[i] ? m : v[i];
-    }
-    uint32_t tot;
-    const uint32_t ex = block_exclusive_suffix_min(m, &tot, lds4);
-    uint32_t run = carry < ex ? carry : ex;
-#pragma unroll
-    for (int i = kScanItems - 1; i >= 0; --i) {
-      if (p0 + i < nparts) parts[p0 + i] = run;
-      run = run < v[i] ? run : v[i];
-    }
-    carry = carry < tot ? carry : tot;
-  }
-}
-
-// data[i] <- min(data[i..n)) using the exclusive suffix mins of the tiles.
-__global__ __launch_bounds__(256) void smin_apply_kernel(uint32_t* __restrict__ data, int64_t n,
-                                                         const uint32_t* __restrict__ parts) {
-  __shared__ uint32_t lds4[4];
-  const int64_t p0 = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
-  uint32_t v[kScanItems];
-  uint32_t m = 0xFFFFFFFFu;
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    v[i] = (p0 + i < n) ? data[p0 + i] : 0xFFFFFFFFu;
-    m = m < v[i] ? m : v[i];
-  }
-  uint32_t tot;
-  const uint32_t ex = block_exclusive_suffix_min(m, &tot, lds4);
-  const uint32_t right = parts[blockIdx.x];
-  uint32_t run = ex < right ? ex : right;
-#pragma unroll
-  for (int i = kScanItems - 1; i >= 0; --i) {
-    run = run < v[i] ? run : v[i];
-    if (p0 + i < n) data[p0 + i] = run;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Stable LSD radix sort pass with BITS-bit digits over tiles of 4096 items
-// (4 waves x 16 rounds x 64 lanes). Item order inside a tile: wave-major,
-// then round, then lane, so ranks stay stable. The first pass reads the int64
-// indices (dropping out-of-range ones); later passes read nvalid items.
+// Stable LSD radix sort pass with BITS-bit digits over tiles of kRadixSubs
+// sub-tiles of 4096 items (4 waves x 16 rounds x 64 lanes), taken in order.
+// Item order inside a sub-tile: wave-major, then round, then lane, so ranks
+// stay stable. The first pass reads the int64 indices (dropping out-of-range
+// ones); later passes read nvalid items. (Tiles of 4 sub-tiles shrink the
+// per-tile digit histogram 4x but leave a quarter of the blocks: measured
+// slower at 4 M lookups.)
 // ---------------------------------------------------------------------------
 constexpr int kRadixItems = 16;
-constexpr int kRadixTile = 256 * kRadixItems;
+constexpr int kRadixSub = 256 * kRadixItems;
+constexpr int kRadixSubs = 1;
+constexpr int kRadixTile = kRadixSub * kRadixSubs;
 
 template <bool FIRST>
 __device__ __forceinline__ bool radix_item(int64_t p, int64_t N, uint32_t nv, const int64_t* __restrict__ idx,
@@ -285,7 +197,7 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restri
   const uint32_t nv = FIRST ? 0u : *nvalid;
   const int64_t base = (int64_t)blockIdx.x * kRadixTile;
 #pragma unroll 4
-  for (int i = 0; i < kRadixItems; ++i) {
+  for (int i = 0; i < kRadixItems * kRadixSubs; ++i) {
     const int64_t p = base + (int64_t)i * 256 + threadIdx.x;
     uint32_t k;
     if (radix_item<FIRST>(p, N, nv, idx, keys, K, &k)) {
@@ -298,10 +210,11 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restri
   for (int d = threadIdx.x; d < R; d += 256) hist[(int64_t)d * ntiles + blockIdx.x] = h[d];
 }
 
-// Stable scatter of one tile by digit. The tile is first ordered by digit in
-// LDS (per digit in item order), then written out in that order, so each
-// digit's run of the tile goes to consecutive addresses: keys first, then
-// values, through one LDS buffer.
+// Stable scatter of one tile by digit, sub-tile by sub-tile. Each sub-tile is
+// first ordered by digit in LDS (per digit in item order), then written out in
+// that order, so each digit's run of the sub-tile goes to consecutive
+// addresses, right after the previous sub-tile's run of that digit: keys first,
+// then values, through one LDS buffer.
 template <bool FIRST, int BITS>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __restrict__ idx,
                                                             const uint32_t* __restrict__ keys_in,
@@ -313,120 +226,141 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
   constexpr int R = 1 << BITS;
   constexpr int DPT = R / 256;  // digits per thread in the digit scan
   static_assert(R % 256 == 0, "digit count per thread");
-  __shared__ uint32_t wcnt[4][R];        // per-wave digit counts, then their starts inside the tile
-  __shared__ uint32_t gofs[R];           // per digit: global start - start inside the tile
-  __shared__ uint32_t stage[kRadixTile];  // the tile in digit order (keys, then values)
+  __shared__ uint32_t wcnt[4][R];        // per-wave digit counts, then their starts inside the sub-tile
+  __shared__ uint32_t gofs[R];           // per digit: global start - start inside the sub-tile
+  __shared__ uint32_t stage[kRadixSub];  // the sub-tile in digit order (keys, then values)
   __shared__ uint32_t wsum[4];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  for (int d = threadIdx.x; d < R; d += 256) {
+  // per owned digit (thread t: digits DPT t .. DPT t + DPT - 1): the global
+  // position of its next item in this tile
+  uint32_t running[DPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wcnt[i][d] = 0;
-  }
-  __syncthreads();
-
+  for (int j = 0; j < DPT; ++j) running[j] = ofs[(int64_t)(threadIdx.x * DPT + j) * ntiles + blockIdx.x];
   const uint32_t nv = FIRST ? 0u : *nvalid;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int64_t base = (int64_t)blockIdx.x * kRadixTile + (int64_t)w * (kRadixItems * 64);
-  uint32_t k[kRadixItems], v[kRadixItems], pre[kRadixItems];
-  uint32_t validmask = 0;
+
+#pragma unroll 1
+  for (int sub = 0; sub < kRadixSubs; ++sub) {
+    for (int d = threadIdx.x; d < R; d += 256) {
 #pragma unroll
-  for (int i = 0; i < kRadixItems; ++i) {
-    const int64_t p = base + (int64_t)i * 64 + lane;
-    k[i] = 0;
-    const bool valid = radix_item<FIRST>(p, N, nv, idx, keys_in, K, &k[i]);
-    v[i] = valid ? (FIRST ? (uint32_t)p : vals_in[p]) : 0u;
-    validmask |= valid ? (1u << i) : 0u;
-    const uint32_t d = (k[i] >> shift) & (R - 1);
-    uint64_t peers = __ballot(valid);
-#pragma unroll
-    for (int bit = 0; bit < BITS; ++bit) {
-      const bool on = (d >> bit) & 1u;
-      const uint64_t bb = __ballot(on);
-      peers &= on ? bb : ~bb;
+      for (int i = 0; i < 4; ++i) wcnt[i][d] = 0;
     }
-    const uint32_t rank = (uint32_t)__popcll(peers & below);
-    const uint32_t old = wcnt[w][d];
-    if (valid && rank == 0) wcnt[w][d] = old + (uint32_t)__popcll(peers);
-    pre[i] = old + rank;
-  }
-  __syncthreads();
-  // digit starts inside the tile: exclusive scan over the digits (thread t
-  // owns digits DPT t .. DPT t + DPT - 1) of the tile's digit counts
-  uint32_t tot[DPT], mine = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kRadixTile + (int64_t)sub * kRadixSub + (int64_t)w * (kRadixItems * 64);
+    uint32_t k[kRadixItems], v[kRadixItems], pre[kRadixItems];
+    uint32_t validmask = 0;
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int d = threadIdx.x * DPT + j;
-    tot[j] = wcnt[0][d] + wcnt[1][d] + wcnt[2][d] + wcnt[3][d];
-    mine += tot[j];
-  }
-  uint32_t incl = mine;
+    for (int i = 0; i < kRadixItems; ++i) {
+      const int64_t p = base + (int64_t)i * 64 + lane;
+      k[i] = 0;
+      const bool valid = radix_item<FIRST>(p, N, nv, idx, keys_in, K, &k[i]);
+      v[i] = valid ? (FIRST ? (uint32_t)p : vals_in[p]) : 0u;
+      validmask |= valid ? (1u << i) : 0u;
+      const uint32_t d = (k[i] >> shift) & (R - 1);
+      uint64_t peers = __ballot(valid);
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = (uint32_t)__shfl_up((int)incl, o);
-    if (lane >= o) incl += y;
-  }
-  if (lane == 63) wsum[w] = incl;
-  __syncthreads();
-  uint32_t run = incl - mine;
-  for (int i = 0; i < w; ++i) run += wsum[i];
-  const uint32_t nloc = wsum[0] + wsum[1] + wsum[2] + wsum[3];  // valid items of the tile
-#pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int d = threadIdx.x * DPT + j;
-    gofs[d] = ofs[(int64_t)d * ntiles + blockIdx.x] - run;
-    uint32_t r2 = run;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t t = wcnt[i][d];
-      wcnt[i][d] = r2;
-      r2 += t;
+      for (int bit = 0; bit < BITS; ++bit) {
+        const bool on = (d >> bit) & 1u;
+        const uint64_t bb = __ballot(on);
+        peers &= on ? bb : ~bb;
+      }
+      const uint32_t rank = (uint32_t)__popcll(peers & below);
+      const uint32_t old = wcnt[w][d];
+      if (valid && rank == 0) wcnt[w][d] = old + (uint32_t)__popcll(peers);
+      pre[i] = old + rank;
     }
-    run += tot[j];
-  }
-  __syncthreads();
-  uint32_t lp[kRadixItems];  // position of item i inside the tile's digit order
+    __syncthreads();
+    // digit starts inside the sub-tile: exclusive scan over the digits (thread
+    // t owns digits DPT t .. DPT t + DPT - 1) of the sub-tile's digit counts
+    uint32_t tot[DPT], mine = 0;
 #pragma unroll
-  for (int i = 0; i < kRadixItems; ++i) {
-    lp[i] = wcnt[w][(k[i] >> shift) & (R - 1)] + pre[i];
-    if (validmask & (1u << i)) stage[lp[i]] = k[i];
-  }
-  __syncthreads();
-  // keys out in digit order (consecutive positions of a digit: consecutive
-  // addresses); the destinations are kept for the values
-  uint32_t dst[kRadixItems];
-#pragma unroll
-  for (int i = 0; i < kRadixItems; ++i) {
-    const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
-    dst[i] = 0;
-    if (q < nloc) {
-      const uint32_t key = stage[q];
-      dst[i] = gofs[(key >> shift) & (R - 1)] + q;
-      keys_out[dst[i]] = key;
+    for (int j = 0; j < DPT; ++j) {
+      const int d = threadIdx.x * DPT + j;
+      tot[j] = wcnt[0][d] + wcnt[1][d] + wcnt[2][d] + wcnt[3][d];
+      mine += tot[j];
     }
-  }
-  __syncthreads();
+    uint32_t incl = mine;
 #pragma unroll
-  for (int i = 0; i < kRadixItems; ++i)
-    if (validmask & (1u << i)) stage[lp[i]] = v[i];
-  __syncthreads();
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_up((int)incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    uint32_t run = incl - mine;
+    for (int i = 0; i < w; ++i) run += wsum[i];
+    const uint32_t nloc = wsum[0] + wsum[1] + wsum[2] + wsum[3];  // valid items of the sub-tile
 #pragma unroll
-  for (int i = 0; i < kRadixItems; ++i) {
-    const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
-    if (q < nloc) vals_out[dst[i]] = stage[q];
+    for (int j = 0; j < DPT; ++j) {
+      const int d = threadIdx.x * DPT + j;
+      gofs[d] = running[j] - run;
+      running[j] += tot[j];
+      uint32_t r2 = run;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t = wcnt[i][d];
+        wcnt[i][d] = r2;
+        r2 += t;
+      }
+      run += tot[j];
+    }
+    __syncthreads();
+    uint32_t lp[kRadixItems];  // position of item i inside the sub-tile's digit order
+#pragma unroll
+    for (int i = 0; i < kRadixItems; ++i) {
+      lp[i] = wcnt[w][(k[i] >> shift) & (R - 1)] + pre[i];
+      if (validmask & (1u << i)) stage[lp[i]] = k[i];
+    }
+    __syncthreads();
+    // keys out in digit order (consecutive positions of a digit: consecutive
+    // addresses); the destinations are kept for the values
+    uint32_t dst[kRadixItems];
+#pragma unroll
+    for (int i = 0; i < kRadixItems; ++i) {
+      const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
+      dst[i] = 0;
+      if (q < nloc) {
+        const uint32_t key = stage[q];
+        dst[i] = gofs[(key >> shift) & (R - 1)] + q;
+        keys_out[dst[i]] = key;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kRadixItems; ++i)
+      if (validmask & (1u << i)) stage[lp[i]] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kRadixItems; ++i) {
+      const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
+      if (q < nloc) vals_out[dst[i]] = stage[q];
+    }
+    __syncthreads();  // stage and wcnt are reused by the next sub-tile
   }
 }
 
-// offs[key] <- position of each run start of the sorted keys; offs[K] <- nvalid.
-__global__ void run_starts_kernel(const uint32_t* __restrict__ skeys, const uint32_t* __restrict__ nvalid, int64_t N,
-                                  int64_t K, uint32_t* __restrict__ offs) {
+// offs[r] <- the first sorted position whose key is >= r (a binary search of
+// the nvalid sorted keys per row; the searches of neighbouring rows follow the
+// same path, so a wave's loads mostly share cache lines); offs[K] <- nvalid.
+__global__ void row_offsets_kernel(const uint32_t* __restrict__ skeys, const uint32_t* __restrict__ nvalid, int64_t K,
+                                   uint32_t* __restrict__ offs) {
   const uint32_t nv = *nvalid;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N; i += (int64_t)gridDim.x * blockDim.x) {
-    if (i >= (int64_t)nv) break;
-    const uint32_t k = skeys[i];
-    if (i == 0 || skeys[i - 1] != k) offs[k] = (uint32_t)i;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r <= K; r += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t lo = 0, hi = nv;
+    if (r == K) {
+      lo = nv;
+    } else {
+      while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (skeys[mid] < (uint32_t)r)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+    }
+    offs[r] = lo;
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0) offs[K] = nv;
 }
 
 // ---------------------------------------------------------------------------
@@ -837,6 +771,7 @@ __global__ void occ_meta_kernel(const uint32_t* __restrict__ svals, const uint32
   }
 }
 
+
 // gpsw[position] <- psw-gradient dots computed in sorted order.
 __global__ void gpsw_scatter_kernel(const uint32_t* __restrict__ svals, const float* __restrict__ dsorted,
                                     const uint32_t* __restrict__ nvalid, int64_t N, void* __restrict__ gpsw, int pdt) {
@@ -923,14 +858,6 @@ static void device_exclusive_sum(uint32_t* data, int64_t n, uint32_t* parts, hip
   hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
   hipLaunchKernelGGL(scan_parts_kernel, dim3(1), dim3(kScanThreads), 0, st, parts, tiles);
   hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
-}
-
-// In-place inclusive suffix min of data[0..n).
-static void device_suffix_min(uint32_t* data, int64_t n, uint32_t* parts, hipStream_t st) {
-  const int64_t tiles = cdiv(n, kScanTile);
-  hipLaunchKernelGGL(smin_reduce_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
-  hipLaunchKernelGGL(smin_parts_kernel, dim3(1), dim3(kScanThreads), 0, st, parts, tiles);
-  hipLaunchKernelGGL(smin_apply_kernel, dim3((unsigned)tiles), dim3(kScanThreads), 0, st, data, n, parts);
 }
 
 static unsigned grid_for(int64_t n, int threads, int64_t cap = 65536) {
@@ -1127,17 +1054,21 @@ extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int
     for (int pass = 0; pass < l.plan.passes; ++pass) {
       const int nxt = pass == 0 ? 0 : 1 - cur;
       switch (l.plan.bits) {
-        case 8: radix_pass<8>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st); break;
-        case 10: radix_pass<10>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st); break;
-        default: radix_pass<11>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st); break;
+        case 8:
+          radix_pass<8>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st);
+          break;
+        case 10:
+          radix_pass<10>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st);
+          break;
+        default:
+          radix_pass<11>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st);
+          break;
       }
       cur = nxt;
     }
-    // 2. row offsets: run starts + suffix min
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 1, 256, 4096)), dim3(256), 0, st, offs, 0xFFFFFFFFu, K + 1);
-    hipLaunchKernelGGL(run_starts_kernel, dim3(grid_for(N, 256, 8192)), dim3(256), 0, st, (const uint32_t*)keys[cur],
-                       nvalid, N, K, offs);
-    device_suffix_min(offs, K + 1, parts, st);
+    // 2. row offsets: a binary search of the sorted keys per row
+    hipLaunchKernelGGL(row_offsets_kernel, dim3(grid_for(K + 1, 256, 65536)), dim3(256), 0, st,
+                       (const uint32_t*)keys[cur], nvalid, K, offs);
   } else {
     hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 1, 256, 4096)), dim3(256), 0, st, offs, 0u, K + 1);
   }

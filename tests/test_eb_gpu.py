@@ -387,6 +387,31 @@ def test_backward_large_gradient_parity(B, L, K, D, dtype, device):
     assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
 
 
+# Row counts past 2^20 change the sort's digit plan: 2 passes of 11-bit digits
+# up to 2^22 rows, 3 passes of 10-bit digits beyond. Indices also sit on the
+# digit boundaries and at the last row.
+WIDE_K = [(700, 40, 3_000_000, 16), (300, 50, 5_000_000, 8)]
+
+
+@pytest.mark.parametrize("B,L,K,D", WIDE_K, ids=lambda v: str(v))
+def test_backward_wide_key_range(B, L, K, D, device):
+    from modelos_amd import embedding_bag as eb
+
+    dtype = torch.float32
+    W, _, p, g = eb_inputs(B, L, K, D, dtype, seed=51 + D)
+    idx = _hot_indices(B, L, K, seed=52 + D)
+    edge = torch.tensor([0, 1, (1 << 10) - 1, 1 << 10, (1 << 11) - 1, 1 << 11, (1 << 20) - 1, 1 << 20,
+                         (1 << 21) + 5, (1 << 22) - 1, K - 2, K - 1])
+    edge = edge[edge < K]
+    idx.view(-1)[-3 * edge.numel():] = edge.repeat(3)
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    cW, cp = ref.eb_backward(idx, W.abs(), p.abs(), g.abs())
+    assert_rel_close(gW, eW, REL_TOL[dtype], "grad_weight", cond=cW)
+    assert_rel_close(gp, ep, REL_TOL[dtype], "grad_psw", cond=cp)
+    assert (gp.cpu()[idx < 0] == 0).all()
+
+
 def test_backward_large_gradient_unweighted(device):
     from modelos_amd import embedding_bag as eb
 
