@@ -381,7 +381,32 @@ def run_layer(args, dev):
         "cache_flush": {"ms_per_step": round(flushed_ms, 4), "ms_per_step_no_flush": round(step_ms, 4),
                         "note": "median HIP-event time of a step run right after a 512 MB write; "
                                 "ms_per_step_no_flush: the same median for back-to-back steps"},
+        "layer_floor": layer_floor(tokens, H, n, k, knn, C, D, U, ms_per_step),
         "cpu_baseline": cpu,
+    }
+
+
+def layer_floor(tokens, H, n, k, knn, C, D, U, ms_per_step):
+    """The layer step's lower bound from its algorithmic work at MI355X peaks:
+    the value gather and the value backward at HBM bandwidth (algorithmic
+    bytes as in the roofline), the sub-key scoring and the dense projections
+    (query C -> H k, swilu gate C -> D, output D -> C; forward and two
+    backward products each) at the bf16 MFMA peak. frac = floor / measured."""
+    L = H * knn
+    a_fwd, a_bwd = eb_algorithmic_bytes(tokens, L, n * n, D, U)
+    proj_flops = 3 * 2 * tokens * (C * H * k + C * D + D * C)
+    parts_ms = {
+        "values_fwd": a_fwd / (HBM_PEAK_GBS * 1e9) * 1e3,
+        "values_bwd": a_bwd / (HBM_PEAK_GBS * 1e9) * 1e3,
+        "scoring": score_flops(tokens, H, n, k) / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3,
+        "projections": proj_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3,
+    }
+    floor_ms = sum(parts_ms.values())
+    return {
+        "ms": round(floor_ms, 4), "tokens_per_s": round(tokens / (floor_ms * 1e-3), 1),
+        "frac": round(floor_ms / ms_per_step, 4), "parts_ms": {kk: round(v, 4) for kk, v in parts_ms.items()},
+        "note": "value gather and backward at 8 TB/s (algorithmic bytes), scoring and projection GEMMs "
+                "(fwd + 2 bwd products) at 2516.6 TFLOP/s bf16; frac = floor / measured ms_per_step",
     }
 
 
