@@ -448,6 +448,7 @@ __device__ __forceinline__ void add_heavy_partials(uint32_t beg, uint32_t end, c
                                                    int64_t D, int64_t col0, float* acc) {
   constexpr int VSTRIDE = LPG * EPV;
   const uint32_t c_first = beg / kHeavyT, c_last = (end - 1) / kHeavyT;
+#pragma unroll 4
   for (uint32_t c = c_first; c <= c_last; ++c) {
     const int slot = (c == c_first && beg != c * (uint32_t)kHeavyT) ? 1 : 0;
     const float* prow = partials + (2 * (int64_t)c + slot) * D + col0;
@@ -603,12 +604,62 @@ struct RowMeta {
   float w[U];
 };
 
+// acc += sum_{u < nh} w[u] * gvec[u] over a row's U prefetch slots; the
+// returned value holds, on lane dot_slot_of<U>(lane), the psw-gradient dot
+// <wraw, gvec[slot]> (slots u >= nh, wave-uniform, are skipped).
+template <int U>
+__device__ __forceinline__ int dot_slot_of(int lane) {
+  return U == 8 ? 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1) : lane;
+}
+// whether this lane stores its slot's dot (one lane per slot)
+template <int U>
+__device__ __forceinline__ bool dot_store_of(int lane) {
+  return U == 8 ? (lane & 7) == 0 : true;
+}
+template <typename TW, int VPL, int U>
+__device__ __forceinline__ float accumulate_slots(const RowData<VPL, U>& R, const float* w, uint32_t nh, float* acc,
+                                                  bool want_dot, int lane) {
+  constexpr int EPV = VecTraits<TW>::EPV;
+  constexpr int NE = VPL * EPV;
+  float d[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    d[u] = 0.f;
+    if ((uint32_t)u < nh) {
+      float f[NE];
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.gvec[u][v], f + v * EPV);
+#pragma unroll
+      for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
+      if (want_dot) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) d[u] = vec_dot<TW>(R.wraw[v], R.gvec[u][v], d[u]);
+      }
+    }
+  }
+  float mydot = 0.f;
+  if (want_dot) {
+    if constexpr (U == 8) {
+      mydot = reduce8_slots(d, lane);  // the total of slot dot_slot_of<8>(lane) (slots >= nh hold 0)
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if ((uint32_t)u < nh) {
+          const float t = group_sum<64>(d[u]);
+          mydot = lane == u ? t : mydot;
+        }
+      }
+    }
+  }
+  return mydot;
+}
+
 template <typename TW, int VPL, int U>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 && U <= 4) ? 5 : ((VPL == 1 || (VPL == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows64_kernel(
     const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TW* __restrict__ g,
     const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
     const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
-    uint32_t dummy_slot) {
+    uint32_t dummy_slot, uint32_t* __restrict__ long_rows, uint32_t* __restrict__ long_count) {
   __shared__ uint2 smeta[4][kMetaChunk];
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
@@ -642,6 +693,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   };
   load_chunk(cbase);
 
+  uint64_t deferred = 0;  // long light rows (bit i: row r0 + i), listed after the main loop
   auto get_meta = [&](int i, RowMeta<U>& M) {
     if (i < 64) {
       M.beg = (uint32_t)__builtin_amdgcn_readlane((int)my_beg, i);
@@ -650,7 +702,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
       M.beg = M.end = tail;
     }
     const uint32_t cnt = M.end - M.beg;
-    M.nh = cnt > (uint32_t)kHeavyT ? 0u : (cnt < (uint32_t)U ? cnt : (uint32_t)U);
+    // rows longer than the prefetch (and light) are listed for the long-row kernel
+    const bool longrow = cnt > (uint32_t)U && cnt <= (uint32_t)kHeavyT;
+    if (longrow) deferred |= 1ull << i;
+    M.nh = (cnt > (uint32_t)kHeavyT || longrow) ? 0u : cnt;
     if (M.beg + U > cbase + kMetaChunk) load_chunk(M.beg);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -672,6 +727,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   };
   // acc += sum_{u < nh} w[u] * gvec[u]; lane u of the returned value holds
   // <wraw, gvec[u]> (slots u >= nh, wave-uniform, are skipped)
+  // acc += sum_{u < nh} w[u] * gvec[u]; the returned value holds, on lane
+  // dot_slot, the dot of that slot (as accumulate_slots, written out here: as
+  // a call it costs this kernel registers and spills)
   auto accumulate = [&](const RowData<VPL, U>& R, const float* w, uint32_t nh, float* acc) {
     float d[U];
 #pragma unroll
@@ -692,7 +750,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     float mydot = 0.f;
     if (want_dot) {
       if constexpr (U == 8) {
-        mydot = reduce8_slots(d, lane);  // the total of slot dot_slot (slots >= nh hold 0)
+        mydot = reduce8_slots(d, lane);
       } else {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -705,35 +763,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     }
     return mydot;
   };
-  // the slot whose dot this lane returns, and whether it stores it (one lane per slot)
-  const int dot_slot = U == 8 ? 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1) : lane;
-  const bool dot_store = U == 8 ? (lane & 7) == 0 : true;
+  const int dot_slot = dot_slot_of<U>(lane);
+  const bool dot_store = dot_store_of<U>(lane);
   auto process = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
+    if ((deferred >> i) & 1ull) return;  // a long light row: reduced by the long-row kernel
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
-    float mydot = accumulate(R, M.w, M.nh, acc);
+    const float mydot = accumulate(R, M.w, M.nh, acc);
     if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
-    const uint32_t cnt = M.end - M.beg;
-    if (cnt > (uint32_t)kHeavyT) {
-      add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
-    } else if (cnt > (uint32_t)U) {
-      // rows longer than the prefetch: U more occurrences at a time, in order
-      for (uint32_t s = M.beg + U; s < M.end; s += U) {
-        const uint32_t nh = (M.end - s) < (uint32_t)U ? (M.end - s) : (uint32_t)U;
-        float w[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const uint2 m = meta[s + u];
-          const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * rowbytes : zb;
-          w[u] = (uint32_t)u < nh ? __uint_as_float(m.y) : 0.f;
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
-        }
-        mydot = accumulate(R, w, nh, acc);
-        if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nh ? s + dot_slot : dummy_slot] = mydot;
-      }
-    }
+    if (M.end - M.beg > (uint32_t)kHeavyT) add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
     char* orow = (r0 + i < K) ? (char*)gW + (uint64_t)(r0 + i) * rowbytes : (char*)dummy_row;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
@@ -751,6 +790,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     issue(i + 2, MA, DA);
     process(i + 1, MB, DB);
     get_meta(i + 3, MB);
+  }
+
+  // long light rows (U < count <= kHeavyT) go to the list that
+  // eb_bwd_long_rows_kernel reduces, one row per wave
+  if (deferred != 0ull) {
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(long_count, (uint32_t)__popcll(deferred));
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    if ((deferred >> lane) & 1ull) {
+      const uint64_t below = lane == 0 ? 0ull : (deferred & (~0ull >> (64 - lane)));
+      long_rows[base + (uint32_t)__popcll(below)] = (uint32_t)(r0 + lane);
+    }
+  }
+}
+
+// The long light rows the row kernel listed: each wave takes one row at a time
+// (grid-stride over the list, whose length every wave reads, so every wave
+// ends) and reduces it U occurrences at a time, in order, the next chunk's
+// metadata and gradient rows in flight while the current chunk is reduced.
+// One wave per row keeps each row's sums in position order.
+template <typename TW, int VPL, int U>
+__global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
+    const TW* __restrict__ W, int64_t D, int want_dot, const TW* __restrict__ g, const uint32_t* __restrict__ offs,
+    const uint2* __restrict__ meta, const TW* __restrict__ zrow, TW* __restrict__ gW, float* __restrict__ dsorted,
+    uint32_t dummy_slot, const uint32_t* __restrict__ long_rows, const uint32_t* __restrict__ long_count) {
+  constexpr int EPV = VecTraits<TW>::EPV;
+  constexpr int NE = VPL * EPV;
+  const int lane = threadIdx.x & 63;
+  const uint32_t lane_byte = (uint32_t)lane * 16u;
+  const uint64_t rowbytes = (uint64_t)D * sizeof(TW);
+  const char* Wb = (const char*)W;
+  const char* gb = (const char*)g;
+  const char* zb = (const char*)zrow;
+  const int dot_slot = dot_slot_of<U>(lane);
+  const bool dot_store = dot_store_of<U>(lane);
+  const uint32_t n = *long_count;
+  const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+  auto fetch = [&](uint32_t s, uint32_t end, RowData<VPL, U>& R, float* w) {
+    const uint32_t nh = (end - s) < (uint32_t)U ? (end - s) : (uint32_t)U;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint2 m = meta[(uint32_t)u < nh ? s + (uint32_t)u : s];  // uniform: scalar loads
+      w[u] = (uint32_t)u < nh ? __uint_as_float(m.y) : 0.f;
+      const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * rowbytes : zb;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+    }
+    return nh;
+  };
+  for (uint32_t t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); t < n; t += nwaves) {
+    const uint32_t r = (uint32_t)__builtin_amdgcn_readfirstlane((int)long_rows[t]);
+    const uint32_t beg = offs[r], end = offs[r + 1];
+    const char* wrow = want_dot ? Wb + (uint64_t)r * rowbytes : zb;
+    RowData<VPL, U> DA, DB;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      DA.wraw[v] = ld16(wrow + lane_byte + v * 1024u);
+      DB.wraw[v] = ld16(wrow + lane_byte + v * 1024u);
+    }
+    float acc[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) acc[e] = 0.f;
+    float wA[U], wB[U];
+    uint32_t nA = fetch(beg, end, DA, wA), nB = 0;
+    for (uint32_t s = beg;;) {
+      const uint32_t s2 = s + U;
+      if (s2 < end) nB = fetch(s2, end, DB, wB);
+      float d = accumulate_slots<TW, VPL, U>(DA, wA, nA, acc, want_dot, lane);
+      if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nA ? s + dot_slot : dummy_slot] = d;
+      if (s2 >= end) break;
+      const uint32_t s3 = s2 + U;
+      if (s3 < end) nA = fetch(s3, end, DA, wA);
+      d = accumulate_slots<TW, VPL, U>(DB, wB, nB, acc, want_dot, lane);
+      if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nB ? s2 + dot_slot : dummy_slot] = d;
+      if (s3 >= end) break;
+      s = s3;
+    }
+    char* orow = (char*)gW + (uint64_t)r * rowbytes;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
   }
 }
 
@@ -807,7 +926,7 @@ static RadixPlan radix_plan(int64_t K) {
 }
 
 struct BwdLayout {
-  size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, total;
+  size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, long_rows, total;
   int64_t ntiles, nbins, nchunks, nmeta;
   RadixPlan plan;
 };
@@ -848,6 +967,9 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   off += align256((size_t)D * 4);
   l.dummy_row = off;
   off += align256((size_t)D * 4);
+  // long light rows listed by the row kernel (at most one entry per row), then their count
+  l.long_rows = off;
+  off += align256((size_t)(K + 1) * 4);
   l.total = off;
   return l;
 }
@@ -895,12 +1017,19 @@ static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], ui
 template <typename TW, int VPL, int U>
 static void launch_rows64(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
                           const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
-                          float* dsorted, uint32_t dummy_slot, hipStream_t st) {
+                          float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, hipStream_t st) {
   const unsigned rb = (unsigned)cdiv(K, 4 * 64);
+  uint32_t* long_count = long_rows + K;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, long_count, 0u, (int64_t)1);
   KernelSpan span("eb_bwd_rows", st);
   hipLaunchKernelGGL((eb_bwd_rows64_kernel<TW, VPL, U>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, want_dot,
                      (const TW*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW, dsorted,
-                     dummy_slot);
+                     dummy_slot, long_rows, long_count);
+  // grid-stride over the list: enough waves to spread the long rows, bounded by the row count
+  const unsigned lb = (unsigned)(rb < 1024u ? rb : 1024u);
+  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, VPL, U>), dim3(lb), dim3(256), 0, st, (const TW*)W, D, want_dot,
+                     (const TW*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
+                     (const uint32_t*)long_rows, (const uint32_t*)long_count);
 }
 
 template <typename TW, int LPG, int VPL>
@@ -931,20 +1060,21 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       const bool dense = N > 3 * K;  // more than ~3 lookups per row on average: prefetch 8
       const uint32_t dslot = (uint32_t)N;
       void* dummy = ws + l.dummy_row;
+      uint32_t* long_rows = (uint32_t*)(ws + l.long_rows);
       if constexpr (VPL == 1) {
         if (dense)
-          launch_rows64<TW, 1, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+          launch_rows64<TW, 1, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
         else
-          launch_rows64<TW, 1, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+          launch_rows64<TW, 1, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
       } else if constexpr (VPL == 2) {
         if (dense)
-          launch_rows64<TW, 2, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+          launch_rows64<TW, 2, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
         else
-          launch_rows64<TW, 2, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+          launch_rows64<TW, 2, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
       } else if constexpr (VPL == 4) {
-        launch_rows64<TW, 4, 2>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+        launch_rows64<TW, 4, 2>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
       } else {
-        launch_rows64<TW, 8, 1>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, st);
+        launch_rows64<TW, 8, 1>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
       }
     }
     if (N > 0 && psw != nullptr)

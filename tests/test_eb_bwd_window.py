@@ -4,11 +4,13 @@
 A wave walks its 64 rows two rows ahead of the reduction: get_meta(i + 2)
 may move the LDS window of occurrence metadata before row i is reduced, so
 everything a row needs from the window (its bags and weights) is read inside
-get_meta. This test replays the kernel's order of window loads and reads for
-random row layouts (empty, light, long and heavy rows, partial last waves)
-and checks every index, including the padded reads of the metadata array. It
-also checks that a read of a row's window entries at reduction time could
-fall outside the window.
+get_meta. Rows longer than the prefetch and at most kHeavyT long are reduced
+after the main loop, each with the window moved to its start. This test
+replays the kernel's order of window loads and reads for random row layouts
+(empty, light, long and heavy rows, partial last waves) and checks every
+index, including the padded reads of the metadata array. It also checks that
+a read of a row's window entries at reduction time could fall outside the
+window.
 """
 import random
 
@@ -32,10 +34,15 @@ def _replay(offs, K, U, r0, read_at_process=False):
 
     load_chunk(beg_l[0])
 
+    deferred = []
+
     def get_meta(i):
         beg, end = (beg_l[i], end_l[i]) if i < 64 else (tail, tail)
         cnt = end - beg
-        nh = 0 if cnt > HEAVY_T else min(cnt, U)
+        longrow = U < cnt <= HEAVY_T
+        if longrow:
+            deferred.append(i)
+        nh = 0 if (cnt > HEAVY_T or longrow) else cnt
         if beg + U > st["cbase"] + META_CHUNK:
             load_chunk(beg)
         for lane in range(max(U, 1)):
@@ -49,9 +56,7 @@ def _replay(offs, K, U, r0, read_at_process=False):
         if read_at_process:
             for lane in range(nh):
                 assert 0 <= beg - st["cbase"] + lane < META_CHUNK, "stale window"
-        if U < end - beg <= HEAVY_T:
-            for s in range(beg + U, end, U):
-                assert s + U - 1 < nmeta
+        assert nh <= U
 
     ma, mb = get_meta(0), get_meta(1)
     for i in range(0, 64, 2):
@@ -59,6 +64,21 @@ def _replay(offs, K, U, r0, read_at_process=False):
         ma = get_meta(i + 2)
         process(mb)
         mb = get_meta(i + 3)
+
+    # deferred long rows, in row order: window at the row's start, U at a time
+    assert deferred == sorted(set(deferred))
+    for i in deferred:
+        beg, end = beg_l[i], end_l[i]
+        assert U < end - beg <= HEAVY_T
+        load_chunk(beg)
+        for s in range(beg, end, U):
+            nh = min(end - s, U)
+            for u in range(U):
+                at = s - st["cbase"] + u
+                idx = at if at < META_CHUNK else 0  # the kernel clamps the unused slots' reads
+                assert 0 <= idx < META_CHUNK
+                if u < nh:
+                    assert at < META_CHUNK and beg <= st["cbase"] + at < end
 
 
 def _layouts(seed, n):

@@ -387,6 +387,33 @@ def test_backward_large_gradient_parity(B, L, K, D, dtype, device):
     assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
 
 
+# Rows longer than the row kernel's prefetch but below the heavy threshold
+# (5..250 lookups), packed into the first 64-row windows, beside two heavy rows
+# and uniform rows: with more than 3 lookups per row on average (the 8-slot
+# prefetch) and fewer (4 slots; 2 for float32 rows of 1024).
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("K", [2000, 40000])
+def test_backward_clustered_long_rows(K, dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, D = 512, 128, 1024
+    g = torch.Generator().manual_seed(61)
+    counts = torch.randint(5, 251, (200,), generator=g)
+    ids = [torch.full((int(c),), r) for r, c in enumerate(counts)]
+    ids += [torch.full((400,), 300), torch.full((1000,), 301)]
+    ids = torch.cat(ids)
+    rest = torch.randint(0, K, (B * L - ids.numel(),), generator=g)
+    idx = torch.cat([ids, rest])[torch.randperm(B * L, generator=g)].view(B, L)
+    W, _, p, gr = eb_inputs(B, L, K, D, dtype, seed=62)
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, gr, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, gr)
+    cW, cp = ref.eb_backward(idx, W.abs(), p.abs(), gr.abs())
+    assert_rel_close(gW, eW, REL_TOL[dtype], "grad_weight", cond=cW)
+    assert_rel_close(gp, ep, REL_TOL[dtype], "grad_psw", cond=cp)
+    gW2, gp2 = eb.eb_backward(*_dev(idx, W, p, gr, device=device))
+    assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
+
+
 # Row counts past 2^20 change the sort's digit plan: 2 passes of 11-bit digits
 # up to 2^22 rows, 3 passes of 10-bit digits beyond. Indices also sit on the
 # digit boundaries and at the last row.
