@@ -263,6 +263,42 @@ __device__ __forceinline__ int tile_col(const TileMap& m, int row, int pos) {
   return ((q - tile_rho(m, row)) & (m.slots - 1)) * m.G + g;
 }
 
+// exact_topk over one row of the score tile, for rows whose cheap threshold
+// leaves more than kCandCap candidates (e.g. many equal scores): the row's keys
+// are built once, position by position (the column of a position needs no
+// division), and held in registers (NV per lane, n <= 64 NV) through the
+// threshold search.
+template <typename SLT, int NV>
+__device__ __attribute__((noinline)) typename SLT::Key exact_topk_row(const typename SLT::Store* Srow, TileMap M,
+                                                                      int row, int n, int knn,
+                                                                      typename SLT::Key* scr) {
+  typedef typename SLT::Key Key;
+  constexpr int BITS = 8 * (int)sizeof(Key);
+  const int lane = threadIdx.x & 63;
+  Key kr[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int p = 64 * v + lane;
+    kr[v] = p < n ? SLT::make(Srow[p], (uint32_t)tile_col(M, row, p)) : (Key)0;
+  }
+  Key T = 0;
+  for (int bit = BITS - 1; bit >= 0; --bit) {
+    const Key trial = T | ((Key)1 << bit);
+    uint32_t c = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) c += (uint32_t)__popcll(__ballot(kr[v] >= trial));
+    if (c >= (uint32_t)knn) {
+      T = trial;
+      if (c == (uint32_t)knn) break;  // {keys >= T} is exactly the top-knn
+    }
+  }
+  uint32_t total = 0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wave_append(kr[v] >= T && kr[v] != 0, kr[v], scr, total);
+  __builtin_amdgcn_wave_barrier();
+  return rank_select(scr, total, knn);
+}
+
 // ---------------------------------------------------------------------------
 // LDS layout (host and device agree through score_lds_layout).
 //   S: score tile [TM][n] of order keys; after the second half's selection it
@@ -920,8 +956,9 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
         if (!((ov >> (rr * LPR)) & 1ull)) continue;
         const int row = w * RPW + rr;
         const Store* Srow = S + row * n;
-        const Key best = exact_topk<Key>(
-            [&](int col) { return SL::make(Srow[tile_pos(M, row, col)], (uint32_t)col); }, n, knn, wscr);
+        const Key best = n <= 512    ? exact_topk_row<SL, 8>(Srow, M, row, n, knn, wscr)
+                         : n <= 1024 ? exact_topk_row<SL, 16>(Srow, M, row, n, knn, wscr)
+                                     : exact_topk_row<SL, 32>(Srow, M, row, n, knn, wscr);
         if (lane < knn) ((Key*)(R + L.list_off) + row * L.kl)[lane] = best;
         __builtin_amdgcn_wave_barrier();
       }
