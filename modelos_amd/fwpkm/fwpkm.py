@@ -279,7 +279,12 @@ class FastWeightProductKeyMemory(nn.Module):
         [N, K] (the rest masked to -inf) (fwpkm.py:117-147)."""
         if self.addr_loss_weight == 0.0:
             return torch.tensor(0.0, device=M.device, dtype=M.dtype)
-        kth = torch.topk(M, self.topk, dim=1)[0][:, -1:]
+        return self._marginal_entropy(M, torch.topk(M, self.topk, dim=1)[0][:, -1:], epsilon)
+
+    @staticmethod
+    def _marginal_entropy(M, kth, epsilon=1e-8):
+        """compute_marginal_entropy with each row's k-th largest value kth [N, 1]
+        given (it only enters the comparison, so it carries no gradient)."""
         masked = torch.where(M >= kth, M, torch.full_like(M, float("-inf")))
         p_bar = F.softmax(masked.float(), dim=1).mean(dim=0)
         return (-(p_bar * torch.log(p_bar + epsilon)).sum()).to(M.dtype)
@@ -303,9 +308,19 @@ class FastWeightProductKeyMemory(nn.Module):
             return None
         if self.addr_loss != "me":
             raise NotImplementedError(f"Addressing loss {self.addr_loss} not implemented.")
-        h1 = self.compute_marginal_entropy(all_sub_scores1.view(-1, self.subsize))
-        h2 = self.compute_marginal_entropy(all_sub_scores2.view(-1, self.subsize))
-        return self.addr_loss_weight * (-1.0 * h1 + -1.0 * h2)
+        if self.addr_loss_weight == 0.0:
+            h1 = self.compute_marginal_entropy(all_sub_scores1.view(-1, self.subsize))
+            h2 = self.compute_marginal_entropy(all_sub_scores2.view(-1, self.subsize))
+            return self.addr_loss_weight * (-1.0 * h1 + -1.0 * h2)
+
+        # each row's topk-th largest sub-score is that of its topk-th best sub-key
+        # (the retrieval's per-half lists, best first): the value torch.topk gives
+        def h(all_sub_scores, sub_indices):
+            M = all_sub_scores.view(-1, self.subsize)
+            kth = M.detach().gather(1, sub_indices.reshape(-1, self.topk)[:, -1:])
+            return self._marginal_entropy(M, kth)
+
+        return self.addr_loss_weight * (-1.0 * h(all_sub_scores1, sub_indices1) + -1.0 * h(all_sub_scores2, sub_indices2))
 
     # ---- inner update -----------------------------------------------------------------------
 

@@ -235,3 +235,27 @@ def test_full_shape_fast_weight_step(dtype, device):
     for r in rows:
         assert_rel_close(vf1[r].cpu(), expected[r], 1e-4 if dtype == torch.float32 else 2e-2, f"updated row {r}",
                          elem_frac=None)
+
+
+@pytest.mark.parametrize("dtype,score_type",
+                         [(torch.float32, "idw"), (torch.bfloat16, "idw"), (torch.bfloat16, "dot_product")],
+                         ids=lambda v: str(v).replace("torch.", ""))
+def test_addr_loss_threshold_from_retrieval_lists(dtype, score_type, device):
+    """The marginal-entropy address loss takes each sub-score row's topk-th
+    largest value from the retrieval's per-half lists (the topk-th best
+    sub-key's score) instead of a torch.topk of the row: the same values, ties
+    included (bf16 idw scores tie heavily), so the same loss bit for bit."""
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
+
+    torch.manual_seed(5)
+    mem = FastWeightProductKeyMemory(mem_k_dim=64, mem_v_dim=64, mem_heads=4, mem_topk=8, mem_n_subkeys=128,
+                                     qk_score_type=score_type, addr_loss="me",
+                                     addr_loss_weight=0.1).to(device=device, dtype=dtype)
+    mem.reset_parameters()
+    q = torch.randn(3, 40, 4, 64, generator=gen(6)).to(device=device, dtype=dtype)
+    r = mem.get_indices(q.view(-1, 4, 64), mem.keys)
+    _, _, i1, i2, s1, s2 = r
+    got = mem.compute_addr_loss(i1, i2, s1, s2)
+    want = mem.addr_loss_weight * (-1.0 * mem.compute_marginal_entropy(s1.view(-1, mem.subsize))
+                                   + -1.0 * mem.compute_marginal_entropy(s2.view(-1, mem.subsize)))
+    assert torch.equal(got, want), (got.item(), want.item())
