@@ -297,7 +297,7 @@ def run_layer(args, dev):
     add("pkm_score_topk", ("pkm_score_topk", (tokens, H, n, k // 2)), score_flops(tokens, H, n, k), "TFLOP/s",
         MFMA_BF16_PEAK_TFLOPS, "mfma", "entry point: scoring + per-half top-k kernel, then the cartesian kernel")
     add("pkm_eb_fwd (values)", ("pkm_eb_fwd", (n * n, D)), a_fwd, "GB/s", HBM_PEAK_GBS, "hbm")
-    add("eb_bwd_rows64_kernel (values backward, row reduction)", ("kernel", "eb_bwd_rows"),
+    add("value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)", ("kernel", "eb_bwd_rows"),
         eb_rows_algorithmic_bytes(tokens, L, n * n, D, U), "GB/s", HBM_PEAK_GBS, "hbm")
     add("pkm_eb_bwd (values)", ("pkm_eb_bwd", (n * n, D)), a_bwd, "GB/s", HBM_PEAK_GBS, "hbm",
         "entry point: sort + row reduction + psw-gradient scatter (several kernels)")
@@ -321,7 +321,7 @@ def run_layer(args, dev):
     add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
     add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
     # single kernels timed inside an entry point are part of that entry's time
-    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "eb_bwd_rows64_kernel (values backward, row reduction)")
+    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)")
     for kk in inner:
         if kk in kernels:
             kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd (values)"
@@ -481,7 +481,7 @@ def run_eb(args, dev):
     a_fwd, a_bwd = eb_algorithmic_bytes(B, L, K, D, U)
     kernels = {
         "pkm_eb_fwd (values)": {"ms": round(fwd_ms, 4), "work": a_fwd},
-        "eb_bwd_rows64_kernel (values backward, row reduction)": {
+        "value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)": {
             "ms": round(rows_ms, 4), "work": eb_rows_algorithmic_bytes(B, L, K, D, U),
             "part_of": "pkm_eb_bwd (values)"},
         "pkm_eb_bwd (values)": {"ms": round(bwd_ms, 4), "work": a_bwd,
@@ -491,7 +491,7 @@ def run_eb(args, dev):
         v["achieved"] = round(v["work"] / (v["ms"] * 1e-3) / 1e9, 2)
         v["unit"] = "GB/s"
         v["frac"] = round(v["achieved"] / HBM_PEAK_GBS, 4)
-    dom_name = max(("pkm_eb_fwd (values)", "eb_bwd_rows64_kernel (values backward, row reduction)"),
+    dom_name = max(("pkm_eb_fwd (values)", "value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)"),
                    key=lambda kk: kernels[kk]["ms"])
     dom = kernels[dom_name]
     roofline = {"bound": "hbm", "kernel": dom_name, "achieved": dom["achieved"], "peak": HBM_PEAK_GBS,
