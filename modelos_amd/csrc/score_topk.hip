@@ -1098,7 +1098,7 @@ __global__ __launch_bounds__(kThreads) void pkm_score_cartesian_kernel(int64_t r
 //   * T: the best 32 keys merged so far, sorted, in registers; theta =
 //     T[knn - 1] (0 while fewer than knn are merged).
 //   * Every score whose bf16 value can reach theta is appended to the lane's
-//     LDS slots, branch-free (the slot is written, the count moves on a
+//     LDS slots, branch-free (the slots are written, the count moves on a
 //     pass). The test is one float compare of the raw word
 //     (bf16 bits << 16) | (0xFFFF - index) against tau, the smallest raw word
 //     of theta's value (NaN while theta = 0, which nothing is below): a raw
@@ -1235,7 +1235,8 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Slot budget. Merges are decided once per 64-key block for the whole
 // workgroup. At the start of a block every lane holds at most kTrigger - 1
 // unmerged slots (a merge takes slots [0, 64) and leaves max(cnt - 64, 0)),
-// and a block appends at most 64, so kTrigger + 63 slots suffice; the merge
+// and a block appends at most 64, so kTrigger + 63 slots suffice (the
+// paired append writes one slot past the count, still inside them); the merge
 // moves slots [64, kBuf) to the front.
 constexpr int kTrigger = 28;
 static_assert(kTrigger + 63 <= kBuf && kBuf - 64 >= kTrigger - 1, "slot budget");
@@ -1248,15 +1249,22 @@ __host__ __device__ constexpr int word_key(int w) {
 }
 
 // Append the two scores of word p (keys key, key + 1) that can reach theta;
-// cb is the lane's slot count times the slot stride (kThreads words).
+// cb is the lane's slot count times the slot stride (kThreads words). Both
+// slots cb and cb + 1 are written by one instruction: slot cb takes r0 if it
+// passes and r1 otherwise, slot cb + 1 takes r1, and the count moves by the
+// number that pass, so the slots below the count are exactly the passing
+// scores in order (slot cb + 1 lies past the count unless both pass, and is
+// overwritten later).
 __device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* buf, uint32_t& cb, float tau,
                                             uint32_t hi_mask) {
   const uint32_t r0 = (p << 16) | (0xFFFFu - key);
   const uint32_t r1 = (p & hi_mask) | (0xFFFEu - key);
-  *(uint32_t*)((unsigned char*)buf + cb) = r0;
-  cb += !(__uint_as_float(r0) < tau) ? kThreads * 4u : 0u;
-  *(uint32_t*)((unsigned char*)buf + cb) = r1;
-  cb += !(__uint_as_float(r1) < tau) ? kThreads * 4u : 0u;
+  const bool p0 = !(__uint_as_float(r0) < tau);
+  const bool p1 = !(__uint_as_float(r1) < tau);
+  uint32_t* s = (uint32_t*)((unsigned char*)buf + cb);
+  s[0] = p0 ? r0 : r1;
+  s[kThreads] = r1;
+  cb += (p0 ? kThreads * 4u : 0u) + (p1 ? kThreads * 4u : 0u);
 }
 
 // Words 16 KT + 2 J + {0, 1} from elements 2J, 2J + 1 of the token-set

@@ -219,10 +219,10 @@ def word_key(w: int) -> int:
 
 
 # a block's key order: words in order, each its two keys
-BLOCK_ORDER = [word_key(w) + v for w in range(32) for v in range(2)]
+BLOCK_ORDER = [word_key(w) + v for w in range(K_KB // 2) for v in range(2)]
 
 
-def stream_select(bits: np.ndarray, knn: int) -> np.ndarray:
+def stream_select(bits: np.ndarray, knn: int, stats: dict | None = None) -> np.ndarray:
     """The kernel's selection for the tokens of one workgroup (rows of bits
     [tokens <= 256, n], bf16 scores of one half): returns the okey16-form
     lists [tokens, knn] (okey16 << 16 | 0xFFFF - index)."""
@@ -262,12 +262,21 @@ def stream_select(bits: np.ndarray, knn: int) -> np.ndarray:
     for j in range(nb + 1):
         if j >= 1:
             # the appends of block j - 1's words, during block j (or the drain)
-            for key in BLOCK_ORDER:
-                kk = (j - 1) * K_KB + key
-                r = raw_words(bits[:, kk], np.full(L, kk))
-                buf[lanes, cnt] = r  # the slot is written whether or not it counts
-                cnt += ~(r.view(np.float32) < tau)
-                assert cnt.max() <= K_BUF
+            for key0, key1 in zip(BLOCK_ORDER[0::2], BLOCK_ORDER[1::2]):
+                # a word's two scores: slot cnt takes the first if it passes,
+                # else the second; slot cnt + 1 takes the second (both are
+                # written whether or not they count)
+                k0, k1 = (j - 1) * K_KB + key0, (j - 1) * K_KB + key1
+                r0 = raw_words(bits[:, k0], np.full(L, k0))
+                r1 = raw_words(bits[:, k1], np.full(L, k1))
+                p0 = ~(r0.view(np.float32) < tau)
+                p1 = ~(r1.view(np.float32) < tau)
+                assert cnt.max() + 2 <= K_BUF, "both slots of a word inside the buffer"
+                buf[lanes, cnt] = np.where(p0, r0, r1)
+                buf[lanes, cnt + 1] = r1
+                cnt += p0.astype(np.int64) + p1.astype(np.int64)
+                if stats is not None:
+                    stats["max_cnt"] = max(stats.get("max_cnt", 0), int(cnt.max()))
         if j == 0:
             tau[:] = np.nan  # from the first block's words until the first merge
         if j < nb:
@@ -324,7 +333,8 @@ def test_stream_tie_heavy_and_signed_zeros():
 
 def test_stream_key_orders_that_fill_slots_fastest():
     # increasing scores: every key beats every earlier one, so every block
-    # appends all of its 64 scores; decreasing: only the first block does
+    # appends all of its scores; decreasing: only the blocks before the first
+    # merge do
     n = 2048
     inc = torch.linspace(-4.0, 4.0, n)
     for row in (inc, inc.flip(0), -inc.abs(), inc * 0.0 + torch.arange(n) % 3):
@@ -333,23 +343,40 @@ def test_stream_key_orders_that_fill_slots_fastest():
 
 
 def test_stream_slot_budget_worst_case():
-    # A lane holding kTrigger - 1 unmerged slots (one block appends that many,
-    # too few to trigger a merge) and then appending a whole block: the most
-    # slots a lane can hold. Scores are given as bf16 bits: 0x3F80 + rank is
-    # an increasing run of positive values.
+    # Lanes that reach kTrigger - 1 unmerged slots at the start of a block
+    # (too few for a merge) and then append a whole block: the most slots a
+    # lane can hold. Scores are bf16 bits: 0x3F80 + rank is an increasing run
+    # of positive values, so a key at a higher rank than every earlier one
+    # passes; 0xBF80 (-1.0) is below everything, so once a merge has set
+    # theta it never passes (before the first merge every score passes).
     rng = np.random.default_rng(40)
-    n, L = 64 * 8, 256
-    bits = np.empty((L, n), dtype=np.int64)
-    for t in range(L):
-        bits[t, :64] = 0x3F80 + rng.permutation(64)
-        b1 = np.full(64, 0xBF80)  # -1.0: below everything
-        b1[rng.choice(64, K_TRIGGER - 1, replace=False)] = 0x3F80 + 100 + np.arange(K_TRIGGER - 1)
-        bits[t, 64:128] = b1
-        bits[t, 128:] = 0x3F80 + 200 + np.arange(n - 128)  # every later key beats all before it
-        if t % 2:
-            bits[t, 128:] = bits[t, 128:][::-1]  # half of the lanes: only block 2 appends
+    first = -(-K_TRIGGER // K_KB)  # blocks of all-passing scores until the first merge
+    left = first * K_KB - 64  # slots the first merge leaves
+    assert 0 <= left < K_TRIGGER
+    fill = []  # passing counts of the following blocks up to kTrigger - 1 slots
+    while left + sum(fill) < K_TRIGGER - 1:
+        fill.append(min(K_KB, K_TRIGGER - 1 - left - sum(fill)))
+    nblk = first + len(fill) + 3
+    n, L = K_KB * nblk, 256
     for knn in (1, 32):
+        bits = np.empty((L, n), dtype=np.int64)
+        for t in range(L):
+            rank = 0
+            for b in range(nblk):
+                seg = np.full(K_KB, 0xBF80, dtype=np.int64)
+                cnt_b = K_KB if (b < first or b >= first + len(fill)) else fill[b - first]
+                pos = np.sort(rng.choice(K_KB, cnt_b, replace=False))
+                seg[pos] = 0x3F80 + rank + np.arange(cnt_b)
+                rank += cnt_b
+                bits[t, b * K_KB:(b + 1) * K_KB] = seg
+            if t % 2:  # half of the lanes: the full blocks after the fill reversed
+                tail = bits[t, (first + len(fill)) * K_KB:]
+                bits[t, (first + len(fill)) * K_KB:] = tail[::-1]
+        stats = {}
+        lists = stream_select(bits, knn, stats)
+        assert stats["max_cnt"] == K_TRIGGER - 1 + K_KB <= K_BUF, stats
         check_rows(bits, knn)
+        assert lists.shape == (L, knn)
 
 
 def test_stream_extremes():
