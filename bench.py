@@ -297,10 +297,13 @@ def run_layer(args, dev):
     add("pkm_score_topk", ("pkm_score_topk", (tokens, H, n, k // 2)), score_flops(tokens, H, n, k), "TFLOP/s",
         MFMA_BF16_PEAK_TFLOPS, "mfma", "entry point: scoring + per-half top-k kernel, then the cartesian kernel")
     add("pkm_eb_fwd (values)", ("pkm_eb_fwd", (n * n, D)), a_fwd, "GB/s", HBM_PEAK_GBS, "hbm")
-    add("value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)", ("kernel", "eb_bwd_rows"),
+    add("value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)", ("kernel", "eb_bwd_rows"),
         eb_rows_algorithmic_bytes(tokens, L, n * n, D, U), "GB/s", HBM_PEAK_GBS, "hbm")
-    add("pkm_eb_bwd (values)", ("pkm_eb_bwd", (n * n, D)), a_bwd, "GB/s", HBM_PEAK_GBS, "hbm",
-        "entry point: sort + row reduction + psw-gradient scatter (several kernels)")
+    add("pkm_eb_bwd_prepared (values: reduction)", ("pkm_eb_bwd_prepared", (n * n, D)), a_bwd, "GB/s",
+        HBM_PEAK_GBS, "hbm", "entry point: row reduction + psw-gradient scatter; its sort ran with the forward")
+    add("pkm_eb_bwd_prepare (values: sort, side stream)", ("pkm_eb_bwd_prepare", (n * n, D)), a_bwd, "GB/s",
+        HBM_PEAK_GBS, "hbm", "entry point: sort, row offsets, metadata; queued at the start of the layer's backward "
+        "on a side stream, beside the value projection / gate backward")
 
     def add_ms(name, entry, note):
         """Every call of one entry point, whatever its sizes."""
@@ -321,10 +324,12 @@ def run_layer(args, dev):
     add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
     add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
     # single kernels timed inside an entry point are part of that entry's time
-    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)")
-    for kk in inner:
+    # and work on the side stream overlaps the current stream's: neither adds to the step
+    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)",
+             "pkm_eb_bwd_prepare (values: sort, side stream)")
+    for kk in inner[:2]:
         if kk in kernels:
-            kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd (values)"
+            kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd_prepared (values: reduction)"
     hip_ms = sum(v["ms"] * v["calls_per_step"] for kk, v in kernels.items() if kk not in inner)
     kernels["other (query/swilu/value GEMMs, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
 
@@ -481,7 +486,7 @@ def run_eb(args, dev):
     a_fwd, a_bwd = eb_algorithmic_bytes(B, L, K, D, U)
     kernels = {
         "pkm_eb_fwd (values)": {"ms": round(fwd_ms, 4), "work": a_fwd},
-        "value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)": {
+        "value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)": {
             "ms": round(rows_ms, 4), "work": eb_rows_algorithmic_bytes(B, L, K, D, U),
             "part_of": "pkm_eb_bwd (values)"},
         "pkm_eb_bwd (values)": {"ms": round(bwd_ms, 4), "work": a_bwd,
@@ -491,7 +496,7 @@ def run_eb(args, dev):
         v["achieved"] = round(v["work"] / (v["ms"] * 1e-3) / 1e9, 2)
         v["unit"] = "GB/s"
         v["frac"] = round(v["achieved"] / HBM_PEAK_GBS, 4)
-    dom_name = max(("pkm_eb_fwd (values)", "value backward row reduction (eb_bwd_rows64_kernel + eb_bwd_long_rows_kernel)"),
+    dom_name = max(("pkm_eb_fwd (values)", "value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)"),
                    key=lambda kk: kernels[kk]["ms"])
     dom = kernels[dom_name]
     roofline = {"bound": "hbm", "kernel": dom_name, "achieved": dom["achieved"], "peak": HBM_PEAK_GBS,

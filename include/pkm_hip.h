@@ -89,6 +89,34 @@ int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dty
                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * pkm_eb_bwd in two steps, so that the part that depends only on the lookups
+ * can run early (e.g. during the forward pass, on another stream, beside the
+ * gather) and the backward pass keeps only the reduction:
+ *   pkm_eb_bwd_prepare  sorts the lookups by row, builds the row offsets, the
+ *                       per-lookup metadata (bag, weight) and the row
+ *                       kernel's lists in `workspace`. It reads indices and
+ *                       psw, not weight or grad_out.
+ *   pkm_eb_bwd_prepared runs the reduction (grad_weight, grad_psw) on a
+ *                       workspace that pkm_eb_bwd_prepare filled, with the
+ *                       same num_rows, dim, weight_dtype, indices, psw, bags
+ *                       and bag_size (psw unchanged in between; the caller
+ *                       orders the two calls, e.g. with an event).
+ * pkm_eb_bwd(args) == pkm_eb_bwd_prepare + pkm_eb_bwd_prepared, bit for bit.
+ * Together they replace the same reference code as pkm_eb_bwd (its
+ * count/argsort/map steps, pkm/xformer_embeddingbag.py:261-288, are the
+ * prepare step; aggregate_gradient_for_embedding_k, :291-328, the reduction).
+ */
+int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtype,
+                       const int64_t* indices, const void* psw, int psw_dtype,
+                       int64_t bags, int64_t bag_size,
+                       void* workspace, size_t workspace_bytes, void* stream);
+int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                        const int64_t* indices, const void* psw, int psw_dtype,
+                        const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
+                        void* grad_weight, void* grad_psw,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * pkm_eb_bwd without a workspace argument: the same kernels and results
  * (bit-identical outputs), with their workspace in a fixed scratch array of
  * 64 MiB that the library holds on each GPU it runs on until the process ends.

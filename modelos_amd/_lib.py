@@ -35,6 +35,26 @@ SIGNATURES = {
             c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),
+    "pkm_eb_bwd_prepare": (
+        c_int,
+        [
+            c_int64, c_int64, c_int,  # num_rows, dim, weight_dtype
+            c_void_p, c_void_p, c_int,  # indices, psw, psw_dtype
+            c_int64, c_int64,  # bags, bag_size
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+    "pkm_eb_bwd_prepared": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64, c_int,  # weight, num_rows, dim, weight_dtype
+            c_void_p, c_void_p, c_int,  # indices, psw, psw_dtype
+            c_void_p, c_int,  # grad_out, grad_dtype
+            c_int64, c_int64,  # bags, bag_size
+            c_void_p, c_void_p,  # grad_weight, grad_psw
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
     "pkm_eb_bwd_noalloc": (
         c_int,
         [
@@ -251,6 +271,8 @@ _SIZE_ARGS = {
     "pkm_eb_fwd": (1, 2),  # num_rows, dim
     "pkm_eb_bwd": (1, 2),
     "pkm_eb_bwd_noalloc": (1, 2),
+    "pkm_eb_bwd_prepare": (0, 1),
+    "pkm_eb_bwd_prepared": (1, 2),
     "pkm_eb_bwd2": (1, 2),
     "pkm_score_topk": (2, 3, 4, 5),  # num_tokens, heads, n_keys, half
     "pkm_score_grad_sparse": (3, 4, 5, 6),  # num_tokens, heads, n_keys, half

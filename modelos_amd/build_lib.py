@@ -37,9 +37,18 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-source flags. eb_bwd.hip: its atomics are issued by one lane on purpose
+# and their results are used late (ticket counters taken ahead of use); the
+# atomic optimizer would rewrite each into a wave-wide form whose result is
+# read right after the atomic, a wait for every load in flight.
+SOURCE_FLAGS = {
+    "eb_bwd.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *DEVICE_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)

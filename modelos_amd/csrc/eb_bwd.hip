@@ -23,13 +23,15 @@
 //              T sorted occurrences; each chunk writes a float32 partial sum
 //              (2 slots per chunk: the row running in from the previous chunk
 //              and the row starting inside this one).
-//  4. rows:    a wave owns 64 consecutive rows and walks them in order with the
-//              row offsets and a 64-entry window of occurrence metadata
-//              (position, bag, weight) in lane registers: one memory round trip
-//              per touched row. Untouched rows get zeros, light rows are reduced
-//              in position order while the wave holds W[r] in registers for the
-//              psw-gradient dot products, heavy rows add their chunk partials in
-//              chunk order.
+//  4. rows:    a wave reduces one row at a time, in position order, with the
+//              next row's loads in flight; rows are handed out in chunks of 4
+//              through per-XCD ticket counters so that the waves of one XCD
+//              work on the same block of 1024 rows at once (PKM's lookups of a
+//              bag share sub-key blocks: their gradient rows are re-read from
+//              that XCD's L2). Untouched rows get zeros, light rows are reduced
+//              while the wave holds W[r] in registers for the psw-gradient dot
+//              products, heavy rows add their chunk partials in chunk order,
+//              rows longer than the prefetch go to a one-row-per-wave kernel.
 // HBM traffic: W is read once per distinct row, gW written once per row, the
 // upstream gradient g (B x D, tens of MB) is re-read per occurrence from
 // L2 / Infinity Cache.
@@ -184,12 +186,16 @@ __device__ __forceinline__ bool radix_item(int64_t p, int64_t N, uint32_t nv, co
   return true;
 }
 
+// FIRST pass: lookups whose index is outside [0, K) are dropped from the sort
+// and their positions listed (invalid[0] = count, then the positions; one
+// atomic per wave that holds any), so the reduction can zero their
+// psw-gradients.
 template <bool FIRST, int BITS>
 __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restrict__ idx,
                                                          const uint32_t* __restrict__ keys, int64_t N,
                                                          const uint32_t* __restrict__ nvalid, int64_t K, int shift,
                                                          uint32_t* __restrict__ hist, int64_t ntiles,
-                                                         void* __restrict__ gpsw, int pdt) {
+                                                         uint32_t* __restrict__ invalid) {
   constexpr int R = 1 << BITS;
   __shared__ uint32_t h[R];
   for (int d = threadIdx.x; d < R; d += 256) h[d] = 0;
@@ -200,10 +206,18 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restri
   for (int i = 0; i < kRadixItems * kRadixSubs; ++i) {
     const int64_t p = base + (int64_t)i * 256 + threadIdx.x;
     uint32_t k;
-    if (radix_item<FIRST>(p, N, nv, idx, keys, K, &k)) {
-      atomicAdd(&h[(k >> shift) & (R - 1)], 1u);
-    } else if (FIRST && p < N && gpsw != nullptr) {
-      store_scalar(gpsw, pdt, p, 0.f);  // out-of-range index: zero psw-gradient
+    const bool valid = radix_item<FIRST>(p, N, nv, idx, keys, K, &k);
+    if (valid) atomicAdd(&h[(k >> shift) & (R - 1)], 1u);
+    if (FIRST) {
+      const bool bad = !valid && p < N;
+      const uint64_t m = __ballot(bad);
+      if (m != 0ull) {
+        const int lane = threadIdx.x & 63;
+        uint32_t at = 0;
+        if (lane == 0) at = atomicAdd(invalid, (uint32_t)__popcll(m));
+        at = (uint32_t)__builtin_amdgcn_readlane((int)at, 0);
+        if (bad) invalid[1 + at + (uint32_t)__popcll(lane == 0 ? 0ull : (m & (~0ull >> (64 - lane))))] = (uint32_t)p;
+      }
     }
   }
   __syncthreads();
@@ -556,17 +570,16 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
   }
 }
 
-// Wave-per-64-rows kernel (rows of 64*VPL 16-byte vectors), software-pipelined.
+// Row kernel (a wave per row; rows of 64*VPL 16-byte vectors), software-pipelined.
 //
 // Row i+1's W row and its first U gradient rows are in flight while row i is
 // reduced and stored. gfx9 counts loads and stores in one in-order vmcnt, so
 // the loads must be issued before the current row's stores, and every row
 // issues the same number of vector loads (unused slots read a zero row, tail
-// rows past K write a dummy row) so the compiler's waits stay partial.
-// Occurrence metadata comes from an LDS window (lgkmcnt, not vmcnt); the
+// rows past K write a dummy row) so the compiler's waits stay partial. The
 // psw-gradient dots of a row leave in one store into sorted order and are
 // scattered by position afterwards.
-constexpr int kMetaChunk = 256;  // per-wave LDS window of occurrence metadata (entries)
+constexpr int kMetaPad = 16;  // metadata entries past the last lookup (a row's U-slot reads stay in bounds)
 
 // Sums of 8 per-lane partials over the 64 lanes of a wave, one butterfly for
 // all 8 (18 lane operations instead of 8 full-wave reductions): lane l gets the
@@ -654,158 +667,7 @@ __device__ __forceinline__ float accumulate_slots(const RowData<VPL, U>& R, cons
   return mydot;
 }
 
-template <typename TW, int VPL, int U>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 && U <= 4) ? 5 : ((VPL == 1 || (VPL == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows64_kernel(
-    const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TW* __restrict__ g,
-    const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
-    const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
-    uint32_t dummy_slot, uint32_t* __restrict__ long_rows, uint32_t* __restrict__ long_count) {
-  __shared__ uint2 smeta[4][kMetaChunk];
-  constexpr int EPV = VecTraits<TW>::EPV;
-  constexpr int NE = VPL * EPV;
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int64_t r0 = ((int64_t)blockIdx.x * 4 + wv) * 64;
-  if (r0 >= K) return;
-  const int nrows = (int)((K - r0) < 64 ? (K - r0) : 64);
-  const int64_t col0 = (int64_t)lane * EPV;
-  const uint32_t lane_byte = (uint32_t)lane * 16u;  // lane's byte offset inside a row
-  const uint64_t rowbytes = (uint64_t)D * sizeof(TW);
-  const char* Wb = (const char*)W;
-  const char* gb = (const char*)g;
-  const char* zb = (const char*)zrow;
-
-  // lane i: [begin, end) of row r0 + i in the sorted stream; lanes past the
-  // last row describe an empty row at the end of the wave's stream
-  const uint32_t tail = offs[r0 + nrows];
-  uint32_t my_beg = tail, my_end = tail;
-  if (lane < nrows) {
-    my_beg = offs[r0 + lane];
-    my_end = offs[r0 + lane + 1];
-  }
-
-  uint2* sm = smeta[wv];
-  uint32_t cbase = (uint32_t)__builtin_amdgcn_readlane((int)my_beg, 0);
-  auto load_chunk = [&](uint32_t start) {
-    cbase = start;
-#pragma unroll
-    for (int k = 0; k < kMetaChunk / 64; ++k) sm[lane + 64 * k] = meta[start + lane + 64 * k];
-  };
-  load_chunk(cbase);
-
-  uint64_t deferred = 0;  // long light rows (bit i: row r0 + i), listed after the main loop
-  auto get_meta = [&](int i, RowMeta<U>& M) {
-    if (i < 64) {
-      M.beg = (uint32_t)__builtin_amdgcn_readlane((int)my_beg, i);
-      M.end = (uint32_t)__builtin_amdgcn_readlane((int)my_end, i);
-    } else {
-      M.beg = M.end = tail;
-    }
-    const uint32_t cnt = M.end - M.beg;
-    // rows longer than the prefetch (and light) are listed for the long-row kernel
-    const bool longrow = cnt > (uint32_t)U && cnt <= (uint32_t)kHeavyT;
-    if (longrow) deferred |= 1ull << i;
-    M.nh = (cnt > (uint32_t)kHeavyT || longrow) ? 0u : cnt;
-    if (M.beg + U > cbase + kMetaChunk) load_chunk(M.beg);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint2 m = sm[M.beg - cbase + u];
-      M.b[u] = (uint32_t)__builtin_amdgcn_readfirstlane((int)m.x);
-      M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readfirstlane((int)m.y)) : 0.f;
-    }
-  };
-  auto issue = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
-    const char* wrow = (want_dot && M.nh) ? Wb + (uint64_t)(r0 + i) * rowbytes : zb;
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16(wrow + lane_byte + v * 1024u);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * rowbytes : zb;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
-    }
-  };
-  // acc += sum_{u < nh} w[u] * gvec[u]; lane u of the returned value holds
-  // <wraw, gvec[u]> (slots u >= nh, wave-uniform, are skipped)
-  // acc += sum_{u < nh} w[u] * gvec[u]; the returned value holds, on lane
-  // dot_slot, the dot of that slot (as accumulate_slots, written out here: as
-  // a call it costs this kernel registers and spills)
-  auto accumulate = [&](const RowData<VPL, U>& R, const float* w, uint32_t nh, float* acc) {
-    float d[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      d[u] = 0.f;
-      if ((uint32_t)u < nh) {
-        float f[NE];
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.gvec[u][v], f + v * EPV);
-#pragma unroll
-        for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
-        if (want_dot) {
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) d[u] = vec_dot<TW>(R.wraw[v], R.gvec[u][v], d[u]);
-        }
-      }
-    }
-    float mydot = 0.f;
-    if (want_dot) {
-      if constexpr (U == 8) {
-        mydot = reduce8_slots(d, lane);
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if ((uint32_t)u < nh) {
-            const float t = group_sum<64>(d[u]);
-            mydot = lane == u ? t : mydot;
-          }
-        }
-      }
-    }
-    return mydot;
-  };
-  const int dot_slot = dot_slot_of<U>(lane);
-  const bool dot_store = dot_store_of<U>(lane);
-  auto process = [&](int i, const RowMeta<U>& M, RowData<VPL, U>& R) {
-    if ((deferred >> i) & 1ull) return;  // a long light row: reduced by the long-row kernel
-    float acc[NE];
-#pragma unroll
-    for (int e = 0; e < NE; ++e) acc[e] = 0.f;
-    const float mydot = accumulate(R, M.w, M.nh, acc);
-    if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
-    if (M.end - M.beg > (uint32_t)kHeavyT) add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
-    char* orow = (r0 + i < K) ? (char*)gW + (uint64_t)(r0 + i) * rowbytes : (char*)dummy_row;
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
-  };
-
-  RowMeta<U> MA, MB;
-  RowData<VPL, U> DA, DB;
-  get_meta(0, MA);
-  issue(0, MA, DA);
-  get_meta(1, MB);
-  for (int i = 0; i < 64; i += 2) {
-    issue(i + 1, MB, DB);
-    process(i, MA, DA);
-    get_meta(i + 2, MA);
-    issue(i + 2, MA, DA);
-    process(i + 1, MB, DB);
-    get_meta(i + 3, MB);
-  }
-
-  // long light rows (U < count <= kHeavyT) go to the list that
-  // eb_bwd_long_rows_kernel reduces, one row per wave
-  if (deferred != 0ull) {
-    uint32_t base = 0;
-    if (lane == 0) base = atomicAdd(long_count, (uint32_t)__popcll(deferred));
-    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-    if ((deferred >> lane) & 1ull) {
-      const uint64_t below = lane == 0 ? 0ull : (deferred & (~0ull >> (64 - lane)));
-      long_rows[base + (uint32_t)__popcll(below)] = (uint32_t)(r0 + lane);
-    }
-  }
-}
-
-// The long light rows the row kernel listed: each wave takes one row at a time
+// The long light rows list_long_rows_kernel listed: each wave takes one row at a time
 // (grid-stride over the list, whose length every wave reads, so every wave
 // ends) and reduces it U occurrences at a time, in order, the next chunk's
 // metadata and gradient rows in flight while the current chunk is reduced.
@@ -873,6 +735,217 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row reduction scheduled for L2 reuse of the upstream gradient.
+//
+// PKM lookups are not uniform over the table: a bag's lookups for one head
+// are the best pairs (i1, i2) of two short sub-key lists, so they share a few
+// i1 values, and row i1 * n + i2 lies in the block of n consecutive rows of
+// its i1. A block of 1024 rows is touched by ~1500 distinct bags at the
+// layer shape, most of them ~2.7 times. If the waves of one XCD (one L2)
+// reduce the same block at the same time, those re-reads of a bag's gradient
+// row hit that L2 instead of going out to the Infinity Cache.
+//
+// Rows are split into blocks of `blk` rows; block k belongs to row group
+// k % 8, and workgroup w works for group w % 8 (the XCD that round-robin
+// dispatch places it on). Each group hands out its rows in chunks of kDynRC
+// consecutive rows, block after block, through kDynSub ticket counters
+// (counter s serves chunks s, s + kDynSub, ... of every block; workgroup w
+// uses counter (w / 8) % kDynSub, each counter on its own cache line): a
+// wave takes the next ticket when it needs work, so the XCD's waves stay on
+// one or two blocks at a time (a static split drifts apart over a kernel's
+// length). Tickets are taken two chunks ahead and each chunk's row offsets
+// and metadata are loaded one chunk ahead, so their latency hides under the
+// current chunk's rows. Each row is still reduced by one wave in position
+// order, so the sums are those of the per-64-rows kernel, bit for bit.
+// Rows longer than the prefetch (and light) are listed beforehand by
+// list_long_rows_kernel and skipped here.
+// ---------------------------------------------------------------------------
+constexpr int kDynRC = 4;       // rows per ticket
+constexpr int kDynGroups = 8;   // row groups: one per XCD
+constexpr int kDynSub = 4;      // ticket counters per group (one counter serves ~70 M tickets/s)
+constexpr int kCtrStride = 64;  // u32 entries between counters: one 256-byte line each
+
+struct DynChunk {
+  uint32_t row0;  // first row (wave-uniform); K for a chunk past the group's end
+  uint32_t off;   // lane i <= kDynRC: offs[min(row0 + i, K)]
+  uint32_t mb;    // lane l < kDynRC * U: bag of row l / U, slot l % U
+  uint32_t mw;    // ... its weight (float32 bits)
+};
+
+// Rows with offs[r + 1] - offs[r] in (U, kHeavyT], listed for
+// eb_bwd_long_rows_kernel. A workgroup owns rows_per_wg consecutive rows: it
+// counts its long rows, takes its range of the list with one atomic (atomics
+// on one address serialise, ~15 ns each), then writes them.
+__global__ __launch_bounds__(256) void list_long_rows_kernel(const uint32_t* __restrict__ offs, int64_t K,
+                                                             uint32_t U, int64_t rows_per_wg,
+                                                             uint32_t* __restrict__ long_rows,
+                                                             uint32_t* __restrict__ long_count) {
+  __shared__ uint32_t wave_cnt[4];
+  __shared__ uint32_t wg_base;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t r_beg = (int64_t)blockIdx.x * rows_per_wg;
+  const int64_t r_end = r_beg + rows_per_wg < K ? r_beg + rows_per_wg : K;
+  auto is_long = [&](int64_t r) {
+    const uint32_t cnt = r < r_end ? offs[r + 1] - offs[r] : 0u;
+    return cnt > U && cnt <= (uint32_t)kHeavyT;
+  };
+  uint32_t n = 0;
+  for (int64_t r0 = r_beg + wv * 64; r0 < r_end; r0 += 256) n += (uint32_t)__popcll(__ballot(is_long(r0 + lane)));
+  if (lane == 0) wave_cnt[wv] = n;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t total = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    wg_base = total ? atomicAdd(long_count, total) : 0u;
+  }
+  __syncthreads();
+  uint32_t at = wg_base;
+  for (int w = 0; w < wv; ++w) at += wave_cnt[w];
+  if (n == 0) return;
+  for (int64_t r0 = r_beg + wv * 64; r0 < r_end; r0 += 256) {
+    const bool lng = is_long(r0 + lane);
+    const uint64_t mask = __ballot(lng);
+    if (lng) {
+      const uint64_t below = lane == 0 ? 0ull : (mask & (~0ull >> (64 - lane)));
+      long_rows[at + (uint32_t)__popcll(below)] = (uint32_t)(r0 + lane);
+    }
+    at += (uint32_t)__popcll(mask);
+  }
+}
+
+template <typename TW, int VPL, int U>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 && U <= 4) ? 5 : ((VPL == 1 || (VPL == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows_dyn_kernel(
+    const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TW* __restrict__ g,
+    const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
+    const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
+    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk) {
+  static_assert(kDynRC * U <= 64, "a chunk's metadata must fit one load per lane");
+  constexpr int EPV = VecTraits<TW>::EPV;
+  constexpr int NE = VPL * EPV;
+  const int lane = threadIdx.x & 63;
+  const uint32_t grp = blockIdx.x % kDynGroups;
+  const uint32_t sub = (blockIdx.x / kDynGroups) % kDynSub;
+  const uint32_t nblk = (uint32_t)((K + blk - 1) / blk);
+  const uint32_t grp_blocks = nblk > grp ? (nblk - grp + kDynGroups - 1) / kDynGroups : 0u;
+  const uint32_t cpb = blk / (kDynRC * kDynSub);  // chunks per block and counter
+  const uint32_t nchunks = grp_blocks * cpb;
+  const uint32_t K32 = (uint32_t)K;
+  const uint32_t lane_byte = (uint32_t)lane * 16u;
+  const uint64_t rowbytes = (uint64_t)D * sizeof(TW);
+  const char* Wb = (const char*)W;
+  const char* gb = (const char*)g;
+  const char* zb = (const char*)zrow;
+  uint32_t* ticket_ctr = tickets + (grp * kDynSub + sub) * kCtrStride;
+
+  auto take_ticket = [&]() {
+    uint32_t t = 0;
+    if (lane == 0) t = atomicAdd(ticket_ctr, 1u);
+    return t;  // lane 0's value; read with readlane when used
+  };
+  auto fetch_offs = [&](uint32_t t_lane0, DynChunk& C) {
+    const uint32_t t = (uint32_t)__builtin_amdgcn_readlane((int)t_lane0, 0);
+    C.row0 = K32;
+    if (t < nchunks) C.row0 = (grp + kDynGroups * (t / cpb)) * blk + ((t % cpb) * kDynSub + sub) * kDynRC;
+    const uint32_t i = (uint32_t)(lane < kDynRC ? lane : kDynRC);
+    const uint32_t r = C.row0 + i < K32 ? C.row0 + i : K32;
+    C.off = offs[r];
+  };
+  auto fetch_meta = [&](DynChunk& C) {
+    const int ri = (lane / U) & (kDynRC - 1);
+    const uint32_t beg = (uint32_t)__shfl((int)C.off, ri);
+    const uint2 m = meta[beg + (uint32_t)(lane % U)];  // in bounds: meta is padded past every row start
+    C.mb = m.x;
+    C.mw = m.y;
+  };
+  auto get_meta = [&](const DynChunk& C, int i, RowMeta<U>& M, uint32_t& row, bool& skip) {
+    M.beg = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i);
+    M.end = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i + 1);
+    const uint32_t cnt = M.end - M.beg;
+    skip = cnt > (uint32_t)U && cnt <= (uint32_t)kHeavyT;  // listed for the long-row kernel
+    M.nh = cnt <= (uint32_t)U ? cnt : 0u;
+    row = C.row0 + (uint32_t)i;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      M.b[u] = (uint32_t)__builtin_amdgcn_readlane((int)C.mb, i * U + u);
+      M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readlane((int)C.mw, i * U + u)) : 0.f;
+    }
+  };
+  auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U>& R) {
+    const char* wrow = (want_dot && M.nh) ? Wb + (uint64_t)row * rowbytes : zb;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);  // read once: keep L2 for g
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * rowbytes : zb;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+    }
+  };
+  const int dot_slot = dot_slot_of<U>(lane);
+  const bool dot_store = dot_store_of<U>(lane);
+  const int64_t col0 = (int64_t)lane * EPV;
+  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, const RowData<VPL, U>& R) {
+    if (skip) return;  // a long light row: reduced by the long-row kernel
+    float acc[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) acc[e] = 0.f;
+    const float mydot = accumulate_slots<TW, VPL, U>(R, M.w, M.nh, acc, want_dot != 0, lane);
+    if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
+    if (M.end - M.beg > (uint32_t)kHeavyT) add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
+    char* orow = row < K32 ? (char*)gW + (uint64_t)row * rowbytes : (char*)dummy_row;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
+  };
+
+  // prologue: chunk 0's offsets and metadata, chunk 1's offsets, chunk 2's ticket
+  DynChunk cur, nxt, nn;
+  const uint32_t t0 = take_ticket();
+  const uint32_t t1 = take_ticket();
+  uint32_t tk = take_ticket();
+  fetch_offs(t0, cur);
+  if (cur.row0 >= K32) return;  // nothing left for this group
+  fetch_meta(cur);
+  fetch_offs(t1, nxt);
+
+  RowMeta<U> MA, MB;
+  RowData<VPL, U> DA, DB;
+  uint32_t rowA, rowB;
+  bool skA, skB;
+  get_meta(cur, 0, MA, rowA, skA);
+  issue(MA, rowA, DA);
+  get_meta(cur, 1, MB, rowB, skB);
+  // One chunk's 4 rows per trip, rows i and i + 1 in flight across chunk
+  // boundaries. The order keeps every wait partial: each load is first used
+  // after a row whose gradient loads were issued after it (gfx9's vmcnt is
+  // in order), so no use waits for loads still needed in flight, and the
+  // chunk states are copied only once their loads have landed.
+  static_assert(kDynRC == 4, "the loop body walks 4 rows per chunk");
+  while (true) {
+    fetch_offs(tk, nn);   // the chunk after next (its ticket was taken one trip ago)
+    tk = take_ticket();
+    issue(MB, rowB, DB);  // row 1
+    fetch_meta(nxt);      // its offsets were loaded one trip ago
+    process(MA, rowA, skA, DA);  // row 0
+    get_meta(cur, 2, MA, rowA, skA);
+    issue(MA, rowA, DA);  // row 2
+    process(MB, rowB, skB, DB);  // row 1
+    get_meta(cur, 3, MB, rowB, skB);
+    issue(MB, rowB, DB);  // row 3
+    process(MA, rowA, skA, DA);  // row 2 (its wait covers nxt's metadata)
+    const bool more = nxt.row0 < K32;
+    if (more) {
+      get_meta(nxt, 0, MA, rowA, skA);
+      issue(MA, rowA, DA);  // next chunk's row 0
+    }
+    process(MB, rowB, skB, DB);  // row 3
+    if (!more) break;
+    get_meta(nxt, 1, MB, rowB, skB);
+    cur = nxt;
+    nxt = nn;
+  }
+}
+
 // meta[i] = {bag, weight as float32 bits} of sorted occurrence i;
 // entries past the valid count (padding included) are zero.
 __global__ void occ_meta_kernel(const uint32_t* __restrict__ svals, const uint32_t* __restrict__ nvalid,
@@ -901,6 +974,13 @@ __global__ void gpsw_scatter_kernel(const uint32_t* __restrict__ svals, const fl
   }
 }
 
+// gpsw[p] <- 0 for the positions the sort listed as out-of-range lookups.
+__global__ void zero_invalid_gpsw_kernel(const uint32_t* __restrict__ invalid, void* __restrict__ gpsw, int pdt) {
+  const uint32_t n = invalid[0];
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    store_scalar(gpsw, pdt, invalid[1 + i], 0.f);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -926,7 +1006,8 @@ static RadixPlan radix_plan(int64_t K) {
 }
 
 struct BwdLayout {
-  size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, long_rows, total;
+  size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, long_rows, tickets,
+      invalid, total;
   int64_t ntiles, nbins, nchunks, nmeta;
   RadixPlan plan;
 };
@@ -955,10 +1036,10 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   l.nchunks = cdiv(N, kHeavyT);
   l.partials = off;
   off += align256((size_t)(2 * l.nchunks) * (size_t)D * 4);
-  // wave-per-64-rows path: sorted occurrence metadata (padded so a wave can read
-  // a full LDS window past any row start), dots in sorted order (+1 dummy slot),
-  // a zero row read by unused prefetch slots and a dummy row written by tail rows
-  l.nmeta = N + kMetaChunk + 16;
+  // row kernels: sorted occurrence metadata (padded so a row's U slots can be
+  // read past any row start), dots in sorted order (+1 dummy slot), a zero row
+  // read by unused prefetch slots and a dummy row written by tail rows
+  l.nmeta = N + kMetaPad;
   l.meta = off;
   off += align256((size_t)l.nmeta * 8);
   l.dsorted = off;
@@ -967,9 +1048,14 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   off += align256((size_t)D * 4);
   l.dummy_row = off;
   off += align256((size_t)D * 4);
-  // long light rows listed by the row kernel (at most one entry per row), then their count
+  // long light rows (at most one entry per row) and their count; the row kernel's ticket counters
   l.long_rows = off;
   off += align256((size_t)(K + 1) * 4);
+  l.tickets = off;
+  off += (size_t)kDynGroups * kDynSub * kCtrStride * 4;
+  // out-of-range lookups: count, then positions
+  l.invalid = off;
+  off += align256((size_t)(N + 1) * 4);
   l.total = off;
   return l;
 }
@@ -991,13 +1077,13 @@ static unsigned grid_for(int64_t n, int threads, int64_t cap = 65536) {
 template <int BITS>
 static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], uint32_t* const vals[2], int cur,
                        int nxt, int64_t N, int64_t K, const BwdLayout& l, uint32_t* hist, uint32_t* parts,
-                       void* gpsw, int pdt, hipStream_t st) {
+                       uint32_t* invalid, hipStream_t st) {
   const int shift = pass * BITS;
   const uint32_t* nvalid = hist + l.nbins;  // total of the previous pass's scan
   const dim3 grid((unsigned)l.ntiles), block(256);
   if (pass == 0) {
     hipLaunchKernelGGL((radix_hist_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr, N,
-                       (const uint32_t*)nullptr, K, shift, hist, l.ntiles, gpsw, pdt);
+                       (const uint32_t*)nullptr, K, shift, hist, l.ntiles, invalid);
     device_exclusive_sum(hist, l.nbins, parts, st);
     hipLaunchKernelGGL((radix_scatter_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr,
                        (const uint32_t*)nullptr, N, (const uint32_t*)nullptr, K, shift, (const uint32_t*)hist,
@@ -1006,7 +1092,7 @@ static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], ui
     // the previous scan's total (nvalid) lives at hist[nbins]; this pass's hist
     // kernel reads it before the scan below rewrites it with the same value
     hipLaunchKernelGGL((radix_hist_kernel<false, BITS>), grid, block, 0, st, (const int64_t*)nullptr,
-                       (const uint32_t*)keys[cur], N, nvalid, K, shift, hist, l.ntiles, (void*)nullptr, 0);
+                       (const uint32_t*)keys[cur], N, nvalid, K, shift, hist, l.ntiles, (uint32_t*)nullptr);
     device_exclusive_sum(hist, l.nbins, parts, st);
     hipLaunchKernelGGL((radix_scatter_kernel<false, BITS>), grid, block, 0, st, (const int64_t*)nullptr,
                        (const uint32_t*)keys[cur], (const uint32_t*)vals[cur], N, nvalid, K, shift,
@@ -1014,22 +1100,72 @@ static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], ui
   }
 }
 
-template <typename TW, int VPL, int U>
-static void launch_rows64(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
-                          const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
-                          float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, hipStream_t st) {
-  const unsigned rb = (unsigned)cdiv(K, 4 * 64);
+// Row-kernel prefetch depth (lookups per row reduced in the row kernel) for
+// rows of 64 * VPL vectors: 8 when the lookups average more than ~3 per row.
+template <int VPL>
+static int rows_prefetch(int64_t N, int64_t K) {
+  if (VPL <= 2) return N > 3 * K ? 8 : 4;
+  return VPL == 4 ? 2 : 1;
+}
+
+// Prepare the row kernel's lists: the long light rows, the cleared ticket
+// counters.
+static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* long_rows, uint32_t* tickets,
+                             hipStream_t st) {
   uint32_t* long_count = long_rows + K;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, long_count, 0u, (int64_t)1);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
+                     (int64_t)kDynGroups * kDynSub * kCtrStride);
+  const int64_t lwg = cdiv(K, 1024) < 256 ? cdiv(K, 1024) : 256;
+  hipLaunchKernelGGL(list_long_rows_kernel, dim3((unsigned)lwg), dim3(256), 0, st, offs, K, (uint32_t)U,
+                     cdiv(cdiv(K, lwg), 256) * 256, long_rows, long_count);
+}
+
+// The row reduction on the ticket schedule: the rows kernel, then the long
+// rows listed by prepare_rows_dyn.
+template <typename TW, int VPL, int U>
+static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
+                            const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
+                            float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, uint32_t* tickets,
+                            hipStream_t st) {
+  const uint32_t* long_count = long_rows + K;
+  // blocks of 1024 rows (the sub-key blocks of a 1024-key half) once every
+  // group gets several; smaller tables use the smallest block
+  const uint32_t blk = K >= (int64_t)kDynGroups * 8 * 1024 ? 1024u : (uint32_t)(kDynRC * kDynSub);
+  int64_t wgs = cdiv(K, 64);
+  wgs = wgs < 1280 ? wgs : 1280;
+  wgs = cdiv(wgs, kDynGroups * kDynSub) * kDynGroups * kDynSub;  // every counter gets workgroups
   KernelSpan span("eb_bwd_rows", st);
-  hipLaunchKernelGGL((eb_bwd_rows64_kernel<TW, VPL, U>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, want_dot,
-                     (const TW*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW, dsorted,
-                     dummy_slot, long_rows, long_count);
-  // grid-stride over the list: enough waves to spread the long rows, bounded by the row count
-  const unsigned lb = (unsigned)(rb < 1024u ? rb : 1024u);
+  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, VPL, U>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W, K, D,
+                     want_dot, (const TW*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW, dsorted,
+                     dummy_slot, tickets, blk);
+  const int64_t rb = cdiv(K, 4 * 64);
+  const unsigned lb = (unsigned)(rb < 1024 ? rb : 1024);
   hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, VPL, U>), dim3(lb), dim3(256), 0, st, (const TW*)W, D, want_dot,
                      (const TW*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
-                     (const uint32_t*)long_rows, (const uint32_t*)long_count);
+                     (const uint32_t*)long_rows, long_count);
+}
+
+// Everything of the backward that depends only on the lookups (run by
+// pkm_eb_bwd_prepare): for 64-lane rows, the occurrence metadata, the zero
+// row and the row kernel's lists.
+template <typename TW, int LPG, int VPL>
+static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64_t L, const uint32_t* offs,
+                           const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l, char* ws,
+                           hipStream_t st) {
+  if constexpr (LPG == 64) {
+    uint2* meta = (uint2*)(ws + l.meta);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(D, 256, 64)), dim3(256), 0, st, (uint32_t*)(ws + l.zrow), 0u, D);
+    if (N > 0)
+      hipLaunchKernelGGL(occ_meta_kernel, dim3(grid_for(l.nmeta, 256, 16384)), dim3(256), 0, st, svals, nvalid,
+                         l.nmeta, (uint32_t)L, psw, pdt, meta);
+    else
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * l.nmeta, 256, 4096)), dim3(256), 0, st,
+                         (uint32_t*)meta, 0u, 2 * l.nmeta);
+    if (K > 0)
+      prepare_rows_dyn(K, rows_prefetch<VPL>(N, K), offs, (uint32_t*)(ws + l.long_rows), (uint32_t*)(ws + l.tickets),
+                       st);
+  }
 }
 
 template <typename TW, int LPG, int VPL>
@@ -1041,40 +1177,34 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
   float* partials = (float*)(ws + l.partials);
   const unsigned hb = (unsigned)cdiv(l.nchunks, groups_per_block);
   if constexpr (LPG == 64) {
-    uint2* meta = (uint2*)(ws + l.meta);
+    const uint2* meta = (const uint2*)(ws + l.meta);
     float* dsorted = (float*)(ws + l.dsorted);
     void* zrow = ws + l.zrow;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(D, 256, 64)), dim3(256), 0, st, (uint32_t*)zrow, 0u, D);
-    if (N > 0) {
-      hipLaunchKernelGGL(occ_meta_kernel, dim3(grid_for(l.nmeta, 256, 16384)), dim3(256), 0, st, svals, nvalid,
-                         l.nmeta, (uint32_t)L, psw, pdt, meta);
+    if (N > 0)
       hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D, psw,
                          pdt, (const TW*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
                          dsorted);
-    } else {
-      hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * l.nmeta, 256, 4096)), dim3(256), 0, st,
-                         (uint32_t*)meta, 0u, 2 * l.nmeta);
-    }
     if (K > 0) {
       const int want_dot = psw != nullptr ? 1 : 0;
-      const bool dense = N > 3 * K;  // more than ~3 lookups per row on average: prefetch 8
+      const bool dense = rows_prefetch<VPL>(N, K) == 8;
       const uint32_t dslot = (uint32_t)N;
       void* dummy = ws + l.dummy_row;
       uint32_t* long_rows = (uint32_t*)(ws + l.long_rows);
+      uint32_t* tickets = (uint32_t*)(ws + l.tickets);
       if constexpr (VPL == 1) {
         if (dense)
-          launch_rows64<TW, 1, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
+          launch_rows_dyn<TW, 1, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
         else
-          launch_rows64<TW, 1, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
+          launch_rows_dyn<TW, 1, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
       } else if constexpr (VPL == 2) {
         if (dense)
-          launch_rows64<TW, 2, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
+          launch_rows_dyn<TW, 2, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
         else
-          launch_rows64<TW, 2, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
+          launch_rows_dyn<TW, 2, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
       } else if constexpr (VPL == 4) {
-        launch_rows64<TW, 4, 2>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
+        launch_rows_dyn<TW, 4, 2>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
       } else {
-        launch_rows64<TW, 8, 1>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, st);
+        launch_rows_dyn<TW, 8, 1>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
       }
     }
     if (N > 0 && psw != nullptr)
@@ -1097,14 +1227,16 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
 }
 
 template <typename TW>
-static bool dispatch_reduce(const GroupCfg& c, const void* W, int64_t K, int64_t D, const void* psw, int pdt,
+static bool dispatch_reduce(bool prepare, const GroupCfg& c, const void* W, int64_t K, int64_t D, const void* psw, int pdt,
                             const void* g, int64_t L, const uint32_t* offs, const uint32_t* skeys,
                             const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l,
                             char* ws, void* gW, void* gpsw, hipStream_t st) {
 #define PKM_RED_CASE(LPG_, VPL_)                                                                                  \
   if (c.lpg == LPG_ && c.vpl == VPL_) {                                                                           \
-    launch_reduce<TW, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, gpsw, \
-                                  st);                                                                            \
+    if (prepare)                                                                                                  \
+      launch_prepare<TW, LPG_, VPL_>(K, D, psw, pdt, L, offs, svals, nvalid, N, l, ws, st);                       \
+    else                                                                                                          \
+      launch_reduce<TW, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, gpsw, st); \
     return true;                                                                                                  \
   }
   PKM_RED_CASE(64, 1)
@@ -1132,90 +1264,163 @@ extern "C" size_t pkm_eb_bwd_workspace_size(int64_t num_rows, int64_t dim, int64
   return bwd_layout(num_rows, dim, bags * bag_size).total;
 }
 
-extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,
-                          const void* psw, int psw_dtype, const void* grad_out, int grad_dtype, int64_t bags,
-                          int64_t bag_size, void* grad_weight, void* grad_psw, void* workspace,
-                          size_t workspace_bytes, void* stream) {
-  PKM_REQUIRE(valid_dt(weight_dtype), PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: bad weight dtype %d", weight_dtype);
-  PKM_REQUIRE(grad_dtype == weight_dtype, PKM_ERR_UNSUPPORTED,
-              "pkm_eb_bwd: grad_out dtype %d differs from weight dtype %d", grad_dtype, weight_dtype);
+namespace pkm {
+
+// Checks shared by the backward's entry points; fills the kernel group
+// configuration and the workspace layout.
+static int eb_bwd_check(const char* fn, int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,
+                        const void* psw, int psw_dtype, int64_t bags, int64_t bag_size, void* workspace,
+                        size_t workspace_bytes, GroupCfg* c, BwdLayout* l) {
+  PKM_REQUIRE(valid_dt(weight_dtype), PKM_ERR_INVALID_ARGUMENT, "%s: bad weight dtype %d", fn, weight_dtype);
   PKM_REQUIRE(psw_dtype == PKM_DTYPE_NONE ? psw == nullptr
                                           : (valid_dt(psw_dtype) && (psw != nullptr || bags * bag_size == 0)),
-              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: psw pointer / dtype %d mismatch", psw_dtype);
+              PKM_ERR_INVALID_ARGUMENT, "%s: psw pointer / dtype %d mismatch", fn, psw_dtype);
   PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
-              "pkm_eb_bwd: bad sizes num_rows=%lld dim=%lld bags=%lld bag_size=%lld", (long long)num_rows,
+              "%s: bad sizes num_rows=%lld dim=%lld bags=%lld bag_size=%lld", fn, (long long)num_rows,
               (long long)dim, (long long)bags, (long long)bag_size);
   const int64_t N = bags * bag_size;
   PKM_REQUIRE(N < ((int64_t)1 << 31) && num_rows < ((int64_t)1 << 31) - 1, PKM_ERR_INVALID_ARGUMENT,
-              "pkm_eb_bwd: bags*bag_size=%lld must be < 2^31 and num_rows=%lld < 2^31-1", (long long)N,
+              "%s: bags*bag_size=%lld must be < 2^31 and num_rows=%lld < 2^31-1", fn, (long long)N,
               (long long)num_rows);
-  PKM_REQUIRE(grad_weight != nullptr || num_rows == 0, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_weight");
-  PKM_REQUIRE(N == 0 || (indices != nullptr && grad_out != nullptr), PKM_ERR_INVALID_ARGUMENT,
-              "pkm_eb_bwd: null indices / grad_out");
-  PKM_REQUIRE(psw == nullptr || N == 0 || (grad_psw != nullptr && (weight != nullptr || num_rows == 0)),
-              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null weight / grad_psw");
+  PKM_REQUIRE(N == 0 || indices != nullptr, PKM_ERR_INVALID_ARGUMENT, "%s: null indices", fn);
   const int epv = weight_dtype == PKM_DTYPE_F32 ? 4 : 8;
-  GroupCfg c;
-  PKM_REQUIRE(choose_group_cfg(dim, epv, true, &c), PKM_ERR_UNSUPPORTED,
-              "pkm_eb_bwd: dim %lld not supported (need dim/%d = LPG*VPL with LPG<=64, VPL<=8)", (long long)dim, epv);
-  const BwdLayout l = bwd_layout(num_rows, dim, N);
-  PKM_REQUIRE(workspace != nullptr && workspace_bytes >= l.total, PKM_ERR_WORKSPACE,
-              "pkm_eb_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, l.total);
-  PKM_REQUIRE((uintptr_t)weight % 16 == 0 && (uintptr_t)grad_out % 16 == 0 && (uintptr_t)grad_weight % 16 == 0 &&
-                  (uintptr_t)workspace % 256 == 0,
-              PKM_ERR_INVALID_ARGUMENT,
-              "pkm_eb_bwd: weight, grad_out, grad_weight must be 16-byte and workspace 256-byte aligned");
+  PKM_REQUIRE(choose_group_cfg(dim, epv, true, c), PKM_ERR_UNSUPPORTED,
+              "%s: dim %lld not supported (need dim/%d = LPG*VPL with LPG<=64, VPL<=8)", fn, (long long)dim, epv);
+  *l = bwd_layout(num_rows, dim, N);
+  PKM_REQUIRE(workspace != nullptr && workspace_bytes >= l->total, PKM_ERR_WORKSPACE,
+              "%s: workspace of %zu bytes given, %zu needed", fn, workspace_bytes, l->total);
+  PKM_REQUIRE((uintptr_t)workspace % 256 == 0, PKM_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned",
+              fn);
+  return PKM_OK;
+}
 
+// Buffers of the sorted lookups: the final ping-pong buffer of the sort
+// (pass p writes buffer 0 for p = 0 and alternates after).
+struct SortedView {
+  uint32_t *offs, *keys, *vals, *hist, *parts, *invalid;
+  const uint32_t* nvalid;
+};
+static SortedView sorted_view(const BwdLayout& l, char* ws) {
+  SortedView v;
+  v.offs = (uint32_t*)(ws + l.offs);
+  const int cur = l.plan.passes % 2 == 1 ? 0 : 1;
+  v.keys = (uint32_t*)(ws + (cur == 0 ? l.keys0 : l.keys1));
+  v.vals = (uint32_t*)(ws + (cur == 0 ? l.vals0 : l.vals1));
+  v.hist = (uint32_t*)(ws + l.hist);
+  v.parts = (uint32_t*)(ws + l.parts);
+  v.invalid = (uint32_t*)(ws + l.invalid);
+  v.nvalid = v.hist + l.nbins;
+  return v;
+}
+
+}  // namespace pkm
+
+extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,
+                                  const void* psw, int psw_dtype, int64_t bags, int64_t bag_size, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  GroupCfg c;
+  BwdLayout l;
+  const int rc = eb_bwd_check("pkm_eb_bwd_prepare", num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags,
+                              bag_size, workspace, workspace_bytes, &c, &l);
+  if (rc != PKM_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  uint32_t* offs = (uint32_t*)(ws + l.offs);
-  uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
-  uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
-  uint32_t* hist = (uint32_t*)(ws + l.hist);
-  uint32_t* parts = (uint32_t*)(ws + l.parts);
-  float* partials = (float*)(ws + l.partials);
-  const int64_t K = num_rows;
-  const uint32_t* nvalid = hist + l.nbins;
-  void* gpsw = psw != nullptr ? grad_psw : nullptr;
-
-  int cur = 0;
+  const int64_t K = num_rows, N = bags * bag_size;
+  const SortedView v = sorted_view(l, ws);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, v.invalid, 0u, (int64_t)1);
   if (N > 0) {
-    // 1. stable LSD radix sort of (row, position); invalid lookups dropped
+    // 1. stable LSD radix sort of (row, position); out-of-range lookups dropped and listed
+    uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
+    uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
+    int cur = 0;
     for (int pass = 0; pass < l.plan.passes; ++pass) {
       const int nxt = pass == 0 ? 0 : 1 - cur;
       switch (l.plan.bits) {
         case 8:
-          radix_pass<8>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st);
+          radix_pass<8>(pass, indices, keys, vals, cur, nxt, N, K, l, v.hist, v.parts, v.invalid, st);
           break;
         case 10:
-          radix_pass<10>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st);
+          radix_pass<10>(pass, indices, keys, vals, cur, nxt, N, K, l, v.hist, v.parts, v.invalid, st);
           break;
         default:
-          radix_pass<11>(pass, indices, keys, vals, cur, nxt, N, K, l, hist, parts, gpsw, psw_dtype, st);
+          radix_pass<11>(pass, indices, keys, vals, cur, nxt, N, K, l, v.hist, v.parts, v.invalid, st);
           break;
       }
       cur = nxt;
     }
     // 2. row offsets: a binary search of the sorted keys per row
     hipLaunchKernelGGL(row_offsets_kernel, dim3(grid_for(K + 1, 256, 65536)), dim3(256), 0, st,
-                       (const uint32_t*)keys[cur], nvalid, K, offs);
+                       (const uint32_t*)v.keys, v.nvalid, K, v.offs);
   } else {
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 1, 256, 4096)), dim3(256), 0, st, offs, 0u, K + 1);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(K + 1, 256, 4096)), dim3(256), 0, st, v.offs, 0u, K + 1);
   }
-
-  // 3-4. heavy-row chunk partials, then every row once
+  // 3. metadata and the row kernel's lists
   bool ok;
   if (weight_dtype == PKM_DTYPE_F32)
-    ok = dispatch_reduce<float>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, offs, keys[cur], vals[cur],
-                                nvalid, N, l, ws, grad_weight, gpsw, st);
+    ok = dispatch_reduce<float>(true, c, nullptr, K, dim, psw, psw_dtype, nullptr, bag_size, v.offs, v.keys, v.vals,
+                                v.nvalid, N, l, ws, nullptr, nullptr, st);
   else if (weight_dtype == PKM_DTYPE_BF16)
-    ok = dispatch_reduce<bf16_t>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, offs, keys[cur], vals[cur],
-                                 nvalid, N, l, ws, grad_weight, gpsw, st);
+    ok = dispatch_reduce<bf16_t>(true, c, nullptr, K, dim, psw, psw_dtype, nullptr, bag_size, v.offs, v.keys, v.vals,
+                                 v.nvalid, N, l, ws, nullptr, nullptr, st);
   else
-    ok = dispatch_reduce<f16_t>(c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, offs, keys[cur], vals[cur],
-                                nvalid, N, l, ws, grad_weight, gpsw, st);
+    ok = dispatch_reduce<f16_t>(true, c, nullptr, K, dim, psw, psw_dtype, nullptr, bag_size, v.offs, v.keys, v.vals,
+                                v.nvalid, N, l, ws, nullptr, nullptr, st);
+  PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd_prepare: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
+  return pkm_check_launch("pkm_eb_bwd_prepare");
+}
+
+extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                                   const int64_t* indices, const void* psw, int psw_dtype, const void* grad_out,
+                                   int grad_dtype, int64_t bags, int64_t bag_size, void* grad_weight, void* grad_psw,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  GroupCfg c;
+  BwdLayout l;
+  const int rc = eb_bwd_check("pkm_eb_bwd_prepared", num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags,
+                              bag_size, workspace, workspace_bytes, &c, &l);
+  if (rc != PKM_OK) return rc;
+  const int64_t N = bags * bag_size;
+  PKM_REQUIRE(grad_dtype == weight_dtype, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd: grad_out dtype %d differs from weight dtype %d", grad_dtype, weight_dtype);
+  PKM_REQUIRE(grad_weight != nullptr || num_rows == 0, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_weight");
+  PKM_REQUIRE(N == 0 || grad_out != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_out");
+  PKM_REQUIRE(psw == nullptr || N == 0 || (grad_psw != nullptr && (weight != nullptr || num_rows == 0)),
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null weight / grad_psw");
+  PKM_REQUIRE((uintptr_t)weight % 16 == 0 && (uintptr_t)grad_out % 16 == 0 && (uintptr_t)grad_weight % 16 == 0,
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: weight, grad_out, grad_weight must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const SortedView v = sorted_view(l, ws);
+  void* gpsw = psw != nullptr ? grad_psw : nullptr;
+  const int64_t K = num_rows;
+  // 4-5. heavy-row chunk partials, then every row once, then the psw-gradients to their positions
+  bool ok;
+  if (weight_dtype == PKM_DTYPE_F32)
+    ok = dispatch_reduce<float>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys, v.vals,
+                                v.nvalid, N, l, ws, grad_weight, gpsw, st);
+  else if (weight_dtype == PKM_DTYPE_BF16)
+    ok = dispatch_reduce<bf16_t>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys,
+                                 v.vals, v.nvalid, N, l, ws, grad_weight, gpsw, st);
+  else
+    ok = dispatch_reduce<f16_t>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys,
+                                v.vals, v.nvalid, N, l, ws, grad_weight, gpsw, st);
   PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
-  return pkm_check_launch("pkm_eb_bwd");
+  if (N > 0 && gpsw != nullptr)
+    hipLaunchKernelGGL(zero_invalid_gpsw_kernel, dim3(64), dim3(256), 0, st, (const uint32_t*)v.invalid, gpsw,
+                       psw_dtype);
+  return pkm_check_launch("pkm_eb_bwd_prepared");
+}
+
+extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,
+                          const void* psw, int psw_dtype, const void* grad_out, int grad_dtype, int64_t bags,
+                          int64_t bag_size, void* grad_weight, void* grad_psw, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  PKM_REQUIRE(grad_dtype == weight_dtype, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd: grad_out dtype %d differs from weight dtype %d", grad_dtype, weight_dtype);
+  const int rc = pkm_eb_bwd_prepare(num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags, bag_size, workspace,
+                                    workspace_bytes, stream);
+  if (rc != PKM_OK) return rc;
+  return pkm_eb_bwd_prepared(weight, num_rows, dim, weight_dtype, indices, psw, psw_dtype, grad_out, grad_dtype, bags,
+                             bag_size, grad_weight, grad_psw, workspace, workspace_bytes, stream);
 }
 
 extern "C" int pkm_count_invalid_indices(const int64_t* indices, int64_t n, int64_t num_rows, int64_t* count_out,

@@ -159,6 +159,11 @@ __device__ __forceinline__ uint4 ld16(const void* p) { return *(const uint4*)p; 
 __device__ __forceinline__ void st16(void* p, const uint4& v) { *(uint4*)p = v; }
 // Streaming store for write-once outputs (dense weight gradient).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// 16-byte load marked non-temporal (read once: streamed through the caches)
+__device__ __forceinline__ uint4 ld16_nt(const void* p) {
+  const u32x4_t x = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
 __device__ __forceinline__ void st16_nt(void* p, const uint4& v) {
   const u32x4_t x = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(x, (u32x4_t*)p);

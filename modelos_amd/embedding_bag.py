@@ -81,16 +81,82 @@ def eb_backward_workspace_bytes(num_rows: int, dim: int, bags: int, bag_size: in
     return int(_lib.load().pkm_eb_bwd_workspace_size(num_rows, dim, bags, bag_size))
 
 
+_side_streams: dict = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """One extra stream per device (default priority) for work that runs beside
+    the current stream."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _side_streams.get(key)
+    if st is None:
+        st = torch.cuda.Stream(device=key)
+        _side_streams[key] = st
+    return st
+
+
+class BackwardPrep:
+    """The lookup-only part of the backward (sort, row offsets, metadata),
+    computed ahead by eb_backward_prepare: its workspace, the sizes it was made
+    for, and the event that marks it done."""
+
+    def __init__(self, workspace: torch.Tensor, ws_bytes: int, key: tuple, done: torch.cuda.Event):
+        self.workspace, self.ws_bytes, self.key, self.done = workspace, ws_bytes, key, done
+
+
+def _prep_key(indices, weight, psw) -> tuple:
+    return (indices.data_ptr(), tuple(indices.shape), tuple(weight.shape), weight.dtype,
+            psw.data_ptr() if psw is not None else 0, psw.dtype if psw is not None else None)
+
+
+def eb_backward_prepare(
+    indices: torch.Tensor, weight: torch.Tensor, per_sample_weights: Optional[torch.Tensor]
+) -> BackwardPrep:
+    """Runs pkm_eb_bwd_prepare for these lookups on a side stream, after the
+    work already queued on the current stream, and returns the handle that
+    eb_backward(prepared=...) consumes. indices / psw must stay unchanged until
+    then (autograd's saved tensors)."""
+    _check_bag_inputs(indices, weight, per_sample_weights, "eb_backward_prepare")
+    dev = _require_device(indices, weight, per_sample_weights)
+    if not (indices.is_contiguous() and (per_sample_weights is None or per_sample_weights.is_contiguous())):
+        raise ValueError("eb_backward_prepare: indices and per_sample_weights must be contiguous")
+    B, L = indices.shape
+    K, D = weight.shape
+    psw = per_sample_weights
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
+    side.wait_stream(main)
+    ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
+    with torch.cuda.stream(side):
+        workspace = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+        _lib.call(
+            "pkm_eb_bwd_prepare",
+            K, D, _lib.dtype_code(weight),
+            _lib.ptr(indices), _lib.ptr(psw), _lib.dtype_code(psw),
+            B, L, _lib.ptr(workspace), ws_bytes, side.cuda_stream,
+        )
+        done = torch.cuda.Event()
+        done.record(side)
+    # the side stream read these: their memory is not reused before it is done
+    indices.record_stream(side)
+    if psw is not None:
+        psw.record_stream(side)
+    return BackwardPrep(workspace, ws_bytes, _prep_key(indices, weight, psw), done)
+
+
 def eb_backward(
     indices: torch.Tensor,
     weight: torch.Tensor,
     per_sample_weights: Optional[torch.Tensor],
     grad_output: torch.Tensor,
+    prepared: Optional[BackwardPrep] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Deterministic backward: (grad_weight [K, D] dense in weight.dtype,
     grad_psw [B, L] in psw.dtype or None when psw is None).
 
     Same outputs as embedding_bag_bw_rev_indices (pkm/xformer_embeddingbag.py:331-386).
+    With `prepared` (eb_backward_prepare of the same indices, weight shape and
+    psw) only the reduction runs here; the results are bit-identical.
     """
     _check_bag_inputs(indices, weight, per_sample_weights, "eb_backward")
     dev = _require_device(indices, weight, per_sample_weights, grad_output)
@@ -104,17 +170,25 @@ def eb_backward(
     grad_output = _aligned(grad_output.to(weight.dtype))
     grad_weight = torch.empty_like(weight, memory_format=torch.contiguous_format)
     grad_psw = torch.empty_like(psw, memory_format=torch.contiguous_format) if psw is not None else None
-    ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
-    workspace = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    _lib.call(
-        "pkm_eb_bwd",
+    args = (
         _lib.ptr(weight), K, D, _lib.dtype_code(weight),
         _lib.ptr(indices), _lib.ptr(psw), _lib.dtype_code(psw),
         _lib.ptr(grad_output), _lib.dtype_code(grad_output),
         B, L,
         _lib.ptr(grad_weight), _lib.ptr(grad_psw),
-        _lib.ptr(workspace), ws_bytes, _lib.stream_of(dev),
     )
+    if prepared is not None:
+        if prepared.key != _prep_key(indices, weight, psw):
+            raise ValueError("eb_backward: `prepared` was made for other lookups or another table shape")
+        main = torch.cuda.current_stream(dev)
+        main.wait_event(prepared.done)
+        prepared.workspace.record_stream(main)
+        _lib.call("pkm_eb_bwd_prepared", *args, _lib.ptr(prepared.workspace), prepared.ws_bytes,
+                  _lib.stream_of(dev))
+        return grad_weight, grad_psw
+    ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
+    workspace = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    _lib.call("pkm_eb_bwd", *args, _lib.ptr(workspace), ws_bytes, _lib.stream_of(dev))
     return grad_weight, grad_psw
 
 

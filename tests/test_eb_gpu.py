@@ -448,3 +448,52 @@ def test_backward_large_gradient_unweighted(device):
     assert gp is None
     eW, _ = ref.eb_backward(idx, W, None, g)
     assert_rel_close(gW, eW, REL_TOL[torch.bfloat16], "unweighted grad_weight")
+
+
+PREP_CASES = [
+    (33, 17, 1000, 1024, torch.bfloat16, True),
+    (9, 65, 300, 256, torch.float32, True),
+    (5, 128, 2000, 2048, torch.float16, False),
+    (17, 31, 100, 128, torch.bfloat16, True),
+    (4, 2, 10, 32, torch.float32, True),
+    (0, 8, 100, 512, torch.bfloat16, True),
+    (512, 256, 70000, 1024, torch.bfloat16, True),
+]
+
+
+@pytest.mark.parametrize("B,L,K,D,dtype,weighted", PREP_CASES, ids=lambda v: str(v).replace("torch.", ""))
+def test_backward_prepared_matches_direct(B, L, K, D, dtype, weighted, device):
+    """pkm_eb_bwd_prepare on the side stream, then pkm_eb_bwd_prepared on the
+    current one, gives pkm_eb_bwd's outputs bit for bit, out-of-range lookups
+    (psw-gradient 0) included."""
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, g = eb_inputs(B, L, K, D, dtype, seed=41 + B)
+    if B > 2:
+        idx[1, 0] = -1
+        idx[2, -1] = K + 5
+    dW, didx, dp, dg = _dev(W, idx, p if weighted else None, g, device=device)
+    gw0, gp0 = eb.eb_backward(didx, dW, dp, dg)
+    prep = eb.eb_backward_prepare(didx, dW, dp)
+    gw1, gp1 = eb.eb_backward(didx, dW, dp, dg, prepared=prep)
+    torch.cuda.synchronize()
+    assert torch.equal(gw0, gw1)
+    if weighted:
+        assert torch.equal(gp0, gp1)
+        if B > 2:
+            assert gp1[1, 0].item() == 0.0 and gp1[2, -1].item() == 0.0
+    eW, ep = ref.eb_backward(idx, W, p if weighted else None, g)
+    tol = REL_TOL[dtype]
+    assert_rel_close(gw1, eW, tol, "prepared weight grad", cond=ref.eb_backward(idx, W.abs(), p.abs() if weighted else None, g.abs())[0])
+    if weighted:
+        assert_rel_close(gp1, ep, tol, "prepared psw grad")
+
+
+def test_backward_prepared_rejects_other_lookups(device):
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, g = eb_inputs(8, 16, 500, 256, torch.bfloat16, seed=43)
+    dW, didx, dp, dg = _dev(W, idx, p, g, device=device)
+    prep = eb.eb_backward_prepare(didx, dW, dp)
+    with pytest.raises(ValueError):
+        eb.eb_backward(didx.clone(), dW, dp, dg, prepared=prep)
