@@ -299,11 +299,8 @@ def run_layer(args, dev):
     add("pkm_eb_fwd (values)", ("pkm_eb_fwd", (n * n, D)), a_fwd, "GB/s", HBM_PEAK_GBS, "hbm")
     add("value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)", ("kernel", "eb_bwd_rows"),
         eb_rows_algorithmic_bytes(tokens, L, n * n, D, U), "GB/s", HBM_PEAK_GBS, "hbm")
-    add("pkm_eb_bwd_prepared (values: reduction)", ("pkm_eb_bwd_prepared", (n * n, D)), a_bwd, "GB/s",
-        HBM_PEAK_GBS, "hbm", "entry point: row reduction + psw-gradient scatter; its sort ran with the forward")
-    add("pkm_eb_bwd_prepare (values: sort, side stream)", ("pkm_eb_bwd_prepare", (n * n, D)), a_bwd, "GB/s",
-        HBM_PEAK_GBS, "hbm", "entry point: sort, row offsets, metadata; queued at the start of the layer's backward "
-        "on a side stream, beside the value projection / gate backward")
+    add("pkm_eb_bwd (values)", ("pkm_eb_bwd", (n * n, D)), a_bwd, "GB/s", HBM_PEAK_GBS, "hbm",
+        "entry point: sort + row reduction + psw-gradient scatter (several kernels)")
 
     def add_ms(name, entry, note):
         """Every call of one entry point, whatever its sizes."""
@@ -324,12 +321,10 @@ def run_layer(args, dev):
     add_ms("pkm_softmax_fwd (scores)", "pkm_softmax_fwd", "softmax of the selected scores")
     add_ms("pkm_softmax_bwd (scores)", "pkm_softmax_bwd", "its gradient")
     # single kernels timed inside an entry point are part of that entry's time
-    # and work on the side stream overlaps the current stream's: neither adds to the step
-    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)",
-             "pkm_eb_bwd_prepare (values: sort, side stream)")
-    for kk in inner[:2]:
+    inner = ("pkm_score_stream_kernel (scoring + per-half top-k)", "value backward row reduction (eb_bwd_rows_dyn_kernel + eb_bwd_long_rows_kernel)")
+    for kk in inner:
         if kk in kernels:
-            kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd_prepared (values: reduction)"
+            kernels[kk]["part_of"] = "pkm_score_topk" if kk.startswith("pkm_score") else "pkm_eb_bwd (values)"
     hip_ms = sum(v["ms"] * v["calls_per_step"] for kk, v in kernels.items() if kk not in inner)
     kernels["other (query/swilu/value GEMMs, glue)"] = {"ms": round(step_ms - hip_ms, 4)}
 
