@@ -126,7 +126,7 @@ int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t dim, int w
  * allocation). Limits:
  *   - sizes whose pkm_eb_bwd_workspace_size() exceeds 64 MiB are rejected with
  *     PKM_ERR_WORKSPACE (e.g. a 2^18 x 1024 table with 8192 x 64 lookups
- *     needs 31.5 MiB, a 2^20 x 1024 table with 2048 x 256 lookups 34.5 MiB);
+ *     needs 34.5 MiB, a 2^20 x 1024 table with 2048 x 256 lookups 40.5 MiB);
  *   - the device current on the calling thread must be the stream's device;
  *   - every call on a GPU shares that GPU's array: calls that overlap on one
  *     GPU (other streams, other threads) race, so serialise them.
