@@ -758,8 +758,9 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
 // and metadata are loaded one chunk ahead, so their latency hides under the
 // current chunk's rows. Each row is still reduced by one wave in position
 // order, so the sums are those of the per-64-rows kernel, bit for bit.
-// Rows longer than the prefetch (and light) are listed beforehand by
-// list_long_rows_kernel and skipped here.
+// Rows of U + 1 .. 2 U lookups are reduced in place U lookups at a time;
+// longer light rows are listed beforehand by list_long_rows_kernel, skipped
+// here and reduced by eb_bwd_long_rows_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kDynRC = 4;       // rows per ticket
 constexpr int kDynGroups = 8;   // row groups: one per XCD
@@ -773,12 +774,12 @@ struct DynChunk {
   uint32_t mw;    // ... its weight (float32 bits)
 };
 
-// Rows with offs[r + 1] - offs[r] in (U, kHeavyT], listed for
+// Rows with offs[r + 1] - offs[r] in (T, kHeavyT] (T = 2 U), listed for
 // eb_bwd_long_rows_kernel. A workgroup owns rows_per_wg consecutive rows: it
 // counts its long rows, takes its range of the list with one atomic (atomics
 // on one address serialise, ~15 ns each), then writes them.
 __global__ __launch_bounds__(256) void list_long_rows_kernel(const uint32_t* __restrict__ offs, int64_t K,
-                                                             uint32_t U, int64_t rows_per_wg,
+                                                             uint32_t T, int64_t rows_per_wg,
                                                              uint32_t* __restrict__ long_rows,
                                                              uint32_t* __restrict__ long_count) {
   __shared__ uint32_t wave_cnt[4];
@@ -789,7 +790,7 @@ __global__ __launch_bounds__(256) void list_long_rows_kernel(const uint32_t* __r
   const int64_t r_end = r_beg + rows_per_wg < K ? r_beg + rows_per_wg : K;
   auto is_long = [&](int64_t r) {
     const uint32_t cnt = r < r_end ? offs[r + 1] - offs[r] : 0u;
-    return cnt > U && cnt <= (uint32_t)kHeavyT;
+    return cnt > T && cnt <= (uint32_t)kHeavyT;
   };
   uint32_t n = 0;
   for (int64_t r0 = r_beg + wv * 64; r0 < r_end; r0 += 256) n += (uint32_t)__popcll(__ballot(is_long(r0 + lane)));
@@ -862,7 +863,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     M.beg = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i);
     M.end = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i + 1);
     const uint32_t cnt = M.end - M.beg;
-    skip = cnt > (uint32_t)U && cnt <= (uint32_t)kHeavyT;  // listed for the long-row kernel
+    skip = cnt > 2u * U && cnt <= (uint32_t)kHeavyT;  // listed for the long-row kernel
     M.nh = cnt <= (uint32_t)U ? cnt : 0u;
     row = C.row0 + (uint32_t)i;
 #pragma unroll
@@ -885,13 +886,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   const int dot_slot = dot_slot_of<U>(lane);
   const bool dot_store = dot_store_of<U>(lane);
   const int64_t col0 = (int64_t)lane * EPV;
-  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, const RowData<VPL, U>& R) {
-    if (skip) return;  // a long light row: reduced by the long-row kernel
+  // A row of U + 1 .. 2 U lookups is reduced in place, U lookups at a time,
+  // in R's registers (its prefetch slots hold nothing for it); the next row's
+  // loads stay in flight meanwhile. Longer light rows (rare at uniform-ish
+  // lookups, crowded when lookups pile onto few rows) go to the long-row
+  // kernel, which spreads them over all XCDs.
+  auto reduce_long = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U>& R, float* acc) {
+    const char* wrow = want_dot ? Wb + (uint64_t)row * rowbytes : zb;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);
+    for (uint32_t s = M.beg; s < M.end; s += U) {
+      const uint32_t nh = (M.end - s) < (uint32_t)U ? (M.end - s) : (uint32_t)U;
+      float w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint2 m = meta[s + (uint32_t)u];  // uniform; in bounds: meta is padded past every row start
+        w[u] = (uint32_t)u < nh ? __uint_as_float(m.y) : 0.f;
+        const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * rowbytes : zb;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+      }
+      const float d = accumulate_slots<TW, VPL, U>(R, w, nh, acc, want_dot != 0, lane);
+      if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nh ? s + dot_slot : dummy_slot] = d;
+    }
+  };
+  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, RowData<VPL, U>& R) {
+    if (skip) return;  // longer than 2 U (and light): reduced by the long-row kernel
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
-    const float mydot = accumulate_slots<TW, VPL, U>(R, M.w, M.nh, acc, want_dot != 0, lane);
-    if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
+    const uint32_t cnt = M.end - M.beg;
+    if (cnt > (uint32_t)U && cnt <= (uint32_t)kHeavyT) {
+      reduce_long(M, row, R, acc);
+    } else {
+      const float mydot = accumulate_slots<TW, VPL, U>(R, M.w, M.nh, acc, want_dot != 0, lane);
+      if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
+    }
     if (M.end - M.beg > (uint32_t)kHeavyT) add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
     char* orow = row < K32 ? (char*)gW + (uint64_t)row * rowbytes : (char*)dummy_row;
 #pragma unroll
@@ -1108,8 +1138,8 @@ static int rows_prefetch(int64_t N, int64_t K) {
   return VPL == 4 ? 2 : 1;
 }
 
-// Prepare the row kernel's lists: the long light rows, the cleared ticket
-// counters.
+// Prepare the row kernel's lists: the light rows longer than 2 U (the
+// row kernel reduces up to 2 U in place), the cleared ticket counters.
 static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* long_rows, uint32_t* tickets,
                              hipStream_t st) {
   uint32_t* long_count = long_rows + K;
@@ -1117,7 +1147,7 @@ static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* l
   hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
                      (int64_t)kDynGroups * kDynSub * kCtrStride);
   const int64_t lwg = cdiv(K, 1024) < 256 ? cdiv(K, 1024) : 256;
-  hipLaunchKernelGGL(list_long_rows_kernel, dim3((unsigned)lwg), dim3(256), 0, st, offs, K, (uint32_t)U,
+  hipLaunchKernelGGL(list_long_rows_kernel, dim3((unsigned)lwg), dim3(256), 0, st, offs, K, (uint32_t)(2 * U),
                      cdiv(cdiv(K, lwg), 256) * 256, long_rows, long_count);
 }
 
