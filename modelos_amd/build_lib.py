@@ -41,8 +41,11 @@ DEVICE_FLAGS = [
 # and their results are used late (ticket counters taken ahead of use); the
 # atomic optimizer would rewrite each into a wave-wide form whose result is
 # read right after the atomic, a wait for every load in flight.
+# score_topk.hip: MFMA accumulators in arch VGPRs, where the score words are
+# packed from them (in AGPRs each element costs a copy out first).
 SOURCE_FLAGS = {
     "eb_bwd.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+    "score_topk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -1155,8 +1155,9 @@ constexpr CeNet clean_net(int N) {
   return t;
 }
 constexpr CeNet kSort32 = oem_net(32);
+constexpr CeNet kSort16 = oem_net(16);
 constexpr CeNet kClean32 = clean_net(32);
-static_assert(kSort32.n == 191 && kClean32.n == 80, "network sizes");
+static_assert(kSort32.n == 191 && kSort16.n == 63 && kClean32.n == 80, "network sizes");
 
 __device__ __forceinline__ void ce_desc(uint32_t& a, uint32_t& b) {
   const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
@@ -1164,13 +1165,17 @@ __device__ __forceinline__ void ce_desc(uint32_t& a, uint32_t& b) {
   b = lo;
 }
 // (positions as template arguments: register indices fixed at compile time)
-template <int A, int B>
-__device__ __forceinline__ void ce_at(uint32_t (&x)[32]) {
+template <int A, int B, int N>
+__device__ __forceinline__ void ce_at(uint32_t (&x)[N]) {
   ce_desc(x[A], x[B]);
 }
 template <size_t... I>
 __device__ __forceinline__ void sort32_desc(uint32_t (&x)[32], std::index_sequence<I...>) {
   (ce_at<kSort32.a[I], kSort32.b[I]>(x), ...);
+}
+template <size_t... I>
+__device__ __forceinline__ void sort16_desc(uint32_t (&x)[16], std::index_sequence<I...>) {
+  (ce_at<kSort16.a[I], kSort16.b[I]>(x), ...);
 }
 template <size_t... I>
 __device__ __forceinline__ void clean32_desc(uint32_t (&x)[32], std::index_sequence<I...>) {
@@ -1203,19 +1208,37 @@ __device__ __forceinline__ uint32_t canon_pair(uint32_t p) {
   return p;
 }
 
-// Merge slots [J0, J0 + 32) (those below cnt) into T.
-template <int J0>
+// Merge slots [J0, J0 + W) (those below cnt) into T, W = 32 or 16. The
+// sorted chunk, reversed and padded with zero keys to 32, meets T elementwise
+// (the larger of each pair): the top 32 of both, as one bitonic sequence,
+// which the cleaner sorts. With W = 16 the padding covers T[0 .. 16), which
+// keeps its keys: the result equals the 32-wide merge of the same slots
+// whenever the wave's counts leave slots [J0 + 16, J0 + 32) unused.
+template <int J0, int W>
 __device__ __forceinline__ void merge_chunk(uint32_t (&T)[kNet], const uint32_t* buf, uint32_t cnt) {
-  uint32_t C[32];
+  static_assert(W == 32 || W == 16, "chunk width");
+  uint32_t C[W];
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
+  for (int j = 0; j < W; ++j) {
     const uint32_t r = buf[(J0 + j) * kThreads];
     C[j] = (uint32_t)(J0 + j) < cnt ? raw_key(r) : 0u;
   }
-  sort32_desc(C, std::make_index_sequence<191>{});
+  if constexpr (W == 32)
+    sort32_desc(C, std::make_index_sequence<191>{});
+  else
+    sort16_desc(C, std::make_index_sequence<63>{});
 #pragma unroll
-  for (int j = 0; j < 32; ++j) T[j] = T[j] > C[31 - j] ? T[j] : C[31 - j];
+  for (int j = 32 - W; j < 32; ++j) T[j] = T[j] > C[31 - j] ? T[j] : C[31 - j];
   clean32_desc(T, std::make_index_sequence<80>{});
+}
+// Merge slots [J0, J0 + 32) with the narrower chunk when no lane of the wave
+// holds a count past J0 + 16.
+template <int J0>
+__device__ __forceinline__ void merge_span(uint32_t (&T)[kNet], const uint32_t* buf, uint32_t cnt) {
+  if (__builtin_amdgcn_ballot_w64(cnt > (uint32_t)(J0 + 16)) != 0)
+    merge_chunk<J0, 32>(T, buf, cnt);
+  else
+    merge_chunk<J0, 16>(T, buf, cnt);
 }
 // tau of theta = T[knn - 1], the smallest of T[0 .. knn) (T is sorted; a
 // minimum rather than an indexed pick keeps T in registers)
@@ -1478,8 +1501,8 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
     }
     while (need) {
       const uint32_t cnt = cb / SB;
-      merge_chunk<0>(T, buf, cnt);
-      if (__builtin_amdgcn_ballot_w64(cnt > 32u) != 0) merge_chunk<32>(T, buf, cnt);
+      merge_span<0>(T, buf, cnt);
+      if (__builtin_amdgcn_ballot_w64(cnt > 32u) != 0) merge_span<32>(T, buf, cnt);
 #pragma unroll
       for (int q = 0; q < kBuf - 64; ++q) buf[q * kThreads] = buf[(64 + q) * kThreads];
       cb = cnt > 64u ? cb - 64u * SB : 0u;

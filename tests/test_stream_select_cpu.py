@@ -168,7 +168,7 @@ def clean_net(N):
     return net
 
 
-SORT32, CLEAN32 = oem_net(32), clean_net(32)
+SORT32, SORT16, CLEAN32 = oem_net(32), oem_net(16), clean_net(32)
 
 
 def run_net(x: np.ndarray, net) -> np.ndarray:
@@ -183,8 +183,8 @@ def run_net(x: np.ndarray, net) -> np.ndarray:
 def test_network_sizes_match_the_kernel():
     with open(SRC) as f:
         src = f.read()
-    assert "kSort32.n == %d && kClean32.n == %d" % (len(SORT32), len(CLEAN32)) in src
-    assert (len(SORT32), len(CLEAN32)) == (191, 80)
+    assert "kSort32.n == %d && kSort16.n == %d && kClean32.n == %d" % (len(SORT32), len(SORT16), len(CLEAN32)) in src
+    assert (len(SORT32), len(SORT16), len(CLEAN32)) == (191, 63, 80)
 
 
 def test_sort32_sorts():
@@ -201,6 +201,24 @@ def test_sort32_sorts():
     # keys with ties
     x = rng.integers(0, 8, size=(20000, 32))
     assert np.array_equal(run_net(x, SORT32), -np.sort(-x, axis=1))
+
+
+def test_sort16_sorts():
+    # 0-1 principle, exhaustive over the 2^16 inputs
+    rows = (np.arange(1 << 16)[:, None] >> np.arange(16)[None, :]) & 1
+    assert np.array_equal(run_net(rows, SORT16), -np.sort(-rows, axis=1))
+
+
+def test_merge16_step_keeps_the_best_32_sorted():
+    # 0-1 principle, exhaustive: T = 1^a 0^(32-a), C = 1^b 0^(16-b); C reversed
+    # meets T[16 .. 32) only
+    T = np.array([[1] * a + [0] * (32 - a) for a in range(33) for _ in range(17)])
+    C = np.array([[1] * b + [0] * (16 - b) for _ in range(33) for b in range(17)])
+    M = T.copy()
+    M[:, 16:] = np.maximum(M[:, 16:], C[:, ::-1])
+    M = run_net(M, CLEAN32)
+    want = -np.sort(-np.concatenate([T, C], axis=1), axis=1)[:, :32]
+    assert np.array_equal(M, want)
 
 
 def test_merge_step_keeps_the_best_32_sorted():
@@ -236,11 +254,20 @@ def stream_select(bits: np.ndarray, knn: int, stats: dict | None = None) -> np.n
     tau = np.full(L, np.inf, dtype=np.float32)
 
     def merge_chunk(j0):
-        nonlocal T
         C = raw_key(buf[:, j0:j0 + 32])
         C = np.where(np.arange(j0, j0 + 32)[None, :] < cnt[:, None], C, U32(0)).astype(U32)
-        C = run_net(C, SORT32)
-        T = run_net(np.maximum(T, C[:, ::-1]), CLEAN32)
+        for w0 in range(0, L, 64):  # each wave picks its chunk width
+            r = slice(w0, w0 + 64)
+            if np.any(cnt[r] > j0 + 16):
+                T[r] = run_net(np.maximum(T[r], run_net(C[r], SORT32)[:, ::-1]), CLEAN32)
+            else:  # 16 wide: slots j0 + 16 .. are past every count of the wave
+                C16 = run_net(C[r, :16], SORT16)
+                M = T[r].copy()
+                M[:, 16:] = np.maximum(M[:, 16:], C16[:, ::-1])
+                T[r] = run_net(M, CLEAN32)
+            if stats is not None:
+                key = "w32" if np.any(cnt[r] > j0 + 16) else "w16"
+                stats[key] = stats.get(key, 0) + 1
 
     def tau_of():
         th = np.min(np.where(np.arange(K_NET)[None, :] < knn, T, U32(M32)), axis=1)
@@ -312,6 +339,16 @@ def test_stream_random_scores(knn):
     g = gen(10 + knn)
     for L, n in ((256, 1024), (37, 2048), (64, 64)):
         check_rows(bf16_bits(torch.randn(L, n, generator=g)), knn)
+
+
+def test_stream_uses_both_chunk_widths():
+    g = gen(77)
+    bits = bf16_bits(torch.randn(256, 1024, generator=g))
+    stats = {}
+    lists = stream_select(bits, 32, stats)
+    assert stats.get("w16", 0) > 0 and stats.get("w32", 0) > 0, stats
+    check_rows(bits, 32)
+    assert np.array_equal(lists, stream_select(bits, 32))
 
 
 def test_stream_tie_heavy_and_signed_zeros():
