@@ -249,11 +249,14 @@ int pkm_rmsnorm_fwd(const void* x, const void* weight, int64_t rows, int64_t dim
                     float* rstd, void* stream);
 
 /*
- * Softmax of the selected scores over each row of cols <= 64 entries (dtype
- * F32 or BF16 for x, y, dy, dx alike; float32 math, sums in column order):
+ * Softmax of the selected scores over each row of 1 to 65536 entries (dtype
+ * F32, BF16 or F16 for x, y, dy, dx alike; float32 math; rows of up to 64
+ * entries sum in column order, longer rows over 64 lane-strided partial sums
+ * combined by a fixed tree):
  *   y[i, j] = dtype(exp(x[i, j] - max_k x[i, k]) / sum_k exp(x[i, k] - max_k x[i, k]))
  * Replaces `F.softmax(scores.float(), dim=-1).type_as(scores)` in
- * HashingMemory.forward (pkm/memory.py:218).
+ * HashingMemory.forward (pkm/memory.py:218) and the softmax over heads x
+ * top-k of FastWeightProductKeyMemory.score_transform (fwpkm/fwpkm.py:105-115).
  */
 int pkm_softmax_fwd(const void* x, int64_t rows, int64_t cols, int dtype, void* y, void* stream);
 
@@ -296,9 +299,9 @@ int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_scaled_grad, c
 size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);
 
 /*
- * Column sums of a row-major [rows, cols] matrix (dtype F32 or BF16; out in
- * out_dtype F32 or BF16; x and the workspace 16-byte aligned, cols a multiple
- * of 4 / 8):
+ * Column sums of a row-major [rows, cols] matrix (dtype and out_dtype F32,
+ * BF16 or F16; the workspace 16-byte aligned; rows of whole 16-byte vectors
+ * take the vector kernel, any other width one column per thread):
  *   out[j] = out_dtype(sum_i x[i, j])   float32, over fixed row blocks in order
  * (deterministic; up to 32 rows need no workspace). Replaces g.sum(0), the bias
  * gradient autograd forms for the Linear layers of HashingMemory and its query

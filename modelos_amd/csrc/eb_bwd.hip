@@ -1138,27 +1138,27 @@ static int rows_prefetch(int64_t N, int64_t K) {
   return VPL == 4 ? 2 : 1;
 }
 
-// Prepare the row kernel's lists: the light rows longer than 2 U (the
-// row kernel reduces up to 2 U in place), the cleared ticket counters.
-static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* long_rows, uint32_t* tickets,
-                             hipStream_t st) {
+// Prepare the row kernel's list: the light rows longer than 2 U (the row
+// kernel reduces up to 2 U in place).
+static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* long_rows, hipStream_t st) {
   uint32_t* long_count = long_rows + K;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, long_count, 0u, (int64_t)1);
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
-                     (int64_t)kDynGroups * kDynSub * kCtrStride);
   const int64_t lwg = cdiv(K, 1024) < 256 ? cdiv(K, 1024) : 256;
   hipLaunchKernelGGL(list_long_rows_kernel, dim3((unsigned)lwg), dim3(256), 0, st, offs, K, (uint32_t)(2 * U),
                      cdiv(cdiv(K, lwg), 256) * 256, long_rows, long_count);
 }
 
 // The row reduction on the ticket schedule: the rows kernel, then the long
-// rows listed by prepare_rows_dyn.
+// rows listed by prepare_rows_dyn. Each reduction clears its own ticket
+// counters first, so a prepared workspace can serve any number of reductions.
 template <typename TW, int VPL, int U>
 static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
                             const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                             float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, uint32_t* tickets,
                             hipStream_t st) {
   const uint32_t* long_count = long_rows + K;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
+                     (int64_t)kDynGroups * kDynSub * kCtrStride);
   // blocks of 1024 rows (the sub-key blocks of a 1024-key half) once every
   // group gets several; smaller tables use the smallest block
   const uint32_t blk = K >= (int64_t)kDynGroups * 8 * 1024 ? 1024u : (uint32_t)(kDynRC * kDynSub);
@@ -1193,8 +1193,7 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * l.nmeta, 256, 4096)), dim3(256), 0, st,
                          (uint32_t*)meta, 0u, 2 * l.nmeta);
     if (K > 0)
-      prepare_rows_dyn(K, rows_prefetch<VPL>(N, K), offs, (uint32_t*)(ws + l.long_rows), (uint32_t*)(ws + l.tickets),
-                       st);
+      prepare_rows_dyn(K, rows_prefetch<VPL>(N, K), offs, (uint32_t*)(ws + l.long_rows), st);
   }
 }
 

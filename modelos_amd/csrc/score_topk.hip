@@ -1414,10 +1414,14 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   float tau = __uint_as_float(0x7F800000u);
   const int64_t tok = tw + lane;  // this lane's token once the scores are swapped
   const bool live = tok < Ntok;
+  // this half's sub-score row; a NULL output (the caller asked for the other
+  // half only) writes nothing
   uint32_t* srow = nullptr;
+  bool write_sub = false;
   if constexpr (SUB) {
     uint32_t* out_s = c == 0 ? out_s1 : out_s2;
-    srow = out_s + (live ? tok * H + h : 0) * (n / 2);
+    write_sub = live && out_s != nullptr;
+    if (write_sub) srow = out_s + (tok * H + h) * (n / 2);
   }
   // 0xFFFF0000 in a register: v_and_or_b32 takes it beside the scalar index
   uint32_t hi_mask = 0xFFFF0000u;
@@ -1476,7 +1480,7 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) PKM_STREAM_WORDS(X[1][0], X[1][1], 1, jj);
       if constexpr (SUB) {
-        if (live) {
+        if (write_sub) {
 #pragma unroll
           for (int q = 0; q < 32; ++q) srow[(j * kKB + word_key(q)) >> 1] = canon_pair(P[q]);
         }
@@ -1684,6 +1688,9 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
               (long long)half, kstep);
   if (num_tokens == 0) return PKM_OK;
   PKM_REQUIRE(query && keys && out_scores && out_indices, PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: null pointer");
+  PKM_REQUIRE((uintptr_t)out_sub_scores1 % 4 == 0 && (uintptr_t)out_sub_scores2 % 4 == 0 &&
+                  (uintptr_t)out_scores % (dtype == PKM_DTYPE_BF16 ? 2 : 4) == 0,
+              PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: score outputs must be 4-byte aligned");
   PKM_REQUIRE((uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
               "pkm_score_topk: query and keys must be 16-byte aligned");
   const int esz = dtype == PKM_DTYPE_BF16 ? 2 : 4;  // score-tile element = order key of the input dtype

@@ -8,15 +8,19 @@
 // and, given dy, the gradient autograd forms through .float(), softmax and
 // .type_as:
 //   dx[i, j] = T(p_j * (dy_j - sum_k dy_k * p_k))            float32, p recomputed
-// T is float32 or bfloat16; rows of at most 64 entries. Rows of 16, 32, 64 or
+// T is float32, bfloat16 or float16. Float32 / bfloat16 rows of 16, 32, 64 or
 // 128 bytes are read as 16-byte vectors by a group of 1-8 lanes (sums in
 // column order within a lane, the lanes' partials combined by a fixed xor
-// tree); other rows by one lane each, in column order.
+// tree); other rows of at most 64 float32 / bfloat16 entries by one lane
+// each, in column order; longer rows (the fast-weight memory's softmax over
+// heads x top-k, up to kSmMaxCols entries) and float16 rows by a wave each
+// (lane l sums columns l, l + 64, ... in order, then a fixed xor tree).
 #include "pkm_common.h"
 
 namespace pkm {
 
-constexpr int kSmMaxCols = 64;
+constexpr int kSmLaneCols = 64;  // longest row one lane handles
+constexpr int kSmMaxCols = 65536;
 
 template <typename T, int MAXC>
 __device__ __forceinline__ void sm_load_row(const T* __restrict__ row, int cols, float* v) {
@@ -155,6 +159,67 @@ __global__ __launch_bounds__(256) void softmax_bwd_vec_kernel(const uint4* __res
   if (valid) dx[gid] = VecTraits<T>::pack(o);
 }
 
+// ---------------------------------------------------------------------------
+// A wave per row: any row length, any of the three dtypes (runtime dtype code).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sm_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float t = __shfl_xor(v, o);
+    v = t > v ? t : v;
+  }
+  return v;
+}
+__device__ __forceinline__ float sm_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// m and s of row `base` (max, and sum of exp(x - m)); every lane gets both
+__device__ __forceinline__ void sm_wave_stats(const void* __restrict__ x, int dt, int64_t base, int cols, int lane,
+                                              float* m_out, float* s_out) {
+  float m = -__builtin_inff();
+  for (int j = lane; j < cols; j += 64) {
+    const float v = load_scalar(x, dt, base + j);
+    m = v > m ? v : m;
+  }
+  m = sm_wave_max(m);
+  float s = 0.f;
+  for (int j = lane; j < cols; j += 64) s += expf(load_scalar(x, dt, base + j) - m);
+  *m_out = m;
+  *s_out = sm_wave_sum(s);
+}
+
+__global__ __launch_bounds__(256) void softmax_fwd_wave_kernel(const void* __restrict__ x, int64_t rows, int cols,
+                                                               int dt, void* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float m, s;
+  sm_wave_stats(x, dt, base, cols, lane, &m, &s);
+  for (int j = lane; j < cols; j += 64) store_scalar(y, dt, base + j, expf(load_scalar(x, dt, base + j) - m) / s);
+}
+
+__global__ __launch_bounds__(256) void softmax_bwd_wave_kernel(const void* __restrict__ dy, const void* __restrict__ x,
+                                                               int64_t rows, int cols, int dt, void* __restrict__ dx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float m, s;
+  sm_wave_stats(x, dt, base, cols, lane, &m, &s);
+  float gs = 0.f;
+  for (int j = lane; j < cols; j += 64)
+    gs += load_scalar(dy, dt, base + j) * (expf(load_scalar(x, dt, base + j) - m) / s);
+  gs = sm_wave_sum(gs);
+  for (int j = lane; j < cols; j += 64) {
+    const float p = expf(load_scalar(x, dt, base + j) - m) / s;
+    store_scalar(dx, dt, base + j, p * (load_scalar(dy, dt, base + j) - gs));
+  }
+}
+
 // lanes per row for the vector path (0: scalar path)
 static int sm_vec_lanes(int64_t cols, int dtype, const void* a, const void* b, const void* c) {
   const int64_t bytes = cols * (dtype == PKM_DTYPE_BF16 ? 2 : 4);
@@ -169,12 +234,16 @@ using namespace pkm;
 
 namespace {
 int sm_check(const char* what, int64_t rows, int64_t cols, int dtype) {
-  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
-              "%s: dtype %d not supported (float32, bfloat16 are)", what, dtype);
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
+              "%s: dtype %d not supported (float32, bfloat16, float16 are)", what, dtype);
   PKM_REQUIRE(rows >= 0 && cols >= 1 && cols <= kSmMaxCols, PKM_ERR_UNSUPPORTED,
               "%s: rows of %lld entries not supported (1 to %d are)", what, (long long)cols, kSmMaxCols);
+  PKM_REQUIRE(rows < ((int64_t)1 << 31) && rows * cols < ((int64_t)1 << 40), PKM_ERR_INVALID_ARGUMENT,
+              "%s: too many rows / elements", what);
   return PKM_OK;
 }
+// the wave-per-row kernels take rows longer than one lane holds, and float16
+bool sm_wave_path(int64_t cols, int dtype) { return cols > kSmLaneCols || dtype == PKM_DTYPE_F16; }
 }  // namespace
 
 extern "C" int pkm_softmax_fwd(const void* x, int64_t rows, int64_t cols, int dtype, void* y, void* stream) {
@@ -184,6 +253,11 @@ extern "C" int pkm_softmax_fwd(const void* x, int64_t rows, int64_t cols, int dt
   PKM_REQUIRE(x && y, PKM_ERR_INVALID_ARGUMENT, "pkm_softmax_fwd: null pointer");
   const dim3 grid((unsigned)((rows + 255) / 256));
   hipStream_t st = (hipStream_t)stream;
+  if (sm_wave_path(cols, dtype)) {
+    hipLaunchKernelGGL(softmax_fwd_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, rows,
+                       (int)cols, dtype, y);
+    return pkm_check_launch("pkm_softmax_fwd");
+  }
   const int C = (int)cols;
   const int lpr = sm_vec_lanes(cols, dtype, x, y, y);
   if (lpr > 0) {
@@ -224,6 +298,11 @@ extern "C" int pkm_softmax_bwd(const void* dy, const void* x, int64_t rows, int6
   PKM_REQUIRE(dy && x && dx, PKM_ERR_INVALID_ARGUMENT, "pkm_softmax_bwd: null pointer");
   const dim3 grid((unsigned)((rows + 255) / 256));
   hipStream_t st = (hipStream_t)stream;
+  if (sm_wave_path(cols, dtype)) {
+    hipLaunchKernelGGL(softmax_bwd_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, dy, x, rows,
+                       (int)cols, dtype, dx);
+    return pkm_check_launch("pkm_softmax_bwd");
+  }
   const int C = (int)cols;
   const int lpr = sm_vec_lanes(cols, dtype, dy, x, dx);
   if (lpr > 0) {

@@ -105,8 +105,12 @@ class BackwardPrep:
 
 
 def _prep_key(indices, weight, psw) -> tuple:
-    return (indices.data_ptr(), tuple(indices.shape), tuple(weight.shape), weight.dtype,
-            psw.data_ptr() if psw is not None else 0, psw.dtype if psw is not None else None)
+    """What a prepared workspace depends on: the lookups' storage, shape and
+    version counter (an in-place write to indices or psw after the prepare
+    changes the version), the table shape and dtype, psw's storage and dtype."""
+    return (indices.data_ptr(), tuple(indices.shape), indices._version, tuple(weight.shape), weight.dtype,
+            psw.data_ptr() if psw is not None else 0, psw.dtype if psw is not None else None,
+            psw._version if psw is not None else 0)
 
 
 def eb_backward_prepare(
@@ -179,7 +183,10 @@ def eb_backward(
     )
     if prepared is not None:
         if prepared.key != _prep_key(indices, weight, psw):
-            raise ValueError("eb_backward: `prepared` was made for other lookups or another table shape")
+            raise ValueError(
+                "eb_backward: `prepared` was made for other lookups or another table shape, "
+                "or indices / per_sample_weights were modified in place since"
+            )
         main = torch.cuda.current_stream(dev)
         main.wait_event(prepared.done)
         prepared.workspace.record_stream(main)

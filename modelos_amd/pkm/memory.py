@@ -99,17 +99,20 @@ class _Linear(torch.autograd.Function):
 
 
 def _column_sum(g: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """g.sum(0) of a 2-D matrix in out_dtype (default g's): on the GPU for
-    float32 / bfloat16 rows of whole 16-byte vectors (pkm_column_sum: float32
-    sums over fixed row blocks, deterministic), else torch's sum."""
+    """g.sum(0) of a 2-D matrix in out_dtype (default g's). On the GPU always
+    pkm_column_sum (float32 / bfloat16 / float16, float32 sums over fixed row
+    blocks, deterministic); other dtypes raise. CPU tensors (the wrapper's
+    host-side tests: the layer itself has no CPU path) use torch's sum."""
     out_dtype = out_dtype or g.dtype
-    if not (g.is_cuda and g.dim() == 2 and g.dtype in (torch.float32, torch.bfloat16)
-            and out_dtype in (torch.float32, torch.bfloat16)
-            and g.shape[1] % (16 // g.element_size()) == 0 and g.shape[1] > 0):
+    if not g.is_cuda:
         return g.sum(0).to(out_dtype)
-    g = _aligned(g)
+    if g.dim() != 2 or g.dtype not in _lib.DTYPE_CODES or out_dtype not in _lib.DTYPE_CODES:
+        raise NotImplementedError(f"column sum of a {g.dim()}-D {g.dtype} matrix into {out_dtype} is not supported")
     rows, cols = g.shape
     out = torch.empty(cols, dtype=out_dtype, device=g.device)
+    if cols == 0:
+        return out
+    g = g.contiguous()
     ws_bytes = int(_lib.load().pkm_column_sum_workspace_size(rows, cols))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=g.device)
     _lib.call("pkm_column_sum", _lib.ptr(g), rows, cols, _lib.dtype_code(g), _lib.DTYPE_CODES[out_dtype],

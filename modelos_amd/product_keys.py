@@ -290,18 +290,21 @@ class _ScoreSoftmax(torch.autograd.Function):
         y = torch.empty_like(x2)
         _lib.call("pkm_softmax_fwd", _lib.ptr(x2), rows, cols, _lib.dtype_code(x2), _lib.ptr(y),
                   _lib.stream_of(x2.device))
-        ctx.save_for_backward(x2)
+        # the input itself: a create_graph backward differentiates through it
+        # (an aligned copy made here, with grad off, would cut that path)
+        ctx.save_for_backward(x)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        (x2,) = ctx.saved_tensors
+        (x,) = ctx.saved_tensors
         if torch.is_grad_enabled():
             # a create_graph backward (the fast-weight inner step): the same float32 expression in
             # torch ops, so that it is differentiable in turn
-            p = torch.softmax(x2.float(), dim=-1)
+            p = torch.softmax(x.float(), dim=-1)
             dyf = dy.float()
-            return (p * (dyf - (dyf * p).sum(-1, keepdim=True))).to(x2.dtype)
+            return (p * (dyf - (dyf * p).sum(-1, keepdim=True))).to(x.dtype)
+        x2 = _aligned(x)
         rows, cols = x2.shape
         dy2 = _aligned(dy.to(x2.dtype))
         dx = torch.empty_like(x2)
@@ -310,16 +313,20 @@ class _ScoreSoftmax(torch.autograd.Function):
         return dx
 
 
+_SOFTMAX_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
 def score_softmax(scores: torch.Tensor) -> torch.Tensor:
     """F.softmax(scores.float(), dim=-1).type_as(scores) (pkm/memory.py:218)
-    with one kernel each way (pkm_softmax_fwd / pkm_softmax_bwd) for float32
-    or bfloat16 rows of at most 64 scores on the GPU; other cases use that
-    expression."""
+    with one kernel each way (pkm_softmax_fwd / pkm_softmax_bwd): float32,
+    bfloat16 or float16 rows of 1 to 65536 scores. Other dtypes raise."""
     _require_device(scores)
     k = scores.shape[-1]
-    if scores.dtype in (torch.float32, torch.bfloat16) and 1 <= k <= 64 and scores.numel() > 0:
-        return _ScoreSoftmax.apply(scores.reshape(-1, k)).view(scores.shape)
-    return torch.softmax(scores.float(), dim=-1).type_as(scores)
+    if scores.dtype not in _SOFTMAX_DTYPES:
+        raise NotImplementedError(f"score_softmax: dtype {scores.dtype} not supported (float32, bfloat16, float16 are)")
+    if k == 0:
+        return torch.empty_like(scores)
+    return _ScoreSoftmax.apply(scores.reshape(-1, k)).view(scores.shape)
 
 
 def product_key_topk(

@@ -11,9 +11,9 @@ and the gradients autograd forms through those ops, in two kernels
 elementwise and reduction passes over the [tokens, heads * k_dim] query.
 The weight gradient is a deterministic column reduction.
 
-Supported: float32 or bfloat16 input with a weight of the same dtype, on the
-GPU; other dtype combinations use the reference expression (plain torch ops).
-There is no CPU path: CPU tensors raise.
+Supported: float32 or bfloat16 input with a weight of the same dtype, rows
+of whole 16-byte vectors, on the GPU; anything else raises
+NotImplementedError. There is no CPU path: CPU tensors raise.
 """
 from __future__ import annotations
 
@@ -60,11 +60,12 @@ class _RMSNormFn(torch.autograd.Function):
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """weight * (x.float() * rsqrt(mean(x.float()^2, -1) + eps)).to(x.dtype) over the last dim."""
     _require_device(x, weight)
-    if x.dtype == weight.dtype and x.dtype in _FUSED_DTYPES and x.shape[-1] % (16 // x.element_size()) == 0:
-        return _RMSNormFn.apply(x, weight, eps)
-    h = x.to(torch.float32)
-    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
-    return weight * h.to(x.dtype)
+    if x.dtype != weight.dtype or x.dtype not in _FUSED_DTYPES or x.shape[-1] % (16 // x.element_size()) != 0:
+        raise NotImplementedError(
+            f"rms_norm: input {x.dtype} with weight {weight.dtype} over rows of {x.shape[-1]} is not supported "
+            "(float32 or bfloat16 input and weight of the same dtype, rows of whole 16-byte vectors are)"
+        )
+    return _RMSNormFn.apply(x, weight, eps)
 
 
 class QueryRMSNorm(nn.Module):

@@ -497,3 +497,40 @@ def test_backward_prepared_rejects_other_lookups(device):
     prep = eb.eb_backward_prepare(didx, dW, dp)
     with pytest.raises(ValueError):
         eb.eb_backward(didx.clone(), dW, dp, dg, prepared=prep)
+
+
+@pytest.mark.parametrize("K", [70000, 3000])
+def test_backward_prepared_workspace_serves_two_reductions(K, device):
+    """One prepared workspace, two reductions with different upstream
+    gradients (retain_graph, or the same lookups reused): each reduction
+    clears its own row-schedule counters, so both equal pkm_eb_bwd's."""
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, g = eb_inputs(512, 256, K, 1024, torch.bfloat16, seed=47)
+    g2 = (torch.randn(g.shape, generator=torch.Generator().manual_seed(48)) * 0.5).to(g.dtype)
+    dW, didx, dp, dg, dg2 = _dev(W, idx, p, g, g2, device=device)
+    prep = eb.eb_backward_prepare(didx, dW, dp)
+    gw1, gp1 = eb.eb_backward(didx, dW, dp, dg, prepared=prep)
+    gw2, gp2 = eb.eb_backward(didx, dW, dp, dg2, prepared=prep)
+    ew1, ep1 = eb.eb_backward(didx, dW, dp, dg)
+    ew2, ep2 = eb.eb_backward(didx, dW, dp, dg2)
+    torch.cuda.synchronize()
+    assert torch.equal(gw1, ew1) and torch.equal(gp1, ep1)
+    assert torch.equal(gw2, ew2) and torch.equal(gp2, ep2)
+
+
+def test_backward_prepared_rejects_in_place_changes(device):
+    """An in-place write to indices or psw after the prepare is refused (the
+    workspace holds the sorted lookups and their weights)."""
+    from modelos_amd import embedding_bag as eb
+
+    W, idx, p, g = eb_inputs(8, 16, 500, 256, torch.bfloat16, seed=44)
+    dW, didx, dp, dg = _dev(W, idx, p, g, device=device)
+    prep = eb.eb_backward_prepare(didx, dW, dp)
+    dp.mul_(2.0)
+    with pytest.raises(ValueError):
+        eb.eb_backward(didx, dW, dp, dg, prepared=prep)
+    prep = eb.eb_backward_prepare(didx, dW, dp)
+    didx[0, 0] = 3
+    with pytest.raises(ValueError):
+        eb.eb_backward(didx, dW, dp, dg, prepared=prep)

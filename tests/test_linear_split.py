@@ -55,8 +55,9 @@ def test_split_k_weight_grad_gpu(device, rows, in_f, out_f):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("rows,cols", [(16384, 4096), (16384, 1024), (1000, 24), (33, 8), (1, 64)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", [(16384, 4096), (16384, 1024), (1000, 24), (33, 8), (1, 64), (500, 1001),
+                                       (40, 3), (2, 7)])
 def test_column_sum_gpu(device, dtype, rows, cols):
     """pkm_column_sum against a float64 sum, deterministic run to run."""
     from modelos_amd.pkm.memory import _column_sum

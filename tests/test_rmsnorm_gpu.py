@@ -94,3 +94,14 @@ def test_module_is_a_qwen3_rmsnorm_drop_in(device):
 def test_cpu_tensors_raise():
     with pytest.raises(RuntimeError, match="no CPU path"):
         rms_norm(torch.ones(2, 8), torch.ones(8), 1e-6)
+
+
+def test_unsupported_inputs_raise(device):
+    """No silent torch path: other dtype combinations and row widths raise."""
+    x = torch.randn((4, 4096), device=device).to(torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        rms_norm(x, torch.ones(4096, device=device), 1e-6)  # float32 weight, bfloat16 rows
+    with pytest.raises(NotImplementedError):
+        rms_norm(torch.randn((4, 4094), device=device), torch.ones(4094, device=device), 1e-6)
+    with pytest.raises(NotImplementedError):
+        rms_norm(x.half(), torch.ones(4096, device=device).half(), 1e-6)

@@ -142,3 +142,30 @@ def test_signed_zero_ties(device):
     i1 = _check_exact(q, k, H, knn, device)
     zeros = [i for i in range(n) if vals[i] == 0][: knn - 6]
     assert i1[0, 0].tolist() == [5, 77, 130, 200, 201, 255] + zeros
+
+
+@pytest.mark.parametrize("which", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_single_sub_score_output_through_c_abi(device, which, dtype):
+    """One sub-score pointer NULL, the other given, straight through the C ABI
+    (the streaming kernel for bf16, the tile kernel for float32): the given
+    half equals the full call's and the call does not touch the NULL one."""
+    from modelos_amd import _lib
+
+    N, H, n, half, knn = 300, 4, 512, 128, 32
+    g = gen(77 + which)
+    q = torch.randn((N, H, 2 * half), generator=g).to(dtype).to(device)
+    k = torch.randn((2 * H * n, half), generator=g).to(dtype).to(device)
+    full = score_topk(q, k, H, knn, "dot", sub_outputs=True)
+    scores = torch.empty((N * H, knn), dtype=dtype, device=device)
+    idx = torch.empty((N * H, knn), dtype=torch.long, device=device)
+    s_out = torch.empty((N, H, n), dtype=dtype, device=device)
+    s1, s2 = (s_out, None) if which == 1 else (None, s_out)
+    _lib.call(
+        "pkm_score_topk",
+        _lib.ptr(q), _lib.ptr(k), N, H, n, half, knn, _lib.SCORE_CODES["dot"], _lib.dtype_code(q),
+        _lib.ptr(scores), _lib.ptr(idx), None, None, _lib.ptr(s1), _lib.ptr(s2), _lib.stream_of(q.device),
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(idx, full[1]) and torch.equal(scores, full[0])
+    assert torch.equal(s_out, full[4] if which == 1 else full[5])

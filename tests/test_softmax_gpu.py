@@ -26,9 +26,11 @@ def _ref(x):
     return torch.softmax(x.float(), dim=-1).type_as(x)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
-@pytest.mark.parametrize("shape", [(131072, 32), (300, 64), (77, 7), (5, 1), (3, 4, 33), (101, 8), (99, 16), (50, 4)],
-                         ids=["layer", "k64", "k7", "k1", "3d-k33", "k8", "k16", "k4"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16], ids=["bf16", "f32", "f16"])
+@pytest.mark.parametrize("shape", [(131072, 32), (300, 64), (77, 7), (5, 1), (3, 4, 33), (101, 8), (99, 16), (50, 4),
+                                   (8192, 64 * 4), (33, 65), (7, 1000), (3, 5000)],
+                         ids=["layer", "k64", "k7", "k1", "3d-k33", "k8", "k16", "k4", "fw-h4k64", "k65", "k1000",
+                              "k5000"])
 def test_matches_torch(device, dtype, shape):
     g = gen(11)
     x = (torch.randn(shape, generator=g) * 4).to(dtype).to(device)
@@ -40,7 +42,8 @@ def test_matches_torch(device, dtype, shape):
     assert_rel_close(y, e_y, REL_TOL[dtype], "y")
     assert_rel_close(dx, e_dx, REL_TOL[dtype], "dx")
     # rows sum to one (float32 probabilities before the rounding)
-    assert_rel_close(y.double().sum(-1), torch.ones(shape[:-1], dtype=torch.float64), 5e-2 if dtype == torch.bfloat16 else 1e-5, "row sums")
+    sum_tol = {torch.bfloat16: 5e-2, torch.float16: 5e-3, torch.float32: 1e-5}[dtype]
+    assert_rel_close(y.double().sum(-1), torch.ones(shape[:-1], dtype=torch.float64), sum_tol, "row sums")
 
 
 def test_equal_and_extreme_scores(device):
@@ -57,5 +60,21 @@ def test_deterministic_and_limits(device):
     x = torch.randn((1000, 32), generator=gen(13)).to(torch.bfloat16).to(device)
     assert torch.equal(score_softmax(x), score_softmax(x))
     with pytest.raises(_lib.PkmError):
-        y = torch.empty((2, 65), device=device)
-        _lib.call("pkm_softmax_fwd", _lib.ptr(y), 2, 65, _lib.dtype_code(y), _lib.ptr(y), _lib.stream_of(y.device))
+        y = torch.empty((2, 65537), device=device)
+        _lib.call("pkm_softmax_fwd", _lib.ptr(y), 2, 65537, _lib.dtype_code(y), _lib.ptr(y), _lib.stream_of(y.device))
+    with pytest.raises(NotImplementedError):
+        score_softmax(torch.zeros((2, 4), dtype=torch.float64, device=device))
+
+
+def test_long_rows_extreme_scores(device):
+    """The wave-per-row kernel (rows longer than 64): equal scores, one
+    dominant score, a -inf entry."""
+    x = torch.zeros((3, 256), device=device)
+    x[1, 0], x[1, 1:] = 1e4, -1e4
+    x[2, 5] = float("-inf")
+    dy = torch.randn(x.shape, generator=gen(14)).to(device)
+    y, dx = _run(score_softmax, x, dy)
+    e_y, e_dx = _run(_ref, x, dy)
+    torch.cuda.synchronize()
+    assert_rel_close(y, e_y, 1e-6, "y")
+    assert_rel_close(dx, e_dx, 1e-5, "dx")
