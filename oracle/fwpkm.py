@@ -139,7 +139,11 @@ def retrieve(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, cfg: FwC
     sc = s1.gather(2, idx // n) + s2.gather(2, idx % n)
     w = transform(sc.reshape(B * T, cfg.heads * cfg.topk), cfg)
     hyp = _Bag.apply(values, idx.reshape(B * T, cfg.heads * cfg.topk), w)
-    return {"hyp": hyp, "scores": sc, "normed": w, "indices": idx, "s1": s1, "s2": s2}
+    # sum over the bag of |w| |V[idx]|: the scale of each retrieved value's terms (a test's
+    # rounding bound for sums with cancellation), no gradient
+    with torch.no_grad():
+        mag = _Bag.apply(values.detach().abs(), idx.reshape(B * T, cfg.heads * cfg.topk), w.detach().abs())
+    return {"hyp": hyp, "scores": sc, "normed": w, "indices": idx, "s1": s1, "s2": s2, "mag": mag}
 
 
 def marginal_entropy(M: torch.Tensor, cfg: FwConfig, eps: float = 1e-8, M_sel: Optional[torch.Tensor] = None
@@ -216,12 +220,13 @@ def forward_wo_past(q, ref_v, keys, values, cfg: FwConfig, chunk_size: int, gate
     decides the address loss's top-k masks (marginal_entropy)."""
     B, T = q.shape[:2]
     in_dtype = q.dtype
+    v0_abs = values.detach().abs().to(torch.float64)
     if cfg.fp32_fw:
         q, ref_v = q.float(), ref_v.float()
         params = {"keys": keys.float(), "values": values.float()}
     else:
         params = {"keys": keys, "values": values}
-    outs, idxs, scs, losses, alosses, steps = [], [], [], [], [], []
+    outs, idxs, scs, losses, alosses, steps, mags, step_mags = [], [], [], [], [], [], [], []
     sel_iter = iter(selections) if selections is not None else None
     score_iter = iter(sel_scores) if sel_scores is not None else None
     for s in range(0, T, chunk_size):
@@ -230,6 +235,7 @@ def forward_wo_past(q, ref_v, keys, values, cfg: FwConfig, chunk_size: int, gate
         r = retrieve(q[:, s:e], params["keys"], params["values"], cfg, next(sel_iter) if sel_iter else None)
         hyp = r["hyp"].reshape(B, cT, -1)
         outs.append(hyp)
+        mags.append(r["mag"].reshape(B, cT, -1))
         idxs.append(r["indices"].reshape(B, cT, -1))
         scs.append(r["normed"].reshape(B, cT, -1))
         cg = gates[:, s:e] if gates is not None else None
@@ -239,6 +245,18 @@ def forward_wo_past(q, ref_v, keys, values, cfg: FwConfig, chunk_size: int, gate
                         u_m.reshape(-1) if u_m is not None else None, u_w.reshape(-1) if u_w is not None else None)
         al = addr_loss(r, cfg, next(score_iter) if score_iter else None)
         ns = int((u_m > 0).sum()) if u_m is not None else B * cT
+        if cfg.mem_grad_to_values_only:
+            # the scale of this chunk's value step: lr * scale / count * sum over the lookups of
+            # |w| |dL/dhyp| (the terms of the value gradient's sums), no gradient
+            (dh,) = torch.autograd.grad(0.5 * ml.mean(), r["hyp"], retain_graph=True)
+            v = params["values"]
+            with torch.no_grad():
+                ix = r["indices"].reshape(-1)
+                contrib = (r["normed"].detach().abs().reshape(-1, 1)
+                           * dh.abs().repeat_interleave(cfg.heads * cfg.topk, 0))
+                gabs = torch.zeros(v.shape, dtype=contrib.dtype).index_add_(0, ix, contrib)
+                cnt = torch.bincount(ix, minlength=v.shape[0]).clamp_min(1).to(gabs.dtype)
+                step_mags.append(cfg.learning_rate * gabs * (ns * cfg.v_dim * cfg.topk * cfg.heads) / cnt[:, None])
         params, g = update(params, cfg, ns, r["indices"], ml.mean(), al)
         steps.append([x.detach() for x in g])
         losses.append(ml.reshape(B, -1).detach())
@@ -253,6 +271,9 @@ def forward_wo_past(q, ref_v, keys, values, cfg: FwConfig, chunk_size: int, gate
         values.data.copy_(params["values"].data.to(values.dtype))
     return {
         "output": torch.cat(outs, 1).to(in_dtype),
+        "output_mag": torch.cat(mags, 1),
+        # |initial values| + the chunks' value-step scales: the final values' rounding bound
+        "values_mag": (v0_abs + sum(m.to(torch.float64) for m in step_mags)) if step_mags else None,
         "indices": torch.cat(idxs, 1).reshape(B, T, cfg.heads, cfg.topk),
         "scores": torch.cat(scs, 1).reshape(B, T, cfg.heads, cfg.topk),
         "losses": torch.cat(losses, 1),

@@ -81,19 +81,23 @@ def get_indices_torch(query: torch.Tensor, keys: torch.Tensor, heads: int, knn: 
 
 def hashing_memory_forward(x: torch.Tensor, P: Dict[str, torch.Tensor], heads: int, knn: int,
                            batchnorm: bool = False, idx: torch.Tensor | None = None,
-                           reference_ops: bool = False, bag_idx: torch.Tensor | None = None):
+                           reference_ops: bool = False, bag_idx: torch.Tensor | None = None,
+                           trace: dict | None = None):
     """(out [B, T, out_dim], indices [B, T, H*knn]) of HashingMemory.forward
     with swilu projection and no gating (the layer's defaults). `idx` forces
     the selection (to evaluate the layer at another implementation's ids);
     reference_ops selects with the reference's einsum/topk sequence instead of
     the stable-tie oracle (the CPU baseline). `bag_idx` [N*H, knn], when
     given, addresses P["values.weight"] instead of idx (a compact table of
-    just the rows idx reads)."""
+    just the rows idx reads). `trace`, when given, receives the intermediate
+    tensors (query Linear output "q_lin", swilu projection output "s", the
+    value projection's input "h"), so a test can bound each output element by
+    the sum of its terms' magnitudes."""
     B, T, C = x.shape
     X = x.reshape(-1, C)
     N = X.shape[0]
-    q = F.linear(X, P["query_proj.query_mlps.0.weight"], P.get("query_proj.query_mlps.0.bias"))
-    q = _norm(q, P, batchnorm)
+    q_lin = F.linear(X, P["query_proj.query_mlps.0.weight"], P.get("query_proj.query_mlps.0.bias"))
+    q = _norm(q_lin, P, batchnorm)
     k_dim = q.shape[1] // heads
     if reference_ops:
         scores, idx = get_indices_torch(q.reshape(N * heads, k_dim), P["keys"], heads, knn)
@@ -102,6 +106,9 @@ def hashing_memory_forward(x: torch.Tensor, P: Dict[str, torch.Tensor], heads: i
     p = F.softmax(scores.float(), dim=-1).type_as(scores)
     E = F.embedding_bag((idx if bag_idx is None else bag_idx).reshape(N, heads * knn), P["values.weight"],
                         per_sample_weights=p.reshape(N, heads * knn), mode="sum")
-    gate = F.silu(F.linear(X, P["swilu_projection.weight"], P["swilu_projection.bias"]))
-    out = F.linear(E * gate, P["value_proj.weight"], P["value_proj.bias"])
+    s = F.linear(X, P["swilu_projection.weight"], P["swilu_projection.bias"])
+    h = E * F.silu(s)
+    out = F.linear(h, P["value_proj.weight"], P["value_proj.bias"])
+    if trace is not None:
+        trace.update(q_lin=q_lin, s=s, h=h)
     return out.reshape(B, T, -1), idx.reshape(B, T, -1)

@@ -146,12 +146,20 @@ def test_bf16_chain_vs_fp64_oracle(score_type, device):
     e = ofw.forward_wo_past(q64, r64, k64, v64, cfg, chunk, selections=sel, sel_scores=sub)
     e["output"].backward(dout.double())
     tol = 2e-2
-    assert_rel_close(out["output"], e["output"], tol, "output", elem_frac=None)
-    assert_rel_close(out["losses"], e["losses"], tol, "losses", elem_frac=None)
+    # normwise, and elementwise: each retrieved value against the sum of its terms' magnitudes
+    # (a bag sum with cancellation); the per-token losses on the elements >= 0.1 of their maximum
+    assert_rel_close(out["output"], e["output"], tol, "output", cond=e["output_mag"])
+    assert_rel_close(out["losses"], e["losses"], tol, "losses")
+    # The other tensors normwise: after two chunks of bf16 inner updates (bf16 scores through the
+    # softmax, bf16 gradients through a step scaled by tokens * v_dim * topk * heads / count) single
+    # entries move by a few % of their own size against float64, beyond bf16's 2e-2 elementwise
+    # (measured: up to 4% on 0.01-0.6% of the entries; the reference's op sequence run in bf16
+    # shows the same spread)
     assert_rel_close(mem.values, e["final"]["values"], tol, "final values", elem_frac=None)
     assert_rel_close(qd.grad, q64.grad, tol, "dq", elem_frac=None)
     assert_rel_close(rd.grad, r64.grad, tol, "dref_v", elem_frac=None)
     assert_rel_close(mem.values.grad, v64.grad, tol, "dvalues", elem_frac=None)
+
     # a key's gradient sums every token's 2 u (q - k) with heavy cancellation; the bf16 sub-score
     # gradient (the reference's bf16 autograd rounds it too) moves single entries by a few % of the
     # maximum: 2-norm relative error here
@@ -233,8 +241,7 @@ def test_full_shape_fast_weight_step(dtype, device):
             gv = (wc[bags, slots, None] * dh[bags]).sum(0)
             expected[r] = expected[r] - 0.1 * gv * (4096 * 1024 * 16 * 4 / bags.numel())
     for r in rows:
-        assert_rel_close(vf1[r].cpu(), expected[r], 1e-4 if dtype == torch.float32 else 2e-2, f"updated row {r}",
-                         elem_frac=None)
+        assert_rel_close(vf1[r].cpu(), expected[r], tol, f"updated row {r}")
 
 
 @pytest.mark.parametrize("dtype,score_type",

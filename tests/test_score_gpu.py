@@ -252,7 +252,18 @@ def test_fwpkm_drop_in(device, score_type):
     assert_rel_close(s1.cpu(), e_s1, REL_TOL[torch.float32], "s1")
     kv = k.view(m.heads, 2, m.subsize, m.k_dim // 2)[:, 0].contiguous().to(device)
     dense = m.compute_qk_scores(q[:, :, : m.k_dim // 2].contiguous().to(device), kv)
-    assert_rel_close(dense.cpu(), e_s1, 1e-4, "compute_qk_scores")
+    # 1e-5 against each score's rounding bound: |q| . |k| for a dot product; for idw the float32
+    # rounding of d^2 = |q|^2 + |k|^2 - 2 <q, k> (bounded by (|q| + |k|)^2) divided by 1e-3 + d^2
+    q1 = q[:, :, : m.k_dim // 2].double()
+    k1 = k.view(m.heads, 2, m.subsize, m.k_dim // 2)[:, 0].double()
+    mag = torch.einsum("bhd,hnd->bhn", q1.abs(), k1.abs())
+    if st == "dot":
+        cond = mag
+    else:
+        qq, kk = (q1 * q1).sum(-1)[:, :, None], (k1 * k1).sum(-1)[None]
+        d2 = (qq + kk - 2 * torch.einsum("bhd,hnd->bhn", q1, k1)).clamp_min(0.0)
+        cond = (qq + kk + 2 * mag) / (1e-3 + d2) + e_s1.abs()
+    assert_rel_close(dense.cpu(), e_s1, REL_TOL[torch.float32], "compute_qk_scores", cond=cond)
 
 
 def test_bf16_knn_growing_in_one_process(device):
