@@ -73,7 +73,11 @@ size_t pkm_eb_bwd_workspace_size(int64_t num_rows, int64_t dim, int64_t bags, in
  *       dense [num_rows, dim] in weight_dtype; untouched rows are written as 0.
  *   grad_psw[b, j]    = <weight[indices[b, j], :], grad_out[b, :]>   (float32 dot)
  *       [bags, bag_size] in psw_dtype; not written when psw is NULL.
- * grad_out: [bags, dim] in grad_dtype.
+ * grad_out: [bags, dim] in grad_dtype: weight_dtype, or F32 beside a BF16 /
+ * F16 table (read as float32, unrounded, as the reference's kernel widens it,
+ * pkm/xformer_embeddingbag.py:322); other combinations return
+ * PKM_ERR_UNSUPPORTED (a caller widens a 16-bit gradient to float32 first,
+ * which is exact).
  * workspace: device buffer of at least pkm_eb_bwd_workspace_size() bytes.
  *
  * Replaces embedding_bag_bw_rev_indices
@@ -143,7 +147,11 @@ int pkm_eb_bwd_noalloc(const void* weight, int64_t num_rows, int64_t dim, int we
  *   d_grad_out[b, :] = sum_j a[b, j] * gbar[indices[b, j], :]     [bags, dim], grad_dtype
  *   d_a[b, j]        = <gbar[indices[b, j], :], grad_out[b, :]>   [bags, bag_size], a_dtype
  * a may be NULL (unweighted): then d_a is not written.
- * gbar: [num_rows, dim] in gbar_dtype.
+ * gbar: [num_rows, dim] in gbar_dtype, read in that dtype.
+ * grad_out and d_grad_out: [bags, dim] in grad_dtype, which is gbar_dtype or
+ * F32 beside a BF16 / F16 gbar (float32 sums in both cases, as the
+ * reference's type promotion gives; other combinations return
+ * PKM_ERR_UNSUPPORTED).
  *
  * Replaces EmbeddingBagBW.backward (fwpkm/xformer_embeddingbag_grad_wrapper.py:42-74).
  */

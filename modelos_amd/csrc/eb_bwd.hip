@@ -387,16 +387,18 @@ struct BwdUnroll {
 
 // acc += sum over sorted occurrences [i_beg, i_end) (in order) of psw[p] * g[p / L];
 // with want_dot, gpsw[p] = <wv, g[p / L]> for each of them.
-template <typename TW, int LPG, int VPL>
+template <typename TW, typename TG, int LPG, int VPL>
 __device__ __forceinline__ void reduce_occurrences(uint32_t i_beg, uint32_t i_end, const uint32_t* __restrict__ svals,
                                                    const void* __restrict__ psw, int pdt,
-                                                   const TW* __restrict__ g, int64_t D, uint32_t L32,
+                                                   const TG* __restrict__ g, int64_t D, uint32_t L32,
                                                    int64_t col0, int glane, const float* wv, bool want_dot,
                                                    void* __restrict__ gpsw, float* acc,
                                                    float* __restrict__ dsorted = nullptr) {
+  using GT = GradTraits<TW, TG>;
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
-  constexpr int U = BwdUnroll<VPL>::U;
+  constexpr int NV = GT::NV;
+  constexpr int U = BwdUnroll<VPL * NV>::U;
   constexpr int VSTRIDE = LPG * EPV;
   for (uint32_t i0 = i_beg; i0 < i_end; i0 += LPG) {
     const int n = (int)((i_end - i0) < (uint32_t)LPG ? (i_end - i0) : (uint32_t)LPG);
@@ -409,7 +411,7 @@ __device__ __forceinline__ void reduce_occurrences(uint32_t i_beg, uint32_t i_en
     }
     float my_dot = 0.f;
     for (int jj = 0; jj < n; jj += U) {
-      uint4 gvec[U][VPL];
+      uint4 gvec[U][VPL * NV];
       float w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -417,9 +419,11 @@ __device__ __forceinline__ void reduce_occurrences(uint32_t i_beg, uint32_t i_en
         if (jj + u < n) {
           const uint32_t b = (uint32_t)bcast_i32<LPG>((int)my_b, jj + u);
           w[u] = bcast_f32<LPG>(my_w, jj + u);
-          const TW* grow = g + (int64_t)b * D + col0;
+          const TG* grow = g + (int64_t)b * D + col0;
 #pragma unroll
-          for (int v = 0; v < VPL; ++v) gvec[u][v] = ld16(grow + v * VSTRIDE);
+          for (int v = 0; v < VPL; ++v)
+#pragma unroll
+            for (int h = 0; h < NV; ++h) gvec[u][v * NV + h] = ld16(grow + v * VSTRIDE + h * (EPV / NV));
         }
       }
 #pragma unroll
@@ -427,7 +431,7 @@ __device__ __forceinline__ void reduce_occurrences(uint32_t i_beg, uint32_t i_en
         if (jj + u < n) {
           float f[NE];
 #pragma unroll
-          for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(gvec[u][v], f + v * EPV);
+          for (int v = 0; v < VPL; ++v) GT::unpack(&gvec[u][v * NV], f + v * EPV);
 #pragma unroll
           for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
           if (want_dot) {
@@ -481,10 +485,10 @@ __device__ __forceinline__ void add_heavy_partials(uint32_t beg, uint32_t end, c
 
 // Heavy rows: chunk c = sorted occurrences [c*T, (c+1)*T). A row with more
 // than T occurrences always contains the chunk's first or last occurrence.
-template <typename TW, int LPG, int VPL>
+template <typename TW, typename TG, int LPG, int VPL>
 __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict__ W, int64_t K, int64_t D,
                                                            const void* __restrict__ psw, int pdt,
-                                                           const TW* __restrict__ g, uint32_t L32,
+                                                           const TG* __restrict__ g, uint32_t L32,
                                                            const uint32_t* __restrict__ offs,
                                                            const uint32_t* __restrict__ skeys,
                                                            const uint32_t* __restrict__ svals,
@@ -519,8 +523,8 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
-    reduce_occurrences<TW, LPG, VPL>(s_beg, s_end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw, acc,
-                                     dsorted);
+    reduce_occurrences<TW, TG, LPG, VPL>(s_beg, s_end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw,
+                                         acc, dsorted);
     float* prow = partials + (2 * c + slot) * D + col0;
 #pragma unroll
     for (int v = 0; v < VPL; ++v)
@@ -530,10 +534,10 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
 }
 
 // Generic rows kernel (lane groups smaller than a wave, small rows).
-template <typename TW, int LPG, int VPL>
+template <typename TW, typename TG, int LPG, int VPL>
 __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__ W, int64_t K, int64_t D,
                                                           const void* __restrict__ psw, int pdt,
-                                                          const TW* __restrict__ g, uint32_t L32,
+                                                          const TG* __restrict__ g, uint32_t L32,
                                                           const uint32_t* __restrict__ offs,
                                                           const uint32_t* __restrict__ svals,
                                                           const float* __restrict__ partials, int rows_per_group,
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
     } else if (cnt > 0) {
       float wv[NE];
       if (want_dot) load_row_f32<TW, LPG, VPL>(W + r * D, col0, wv);
-      reduce_occurrences<TW, LPG, VPL>(beg, end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw, acc);
+      reduce_occurrences<TW, TG, LPG, VPL>(beg, end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw, acc);
     }
     TW* orow = gW + r * D + col0;
 #pragma unroll
@@ -605,10 +609,10 @@ __device__ __forceinline__ float reduce8_slots(const float (&d)[8], int lane) {
   return group_sum<8>(t);
 }
 
-template <int VPL, int U>
+template <int VPL, int U, int NV>
 struct RowData {
   uint4 wraw[VPL];
-  uint4 gvec[U][VPL];
+  uint4 gvec[U][VPL * NV];  // NV 16-byte loads per table vector (GradTraits)
 };
 template <int U>
 struct RowMeta {
@@ -629,9 +633,11 @@ template <int U>
 __device__ __forceinline__ bool dot_store_of(int lane) {
   return U == 8 ? (lane & 7) == 0 : true;
 }
-template <typename TW, int VPL, int U>
-__device__ __forceinline__ float accumulate_slots(const RowData<VPL, U>& R, const float* w, uint32_t nh, float* acc,
-                                                  bool want_dot, int lane) {
+template <typename TW, typename TG, int VPL, int U>
+__device__ __forceinline__ float accumulate_slots(const RowData<VPL, U, GradTraits<TW, TG>::NV>& R, const float* w,
+                                                  uint32_t nh, float* acc, bool want_dot, int lane) {
+  using GT = GradTraits<TW, TG>;
+  constexpr int NV = GT::NV;
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   float d[U];
@@ -641,12 +647,12 @@ __device__ __forceinline__ float accumulate_slots(const RowData<VPL, U>& R, cons
     if ((uint32_t)u < nh) {
       float f[NE];
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.gvec[u][v], f + v * EPV);
+      for (int v = 0; v < VPL; ++v) GT::unpack(&R.gvec[u][v * NV], f + v * EPV);
 #pragma unroll
       for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
       if (want_dot) {
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) d[u] = vec_dot<TW>(R.wraw[v], R.gvec[u][v], d[u]);
+        for (int v = 0; v < VPL; ++v) d[u] = GT::dot(R.wraw[v], &R.gvec[u][v * NV], d[u]);
       }
     }
   }
@@ -672,16 +678,19 @@ __device__ __forceinline__ float accumulate_slots(const RowData<VPL, U>& R, cons
 // ends) and reduces it U occurrences at a time, in order, the next chunk's
 // metadata and gradient rows in flight while the current chunk is reduced.
 // One wave per row keeps each row's sums in position order.
-template <typename TW, int VPL, int U>
+template <typename TW, typename TG, int VPL, int U>
 __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
-    const TW* __restrict__ W, int64_t D, int want_dot, const TW* __restrict__ g, const uint32_t* __restrict__ offs,
+    const TW* __restrict__ W, int64_t D, int want_dot, const TG* __restrict__ g, const uint32_t* __restrict__ offs,
     const uint2* __restrict__ meta, const TW* __restrict__ zrow, TW* __restrict__ gW, float* __restrict__ dsorted,
     uint32_t dummy_slot, const uint32_t* __restrict__ long_rows, const uint32_t* __restrict__ long_count) {
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
+  constexpr int NV = GradTraits<TW, TG>::NV;
   const int lane = threadIdx.x & 63;
   const uint32_t lane_byte = (uint32_t)lane * 16u;
+  const uint32_t glane_byte = lane_byte * NV;  // the lane's gradient elements (NV 16-byte pieces each)
   const uint64_t rowbytes = (uint64_t)D * sizeof(TW);
+  const uint64_t growbytes = (uint64_t)D * sizeof(TG);
   const char* Wb = (const char*)W;
   const char* gb = (const char*)g;
   const char* zb = (const char*)zrow;
@@ -689,15 +698,15 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
   const bool dot_store = dot_store_of<U>(lane);
   const uint32_t n = *long_count;
   const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
-  auto fetch = [&](uint32_t s, uint32_t end, RowData<VPL, U>& R, float* w) {
+  auto fetch = [&](uint32_t s, uint32_t end, RowData<VPL, U, NV>& R, float* w) {
     const uint32_t nh = (end - s) < (uint32_t)U ? (end - s) : (uint32_t)U;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint2 m = meta[(uint32_t)u < nh ? s + (uint32_t)u : s];  // uniform: scalar loads
       w[u] = (uint32_t)u < nh ? __uint_as_float(m.y) : 0.f;
-      const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * rowbytes : zb;
+      const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * growbytes : zb;
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+      for (int v = 0; v < VPL * NV; ++v) R.gvec[u][v] = ld16(grow + glane_byte + (v / NV) * 1024u * NV + (v % NV) * 16u);
     }
     return nh;
   };
@@ -705,7 +714,7 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
     const uint32_t r = (uint32_t)__builtin_amdgcn_readfirstlane((int)long_rows[t]);
     const uint32_t beg = offs[r], end = offs[r + 1];
     const char* wrow = want_dot ? Wb + (uint64_t)r * rowbytes : zb;
-    RowData<VPL, U> DA, DB;
+    RowData<VPL, U, NV> DA, DB;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       DA.wraw[v] = ld16(wrow + lane_byte + v * 1024u);
@@ -719,12 +728,12 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
     for (uint32_t s = beg;;) {
       const uint32_t s2 = s + U;
       if (s2 < end) nB = fetch(s2, end, DB, wB);
-      float d = accumulate_slots<TW, VPL, U>(DA, wA, nA, acc, want_dot, lane);
+      float d = accumulate_slots<TW, TG, VPL, U>(DA, wA, nA, acc, want_dot, lane);
       if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nA ? s + dot_slot : dummy_slot] = d;
       if (s2 >= end) break;
       const uint32_t s3 = s2 + U;
       if (s3 < end) nA = fetch(s3, end, DA, wA);
-      d = accumulate_slots<TW, VPL, U>(DB, wB, nB, acc, want_dot, lane);
+      d = accumulate_slots<TW, TG, VPL, U>(DB, wB, nB, acc, want_dot, lane);
       if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nB ? s2 + dot_slot : dummy_slot] = d;
       if (s3 >= end) break;
       s = s3;
@@ -758,7 +767,7 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
 // and metadata are loaded one chunk ahead, so their latency hides under the
 // current chunk's rows. Each row is still reduced by one wave in position
 // order, so the sums are those of the per-64-rows kernel, bit for bit.
-// Rows of U + 1 .. 2 U lookups are reduced in place U lookups at a time;
+// Rows of U + 1 .. long_min lookups are reduced in place U lookups at a time;
 // longer light rows are listed beforehand by list_long_rows_kernel, skipped
 // here and reduced by eb_bwd_long_rows_kernel.
 // ---------------------------------------------------------------------------
@@ -815,12 +824,17 @@ __global__ __launch_bounds__(256) void list_long_rows_kernel(const uint32_t* __r
   }
 }
 
-template <typename TW, int VPL, int U>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 && U <= 4) ? 5 : ((VPL == 1 || (VPL == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows_dyn_kernel(
-    const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TW* __restrict__ g,
+// Register footprint of a row's loads in 16-byte vectors per lane: the table
+// row plus, per prefetch slot, the gradient row in its own dtype.
+template <typename TW, typename TG, int VPL>
+constexpr int kRowVecs = VPL * GradTraits<TW, TG>::NV;
+
+template <typename TW, typename TG, int VPL, int U>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<TW, TG, VPL> == 1 && U <= 4) ? 5 : ((kRowVecs<TW, TG, VPL> == 1 || (kRowVecs<TW, TG, VPL> == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows_dyn_kernel(
+    const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TG* __restrict__ g,
     const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
     const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
-    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk) {
+    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk, uint32_t long_min) {
   static_assert(kDynRC * U <= 64, "a chunk's metadata must fit one load per lane");
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
@@ -832,8 +846,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   const uint32_t cpb = blk / (kDynRC * kDynSub);  // chunks per block and counter
   const uint32_t nchunks = grp_blocks * cpb;
   const uint32_t K32 = (uint32_t)K;
+  constexpr int NV = GradTraits<TW, TG>::NV;
   const uint32_t lane_byte = (uint32_t)lane * 16u;
+  const uint32_t glane_byte = lane_byte * NV;  // the lane's gradient elements (NV 16-byte pieces each)
   const uint64_t rowbytes = (uint64_t)D * sizeof(TW);
+  const uint64_t growbytes = (uint64_t)D * sizeof(TG);
   const char* Wb = (const char*)W;
   const char* gb = (const char*)g;
   const char* zb = (const char*)zrow;
@@ -863,7 +880,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     M.beg = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i);
     M.end = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i + 1);
     const uint32_t cnt = M.end - M.beg;
-    skip = cnt > 2u * U && cnt <= (uint32_t)kHeavyT;  // listed for the long-row kernel
+    skip = cnt > long_min && cnt <= (uint32_t)kHeavyT;  // listed for the long-row kernel
     M.nh = cnt <= (uint32_t)U ? cnt : 0u;
     row = C.row0 + (uint32_t)i;
 #pragma unroll
@@ -872,15 +889,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
       M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readlane((int)C.mw, i * U + u)) : 0.f;
     }
   };
-  auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U>& R) {
+  auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R) {
     const char* wrow = (want_dot && M.nh) ? Wb + (uint64_t)row * rowbytes : zb;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);  // read once: keep L2 for g
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * rowbytes : zb;
+      const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * growbytes : zb;
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+      for (int v = 0; v < VPL * NV; ++v) R.gvec[u][v] = ld16(grow + glane_byte + (v / NV) * 1024u * NV + (v % NV) * 16u);
     }
   };
   const int dot_slot = dot_slot_of<U>(lane);
@@ -891,7 +908,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   // loads stay in flight meanwhile. Longer light rows (rare at uniform-ish
   // lookups, crowded when lookups pile onto few rows) go to the long-row
   // kernel, which spreads them over all XCDs.
-  auto reduce_long = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U>& R, float* acc) {
+  auto reduce_long = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R, float* acc) {
     const char* wrow = want_dot ? Wb + (uint64_t)row * rowbytes : zb;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);
@@ -902,15 +919,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
       for (int u = 0; u < U; ++u) {
         const uint2 m = meta[s + (uint32_t)u];  // uniform; in bounds: meta is padded past every row start
         w[u] = (uint32_t)u < nh ? __uint_as_float(m.y) : 0.f;
-        const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * rowbytes : zb;
+        const char* grow = (uint32_t)u < nh ? gb + (uint64_t)m.x * growbytes : zb;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) R.gvec[u][v] = ld16(grow + lane_byte + v * 1024u);
+        for (int v = 0; v < VPL * NV; ++v) R.gvec[u][v] = ld16(grow + glane_byte + (v / NV) * 1024u * NV + (v % NV) * 16u);
       }
-      const float d = accumulate_slots<TW, VPL, U>(R, w, nh, acc, want_dot != 0, lane);
+      const float d = accumulate_slots<TW, TG, VPL, U>(R, w, nh, acc, want_dot != 0, lane);
       if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nh ? s + dot_slot : dummy_slot] = d;
     }
   };
-  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, RowData<VPL, U>& R) {
+  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, RowData<VPL, U, NV>& R) {
     if (skip) return;  // longer than 2 U (and light): reduced by the long-row kernel
     float acc[NE];
 #pragma unroll
@@ -919,7 +936,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
     if (cnt > (uint32_t)U && cnt <= (uint32_t)kHeavyT) {
       reduce_long(M, row, R, acc);
     } else {
-      const float mydot = accumulate_slots<TW, VPL, U>(R, M.w, M.nh, acc, want_dot != 0, lane);
+      const float mydot = accumulate_slots<TW, TG, VPL, U>(R, M.w, M.nh, acc, want_dot != 0, lane);
       if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
     }
     if (M.end - M.beg > (uint32_t)kHeavyT) add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
@@ -939,7 +956,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((VPL == 1 &
   fetch_offs(t1, nxt);
 
   RowMeta<U> MA, MB;
-  RowData<VPL, U> DA, DB;
+  RowData<VPL, U, NV> DA, DB;
   uint32_t rowA, rowB;
   bool skA, skB;
   get_meta(cur, 0, MA, rowA, skA);
@@ -1151,11 +1168,11 @@ static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* l
 // The row reduction on the ticket schedule: the rows kernel, then the long
 // rows listed by prepare_rows_dyn. Each reduction clears its own ticket
 // counters first, so a prepared workspace can serve any number of reductions.
-template <typename TW, int VPL, int U>
+template <typename TW, typename TG, int VPL, int U>
 static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
                             const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                             float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, uint32_t* tickets,
-                            hipStream_t st) {
+                            uint32_t long_min, hipStream_t st) {
   const uint32_t* long_count = long_rows + K;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
                      (int64_t)kDynGroups * kDynSub * kCtrStride);
@@ -1166,13 +1183,13 @@ static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, c
   wgs = wgs < 1280 ? wgs : 1280;
   wgs = cdiv(wgs, kDynGroups * kDynSub) * kDynGroups * kDynSub;  // every counter gets workgroups
   KernelSpan span("eb_bwd_rows", st);
-  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, VPL, U>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W, K, D,
-                     want_dot, (const TW*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW, dsorted,
-                     dummy_slot, tickets, blk);
+  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, TG, VPL, U>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W, K,
+                     D, want_dot, (const TG*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW,
+                     dsorted, dummy_slot, tickets, blk, long_min);
   const int64_t rb = cdiv(K, 4 * 64);
   const unsigned lb = (unsigned)(rb < 1024 ? rb : 1024);
-  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, VPL, U>), dim3(lb), dim3(256), 0, st, (const TW*)W, D, want_dot,
-                     (const TW*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
+  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, TG, VPL, U>), dim3(lb), dim3(256), 0, st, (const TW*)W, D, want_dot,
+                     (const TG*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
                      (const uint32_t*)long_rows, long_count);
 }
 
@@ -1197,7 +1214,7 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
   }
 }
 
-template <typename TW, int LPG, int VPL>
+template <typename TW, typename TG, int LPG, int VPL>
 static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, int pdt, const void* g, int64_t L,
                           const uint32_t* offs, const uint32_t* skeys, const uint32_t* svals, const uint32_t* nvalid,
                           int64_t N, const BwdLayout& l, char* ws, void* gW, void* gpsw, hipStream_t st) {
@@ -1210,52 +1227,53 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     float* dsorted = (float*)(ws + l.dsorted);
     void* zrow = ws + l.zrow;
     if (N > 0)
-      hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D, psw,
-                         pdt, (const TW*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
+      hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, TG, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D,
+                         psw, pdt, (const TG*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
                          dsorted);
     if (K > 0) {
       const int want_dot = psw != nullptr ? 1 : 0;
-      const bool dense = rows_prefetch<VPL>(N, K) == 8;
+      // the prefetch depth the lists were prepared for (rows longer than twice it go to the
+      // long-row kernel), halved when each gradient row is twice the table row's bytes
+      const int u0 = rows_prefetch<VPL>(N, K);
+      const uint32_t long_min = (uint32_t)(2 * u0);
+      constexpr int NV = GradTraits<TW, TG>::NV;
       const uint32_t dslot = (uint32_t)N;
       void* dummy = ws + l.dummy_row;
       uint32_t* long_rows = (uint32_t*)(ws + l.long_rows);
       uint32_t* tickets = (uint32_t*)(ws + l.tickets);
-      if constexpr (VPL == 1) {
-        if (dense)
-          launch_rows_dyn<TW, 1, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
-        else
-          launch_rows_dyn<TW, 1, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
-      } else if constexpr (VPL == 2) {
-        if (dense)
-          launch_rows_dyn<TW, 2, 8>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
-        else
-          launch_rows_dyn<TW, 2, 4>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
-      } else if constexpr (VPL == 4) {
-        launch_rows_dyn<TW, 4, 2>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
+#define PKM_ROWS(U_) \
+  launch_rows_dyn<TW, TG, VPL, U_>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, st)
+      if constexpr (VPL <= 2 && NV == 1) {
+        if (u0 == 8) PKM_ROWS(8); else PKM_ROWS(4);
+      } else if constexpr (VPL <= 2) {
+        if (u0 == 8) PKM_ROWS(4); else PKM_ROWS(2);
+      } else if constexpr (VPL == 4 && NV == 1) {
+        PKM_ROWS(2);
       } else {
-        launch_rows_dyn<TW, 8, 1>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, st);
+        PKM_ROWS(1);
       }
+#undef PKM_ROWS
     }
     if (N > 0 && psw != nullptr)
       hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, svals,
                          (const float*)dsorted, nvalid, N, gpsw, pdt);
   } else {
     if (N > 0)
-      hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D, psw,
-                         pdt, (const TW*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
+      hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, TG, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D,
+                         psw, pdt, (const TG*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
                          (float*)nullptr);
     if (K == 0) return;
     const int rows_per_group = 4;
     const int64_t groups = cdiv(K, rows_per_group);
     const unsigned rb = (unsigned)cdiv(groups, groups_per_block);
     KernelSpan span("eb_bwd_rows", st);
-    hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, LPG, VPL>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, psw, pdt,
-                       (const TW*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW,
+    hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, TG, LPG, VPL>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, psw,
+                       pdt, (const TG*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW,
                        gpsw);
   }
 }
 
-template <typename TW>
+template <typename TW, typename TG = TW>
 static bool dispatch_reduce(bool prepare, const GroupCfg& c, const void* W, int64_t K, int64_t D, const void* psw, int pdt,
                             const void* g, int64_t L, const uint32_t* offs, const uint32_t* skeys,
                             const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l,
@@ -1265,7 +1283,7 @@ static bool dispatch_reduce(bool prepare, const GroupCfg& c, const void* W, int6
     if (prepare)                                                                                                  \
       launch_prepare<TW, LPG_, VPL_>(K, D, psw, pdt, L, offs, svals, nvalid, N, l, ws, st);                       \
     else                                                                                                          \
-      launch_reduce<TW, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, gpsw, st); \
+      launch_reduce<TW, TG, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, gpsw, st); \
     return true;                                                                                                  \
   }
   PKM_RED_CASE(64, 1)
@@ -1408,8 +1426,10 @@ extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t
                               bag_size, workspace, workspace_bytes, &c, &l);
   if (rc != PKM_OK) return rc;
   const int64_t N = bags * bag_size;
-  PKM_REQUIRE(grad_dtype == weight_dtype, PKM_ERR_UNSUPPORTED,
-              "pkm_eb_bwd: grad_out dtype %d differs from weight dtype %d", grad_dtype, weight_dtype);
+  const bool wide_grad = grad_dtype == PKM_DTYPE_F32 && weight_dtype != PKM_DTYPE_F32;
+  PKM_REQUIRE(grad_dtype == weight_dtype || wide_grad, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd: grad_out dtype %d with weight dtype %d (supported: the same dtype, or a float32 "
+              "grad_out for a 16-bit table)", grad_dtype, weight_dtype);
   PKM_REQUIRE(grad_weight != nullptr || num_rows == 0, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_weight");
   PKM_REQUIRE(N == 0 || grad_out != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd: null grad_out");
   PKM_REQUIRE(psw == nullptr || N == 0 || (grad_psw != nullptr && (weight != nullptr || num_rows == 0)),
@@ -1423,15 +1443,16 @@ extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t
   const int64_t K = num_rows;
   // 4-5. heavy-row chunk partials, then every row once, then the psw-gradients to their positions
   bool ok;
+#define PKM_REDUCE(TW_, TG_)                                                                                    \
+  dispatch_reduce<TW_, TG_>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys, v.vals, \
+                            v.nvalid, N, l, ws, grad_weight, gpsw, st)
   if (weight_dtype == PKM_DTYPE_F32)
-    ok = dispatch_reduce<float>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys, v.vals,
-                                v.nvalid, N, l, ws, grad_weight, gpsw, st);
+    ok = PKM_REDUCE(float, float);
   else if (weight_dtype == PKM_DTYPE_BF16)
-    ok = dispatch_reduce<bf16_t>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys,
-                                 v.vals, v.nvalid, N, l, ws, grad_weight, gpsw, st);
+    ok = wide_grad ? PKM_REDUCE(bf16_t, float) : PKM_REDUCE(bf16_t, bf16_t);
   else
-    ok = dispatch_reduce<f16_t>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys,
-                                v.vals, v.nvalid, N, l, ws, grad_weight, gpsw, st);
+    ok = wide_grad ? PKM_REDUCE(f16_t, float) : PKM_REDUCE(f16_t, f16_t);
+#undef PKM_REDUCE
   PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
   if (N > 0 && gpsw != nullptr)
     hipLaunchKernelGGL(zero_invalid_gpsw_kernel, dim3(64), dim3(256), 0, st, (const uint32_t*)v.invalid, gpsw,
@@ -1443,8 +1464,10 @@ extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int
                           const void* psw, int psw_dtype, const void* grad_out, int grad_dtype, int64_t bags,
                           int64_t bag_size, void* grad_weight, void* grad_psw, void* workspace,
                           size_t workspace_bytes, void* stream) {
-  PKM_REQUIRE(grad_dtype == weight_dtype, PKM_ERR_UNSUPPORTED,
-              "pkm_eb_bwd: grad_out dtype %d differs from weight dtype %d", grad_dtype, weight_dtype);
+  PKM_REQUIRE(grad_dtype == weight_dtype || (grad_dtype == PKM_DTYPE_F32 && valid_dt(weight_dtype)),
+              PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd: grad_out dtype %d with weight dtype %d (supported: the same dtype, or a float32 "
+              "grad_out for a 16-bit table)", grad_dtype, weight_dtype);
   const int rc = pkm_eb_bwd_prepare(num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags, bag_size, workspace,
                                     workspace_bytes, stream);
   if (rc != PKM_OK) return rc;

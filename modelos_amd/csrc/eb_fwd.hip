@@ -18,6 +18,9 @@
 // DOT = true is the double backward (fwpkm/xformer_embeddingbag_grad_wrapper.py:55-74):
 // the same gather over gbar, plus d_a[b, j] = <gbar[idx[b, j]], g[b]>, a dot
 // product against the bag's upstream gradient that the group holds in registers.
+// The upstream gradient g and the gathered sum (d_grad_out) are of type TG:
+// the table's type, or float32 beside a 16-bit gbar (read in its own dtype,
+// float32 arithmetic as the reference's type promotion gives).
 #include "pkm_common.h"
 
 namespace pkm {
@@ -27,13 +30,15 @@ struct FwdUnroll {
   static constexpr int U = VPL >= 8 ? 2 : (VPL >= 4 ? 4 : 8);
 };
 
-template <typename TW, int LPG, int VPL, bool DOT>
+template <typename TW, typename TG, int LPG, int VPL, bool DOT>
 __global__ __launch_bounds__(256) void eb_fwd_kernel(const TW* __restrict__ W, int64_t K, int64_t D,
                                                      const int64_t* __restrict__ idx,
                                                      const void* __restrict__ psw, int pdt, int64_t B,
-                                                     int64_t L, int64_t S, TW* __restrict__ out,
-                                                     const TW* __restrict__ g, void* __restrict__ dot_out,
+                                                     int64_t L, int64_t S, TG* __restrict__ out,
+                                                     const TG* __restrict__ g, void* __restrict__ dot_out,
                                                      int ddt) {
+  using GT = GradTraits<TW, TG>;
+  constexpr int NV = GT::NV;
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int GPW = 64 / LPG;
   constexpr int NE = VPL * EPV;
@@ -54,9 +59,14 @@ __global__ __launch_bounds__(256) void eb_fwd_kernel(const TW* __restrict__ W, i
 
   float gv[DOT ? NE : 1];
   if constexpr (DOT) {
-    const TW* grow = g + b * D + col0;
+    const TG* grow = g + b * D + col0;
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(ld16(grow + v * VSTRIDE), gv + v * EPV);
+    for (int v = 0; v < VPL; ++v) {
+      uint4 raw[NV];
+#pragma unroll
+      for (int h = 0; h < NV; ++h) raw[h] = ld16(grow + v * VSTRIDE + h * (EPV / NV));
+      GT::unpack(raw, gv + v * EPV);
+    }
   }
 
   const int64_t pbase = b * L;
@@ -112,9 +122,14 @@ __global__ __launch_bounds__(256) void eb_fwd_kernel(const TW* __restrict__ W, i
     }
   }
 
-  TW* orow = out + b * D + col0;
+  TG* orow = out + b * D + col0;
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) st16(orow + v * VSTRIDE, VecTraits<TW>::pack(acc + v * EPV));
+  for (int v = 0; v < VPL; ++v) {
+    uint4 raw[NV];
+    GT::pack(acc + v * EPV, raw);
+#pragma unroll
+    for (int h = 0; h < NV; ++h) st16(orow + v * VSTRIDE + h * (EPV / NV), raw[h]);
+  }
 }
 
 // Fallback for a row length that is not a multiple of the 16-byte vector:
@@ -190,7 +205,7 @@ bool choose_group_cfg(int64_t D, int epv, bool single_slice, GroupCfg* c) {
 
 int elem_size(int dt) { return dt == PKM_DTYPE_F32 ? 4 : 2; }
 
-template <typename TW, int LPG, int VPL, bool DOT>
+template <typename TW, typename TG, int LPG, int VPL, bool DOT>
 static void launch_fwd(const void* W, int64_t K, int64_t D, const int64_t* idx, const void* psw, int pdt,
                        int64_t B, int64_t L, int64_t S, void* out, const void* g, void* dot_out, int ddt,
                        hipStream_t stream) {
@@ -199,17 +214,17 @@ static void launch_fwd(const void* W, int64_t K, int64_t D, const int64_t* idx, 
   const int64_t per_block = 4 * GPW;
   const unsigned blocks = (unsigned)((tasks + per_block - 1) / per_block);
   KernelSpan span(DOT ? "eb_bwd2" : "eb_fwd", stream);
-  hipLaunchKernelGGL((eb_fwd_kernel<TW, LPG, VPL, DOT>), dim3(blocks), dim3(256), 0, stream, (const TW*)W, K, D,
-                     idx, psw, pdt, B, L, S, (TW*)out, (const TW*)g, dot_out, ddt);
+  hipLaunchKernelGGL((eb_fwd_kernel<TW, TG, LPG, VPL, DOT>), dim3(blocks), dim3(256), 0, stream, (const TW*)W, K, D,
+                     idx, psw, pdt, B, L, S, (TG*)out, (const TG*)g, dot_out, ddt);
 }
 
-template <typename TW, bool DOT>
+template <typename TW, bool DOT, typename TG = TW>
 static bool dispatch_fwd(const GroupCfg& c, const void* W, int64_t K, int64_t D, const int64_t* idx,
                          const void* psw, int pdt, int64_t B, int64_t L, void* out, const void* g,
                          void* dot_out, int ddt, hipStream_t stream) {
 #define PKM_FWD_CASE(LPG_, VPL_)                                                                      \
   if (c.lpg == LPG_ && c.vpl == VPL_) {                                                               \
-    launch_fwd<TW, LPG_, VPL_, DOT>(W, K, D, idx, psw, pdt, B, L, c.slices, out, g, dot_out, ddt, stream); \
+    launch_fwd<TW, TG, LPG_, VPL_, DOT>(W, K, D, idx, psw, pdt, B, L, c.slices, out, g, dot_out, ddt, stream); \
     return true;                                                                                      \
   }
   PKM_FWD_CASE(64, 1)
@@ -282,8 +297,10 @@ extern "C" int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int 
                            const void* a, int a_dtype, const void* grad_out, int grad_dtype, int64_t bags,
                            int64_t bag_size, void* d_grad_out, void* d_a, void* stream) {
   PKM_REQUIRE(valid_dtype(gbar_dtype), PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd2: bad gbar dtype %d", gbar_dtype);
-  PKM_REQUIRE(grad_dtype == gbar_dtype, PKM_ERR_UNSUPPORTED,
-              "pkm_eb_bwd2: grad_out dtype %d differs from gbar dtype %d", grad_dtype, gbar_dtype);
+  const bool wide_grad = grad_dtype == PKM_DTYPE_F32 && gbar_dtype != PKM_DTYPE_F32;
+  PKM_REQUIRE(grad_dtype == gbar_dtype || wide_grad, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd2: grad_out dtype %d with gbar dtype %d (supported: the same dtype, or a float32 "
+              "grad_out for a 16-bit gbar)", grad_dtype, gbar_dtype);
   PKM_REQUIRE(a_dtype == PKM_DTYPE_NONE ? a == nullptr : (valid_dtype(a_dtype) && (a != nullptr || bags * bag_size == 0)), PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd2: a pointer / dtype %d mismatch", a_dtype);
   PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
@@ -301,14 +318,15 @@ extern "C" int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int 
               (long long)dim, epv_of(gbar_dtype));
   hipStream_t st = (hipStream_t)stream;
   void* dot = a != nullptr ? d_a : nullptr;
+#define PKM_BWD2(TW_, TG_)                                                                                        \
+  dispatch_fwd<TW_, true, TG_>(c, gbar, num_rows, dim, indices, a, a_dtype, bags, bag_size, d_grad_out, grad_out, dot, \
+                               a_dtype, st)
   if (gbar_dtype == PKM_DTYPE_F32)
-    dispatch_fwd<float, true>(c, gbar, num_rows, dim, indices, a, a_dtype, bags, bag_size, d_grad_out, grad_out,
-                              dot, a_dtype, st);
+    PKM_BWD2(float, float);
   else if (gbar_dtype == PKM_DTYPE_BF16)
-    dispatch_fwd<bf16_t, true>(c, gbar, num_rows, dim, indices, a, a_dtype, bags, bag_size, d_grad_out, grad_out,
-                               dot, a_dtype, st);
+    wide_grad ? PKM_BWD2(bf16_t, float) : PKM_BWD2(bf16_t, bf16_t);
   else
-    dispatch_fwd<f16_t, true>(c, gbar, num_rows, dim, indices, a, a_dtype, bags, bag_size, d_grad_out, grad_out,
-                              dot, a_dtype, st);
+    wide_grad ? PKM_BWD2(f16_t, float) : PKM_BWD2(f16_t, f16_t);
+#undef PKM_BWD2
   return pkm_check_launch("pkm_eb_bwd2");
 }

@@ -155,6 +155,48 @@ __device__ __forceinline__ float vec_dot<f16_t>(const uint4& a, const uint4& b, 
   return dot2_f16(a.w, b.w, d);
 }
 
+// ---------------------------------------------------------------------------
+// A gradient read in its own dtype TG beside a table of dtype TW: one slot
+// holds the EPV elements that one 16-byte vector of the table holds, in NV
+// 16-byte loads (1 when TG is TW, 2 for a float32 gradient of a 16-bit table).
+// ---------------------------------------------------------------------------
+template <typename TW, typename TG>
+struct GradTraits {
+  static constexpr int EPV = VecTraits<TW>::EPV;
+  static constexpr int NV = EPV * (int)sizeof(TG) / 16;
+  static_assert(NV == 1 || NV == 2, "a gradient slot is one or two 16-byte vectors");
+  static __device__ __forceinline__ void unpack(const uint4* v, float* f) {
+    if constexpr (NV == 1) {
+      VecTraits<TG>::unpack(v[0], f);
+    } else {
+      VecTraits<float>::unpack(v[0], f);
+      VecTraits<float>::unpack(v[1], f + 4);
+    }
+  }
+  static __device__ __forceinline__ void pack(const float* f, uint4* v) {
+    if constexpr (NV == 1) {
+      v[0] = VecTraits<TG>::pack(f);
+    } else {
+      v[0] = VecTraits<float>::pack(f);
+      v[1] = VecTraits<float>::pack(f + 4);
+    }
+  }
+  // d + <w, g> over one slot: the packed dot instructions when both are of
+  // one type, float32 products of the widened table elements otherwise
+  static __device__ __forceinline__ float dot(const uint4& w, const uint4* g, float d) {
+    if constexpr (NV == 1) {
+      return vec_dot<TW>(w, g[0], d);
+    } else {
+      float wf[EPV], gf[EPV];
+      VecTraits<TW>::unpack(w, wf);
+      unpack(g, gf);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) d = __builtin_fmaf(wf[e], gf[e], d);
+      return d;
+    }
+  }
+};
+
 __device__ __forceinline__ uint4 ld16(const void* p) { return *(const uint4*)p; }
 __device__ __forceinline__ void st16(void* p, const uint4& v) { *(uint4*)p = v; }
 // Streaming store for write-once outputs (dense weight gradient).

@@ -40,6 +40,17 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _grad_in_own_dtype(grad: torch.Tensor, table_dtype: torch.dtype) -> torch.Tensor:
+    """The upstream gradient as the kernels read it: in its own dtype when
+    that is the table's or float32 (a float32 gradient of a 16-bit table is
+    read as float32, as the reference's kernels widen it,
+    pkm/xformer_embeddingbag.py:322); any other dtype as float32 (exact for
+    the 16-bit types)."""
+    if grad.dtype == table_dtype or grad.dtype == torch.float32:
+        return grad
+    return grad.float()
+
+
 def _check_bag_inputs(indices: torch.Tensor, table: torch.Tensor, psw: Optional[torch.Tensor], fn: str) -> None:
     if indices.dtype != torch.long:
         raise TypeError(f"{fn}: indices must be int64 (torch.long), got {indices.dtype}")
@@ -171,7 +182,7 @@ def eb_backward(
     indices = indices.contiguous()
     weight = _aligned(weight)
     psw = per_sample_weights.contiguous() if per_sample_weights is not None else None
-    grad_output = _aligned(grad_output.to(weight.dtype))
+    grad_output = _aligned(_grad_in_own_dtype(grad_output, weight.dtype))
     grad_weight = torch.empty_like(weight, memory_format=torch.contiguous_format)
     grad_psw = torch.empty_like(psw, memory_format=torch.contiguous_format) if psw is not None else None
     args = (
@@ -219,20 +230,25 @@ def eb_double_backward(
         raise ValueError(f"eb_double_backward: grad_output shape {tuple(grad_output.shape)} != {(B, D)}")
     indices = indices.contiguous()
     out_dtype = grad_output.dtype
-    g_bar = _aligned(g_bar.to(out_dtype))
-    grad_output = _aligned(grad_output)
+    # g_bar [K, D] is read in its own dtype (no copy of it); grad_output [B, D] in its own dtype when
+    # that is g_bar's or float32, else as float32 (the reference's type promotion computes in the
+    # wider type; autograd hands the result back in grad_output's dtype)
+    g_bar = _aligned(g_bar)
+    g = _aligned(_grad_in_own_dtype(grad_output, g_bar.dtype))
+    if g_bar.dtype == torch.float32 and g.dtype != torch.float32:
+        g = g.float()
     a = a.contiguous() if a is not None else None
-    d_grad_output = torch.empty((B, D), dtype=out_dtype, device=dev)
+    d_grad_output = torch.empty((B, D), dtype=g.dtype, device=dev)
     d_a = torch.empty_like(a, memory_format=torch.contiguous_format) if a is not None else None
     _lib.call(
         "pkm_eb_bwd2",
         _lib.ptr(g_bar), K, D, _lib.dtype_code(g_bar),
         _lib.ptr(indices), _lib.ptr(a), _lib.dtype_code(a),
-        _lib.ptr(grad_output), _lib.dtype_code(grad_output),
+        _lib.ptr(g), _lib.dtype_code(g),
         B, L,
         _lib.ptr(d_grad_output), _lib.ptr(d_a), _lib.stream_of(dev),
     )
-    return d_grad_output, d_a
+    return d_grad_output.to(out_dtype), d_a
 
 
 def count_invalid_indices(indices: torch.Tensor, num_rows: int) -> int:

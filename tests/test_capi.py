@@ -63,8 +63,8 @@ def test_invalid_arguments_return_status(lib):
     assert st == 1
     # zero bags: nothing to do, no kernel
     assert lib.pkm_eb_fwd(None, 10, 8, 1, None, None, -1, 0, 2, None, None) == 0
-    # backward: grad dtype must equal weight dtype
-    st = lib.pkm_eb_bwd(None, 10, 8, 1, None, None, -1, None, 0, 4, 2, None, None, None, 0, None)
+    # backward: the gradient must be of the weight's dtype or float32 (a bf16 gradient of a float32 table)
+    st = lib.pkm_eb_bwd(None, 10, 8, 0, None, None, -1, None, 1, 4, 2, None, None, None, 0, None)
     assert st == 2
     # backward: unsupported row length for the dot-product kernels
     st = lib.pkm_eb_bwd(
@@ -78,8 +78,8 @@ def test_invalid_arguments_return_status(lib):
         ctypes.c_void_p(16), None, ctypes.c_void_p(256), 16, None,
     )
     assert st == 3
-    # double backward: dtype mismatch
-    st = lib.pkm_eb_bwd2(None, 10, 8, 1, None, None, -1, None, 0, 4, 2, None, None, None)
+    # double backward: a bf16 upstream gradient beside a float32 gbar
+    st = lib.pkm_eb_bwd2(None, 10, 8, 0, None, None, -1, None, 1, 4, 2, None, None, None)
     assert st == 2
 
 
