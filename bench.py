@@ -22,12 +22,14 @@ autograd) timed on this host's cores on a bounded sample of the same workload.
 The default run also reports, under extra keys, the standalone embedding bag
 ("eb_standalone"), the fast-weight PKM layer in float32 and bfloat16
 ("fwpkm"), the CPU parity configuration's forward ("cpu_parity_config"),
-each with its CPU baseline, and the layer step after a 512 MB cache flush
-("cache_flush"). "--workload model" times a Qwen3-0.6B-shaped decoder train
-step with two PKM layers.
+each with its CPU baseline, the layer step after a 512 MB cache flush
+("cache_flush"), the large-memory stress shape (2^22 slots, 16 GiB table,
+Zipf-skewed lookups; "stress") and a Qwen3-0.6B-shaped decoder train step
+with two PKM layers (3 steps; "model_step"). "--workload model" / "stress"
+time those alone.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
-                       [--workload layer|eb|fwupdate|fwpkm|model] [--no-cpu-baseline] [--no-extras]
+                       [--workload layer|eb|fwupdate|fwpkm|model|stress] [--no-cpu-baseline] [--no-extras]
 """
 from __future__ import annotations
 
@@ -780,6 +782,118 @@ def cpu_parity_config(args, dev, budget_s=20.0):
 
 
 # ---------------------------------------------------------------------------
+# Large-memory stress: 4,194,304 slots, 16 GiB bf16 value table, Zipf-skewed lookups
+# ---------------------------------------------------------------------------
+STRESS = dict(B=4, T=4096, C=2048, H=16, n=2048, k=512, knn=64, D=2048)
+
+
+def run_stress(args, dev, steps=3, warmup=1):
+    """HashingMemory fwd+bwd at the large-memory stress shape: x [4, 4096,
+    2048] ~ N(0,1), 16 heads, 2048 keys per half (2^22 slots), k_dim 512,
+    knn 64, value dim 2048 (16 GiB bf16 table), RMSNorm query, bf16. The
+    sub-key scores carry a Zipf(1.1) pre-bias realised through the module's
+    own parameters: in every (head, half) one query coordinate has a zero
+    weight row and bias 1, and the matching key coordinate is
+    -1.1 * ln(rank + 1) * 0.5 over a seeded permutation of the sub-keys, so a
+    few value rows collect thousands of lookups (the backward's heavy-row
+    path). Reported: step time, the gather's rate on per-lookup and on
+    distinct-row bytes, the value backward's rate, the scoring's MFMA rate and
+    the lookup skew. Not graded against the bars (a contention stress)."""
+    import math
+
+    import torch
+
+    from modelos_amd import _lib
+    from modelos_amd.pkm.memory import HashingMemory
+
+    c = STRESS
+    B, T, C, H, n, k, knn, D = c["B"], c["T"], c["C"], c["H"], c["n"], c["k"], c["knn"], c["D"]
+    tokens, half = B * T, k // 2
+    torch.manual_seed(0)
+    with torch.device(dev):
+        mem = HashingMemory(input_dim=C, output_dim=C, mem_k_dim=k, mem_v_dim=D, mem_heads=H, mem_knn=knn,
+                            mem_n_keys=n, mem_share_values=False, mem_query_rmsnorm=True)
+        mem.reset_parameters()
+    gen = torch.Generator(device=dev).manual_seed(5)
+    with torch.no_grad():
+        lin = mem.query_proj.query_mlps[0]
+        cols = torch.tensor([h * k + cc * half for h in range(H) for cc in range(2)], device=dev)
+        lin.weight[cols] = 0.0
+        lin.bias.zero_()
+        lin.bias[cols] = 1.0
+        rank = torch.argsort(torch.rand((2 * H, n), generator=gen, device=dev), dim=1).float()
+        mem.keys.view(2 * H, n, half)[:, :, 0] = -1.1 * torch.log(rank + 1.0) * 0.5
+    mem = mem.to(torch.bfloat16).train()
+    x = torch.randn((B, T, C), generator=gen, device=dev).to(torch.bfloat16).requires_grad_(True)
+    dout = torch.randn((B, T, C), generator=gen, device=dev).to(torch.bfloat16)
+    log(f"stress ready: tokens={tokens} heads={H} n_keys={n} (slots {n * n}) knn={knn} v_dim={D}")
+
+    def step():
+        mem.zero_grad(set_to_none=True)
+        x.grad = None
+        out, idx = mem(x)
+        out.backward(dout)
+        return idx
+
+    for _ in range(warmup):
+        idx = step()
+    torch.cuda.synchronize()
+    flat = idx.reshape(-1)
+    counts = torch.bincount(flat, minlength=n * n)
+    U, top = int((counts > 0).sum()), int(counts.max())
+    heavy = int((counts > 256).sum())
+    del flat, counts
+    ms_per_step, step_ms, calls, ktimer = timed_steps(step, steps)
+
+    def med(key):
+        v = sorted(calls.get(key, []))
+        return v[len(v) // 2] if v else None
+
+    L = H * knn
+    N = tokens * L
+    a_fwd, a_bwd = eb_algorithmic_bytes(tokens, L, n * n, D, U)
+    a_fwd_u = U * D * 2 + N * (8 + 2) + tokens * D * 2  # each distinct row once
+    fwd_ms, bwd_ms = med(("pkm_eb_fwd", (n * n, D))), med(("pkm_eb_bwd", (n * n, D)))
+    sc_ms = med(("pkm_score_topk", (tokens, H, n, half)))
+    rows = ktimer.ms("eb_bwd_rows")
+    rows_ms = sorted(rows)[len(rows) // 2] if rows else None
+    log(f"stress: {ms_per_step:.3f} ms/step; gather {fwd_ms:.3f} ms, value backward {bwd_ms:.3f} ms, "
+        f"scoring {sc_ms:.3f} ms; U={U}, hottest row {top} lookups, {heavy} rows over 256")
+
+    def rate(work, ms, peak):
+        if ms is None:
+            return None
+        r = work / (ms * 1e-3) / (1e12 if peak == MFMA_BF16_PEAK_TFLOPS else 1e9)
+        return {"ms": round(ms, 4), "achieved": round(r, 2), "frac": round(r / peak, 4)}
+
+    return {
+        "metric": "large-memory stress: PKM layer fwd+bwd tokens/sec, 2^22 slots, 16 GiB bf16 table, Zipf lookups",
+        "value": round(tokens / (ms_per_step * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms_per_step, 4),
+        "steps": steps, "warmup": warmup, "dtype": "bf16",
+        "data": "synthetic (N(0,1) input and upstream gradient; Zipf(1.1) pre-bias through a reserved query "
+                "coordinate and a log-rank key coordinate per (head, half))",
+        "config": {"workload": "HashingMemory fwd+bwd (RMSNorm query, swilu), 16 GiB bf16 value table",
+                   "tokens": tokens, "batch": B, "seq_len": T, "input_dim": C, "heads": H, "n_keys": n,
+                   "k_dim": k, "knn": knn, "v_dim": D},
+        "lookups": {"total": N, "distinct_rows": U, "hottest_row": top, "rows_over_256": heavy},
+        "gather_per_lookup": dict(rate(a_fwd, fwd_ms, HBM_PEAK_GBS) or {}, unit="GB/s", work=a_fwd,
+                                  note="every lookup reads its row (N*D*2 + N*10 + B*D*2 bytes)"),
+        "gather_distinct_rows": dict(rate(a_fwd_u, fwd_ms, HBM_PEAK_GBS) or {}, unit="GB/s", work=a_fwd_u,
+                                     note="each distinct row once (U*D*2 + N*10 + B*D*2): the HBM floor "
+                                          "when the hot rows are served from the caches"),
+        "value_backward": dict(rate(a_bwd, bwd_ms, HBM_PEAK_GBS) or {}, unit="GB/s", work=a_bwd,
+                               row_reduction_ms=round(rows_ms, 4) if rows_ms else None,
+                               note="entry point: sort, heavy-row chunk partials, row reduction, scatter"),
+        "scoring": dict(rate(score_flops(tokens, H, n, k), sc_ms, MFMA_BF16_PEAK_TFLOPS) or {}, unit="TFLOP/s",
+                        work=score_flops(tokens, H, n, k),
+                        note="entry point (scoring + per-half top-64 tile kernel, cartesian top-64)"),
+        "cpu_baseline": None,
+        "cpu_baseline_note": "not timed: the 16 GiB table and 268 M lookups per step are beyond the bounded "
+                             "CPU sample; the CPU comparison is the layer benchmark's",
+    }
+
+
+# ---------------------------------------------------------------------------
 # Model step: a Qwen3-0.6B-shaped decoder with PKM layers
 # ---------------------------------------------------------------------------
 def run_model(args, dev):
@@ -856,7 +970,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate", "fwpkm", "model"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "eb", "fwupdate", "fwpkm", "model", "stress"], default="layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="layer workload: skip the extra measurements (standalone embedding bag, fast-weight "
@@ -888,7 +1002,7 @@ def main():
         del src, dst
         log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
     runs = {"layer": run_layer, "eb": run_eb, "fwupdate": run_fwupdate, "fwpkm": run_fwpkm_workload,
-            "model": run_model}
+            "model": run_model, "stress": lambda a, d: run_stress(a, d, a.steps, a.warmup)}
     res = runs[args.workload](args, dev)
     if args.workload == "layer" and not args.no_extras:
         # the other benchmark configurations, reported beside the headline (not part of `value`)
@@ -904,6 +1018,16 @@ def main():
         if not args.no_cpu_baseline:
             log("extra: CPU parity configuration ...")
             res["cpu_parity_config"] = cpu_parity_config(args, dev)
+            torch.cuda.empty_cache()
+        log("extra: large-memory stress ...")
+        res["stress"] = run_stress(args, dev)
+        torch.cuda.empty_cache()
+        log("extra: Qwen3-0.6B-shaped model step ...")
+        margs = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 1})
+        m = run_model(margs, dev)
+        res["model_step"] = {kk: m[kk] for kk in ("metric", "value", "unit", "ms_per_step", "steps", "warmup",
+                                                   "config")}
+        torch.cuda.empty_cache()
     print(json.dumps(res), flush=True)
 
 
