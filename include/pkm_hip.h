@@ -298,10 +298,61 @@ int pkm_fw_sgd_update(const void* values, const void* grad, const int64_t* count
  *   d_values      = dtype(d_new_values + dtype(weight_decay * x))
  *   d             = (grad_clip ? x * [-1 <= scaled_grad <= 1] : x) (+ d_scaled_grad, when not NULL)
  *   d_grad        = dtype(dtype(d / dtype(max(counts, 1))) * scale)
+ * d_grad may be NULL: then only d_values is written.
  */
 int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_scaled_grad, const void* scaled_grad,
                           const int64_t* counts, int64_t num_rows, int64_t dim, int dtype, float scale, float lr,
                           float weight_decay, int grad_clip, void* d_values, void* d_grad, void* stream);
+
+/*
+ * Value backward with the fast-weight SGD step in its epilogue: the reduction
+ * of pkm_eb_bwd (same workspace, same float32 sums in position order), where
+ * each table row, instead of its gradient row, gets the values step of FwPKM's
+ * inner update (dtype F32 or BF16 for values, grad_out and both outputs):
+ *   g                 = dtype(sum_{(b,j): indices[b,j]==r} psw[b,j] * grad_out[b,:])
+ *   scaled_grad[r, :] = dtype(dtype(g * scale) / dtype(max(cnt[r], 1)))    cnt = lookups of row r
+ *   c                 = grad_clip ? clamp(scaled_grad, -1, 1) : scaled_grad
+ *   new_values[r, :]  = dtype(values - dtype(lr * dtype(c + dtype(weight_decay * values))))
+ * with pkm_fw_sgd_update's rounding steps. Every row is written (untouched
+ * rows: g = 0). Optional outputs (NULL = not written): grad_psw as in
+ * pkm_eb_bwd; counts [num_rows] int32 = cnt; row_sumsq [num_rows] float32 =
+ * sum over the row of scaled_grad^2 (the squared norm of the scaled gradient
+ * is their sum).
+ *
+ * Replaces, for the values (fwpkm/fwpkm.py:333-365 with update_fw_param,
+ * 266-272), the table gradient of autograd.grad(mem_loss, values) through
+ * _XEmbeddingBagFn's backward (fwpkm/xformer_embeddingbag_grad_wrapper.py:118-
+ * 155) followed by the bincount-normalised SGD step: one pass over the table
+ * instead of a gradient write and a second pass.
+ */
+int pkm_eb_bwd_sgd(const void* values, int64_t num_rows, int64_t dim, int dtype, const int64_t* indices,
+                   const void* psw, int psw_dtype, const void* grad_out, int64_t bags, int64_t bag_size,
+                   float scale, float lr, float weight_decay, int grad_clip, void* new_values, void* scaled_grad,
+                   void* grad_psw, int32_t* counts, float* row_sumsq, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Double backward through pkm_eb_bwd_sgd's step: pkm_eb_bwd2 whose gathered
+ * rows are the gradient of the table gradient that autograd forms through the
+ * step from d_new_values (and d_scaled_grad, NULL = none), computed per
+ * gathered row (dtype F32 or BF16 for every tensor, counts int32 from
+ * pkm_eb_bwd_sgd):
+ *   x  = dtype(lr * -d_new_values[r])
+ *   d  = grad_clip ? x * [-1 <= scaled_grad[r] <= 1] : x     (+ d_scaled_grad[r], rounded)
+ *   gb = dtype(dtype(d / dtype(max(counts[r], 1))) * scale)
+ *   d_grad_out[b, :] = sum_j a[b, j] * gb[indices[b, j]]      [bags, dim]
+ *   d_a[b, j]        = <gb[indices[b, j]], grad_out[b, :]>    [bags, bag_size], a_dtype
+ * The values' own gradient (d_new_values, plus weight_decay's term) is the
+ * caller's (pkm_fw_sgd_update_bwd with d_grad NULL when weight_decay != 0).
+ *
+ * Replaces pkm_fw_sgd_update_bwd's d_grad followed by EmbeddingBagBW.backward
+ * (fwpkm/xformer_embeddingbag_grad_wrapper.py:42-74): the dense [K, D]
+ * gradient of the table gradient is not materialised.
+ */
+int pkm_eb_bwd2_sgd(const void* d_new_values, const void* d_scaled_grad, const void* scaled_grad,
+                    const int32_t* counts, int64_t num_rows, int64_t dim, int dtype, float scale, float lr,
+                    int grad_clip, const int64_t* indices, const void* a, int a_dtype, const void* grad_out,
+                    int64_t bags, int64_t bag_size, void* d_grad_out, void* d_a, void* stream);
 
 /* Workspace bytes pkm_column_sum needs for these sizes. */
 size_t pkm_column_sum_workspace_size(int64_t rows, int64_t cols);

@@ -124,6 +124,28 @@ SIGNATURES = {
             c_void_p, c_void_p, c_void_p,  # d_values, d_grad, stream
         ],
     ),
+    "pkm_eb_bwd_sgd": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64, c_int,  # values, num_rows, dim, dtype
+            c_void_p, c_void_p, c_int,  # indices, psw, psw_dtype
+            c_void_p, c_int64, c_int64,  # grad_out, bags, bag_size
+            c_float, c_float, c_float, c_int,  # scale, lr, weight_decay, grad_clip
+            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # new_values, scaled_grad, grad_psw, counts, row_sumsq
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+    "pkm_eb_bwd2_sgd": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_void_p,  # d_new_values, d_scaled_grad, scaled_grad, counts
+            c_int64, c_int64, c_int,  # num_rows, dim, dtype
+            c_float, c_float, c_int,  # scale, lr, grad_clip
+            c_void_p, c_void_p, c_int,  # indices, a, a_dtype
+            c_void_p, c_int64, c_int64,  # grad_out, bags, bag_size
+            c_void_p, c_void_p, c_void_p,  # d_grad_out, d_a, stream
+        ],
+    ),
     "pkm_softmax_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_softmax_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_column_sum_workspace_size": (c_size_t, [c_int64, c_int64]),
@@ -274,6 +296,8 @@ _SIZE_ARGS = {
     "pkm_eb_bwd_prepare": (0, 1),
     "pkm_eb_bwd_prepared": (1, 2),
     "pkm_eb_bwd2": (1, 2),
+    "pkm_eb_bwd_sgd": (1, 2),
+    "pkm_eb_bwd2_sgd": (4, 5),
     "pkm_score_topk": (2, 3, 4, 5),  # num_tokens, heads, n_keys, half
     "pkm_score_grad_sparse": (3, 4, 5, 6),  # num_tokens, heads, n_keys, half
     "pkm_rmsnorm_fwd": (2, 3),  # rows, dim

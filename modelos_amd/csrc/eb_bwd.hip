@@ -36,12 +36,83 @@
 // upstream gradient g (B x D, tens of MB) is re-read per occurrence from
 // L2 / Infinity Cache.
 #include <mutex>
+#include <type_traits>
 
 #include "pkm_common.h"
 
 namespace pkm {
 
 constexpr int kHeavyT = 256;  // chunk length and light/heavy row threshold
+
+// ---------------------------------------------------------------------------
+// The fast-weight SGD step in the reduction's epilogue (pkm_eb_bwd_sgd): a
+// row's float32 gradient sums become, instead of a table-gradient row, the
+// scaled gradient and the updated table row of FwPKM's values step
+// (fwpkm/fwpkm.py:351-365 with update_fw_param at 266-272, "sgd"):
+//   g   = T(acc)                                  (the table gradient's rounding)
+//   gs  = T(T(g * scale) / T(max(cnt, 1)))        cnt = the row's lookups (bincount)
+//   gc  = clip ? min(max(gs, -1), 1) : gs
+//   p'  = T(p - T(lr * T(gc + T(wd * p))))
+// every step rounded to T in the reference's order, no contraction. The row
+// of p is the table row the reduction reads anyway (for the psw-gradient
+// dots), so the step costs no extra table read and no gradient round trip.
+// ---------------------------------------------------------------------------
+struct SgdArgs {
+  void* new_values;   // [K, D], table dtype
+  void* scaled_grad;  // [K, D], table dtype
+  int32_t* counts;    // [K]: lookups per row, or NULL
+  float* row_sumsq;   // [K]: sum over the row of gs^2 (float32), or NULL
+  float scale, lr, wd;
+  int clip;
+};
+
+#pragma clang fp contract(off)
+// o_g = gs and o_p = p' of NE elements (acc: float32 sums, p: table
+// elements); returns the sum of gs^2 over them.
+template <typename TW, int NE>
+__device__ __forceinline__ float sgd_step(const float* acc, const float* p, uint32_t cnt, const SgdArgs& S,
+                                          float* o_g, float* o_p) {
+  const float cs = round_to<TW>(cnt == 0 ? 1.f : (float)cnt);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const float g = round_to<TW>(acc[e]);
+    const float gs = round_to<TW>(round_to<TW>(g * S.scale) / cs);
+    float gc = gs;
+    if (S.clip) gc = gc < -1.f ? -1.f : (gc > 1.f ? 1.f : gc);
+    const float wp = round_to<TW>(S.wd * p[e]);
+    const float dp = round_to<TW>(S.lr * round_to<TW>(gc + wp));
+    o_g[e] = gs;
+    o_p[e] = round_to<TW>(p[e] - dp);
+    ss = ss + gs * gs;
+  }
+  return ss;
+}
+#pragma clang fp contract(on)
+
+// The SGD epilogue of one row held by LPG lanes (the lane's VPL vectors at
+// element col0 + v * LPG * EPV): stores gs and p', and from the group's first
+// lane the row's count and sum of gs^2.
+template <typename TW, int LPG, int VPL>
+__device__ __forceinline__ void sgd_store_row(const float* acc, const float* p, uint32_t cnt, int64_t row, int64_t D,
+                                              int64_t col0, int glane, const SgdArgs& S) {
+  constexpr int EPV = VecTraits<TW>::EPV;
+  constexpr int NE = VPL * EPV;
+  float o_g[NE], o_p[NE];
+  float ss = sgd_step<TW, NE>(acc, p, cnt, S, o_g, o_p);
+  TW* grow = (TW*)S.scaled_grad + row * D + col0;
+  TW* prow = (TW*)S.new_values + row * D + col0;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    st16_nt(grow + v * LPG * EPV, VecTraits<TW>::pack(o_g + v * EPV));
+    st16_nt(prow + v * LPG * EPV, VecTraits<TW>::pack(o_p + v * EPV));
+  }
+  ss = group_sum<LPG>(ss);
+  if (glane == 0) {
+    if (S.row_sumsq != nullptr) S.row_sumsq[row] = ss;
+    if (S.counts != nullptr) S.counts[row] = (int32_t)cnt;
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Utilities
@@ -507,7 +578,7 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
   if (i_beg >= nv) return;
   const uint32_t i_end = (uint32_t)((int64_t)i_beg + kHeavyT < (int64_t)nv ? i_beg + kHeavyT : nv);
   const int64_t col0 = (int64_t)glane * EPV;
-  const bool want_dot = psw != nullptr;
+  const bool want_dot = psw != nullptr && (gpsw != nullptr || dsorted != nullptr);
   const uint32_t cand[2] = {skeys[i_beg], skeys[i_end - 1]};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -534,14 +605,15 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
 }
 
 // Generic rows kernel (lane groups smaller than a wave, small rows).
-template <typename TW, typename TG, int LPG, int VPL>
+template <typename TW, typename TG, int LPG, int VPL, bool SGD>
 __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__ W, int64_t K, int64_t D,
                                                           const void* __restrict__ psw, int pdt,
                                                           const TG* __restrict__ g, uint32_t L32,
                                                           const uint32_t* __restrict__ offs,
                                                           const uint32_t* __restrict__ svals,
                                                           const float* __restrict__ partials, int rows_per_group,
-                                                          TW* __restrict__ gW, void* __restrict__ gpsw) {
+                                                          TW* __restrict__ gW, void* __restrict__ gpsw,
+                                                          SgdArgs S) {
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   constexpr int GPW = 64 / LPG;
@@ -553,7 +625,7 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
   if (r0 >= K) return;
   const int64_t r1 = (r0 + rows_per_group < K) ? r0 + rows_per_group : K;
   const int64_t col0 = (int64_t)glane * EPV;
-  const bool want_dot = psw != nullptr;
+  const bool want_dot = gpsw != nullptr;
 
   for (int64_t r = r0; r < r1; ++r) {
     const uint32_t beg = offs[r], end = offs[r + 1];
@@ -568,9 +640,15 @@ __global__ __launch_bounds__(256) void eb_bwd_rows_kernel(const TW* __restrict__
       if (want_dot) load_row_f32<TW, LPG, VPL>(W + r * D, col0, wv);
       reduce_occurrences<TW, TG, LPG, VPL>(beg, end, svals, psw, pdt, g, D, L32, col0, glane, wv, want_dot, gpsw, acc);
     }
-    TW* orow = gW + r * D + col0;
+    if constexpr (SGD) {
+      float p[NE];
+      load_row_f32<TW, LPG, VPL>(W + r * D, col0, p);
+      sgd_store_row<TW, LPG, VPL>(acc, p, cnt, r, D, col0, glane, S);
+    } else {
+      TW* orow = gW + r * D + col0;
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) st16_nt(orow + v * VSTRIDE, VecTraits<TW>::pack(acc + v * EPV));
+      for (int v = 0; v < VPL; ++v) st16_nt(orow + v * VSTRIDE, VecTraits<TW>::pack(acc + v * EPV));
+    }
   }
 }
 
@@ -678,11 +756,12 @@ __device__ __forceinline__ float accumulate_slots(const RowData<VPL, U, GradTrai
 // ends) and reduces it U occurrences at a time, in order, the next chunk's
 // metadata and gradient rows in flight while the current chunk is reduced.
 // One wave per row keeps each row's sums in position order.
-template <typename TW, typename TG, int VPL, int U>
+template <typename TW, typename TG, int VPL, int U, bool SGD>
 __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
     const TW* __restrict__ W, int64_t D, int want_dot, const TG* __restrict__ g, const uint32_t* __restrict__ offs,
     const uint2* __restrict__ meta, const TW* __restrict__ zrow, TW* __restrict__ gW, float* __restrict__ dsorted,
-    uint32_t dummy_slot, const uint32_t* __restrict__ long_rows, const uint32_t* __restrict__ long_count) {
+    uint32_t dummy_slot, const uint32_t* __restrict__ long_rows, const uint32_t* __restrict__ long_count,
+    SgdArgs S) {
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   constexpr int NV = GradTraits<TW, TG>::NV;
@@ -713,7 +792,7 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
   for (uint32_t t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); t < n; t += nwaves) {
     const uint32_t r = (uint32_t)__builtin_amdgcn_readfirstlane((int)long_rows[t]);
     const uint32_t beg = offs[r], end = offs[r + 1];
-    const char* wrow = want_dot ? Wb + (uint64_t)r * rowbytes : zb;
+    const char* wrow = (want_dot || SGD) ? Wb + (uint64_t)r * rowbytes : zb;
     RowData<VPL, U, NV> DA, DB;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
@@ -738,9 +817,16 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
       if (s3 >= end) break;
       s = s3;
     }
-    char* orow = (char*)gW + (uint64_t)r * rowbytes;
+    if constexpr (SGD) {
+      float p[NE];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
+      for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(DA.wraw[v], p + v * EPV);
+      sgd_store_row<TW, 64, VPL>(acc, p, end - beg, r, D, (int64_t)lane * EPV, lane, S);
+    } else {
+      char* orow = (char*)gW + (uint64_t)r * rowbytes;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
+    }
   }
 }
 
@@ -829,12 +915,12 @@ __global__ __launch_bounds__(256) void list_long_rows_kernel(const uint32_t* __r
 template <typename TW, typename TG, int VPL>
 constexpr int kRowVecs = VPL * GradTraits<TW, TG>::NV;
 
-template <typename TW, typename TG, int VPL, int U>
+template <typename TW, typename TG, int VPL, int U, bool SGD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<TW, TG, VPL> == 1 && U <= 4) ? 5 : ((kRowVecs<TW, TG, VPL> == 1 || (kRowVecs<TW, TG, VPL> == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows_dyn_kernel(
     const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TG* __restrict__ g,
     const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
     const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
-    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk, uint32_t long_min) {
+    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk, uint32_t long_min, SgdArgs S) {
   static_assert(kDynRC * U <= 64, "a chunk's metadata must fit one load per lane");
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
@@ -890,7 +976,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
     }
   };
   auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R) {
-    const char* wrow = (want_dot && M.nh) ? Wb + (uint64_t)row * rowbytes : zb;
+    // the SGD epilogue reads every table row (empty ones included); tail rows past K read the zero row
+    const bool read_w = SGD ? row < K32 : (want_dot && M.nh);
+    const char* wrow = read_w ? Wb + (uint64_t)row * rowbytes : zb;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);  // read once: keep L2 for g
 #pragma unroll
@@ -909,7 +997,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
   // lookups, crowded when lookups pile onto few rows) go to the long-row
   // kernel, which spreads them over all XCDs.
   auto reduce_long = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R, float* acc) {
-    const char* wrow = want_dot ? Wb + (uint64_t)row * rowbytes : zb;
+    const char* wrow = (want_dot || SGD) ? Wb + (uint64_t)row * rowbytes : zb;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);
     for (uint32_t s = M.beg; s < M.end; s += U) {
@@ -940,9 +1028,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
       if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < M.nh ? M.beg + dot_slot : dummy_slot] = mydot;
     }
     if (M.end - M.beg > (uint32_t)kHeavyT) add_heavy_partials<64, VPL, EPV>(M.beg, M.end, partials, D, col0, acc);
-    char* orow = row < K32 ? (char*)gW + (uint64_t)row * rowbytes : (char*)dummy_row;
+    if constexpr (SGD) {
+      if (row < K32) {
+        float p[NE];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
+        for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(R.wraw[v], p + v * EPV);
+        sgd_store_row<TW, 64, VPL>(acc, p, cnt, row, D, col0, lane, S);
+      }
+    } else {
+      char* orow = row < K32 ? (char*)gW + (uint64_t)row * rowbytes : (char*)dummy_row;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
+    }
   };
 
   // prologue: chunk 0's offsets and metadata, chunk 1's offsets, chunk 2's ticket
@@ -1168,11 +1265,11 @@ static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* l
 // The row reduction on the ticket schedule: the rows kernel, then the long
 // rows listed by prepare_rows_dyn. Each reduction clears its own ticket
 // counters first, so a prepared workspace can serve any number of reductions.
-template <typename TW, typename TG, int VPL, int U>
+template <typename TW, typename TG, int VPL, int U, bool SGD>
 static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
                             const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                             float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, uint32_t* tickets,
-                            uint32_t long_min, hipStream_t st) {
+                            uint32_t long_min, const SgdArgs& S, hipStream_t st) {
   const uint32_t* long_count = long_rows + K;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
                      (int64_t)kDynGroups * kDynSub * kCtrStride);
@@ -1183,14 +1280,14 @@ static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, c
   wgs = wgs < 1280 ? wgs : 1280;
   wgs = cdiv(wgs, kDynGroups * kDynSub) * kDynGroups * kDynSub;  // every counter gets workgroups
   KernelSpan span("eb_bwd_rows", st);
-  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, TG, VPL, U>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W, K,
-                     D, want_dot, (const TG*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW,
-                     dsorted, dummy_slot, tickets, blk, long_min);
+  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, TG, VPL, U, SGD>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W,
+                     K, D, want_dot, (const TG*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW,
+                     dsorted, dummy_slot, tickets, blk, long_min, S);
   const int64_t rb = cdiv(K, 4 * 64);
   const unsigned lb = (unsigned)(rb < 1024 ? rb : 1024);
-  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, TG, VPL, U>), dim3(lb), dim3(256), 0, st, (const TW*)W, D, want_dot,
-                     (const TG*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
-                     (const uint32_t*)long_rows, long_count);
+  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, TG, VPL, U, SGD>), dim3(lb), dim3(256), 0, st, (const TW*)W, D,
+                     want_dot, (const TG*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
+                     (const uint32_t*)long_rows, long_count, S);
 }
 
 // Everything of the backward that depends only on the lookups (run by
@@ -1214,10 +1311,11 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
   }
 }
 
-template <typename TW, typename TG, int LPG, int VPL>
+template <typename TW, typename TG, int LPG, int VPL, bool SGD>
 static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, int pdt, const void* g, int64_t L,
                           const uint32_t* offs, const uint32_t* skeys, const uint32_t* svals, const uint32_t* nvalid,
-                          int64_t N, const BwdLayout& l, char* ws, void* gW, void* gpsw, hipStream_t st) {
+                          int64_t N, const BwdLayout& l, char* ws, void* gW, void* gpsw, const SgdArgs& S,
+                          hipStream_t st) {
   constexpr int GPW = 64 / LPG;
   const int64_t groups_per_block = 4 * GPW;
   float* partials = (float*)(ws + l.partials);
@@ -1231,7 +1329,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
                          psw, pdt, (const TG*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
                          dsorted);
     if (K > 0) {
-      const int want_dot = psw != nullptr ? 1 : 0;
+      const int want_dot = gpsw != nullptr ? 1 : 0;
       // the prefetch depth the lists were prepared for (rows longer than twice it go to the
       // long-row kernel), halved when each gradient row is twice the table row's bytes
       const int u0 = rows_prefetch<VPL>(N, K);
@@ -1242,7 +1340,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       uint32_t* long_rows = (uint32_t*)(ws + l.long_rows);
       uint32_t* tickets = (uint32_t*)(ws + l.tickets);
 #define PKM_ROWS(U_) \
-  launch_rows_dyn<TW, TG, VPL, U_>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, st)
+  launch_rows_dyn<TW, TG, VPL, U_, SGD>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, S, st)
       if constexpr (VPL <= 2 && NV == 1) {
         if (u0 == 8) PKM_ROWS(8); else PKM_ROWS(4);
       } else if constexpr (VPL <= 2) {
@@ -1254,7 +1352,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       }
 #undef PKM_ROWS
     }
-    if (N > 0 && psw != nullptr)
+    if (N > 0 && gpsw != nullptr)
       hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, svals,
                          (const float*)dsorted, nvalid, N, gpsw, pdt);
   } else {
@@ -1267,23 +1365,34 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     const int64_t groups = cdiv(K, rows_per_group);
     const unsigned rb = (unsigned)cdiv(groups, groups_per_block);
     KernelSpan span("eb_bwd_rows", st);
-    hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, TG, LPG, VPL>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D, psw,
-                       pdt, (const TG*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW,
-                       gpsw);
+    hipLaunchKernelGGL((eb_bwd_rows_kernel<TW, TG, LPG, VPL, SGD>), dim3(rb), dim3(256), 0, st, (const TW*)W, K, D,
+                       psw, pdt, (const TG*)g, (uint32_t)L, offs, svals, (const float*)partials, rows_per_group, (TW*)gW,
+                       gpsw, S);
   }
 }
 
+// sgd != NULL: the reduction ends in the fast-weight SGD epilogue (SgdArgs)
+// instead of writing the table gradient; instantiated where TG is TW.
 template <typename TW, typename TG = TW>
 static bool dispatch_reduce(bool prepare, const GroupCfg& c, const void* W, int64_t K, int64_t D, const void* psw, int pdt,
                             const void* g, int64_t L, const uint32_t* offs, const uint32_t* skeys,
                             const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l,
-                            char* ws, void* gW, void* gpsw, hipStream_t st) {
+                            char* ws, void* gW, void* gpsw, hipStream_t st, const SgdArgs* sgd = nullptr) {
+  static const SgdArgs no_sgd = {};
 #define PKM_RED_CASE(LPG_, VPL_)                                                                                  \
   if (c.lpg == LPG_ && c.vpl == VPL_) {                                                                           \
-    if (prepare)                                                                                                  \
+    if (prepare) {                                                                                                \
       launch_prepare<TW, LPG_, VPL_>(K, D, psw, pdt, L, offs, svals, nvalid, N, l, ws, st);                       \
-    else                                                                                                          \
-      launch_reduce<TW, TG, LPG_, VPL_>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, gpsw, st); \
+    } else if (sgd == nullptr) {                                                                                  \
+      launch_reduce<TW, TG, LPG_, VPL_, false>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, \
+                                               gpsw, no_sgd, st);                                                 \
+    } else {                                                                                                      \
+      if constexpr (std::is_same<TW, TG>::value && !std::is_same<TW, f16_t>::value)                               \
+        launch_reduce<TW, TG, LPG_, VPL_, true>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws,    \
+                                                gW, gpsw, *sgd, st);                                              \
+      else                                                                                                        \
+        return false;                                                                                             \
+    }                                                                                                             \
     return true;                                                                                                  \
   }
   PKM_RED_CASE(64, 1)
@@ -1473,6 +1582,47 @@ extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int
   if (rc != PKM_OK) return rc;
   return pkm_eb_bwd_prepared(weight, num_rows, dim, weight_dtype, indices, psw, psw_dtype, grad_out, grad_dtype, bags,
                              bag_size, grad_weight, grad_psw, workspace, workspace_bytes, stream);
+}
+
+extern "C" int pkm_eb_bwd_sgd(const void* values, int64_t num_rows, int64_t dim, int dtype, const int64_t* indices,
+                              const void* psw, int psw_dtype, const void* grad_out, int64_t bags, int64_t bag_size,
+                              float scale, float lr, float weight_decay, int grad_clip, void* new_values,
+                              void* scaled_grad, void* grad_psw, int32_t* counts, float* row_sumsq, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd_sgd: dtype %d not supported (float32, bfloat16 are)", dtype);
+  GroupCfg c;
+  BwdLayout l;
+  int rc = eb_bwd_check("pkm_eb_bwd_sgd", num_rows, dim, dtype, indices, psw, psw_dtype, bags, bag_size, workspace,
+                        workspace_bytes, &c, &l);
+  if (rc != PKM_OK) return rc;
+  const int64_t N = bags * bag_size;
+  PKM_REQUIRE(num_rows == 0 || (values != nullptr && new_values != nullptr && scaled_grad != nullptr),
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd_sgd: null values / new_values / scaled_grad");
+  PKM_REQUIRE(N == 0 || grad_out != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd_sgd: null grad_out");
+  PKM_REQUIRE(grad_psw == nullptr || psw != nullptr, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd_sgd: grad_psw given without psw");
+  PKM_REQUIRE(((uintptr_t)values | (uintptr_t)grad_out | (uintptr_t)new_values | (uintptr_t)scaled_grad) % 16 == 0,
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd_sgd: values, grad_out and outputs must be 16-byte aligned");
+  rc = pkm_eb_bwd_prepare(num_rows, dim, dtype, indices, psw, psw_dtype, bags, bag_size, workspace, workspace_bytes,
+                          stream);
+  if (rc != PKM_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const SortedView v = sorted_view(l, ws);
+  const SgdArgs S = {new_values, scaled_grad, counts, row_sumsq, scale, lr, weight_decay, grad_clip};
+  bool ok;
+  if (dtype == PKM_DTYPE_F32)
+    ok = dispatch_reduce<float, float>(false, c, values, num_rows, dim, psw, psw_dtype, grad_out, bag_size, v.offs,
+                                       v.keys, v.vals, v.nvalid, N, l, ws, nullptr, grad_psw, st, &S);
+  else
+    ok = dispatch_reduce<bf16_t, bf16_t>(false, c, values, num_rows, dim, psw, psw_dtype, grad_out, bag_size, v.offs,
+                                         v.keys, v.vals, v.nvalid, N, l, ws, nullptr, grad_psw, st, &S);
+  PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd_sgd: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
+  if (N > 0 && grad_psw != nullptr)
+    hipLaunchKernelGGL(zero_invalid_gpsw_kernel, dim3(64), dim3(256), 0, st, (const uint32_t*)v.invalid, grad_psw,
+                       psw_dtype);
+  return pkm_check_launch("pkm_eb_bwd_sgd");
 }
 
 extern "C" int pkm_count_invalid_indices(const int64_t* indices, int64_t n, int64_t num_rows, int64_t* count_out,

@@ -25,18 +25,51 @@
 
 namespace pkm {
 
+// The double backward of the fast-weight values step (pkm_eb_bwd2_sgd): the
+// gathered rows are not a stored table gradient but the gradient that
+// autograd forms for it through the reference's step
+// p' = p - lr * (clip(gs) + wd * p), gs = g * scale / cnt (fwpkm/fwpkm.py:351-365,
+// 266-272), from the gradient of p' (dnew) and optionally of gs (dgs):
+//   x  = T(lr * -dnew)
+//   d  = clip ? (-1 <= gs <= 1 ? x : 0) : x      (+ dgs: d = T(d + dgs))
+//   gb = T(T(d / T(max(cnt, 1))) * scale)
+// computed row by row as the rows are gathered, so the dense [K, D] gradient
+// of the table gradient is never written.
+struct SgdBwdArgs {
+  const void* gs;         // [K, D] scaled gradient (read when clip)
+  const void* dgs;        // [K, D] its upstream gradient, or NULL
+  const int32_t* counts;  // [K] lookups per row
+  float scale, lr;
+  int clip;
+};
+
+#pragma clang fp contract(off)
+template <typename TW, int NE>
+__device__ __forceinline__ void sgd_bwd_row(float* f, uint32_t cnt, const float* fs, const float* fi,
+                                            const SgdBwdArgs& A) {
+  const float cs = round_to<TW>(cnt == 0 ? 1.f : (float)cnt);
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const float x = round_to<TW>(A.lr * -f[e]);
+    float d = A.clip ? ((fs[e] >= -1.f && fs[e] <= 1.f) ? x : 0.f) : x;
+    if (A.dgs != nullptr) d = round_to<TW>(d + fi[e]);
+    f[e] = round_to<TW>(round_to<TW>(d / cs) * A.scale);
+  }
+}
+#pragma clang fp contract(on)
+
 template <int VPL>
 struct FwdUnroll {
   static constexpr int U = VPL >= 8 ? 2 : (VPL >= 4 ? 4 : 8);
 };
 
-template <typename TW, typename TG, int LPG, int VPL, bool DOT>
+template <typename TW, typename TG, int LPG, int VPL, bool DOT, bool SGDB = false>
 __global__ __launch_bounds__(256) void eb_fwd_kernel(const TW* __restrict__ W, int64_t K, int64_t D,
                                                      const int64_t* __restrict__ idx,
                                                      const void* __restrict__ psw, int pdt, int64_t B,
                                                      int64_t L, int64_t S, TG* __restrict__ out,
                                                      const TG* __restrict__ g, void* __restrict__ dot_out,
-                                                     int ddt) {
+                                                     int ddt, SgdBwdArgs A) {
   using GT = GradTraits<TW, TG>;
   constexpr int NV = GT::NV;
   constexpr int EPV = VecTraits<TW>::EPV;
@@ -105,6 +138,17 @@ __global__ __launch_bounds__(256) void eb_fwd_kernel(const TW* __restrict__ W, i
           float f[NE];
 #pragma unroll
           for (int v = 0; v < VPL; ++v) VecTraits<TW>::unpack(rv[u][v], f + v * EPV);
+          if constexpr (SGDB) {
+            // the gathered row is dnew: turn it into the table gradient's gradient
+            float fs[NE], fi[NE];
+            const int64_t ro = r[u] * D + col0;
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+              if (A.clip) VecTraits<TW>::unpack(ld16((const TW*)A.gs + ro + v * VSTRIDE), fs + v * EPV);
+              if (A.dgs != nullptr) VecTraits<TW>::unpack(ld16((const TW*)A.dgs + ro + v * VSTRIDE), fi + v * EPV);
+            }
+            sgd_bwd_row<TW, NE>(f, (uint32_t)A.counts[r[u]], fs, fi, A);
+          }
 #pragma unroll
           for (int e = 0; e < NE; ++e) acc[e] = __builtin_fmaf(f[e], w[u], acc[e]);
           if constexpr (DOT) {
@@ -205,26 +249,26 @@ bool choose_group_cfg(int64_t D, int epv, bool single_slice, GroupCfg* c) {
 
 int elem_size(int dt) { return dt == PKM_DTYPE_F32 ? 4 : 2; }
 
-template <typename TW, typename TG, int LPG, int VPL, bool DOT>
+template <typename TW, typename TG, int LPG, int VPL, bool DOT, bool SGDB>
 static void launch_fwd(const void* W, int64_t K, int64_t D, const int64_t* idx, const void* psw, int pdt,
                        int64_t B, int64_t L, int64_t S, void* out, const void* g, void* dot_out, int ddt,
-                       hipStream_t stream) {
+                       const SgdBwdArgs& A, hipStream_t stream) {
   constexpr int GPW = 64 / LPG;
   const int64_t tasks = B * S;
   const int64_t per_block = 4 * GPW;
   const unsigned blocks = (unsigned)((tasks + per_block - 1) / per_block);
   KernelSpan span(DOT ? "eb_bwd2" : "eb_fwd", stream);
-  hipLaunchKernelGGL((eb_fwd_kernel<TW, TG, LPG, VPL, DOT>), dim3(blocks), dim3(256), 0, stream, (const TW*)W, K, D,
-                     idx, psw, pdt, B, L, S, (TG*)out, (const TG*)g, dot_out, ddt);
+  hipLaunchKernelGGL((eb_fwd_kernel<TW, TG, LPG, VPL, DOT, SGDB>), dim3(blocks), dim3(256), 0, stream, (const TW*)W, K,
+                     D, idx, psw, pdt, B, L, S, (TG*)out, (const TG*)g, dot_out, ddt, A);
 }
 
-template <typename TW, bool DOT, typename TG = TW>
+template <typename TW, bool DOT, typename TG = TW, bool SGDB = false>
 static bool dispatch_fwd(const GroupCfg& c, const void* W, int64_t K, int64_t D, const int64_t* idx,
                          const void* psw, int pdt, int64_t B, int64_t L, void* out, const void* g,
-                         void* dot_out, int ddt, hipStream_t stream) {
+                         void* dot_out, int ddt, hipStream_t stream, const SgdBwdArgs& A = SgdBwdArgs{}) {
 #define PKM_FWD_CASE(LPG_, VPL_)                                                                      \
   if (c.lpg == LPG_ && c.vpl == VPL_) {                                                               \
-    launch_fwd<TW, TG, LPG_, VPL_, DOT>(W, K, D, idx, psw, pdt, B, L, c.slices, out, g, dot_out, ddt, stream); \
+    launch_fwd<TW, TG, LPG_, VPL_, DOT, SGDB>(W, K, D, idx, psw, pdt, B, L, c.slices, out, g, dot_out, ddt, A, stream); \
     return true;                                                                                      \
   }
   PKM_FWD_CASE(64, 1)
@@ -329,4 +373,42 @@ extern "C" int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int 
     wide_grad ? PKM_BWD2(f16_t, float) : PKM_BWD2(f16_t, f16_t);
 #undef PKM_BWD2
   return pkm_check_launch("pkm_eb_bwd2");
+}
+
+extern "C" int pkm_eb_bwd2_sgd(const void* d_new_values, const void* d_scaled_grad, const void* scaled_grad,
+                               const int32_t* counts, int64_t num_rows, int64_t dim, int dtype, float scale, float lr,
+                               int grad_clip, const int64_t* indices, const void* a, int a_dtype,
+                               const void* grad_out, int64_t bags, int64_t bag_size, void* d_grad_out, void* d_a,
+                               void* stream) {
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd2_sgd: dtype %d not supported (float32, bfloat16 are)", dtype);
+  PKM_REQUIRE(a_dtype == PKM_DTYPE_NONE ? a == nullptr : (valid_dtype(a_dtype) && (a != nullptr || bags * bag_size == 0)),
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd2_sgd: a pointer / dtype %d mismatch", a_dtype);
+  PKM_REQUIRE(num_rows >= 0 && dim > 0 && bags >= 0 && bag_size >= 0, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd2_sgd: bad sizes");
+  if (bags == 0) return PKM_OK;
+  PKM_REQUIRE(d_grad_out != nullptr && grad_out != nullptr, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd2_sgd: null pointer");
+  PKM_REQUIRE(a == nullptr || d_a != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd2_sgd: d_a is null");
+  PKM_REQUIRE(bag_size == 0 || num_rows == 0 ||
+                  (indices != nullptr && d_new_values != nullptr && counts != nullptr &&
+                   (!grad_clip || scaled_grad != nullptr)),
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd2_sgd: null input");
+  PKM_REQUIRE(((uintptr_t)d_new_values | (uintptr_t)d_scaled_grad | (uintptr_t)scaled_grad | (uintptr_t)grad_out |
+               (uintptr_t)d_grad_out) % 16 == 0,
+              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd2_sgd: tensors must be 16-byte aligned");
+  GroupCfg c;
+  PKM_REQUIRE(choose_group_cfg(dim, epv_of(dtype), true, &c), PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd2_sgd: dim %lld not supported (need dim/%d = LPG*VPL with LPG<=64, VPL<=8)",
+              (long long)dim, epv_of(dtype));
+  hipStream_t st = (hipStream_t)stream;
+  void* dot = a != nullptr ? d_a : nullptr;
+  const SgdBwdArgs A = {scaled_grad, d_scaled_grad, counts, scale, lr, grad_clip};
+  if (dtype == PKM_DTYPE_F32)
+    dispatch_fwd<float, true, float, true>(c, d_new_values, num_rows, dim, indices, a, a_dtype, bags, bag_size,
+                                           d_grad_out, grad_out, dot, a_dtype, st, A);
+  else
+    dispatch_fwd<bf16_t, true, bf16_t, true>(c, d_new_values, num_rows, dim, indices, a, a_dtype, bags, bag_size,
+                                             d_grad_out, grad_out, dot, a_dtype, st, A);
+  return pkm_check_launch("pkm_eb_bwd2_sgd");
 }

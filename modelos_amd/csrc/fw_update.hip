@@ -15,14 +15,8 @@
 namespace pkm {
 
 template <typename T>
-__device__ __forceinline__ float fw_round(float v);
-template <>
-__device__ __forceinline__ float fw_round<float>(float v) {
-  return v;
-}
-template <>
-__device__ __forceinline__ float fw_round<bf16_t>(float v) {
-  return bf16_to_f32(f32_to_bf16_bits(v));
+__device__ __forceinline__ float fw_round(float v) {
+  return round_to<T>(v);
 }
 
 #pragma clang fp contract(off)
@@ -90,7 +84,7 @@ __global__ __launch_bounds__(256) void fw_sgd_update_bwd_kernel(const T* __restr
       o_g[e] = fw_round<T>(fw_round<T>(d / cs) * scale);
     }
     ((uint4*)dp_out)[v] = VecTraits<T>::pack(o_p);
-    ((uint4*)dg_out)[v] = VecTraits<T>::pack(o_g);
+    if (dg_out != nullptr) ((uint4*)dg_out)[v] = VecTraits<T>::pack(o_g);
   }
 }
 #pragma clang fp contract(on)
@@ -141,7 +135,7 @@ extern "C" int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_sca
               "pkm_fw_sgd_update_bwd: rows of %lld elements (a positive multiple of %d) not supported",
               (long long)dim, epv);
   if (num_rows == 0) return PKM_OK;
-  PKM_REQUIRE(d_new_values && scaled_grad && counts && d_values && d_grad, PKM_ERR_INVALID_ARGUMENT,
+  PKM_REQUIRE(d_new_values && scaled_grad && counts && d_values, PKM_ERR_INVALID_ARGUMENT,
               "pkm_fw_sgd_update_bwd: null pointer");
   PKM_REQUIRE(((uintptr_t)d_new_values | (uintptr_t)d_scaled_grad | (uintptr_t)scaled_grad | (uintptr_t)d_values |
                (uintptr_t)d_grad) % 16 == 0,

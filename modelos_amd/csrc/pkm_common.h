@@ -155,6 +155,23 @@ __device__ __forceinline__ float vec_dot<f16_t>(const uint4& a, const uint4& b, 
   return dot2_f16(a.w, b.w, d);
 }
 
+// Rounding of a float32 value to T, returned as float32 (ATen's narrowing of
+// a float32 result into a T tensor).
+template <typename T>
+__device__ __forceinline__ float round_to(float v);
+template <>
+__device__ __forceinline__ float round_to<float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ float round_to<bf16_t>(float v) {
+  return bf16_to_f32(f32_to_bf16_bits(v));
+}
+template <>
+__device__ __forceinline__ float round_to<f16_t>(float v) {
+  return (float)(f16_t)v;
+}
+
 // ---------------------------------------------------------------------------
 // A gradient read in its own dtype TG beside a table of dtype TW: one slot
 // holds the EPV elements that one 16-byte vector of the table holds, in NV

@@ -132,6 +132,74 @@ class _SgdValueUpdate(torch.autograd.Function):
             None, None, None, None, None
 
 
+class _FusedValueStep(torch.autograd.Function):
+    """FwPKM's values step taken straight from the gradient of the memory loss
+    w.r.t. the bag output: the table gradient EB^T(indices, psw, d_hyp) and the
+    bincount-normalised SGD step in one pass over the table (pkm_eb_bwd_sgd).
+    Returns (new values, scaled gradient, per-row sums of its squares).
+
+    Its backward is the reference's through EmbeddingBagBW and the step
+    (fwpkm/xformer_embeddingbag_grad_wrapper.py:42-74, fwpkm.py:351-365):
+    the values get d_new (plus the weight decay's term); d_hyp and psw get the
+    double backward of the bag over the gradient of the table gradient, which
+    pkm_eb_bwd2_sgd forms row by row as it gathers (never a dense [K, D])."""
+
+    @staticmethod
+    def forward(ctx, values, indices, psw, d_hyp, scale, lr, wd, clip):
+        from ..embedding_bag import eb_backward_workspace_bytes
+
+        V = _aligned(values)
+        idx = indices.contiguous()
+        w = psw.contiguous()
+        g = _aligned(d_hyp.to(V.dtype))
+        K, D = V.shape
+        B, L = idx.shape
+        new = torch.empty_like(V)
+        gs = torch.empty_like(V)
+        counts = torch.empty(K, dtype=torch.int32, device=V.device)
+        sumsq = torch.empty(K, dtype=torch.float32, device=V.device)
+        ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=V.device)
+        _lib.call("pkm_eb_bwd_sgd", _lib.ptr(V), K, D, _lib.dtype_code(V), _lib.ptr(idx), _lib.ptr(w),
+                  _lib.dtype_code(w), _lib.ptr(g), B, L, float(scale), float(lr), float(wd), int(bool(clip)),
+                  _lib.ptr(new), _lib.ptr(gs), None, _lib.ptr(counts), _lib.ptr(sumsq), _lib.ptr(ws), ws_bytes,
+                  _lib.stream_of(V.device))
+        ctx.save_for_backward(gs, counts, idx, w, g)
+        ctx.scale, ctx.lr, ctx.wd, ctx.clip = scale, lr, wd, clip
+        ctx.mark_non_differentiable(sumsq)
+        return new, gs, sumsq
+
+    @staticmethod
+    def backward(ctx, d_new, d_gs, _d_sumsq):
+        gs, counts, idx, w, g = ctx.saved_tensors
+        if d_new is None and d_gs is None:
+            return (None,) * 8
+        K, D = gs.shape
+        B, L = idx.shape
+        dn = _aligned(d_new.to(gs.dtype)) if d_new is not None else torch.zeros_like(gs)
+        dgi = _aligned(d_gs.to(gs.dtype)) if d_gs is not None else None
+        d_values = None
+        if ctx.needs_input_grad[0]:
+            if ctx.wd == 0.0:
+                d_values = dn  # p - lr * (step + 0 * p): the identity path alone
+            else:
+                d_values = torch.empty_like(gs)
+                cnt64 = counts.to(torch.int64)
+                _lib.call("pkm_fw_sgd_update_bwd", _lib.ptr(dn), None, _lib.ptr(gs), _lib.ptr(cnt64), K, D,
+                          _lib.dtype_code(gs), float(ctx.scale), float(ctx.lr), float(ctx.wd), int(bool(ctx.clip)),
+                          _lib.ptr(d_values), None, _lib.stream_of(gs.device))
+        d_hyp = d_psw = None
+        if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
+            d_hyp = torch.empty((B, D), dtype=gs.dtype, device=gs.device)
+            d_psw = torch.empty_like(w)
+            _lib.call("pkm_eb_bwd2_sgd", _lib.ptr(dn), _lib.ptr(dgi), _lib.ptr(gs), _lib.ptr(counts), K, D,
+                      _lib.dtype_code(gs), float(ctx.scale), float(ctx.lr), int(bool(ctx.clip)), _lib.ptr(idx),
+                      _lib.ptr(w), _lib.dtype_code(w), _lib.ptr(g), B, L, _lib.ptr(d_hyp), _lib.ptr(d_psw),
+                      _lib.stream_of(gs.device))
+        return (d_values, None, d_psw if ctx.needs_input_grad[2] else None,
+                d_hyp if ctx.needs_input_grad[3] else None, None, None, None, None)
+
+
 def sgd_value_update(p: torch.Tensor, g: torch.Tensor, indices: torch.Tensor, scale: float, lr: float,
                      weight_decay: float, grad_clip: bool):
     """The values branch of update_fw with the "sgd" optimizer
@@ -367,6 +435,57 @@ class FastWeightProductKeyMemory(nn.Module):
             updated.append(self.update_fw_param(p, step, self.learning_rate, self.weight_decay))
         return OrderedDict(zip(names, updated)), scaled
 
+    def _fused_values_step(self, values: torch.Tensor) -> bool:
+        """Whether the values step can run fused into the value backward
+        (_FusedValueStep): the "sgd" optimizer, the memory loss's gradient to
+        the values only, a float32 / bfloat16 table whose rows the backward's
+        row kernels take whole (v_dim / (16 bytes / element) = 2^a * b, a <= 6,
+        b in 1, 2, 4, 8)."""
+        if self.optimizer_type != "sgd" or not self.mem_grad_to_values_only:
+            return False
+        if values.dtype not in (torch.float32, torch.bfloat16):
+            return False
+        nvec, epv = values.shape[1], 4 if values.dtype == torch.float32 else 8
+        if nvec % epv:
+            return False
+        nvec //= epv
+        return nvec <= 64 and (nvec & (nvec - 1)) == 0 or (nvec % 64 == 0 and nvec // 64 in (1, 2, 4, 8))
+
+    def _update_fw_fused(self, fw_named_params: OrderedDict, num_samples: int, retrieval: dict,
+                         mem_loss: torch.Tensor, addr_loss: Optional[torch.Tensor] = None):
+        """update_fw with the values step fused into the value backward: the
+        same step (fwpkm.py:333-365) and outer gradients, the table gradient
+        and the dense normalisation / SGD passes replaced by one kernel.
+        Returns (updated params, [scaled gradient of each param], [squared
+        norm of each]: the values' from the kernel's row sums)."""
+        mem_loss = mem_loss * 0.5
+        names = list(fw_named_params.keys())
+        params = list(fw_named_params.values())
+        if addr_loss is not None:
+            addr_grads = torch.autograd.grad(addr_loss, params, create_graph=self.training, allow_unused=True)
+        else:
+            addr_grads = [None] * len(params)
+        hyp = retrieval["retireved_values"]
+        (d_hyp,) = torch.autograd.grad(mem_loss, hyp, create_graph=self.training)
+        scale = num_samples * self.v_dim * self.topk * self.heads
+        flat = retrieval["indices"].reshape(hyp.shape[0], -1)
+        psw = retrieval["normed_scores"].reshape(hyp.shape[0], -1)
+        scaled, updated, norms2 = [], [], []
+        for i, (n, p) in enumerate(zip(names, params)):
+            if n == "values":
+                new_p, g_scaled, sumsq = _FusedValueStep.apply(p, flat, psw, d_hyp, scale, self.learning_rate,
+                                                               self.weight_decay, self.grad_clip)
+                scaled.append(g_scaled)
+                updated.append(new_p)
+                norms2.append(sumsq.sum())
+                continue
+            g = addr_grads[i]
+            scaled.append(g)
+            step = torch.clamp(g, min=-1.0, max=1.0) if self.grad_clip else g
+            updated.append(self.update_fw_param(p, step, self.learning_rate, self.weight_decay))
+            norms2.append(None)
+        return OrderedDict(zip(names, updated)), scaled, norms2
+
     def write_ob_log(self, token_ids, indices, scores):
         """Appends, per slot read, (query token, value token, up to 10 tokens
         of context either side of the value token, score) to ob_idx2log
@@ -420,10 +539,11 @@ class FastWeightProductKeyMemory(nn.Module):
         input_dtype = q.dtype
         if self.fp32_fw:
             q, ref_v = q.float(), ref_v.float()
-        outputs, indices, scores, losses, addr_losses, step_grads = [], [], [], [], [], []
+        outputs, indices, scores, losses, addr_losses, step_norms = [], [], [], [], [], []
         with torch.enable_grad():
             params = self.get_fw_named_params()
             n_params = len(params)
+            fused = self._fused_values_step(params["values"])
             for start, end in _chunks(T, chunk_size, chunk_size):
                 cT = end - start
                 cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
@@ -437,16 +557,24 @@ class FastWeightProductKeyMemory(nn.Module):
                                                                  cmask)
                 mem_losses, addr_loss = self._losses(u_hyp, u_ref, u_w, u_mask, r)
                 num_samples = (u_mask > 0).sum().item() if u_mask is not None else B * cT
-                params, grads = self.update_fw(params, num_samples, r["indices"], mem_losses.mean(), addr_loss)
+                if fused:
+                    params, grads, norms2 = self._update_fw_fused(params, num_samples, r, mem_losses.mean(),
+                                                                  addr_loss)
+                else:
+                    params, grads = self.update_fw(params, num_samples, r["indices"], mem_losses.mean(), addr_loss)
+                    norms2 = [None] * len(grads)
                 if self.ob_mode:
                     self.write_ob_log(token_ids=cids.view(B, cT), indices=r["indices"].view(B, cT, -1),
                                       scores=cgates.view(B, cT, -1))
-                step_grads.append([g.detach() for g in grads])
+                with torch.no_grad():
+                    # each param's gradient norm (the values' from the kernel's row sums when fused)
+                    step_norms.append([torch.sqrt(n2).to(g.dtype) if n2 is not None else g.detach().norm()
+                                       for g, n2 in zip(grads, norms2)])
                 losses.append(mem_losses.view(B, -1).detach())
                 if self.addr_loss is not None:
                     addr_losses.append(addr_loss.detach())
         with torch.no_grad():
-            grad_norms = [torch.stack([g[i].norm() for g in step_grads]).mean() for i in range(n_params)]
+            grad_norms = [torch.stack([nr[i] for nr in step_norms]).mean() for i in range(n_params)]
         self._store_fast_weights(params)
         return {
             "output": torch.cat(outputs, dim=1).to(input_dtype),

@@ -117,3 +117,57 @@ def test_update_fw_end_to_end(device, clip):
     assert torch.equal(upd["values"].detach().cpu(), e_v)
     assert torch.equal(grads[1].detach().cpu(), e_gv)
     assert torch.equal(upd["keys"].detach(), e_k)
+
+
+def _fused_case(device, dtype, D, clip, wd, seed, K=3000, BT=96, HK=32):
+    """A values table, a bag over it and a stand-in memory loss whose gradient
+    w.r.t. the bag output drives the step: (values, idx, psw, hyp, loss)."""
+    from modelos_amd.fwpkm.xformer_embeddingbag_grad_wrapper import xformers_embedding_bag
+
+    g = gen(seed)
+    values = (torch.randn((K, D), generator=g) * 0.1).to(dtype).to(device).requires_grad_(True)
+    idx = torch.randint(0, K - 5, (BT, HK), generator=g).to(device)  # the last rows untouched
+    idx[0, :4] = 7  # a row looked up several times by one bag
+    logits = torch.randn((BT, HK), generator=g).to(device).requires_grad_(True)
+    psw = torch.softmax(logits, -1).to(dtype)
+    target = torch.randn((BT, D), generator=g).to(dtype).to(device)
+    hyp = xformers_embedding_bag(indices=idx, weight=values, per_sample_weights=psw)
+    loss = torch.nn.functional.mse_loss(hyp, target, reduction="none").mean(-1).mean()
+    return values, idx, logits, psw, hyp, loss
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("D", [256, 1024, 64])
+@pytest.mark.parametrize("clip,wd", [(False, 0.0), (True, 0.0), (True, 0.01)], ids=["plain", "clip", "clip-wd"])
+def test_fused_values_step_equals_separate_passes(device, dtype, D, clip, wd):
+    """The values step fused into the value backward (pkm_eb_bwd_sgd) gives the
+    separate passes' results bit for bit (table gradient, then
+    pkm_fw_sgd_update), and the same outer gradients of a loss on the new
+    values (its double backward, pkm_eb_bwd2_sgd, against autograd through
+    EmbeddingBagBW and the step's backward) within the dtype's tolerance."""
+    from modelos_amd.fwpkm.fwpkm import _FusedValueStep
+
+    scale, lr = 96 * D * 8 * 4, 0.1
+    outs = []
+    for fused in (False, True):
+        values, idx, logits, psw, hyp, loss = _fused_case(device, dtype, D, clip, wd, seed=9)
+        if fused:
+            (d_hyp,) = torch.autograd.grad(0.5 * loss, hyp, create_graph=True)
+            new, gs, sumsq = _FusedValueStep.apply(values, idx, psw, d_hyp, scale, lr, wd, clip)
+        else:
+            (gv,) = torch.autograd.grad(0.5 * loss, values, create_graph=True)
+            new, gs = sgd_value_update(values, gv, idx, scale, lr, wd, clip)
+            sumsq = None
+        # an outer loss on the updated table, read through a second bag
+        w2 = torch.linspace(-1, 1, D, device=device, dtype=torch.float32)
+        outer = (new.float()[idx[:, :8]].sum(1) * w2).sum() + 1e-3 * (gs.float() * w2).sum()
+        outer.backward()
+        torch.cuda.synchronize()
+        outs.append((new.detach(), gs.detach(), sumsq, values.grad, logits.grad))
+    (n0, g0, _, dv0, dl0), (n1, g1, ss1, dv1, dl1) = outs
+    assert torch.equal(n0, n1) and torch.equal(g0, g1)
+    assert_rel_close(ss1.view(-1, 1).sqrt().cpu(), g0.float().pow(2).sum(1, keepdim=True).sqrt().cpu(), 1e-5,
+                     "row norms")
+    tol = REL_TOL[dtype]
+    assert_rel_close(dv1, dv0, tol, "d_values")
+    assert_rel_close(dl1, dl0, 1e-4 if dtype == torch.float32 else 5e-2, "d_logits")
