@@ -8,8 +8,8 @@
 // with every product, quotient and sum rounded to the tensor dtype T in the
 // reference's order (ATen elementwise ops on T tensors with float scalars),
 // and no contraction of a product into a following sum. Outputs: gs (the
-// scaled, unclipped gradient the reference returns) and p'. T is float32 or
-// bfloat16; 16-byte vectors over rows of D elements.
+// scaled, unclipped gradient the reference returns) and p'. T is float32,
+// bfloat16 or float16; 16-byte vectors over rows of D elements.
 #include "pkm_common.h"
 
 namespace pkm {
@@ -96,9 +96,9 @@ using namespace pkm;
 extern "C" int pkm_fw_sgd_update(const void* values, const void* grad, const int64_t* counts, int64_t num_rows,
                                  int64_t dim, int dtype, float scale, float lr, float weight_decay, int grad_clip,
                                  void* scaled_grad, void* new_values, void* stream) {
-  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
-              "pkm_fw_sgd_update: dtype %d not supported (float32, bfloat16 are)", dtype);
-  const int epv = dtype == PKM_DTYPE_BF16 ? 8 : 4;
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
+              "pkm_fw_sgd_update: dtype %d not supported (float32, bfloat16, float16 are)", dtype);
+  const int epv = dtype == PKM_DTYPE_F32 ? 4 : 8;
   PKM_REQUIRE(num_rows >= 0 && dim >= 1 && dim % epv == 0 && dim < (1 << 30), PKM_ERR_UNSUPPORTED,
               "pkm_fw_sgd_update: rows of %lld elements (a positive multiple of %d) not supported", (long long)dim,
               epv);
@@ -117,6 +117,10 @@ extern "C" int pkm_fw_sgd_update(const void* values, const void* grad, const int
     hipLaunchKernelGGL(fw_sgd_update_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, st, (const bf16_t*)values,
                        (const bf16_t*)grad, counts, num_rows, (int)dim, scale, lr, weight_decay, grad_clip,
                        (bf16_t*)scaled_grad, (bf16_t*)new_values);
+  else if (dtype == PKM_DTYPE_F16)
+    hipLaunchKernelGGL(fw_sgd_update_kernel<f16_t>, dim3((unsigned)blocks), dim3(256), 0, st, (const f16_t*)values,
+                       (const f16_t*)grad, counts, num_rows, (int)dim, scale, lr, weight_decay, grad_clip,
+                       (f16_t*)scaled_grad, (f16_t*)new_values);
   else
     hipLaunchKernelGGL(fw_sgd_update_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)values,
                        (const float*)grad, counts, num_rows, (int)dim, scale, lr, weight_decay, grad_clip,
@@ -128,9 +132,9 @@ extern "C" int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_sca
                                      const int64_t* counts, int64_t num_rows, int64_t dim, int dtype, float scale,
                                      float lr, float weight_decay, int grad_clip, void* d_values, void* d_grad,
                                      void* stream) {
-  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
-              "pkm_fw_sgd_update_bwd: dtype %d not supported (float32, bfloat16 are)", dtype);
-  const int epv = dtype == PKM_DTYPE_BF16 ? 8 : 4;
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
+              "pkm_fw_sgd_update_bwd: dtype %d not supported (float32, bfloat16, float16 are)", dtype);
+  const int epv = dtype == PKM_DTYPE_F32 ? 4 : 8;
   PKM_REQUIRE(num_rows >= 0 && dim >= 1 && dim % epv == 0 && dim < (1 << 30), PKM_ERR_UNSUPPORTED,
               "pkm_fw_sgd_update_bwd: rows of %lld elements (a positive multiple of %d) not supported",
               (long long)dim, epv);
@@ -150,6 +154,10 @@ extern "C" int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_sca
     hipLaunchKernelGGL(fw_sgd_update_bwd_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const bf16_t*)d_new_values, (const bf16_t*)d_scaled_grad, (const bf16_t*)scaled_grad, counts,
                        num_rows, (int)dim, scale, lr, weight_decay, grad_clip, (bf16_t*)d_values, (bf16_t*)d_grad);
+  else if (dtype == PKM_DTYPE_F16)
+    hipLaunchKernelGGL(fw_sgd_update_bwd_kernel<f16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const f16_t*)d_new_values, (const f16_t*)d_scaled_grad, (const f16_t*)scaled_grad, counts,
+                       num_rows, (int)dim, scale, lr, weight_decay, grad_clip, (f16_t*)d_values, (f16_t*)d_grad);
   else
     hipLaunchKernelGGL(fw_sgd_update_bwd_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const float*)d_new_values, (const float*)d_scaled_grad, (const float*)scaled_grad, counts,

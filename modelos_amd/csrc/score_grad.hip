@@ -722,24 +722,39 @@ static bool sparse_grad_supported(int64_t n, int64_t half, int64_t knn) {
 
 using namespace pkm;
 
+namespace pkm {
+int score_grad_dense_generic(const int64_t* indices, const void* d_scores, int dtype, int64_t num_tokens,
+                             int64_t heads, int64_t n_keys, int64_t knn, const void* d_sub1, const void* d_sub2,
+                             void* d_sub_dense, int lds_max, hipStream_t st);
+}
+
 extern "C" int pkm_score_grad_dense(const int64_t* indices, const void* d_scores, int dtype, int64_t num_tokens,
                                     int64_t heads, int64_t n_keys, int64_t knn, const void* d_sub_scores1,
                                     const void* d_sub_scores2, void* d_sub_dense, void* stream) {
-  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
-              "pkm_score_grad_dense: dtype %d not supported (float32 and bfloat16 are)", dtype);
-  PKM_REQUIRE(num_tokens >= 0 && heads >= 1 && n_keys >= 1 && knn >= 1 && knn <= 64, PKM_ERR_INVALID_ARGUMENT,
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
+              "pkm_score_grad_dense: dtype %d not supported (float32, bfloat16 and float16 are)", dtype);
+  PKM_REQUIRE(num_tokens >= 0 && heads >= 1 && n_keys >= 1 && knn >= 1, PKM_ERR_INVALID_ARGUMENT,
               "pkm_score_grad_dense: bad sizes");
-  PKM_REQUIRE(n_keys % 4 == 0 && n_keys <= kGradMaxN, PKM_ERR_UNSUPPORTED,
-              "pkm_score_grad_dense: n_keys %lld must be a multiple of 4 up to %d", (long long)n_keys, kGradMaxN);
   if (num_tokens == 0) return PKM_OK;
   PKM_REQUIRE(indices && d_scores && d_sub_dense, PKM_ERR_INVALID_ARGUMENT, "pkm_score_grad_dense: null pointer");
-  PKM_REQUIRE((uintptr_t)d_sub_dense % 16 == 0 && (uintptr_t)d_sub_scores1 % 16 == 0 &&
-                  (uintptr_t)d_sub_scores2 % 16 == 0,
-              PKM_ERR_INVALID_ARGUMENT, "pkm_score_grad_dense: dense buffers must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const bool tuned = dtype != PKM_DTYPE_F16 && knn <= 64 && n_keys % 4 == 0 && n_keys <= kGradMaxN &&
+                     (uintptr_t)d_sub_dense % 16 == 0 && (uintptr_t)d_sub_scores1 % 16 == 0 &&
+                     (uintptr_t)d_sub_scores2 % 16 == 0;
+  if (!tuned) {
+    int dev = 0, lds_max = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess)
+      return pkm_set_error(PKM_ERR_HIP, "pkm_score_grad_dense: device query failed: %s", hipGetErrorString(e));
+    const int rc = score_grad_dense_generic(indices, d_scores, dtype, num_tokens, heads, n_keys, knn, d_sub_scores1,
+                                            d_sub_scores2, d_sub_dense, lds_max, st);
+    if (rc != PKM_OK) return rc;
+    return pkm_check_launch("pkm_score_grad_dense");
+  }
   const int64_t NH = num_tokens * heads;
   const int64_t blocks = (NH + kGradWaves - 1) / kGradWaves;
   PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_score_grad_dense: too many rows");
-  hipStream_t st = (hipStream_t)stream;
   const size_t lds = (size_t)kGradWaves * 2 * n_keys * sizeof(float);
   if (dtype == PKM_DTYPE_BF16) {
     hipLaunchKernelGGL(score_grad_dense_kernel<bf16_t>, dim3((unsigned)blocks), dim3(64 * kGradWaves), lds, st,

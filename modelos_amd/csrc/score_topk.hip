@@ -1668,31 +1668,29 @@ static int launch_score(int TM, const void* q, const void* keys, int64_t Ntok, i
 
 using namespace pkm;
 
+namespace pkm {
+int score_topk_generic(const void* query, const void* keys, int64_t num_tokens, int64_t heads, int64_t n_keys,
+                       int64_t half, int64_t knn, int score_type, int dtype, void* out_scores, int64_t* out_indices,
+                       int64_t* out_i1, int64_t* out_i2, void* out_s1, void* out_s2, int lds_max, hipStream_t st);
+}
+
 extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_tokens, int64_t heads, int64_t n_keys,
                               int64_t half, int64_t knn, int score_type, int dtype, void* out_scores,
                               int64_t* out_indices, int64_t* out_sub_indices1, int64_t* out_sub_indices2,
                               void* out_sub_scores1, void* out_sub_scores2, void* stream) {
-  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16, PKM_ERR_UNSUPPORTED,
-              "pkm_score_topk: dtype %d not supported (float32 and bfloat16 are)", dtype);
+  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
+              "pkm_score_topk: dtype %d not supported (float32, bfloat16 and float16 are)", dtype);
   PKM_REQUIRE(score_type == PKM_SCORE_DOT || score_type == PKM_SCORE_IDW, PKM_ERR_INVALID_ARGUMENT,
               "pkm_score_topk: bad score type %d", score_type);
   PKM_REQUIRE(num_tokens >= 0 && heads >= 1 && heads < 65536 && n_keys >= 1 && half >= 1 && knn >= 1,
               PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: bad sizes");
   PKM_REQUIRE(knn <= n_keys, PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: knn %lld > n_keys %lld", (long long)knn,
               (long long)n_keys);
-  PKM_REQUIRE(knn <= 64 && n_keys % 64 == 0 && n_keys <= kMaxN, PKM_ERR_UNSUPPORTED,
-              "pkm_score_topk: need knn <= 64 and n_keys a multiple of 64 up to %d (got knn %lld, n_keys %lld)",
-              kMaxN, (long long)knn, (long long)n_keys);
-  const int kstep = dtype == PKM_DTYPE_BF16 ? Sel<bf16_t>::KSTEP : Sel<float>::KSTEP;
-  PKM_REQUIRE(half % kstep == 0, PKM_ERR_UNSUPPORTED, "pkm_score_topk: half key dim %lld must be a multiple of %d",
-              (long long)half, kstep);
   if (num_tokens == 0) return PKM_OK;
   PKM_REQUIRE(query && keys && out_scores && out_indices, PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: null pointer");
   PKM_REQUIRE((uintptr_t)out_sub_scores1 % 4 == 0 && (uintptr_t)out_sub_scores2 % 4 == 0 &&
-                  (uintptr_t)out_scores % (dtype == PKM_DTYPE_BF16 ? 2 : 4) == 0,
+                  (uintptr_t)out_scores % (dtype == PKM_DTYPE_F32 ? 4 : 2) == 0,
               PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: score outputs must be 4-byte aligned");
-  PKM_REQUIRE((uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0, PKM_ERR_INVALID_ARGUMENT,
-              "pkm_score_topk: query and keys must be 16-byte aligned");
   const int esz = dtype == PKM_DTYPE_BF16 ? 2 : 4;  // score-tile element = order key of the input dtype
   const int key_bytes = dtype == PKM_DTYPE_BF16 ? 4 : 8;
   int dev = 0, lds_max = 0;
@@ -1702,6 +1700,18 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
     return pkm_set_error(PKM_ERR_HIP, "pkm_score_topk: device query failed: %s", hipGetErrorString(e));
   if (lds_max > kMaxLds) lds_max = kMaxLds;
   hipStream_t st = (hipStream_t)stream;
+  // the tuned kernels: float32 / bfloat16, knn <= 64, n_keys a multiple of 64 up to kMaxN, half a multiple
+  // of the MFMA k-step, 16-byte aligned operands; anything else takes the generic kernel (score_generic.hip)
+  const int kstep = dtype == PKM_DTYPE_BF16 ? Sel<bf16_t>::KSTEP : Sel<float>::KSTEP;
+  const bool tuned = dtype != PKM_DTYPE_F16 && knn <= 64 && n_keys % 64 == 0 && n_keys <= kMaxN && half % kstep == 0 &&
+                     (uintptr_t)query % 16 == 0 && (uintptr_t)keys % 16 == 0;
+  if (!tuned) {
+    const int rc = score_topk_generic(query, keys, num_tokens, heads, n_keys, half, knn, score_type, dtype, out_scores,
+                                      out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
+                                      out_sub_scores2, lds_max, st);
+    if (rc != PKM_OK) return rc;
+    return pkm_check_launch("pkm_score_topk");
+  }
   if (dtype == PKM_DTYPE_BF16 && score_type == PKM_SCORE_DOT && knn <= stream::kNet && (half == 128 || half == 256) &&
       (int)stream::lds_bytes((int)half) <= lds_max) {
     const int64_t blocks = ((num_tokens + stream::kTok - 1) / stream::kTok) * 2 * heads;
@@ -1719,9 +1729,13 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
                      n_keys > score_max_n(TM, esz)))
     TM /= 2;
   const int lds = score_lds_layout(TM, (int)n_keys, (int)half, (int)knn, esz, key_bytes).total;
-  PKM_REQUIRE(lds <= lds_max, PKM_ERR_UNSUPPORTED,
-              "pkm_score_topk: n_keys %lld / half %lld need %d bytes of LDS, the device allows %d", (long long)n_keys,
-              (long long)half, lds, lds_max);
+  if (lds > lds_max) {  // a tile too large for the device's LDS: the generic kernel
+    const int rc = score_topk_generic(query, keys, num_tokens, heads, n_keys, half, knn, score_type, dtype, out_scores,
+                                      out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
+                                      out_sub_scores2, lds_max, st);
+    if (rc != PKM_OK) return rc;
+    return pkm_check_launch("pkm_score_topk");
+  }
   const int64_t blocks = ((num_tokens + TM - 1) / TM) * heads;
   PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: grid too large");
   int rc;

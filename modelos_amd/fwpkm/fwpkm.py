@@ -205,12 +205,12 @@ def sgd_value_update(p: torch.Tensor, g: torch.Tensor, indices: torch.Tensor, sc
     """The values branch of update_fw with the "sgd" optimizer
     (fwpkm.py:334-365, 266-272): returns (p - lr * (clip(g') + wd * p), g')
     with g' = g * scale / max(bincount(indices), 1) per row, both in p's
-    dtype. float32 / bfloat16 tables on the GPU."""
+    dtype. float32 / bfloat16 / float16 tables on the GPU."""
     _require_device(p, g, indices)
     if p.dim() != 2 or p.shape != g.shape:
         raise ValueError(f"values and gradient must be the same [size, v_dim], got {tuple(p.shape)}, {tuple(g.shape)}")
-    if p.dtype not in (torch.float32, torch.bfloat16):
-        raise TypeError(f"values dtype {p.dtype} not supported (float32, bfloat16 are)")
+    if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError(f"values dtype {p.dtype} not supported (float32, bfloat16, float16 are)")
     counts = torch.bincount(indices.reshape(-1), minlength=p.shape[0])
     return _SgdValueUpdate.apply(p, g, counts, scale, lr, weight_decay, grad_clip)
 

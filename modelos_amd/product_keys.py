@@ -32,28 +32,30 @@ from .embedding_bag import _aligned, _require_device
 SCORE_TYPES = ("dot", "idw")
 
 
-MAX_KNN = 64
-MAX_N_KEYS = 2048
+MAX_KNN = 1024
+MAX_N_KEYS = 16384
 
 
 def check_supported(n_keys: int, k_dim: int, knn: int, v_dim: int | None = None, what: str = "PKM layer") -> None:
     """Raises NotImplementedError, naming the limit, for sizes the HIP kernels
-    have no path for (the reference's torch/Triton code accepts more):
-      retrieval (pkm_score_topk): knn <= 64; n_keys a multiple of 64, at most
-        2048; k_dim / 2 a multiple of 16 (float32) / 32 (bfloat16; checked
-        per call, the dtype is not known at construction);
+    have no path for:
+      retrieval (pkm_score_topk): 1 <= knn <= min(n_keys, 1024), n_keys up to
+        16384, any even k_dim (the tuned kernels take knn <= 64, n_keys a
+        multiple of 64 up to 2048 and k_dim / 2 a multiple of 16 / 32 in
+        float32 / bfloat16; the other shapes and float16 run on the generic
+        kernel);
       value bag backward (pkm_eb_bwd): v_dim a power of two from 4 to 4096
         (2048 for float32), as the reference's Triton kernels need a power of
         two (pkm/xformer_embeddingbag.py:97-113, 291-328)."""
     problems = []
     if not 1 <= knn <= MAX_KNN:
         problems.append(f"knn={knn} (must be 1..{MAX_KNN})")
-    if n_keys % 64 != 0 or not 64 <= n_keys <= MAX_N_KEYS:
-        problems.append(f"n_keys={n_keys} (must be a multiple of 64 up to {MAX_N_KEYS})")
+    if not 1 <= n_keys <= MAX_N_KEYS:
+        problems.append(f"n_keys={n_keys} (must be 1..{MAX_N_KEYS})")
     if knn > n_keys:
         problems.append(f"knn={knn} > n_keys={n_keys}")
-    if (k_dim // 2) % 16 != 0:
-        problems.append(f"k_dim={k_dim} (k_dim / 2 must be a multiple of 16, of 32 in bfloat16)")
+    if k_dim < 2 or k_dim % 2:
+        problems.append(f"k_dim={k_dim} (must be even)")
     if v_dim is not None and (v_dim < 4 or v_dim > 4096 or v_dim & (v_dim - 1)):
         problems.append(f"value dim={v_dim} (must be a power of two from 4 to 4096)")
     if problems:
