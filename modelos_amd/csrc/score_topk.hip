@@ -1083,46 +1083,62 @@ __global__ __launch_bounds__(kThreads) void pkm_score_cartesian_kernel(int64_t r
 // ---------------------------------------------------------------------------
 // Streaming scoring: bfloat16 dot scores, knn <= 32, half key dim 128 or 256.
 //
-// One workgroup (4 waves, one per SIMD) owns 256 tokens of one (head, half).
-// The keys of the half stream through LDS in blocks of 64 (double-buffered,
-// direct global->LDS loads, every key read once per workgroup). A wave
-// multiplies them with its 64 tokens' query halves, held in accumulation
-// registers, on 32x32x16 bf16 MFMA: A = 32 keys from LDS (read four steps
-// ahead), B = 32 tokens, and the wave's two token sets share every A
-// fragment. v_permlane32_swap then gives each lane the scores of one token:
-// lane l owns token l of the wave for the whole stream, and a block's 64
-// scores of a lane are 32 words of two bf16.
+// One workgroup of 8 waves, two per SIMD, owns 256 tokens of one (head, half):
+// while one wave of a SIMD runs its selection on the vector ALUs, the other
+// wave's MFMAs keep the matrix core busy (a wave does not overlap its own
+// vector work with its own MFMAs). The keys of the half stream through LDS in
+// blocks of 64 (double-buffered, direct global->LDS loads, every key read once
+// per workgroup). A wave multiplies them with its 32 tokens' query halves,
+// held in accumulation registers, on 32x32x16 bf16 MFMA: A = 32 keys from LDS
+// (read four steps ahead), B = the 32 tokens. In the MFMA's output lane l
+// holds 16 scores of token l % 32, keys 8 a + 4 (l / 32) + b (a, b < 4) of
+// the 32-key tile: every token has two lanes, l and l + 32, and each selects
+// over its own half of the token's keys. A block's 32 scores of a lane are 16
+// words of two bf16.
 //
 // Selection per lane, exact, on the unique keys
-// (order key of the bf16 score << 16) | (0xFFFF - key index):
-//   * T: the best 32 keys merged so far, sorted, in registers; theta =
-//     T[knn - 1] (0 while fewer than knn are merged).
+// (order key of the bf16 score << 16) | (0xFFFF - index'),
+// where index' is the key index less 4 (l / 32): the same for both lanes of a
+// word position (wave-uniform constants), and within a lane in the order of
+// the true index. The final merge restores the true index.
+//   * T: the lane's best 32 keys merged so far, sorted, in registers.
+//   * The first block's 32 scores of a lane are sorted into T directly.
+//   * theta: the larger of T[31] and a bound on the token's 32nd best value
+//     over both lanes, min(T_lo[a - 1], T_hi[31 - a]) maximised over a in
+//     {12, 16, 20}: 32 keys of the two lists are at least that large.
+//     Neither exceeds the token's knn-th best value (knn <= 32), so no key of
+//     the token's top knn is rejected.
 //   * Every score whose bf16 value can reach theta is appended to the lane's
 //     LDS slots, branch-free (the slots are written, the count moves on a
 //     pass). The test is one float compare of the raw word
-//     (bf16 bits << 16) | (0xFFFF - index) against tau, the smallest raw word
-//     of theta's value (NaN while theta = 0, which nothing is below): a raw
-//     word is a float within its bf16 value's rounding interval, so every key
-//     >= theta passes, and some equal-valued keys below theta too. A block's
-//     appends run between the MFMAs of the next block.
-//   * After each block the workgroup merges if any of its lanes holds 28
-//     slots (all waves at once, at the block's barrier): up to two chunks of
-//     32 slots become keys (-0 counted as +0), are sorted by Batcher's
-//     odd-even merge sort (191 compare-exchanges), and the best 32 of T and
-//     a chunk, max(T[i], C[31 - i]), are sorted by a bitonic half-cleaner
-//     cascade.
-// T[0 .. knn) is the half's list, stored (through an LDS transpose, two
-// tokens' rows per store) as the low (first half) or high (second half) word
-// of the index output, for the cartesian kernel below.
+//     (bf16 bits << 16) | (0xFFFF - index') against tau, the smallest raw
+//     word of theta's value (NaN while theta = 0, which nothing is below): a
+//     raw word is a float within its bf16 value's rounding interval, so every
+//     key >= theta passes, and some equal-valued keys below theta too. A
+//     block's appends run between the MFMAs of the next block (the first
+//     block's words, already in T, are zeroed: none passes tau = +inf).
+//   * After each block the workgroup merges if any of its lanes holds 16
+//     slots (all waves at once, at the block's barrier): a chunk of up to 32
+//     slots becomes keys (-0 counted as +0), sorted by Batcher's odd-even
+//     merge sort (191 compare-exchanges), and the best 32 of T and the chunk,
+//     max(T[i], C[31 - i]), are sorted by a bitonic half-cleaner cascade; a
+//     wave whose counts leave a chunk's upper 16 slots unused merges it 16
+//     wide (63 compare-exchanges), with the same result.
+// At the end the two lanes of a token merge their lists (true indices):
+// max(T_lo[i], T_hi[31 - i]) through the half-cleaner cascade is the token's
+// best 32, stored (through an LDS transpose, two tokens' rows per store) as
+// the low (first half) or high (second half) word of the index output, for
+// the cartesian kernel below.
 // ---------------------------------------------------------------------------
 namespace stream {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kTok = 64 * kWaves;  // tokens per workgroup
+constexpr int kTok = 32 * kWaves;  // tokens per workgroup
 constexpr int kKB = 64;            // keys per staged block
-constexpr int kBuf = 92;           // appended-score slots per token
+constexpr int kBuf = 47;           // appended-score slots per lane
 constexpr int kNet = 32;           // length of the sorted list
+constexpr int kWpb = kKB / 4;      // words per block and lane (32 scores)
 
 struct CeNet {
   int n;
@@ -1208,19 +1224,23 @@ __device__ __forceinline__ uint32_t canon_pair(uint32_t p) {
   return p;
 }
 
-// Merge slots [J0, J0 + W) (those below cnt) into T, W = 32 or 16. The
-// sorted chunk, reversed and padded with zero keys to 32, meets T elementwise
-// (the larger of each pair): the top 32 of both, as one bitonic sequence,
-// which the cleaner sorts. With W = 16 the padding covers T[0 .. 16), which
-// keeps its keys: the result equals the 32-wide merge of the same slots
-// whenever the wave's counts leave slots [J0 + 16, J0 + 32) unused.
+// Merge slots [J0, J0 + W) (those below cnt, and below kBuf) into T, W = 32
+// or 16. The sorted chunk, reversed and padded with zero keys to 32, meets T
+// elementwise (the larger of each pair): the top 32 of both, as one bitonic
+// sequence, which the cleaner sorts. With W = 16 the padding covers
+// T[0 .. 16), which keeps its keys: the result equals the 32-wide merge of
+// the same slots whenever the wave's counts leave slots [J0 + 16, J0 + 32)
+// unused.
 template <int J0, int W>
 __device__ __forceinline__ void merge_chunk(uint32_t (&T)[kNet], const uint32_t* buf, uint32_t cnt) {
   static_assert(W == 32 || W == 16, "chunk width");
   uint32_t C[W];
 #pragma unroll
   for (int j = 0; j < W; ++j) {
-    const uint32_t r = buf[(J0 + j) * kThreads];
+    // the load is unconditional (a slot past the count holds a stale word,
+    // masked below), so that no branch surrounds it
+    uint32_t r = 0u;
+    if (J0 + j < kBuf) r = buf[(J0 + j) * kThreads];
     C[j] = (uint32_t)(J0 + j) < cnt ? raw_key(r) : 0u;
   }
   if constexpr (W == 32)
@@ -1232,22 +1252,35 @@ __device__ __forceinline__ void merge_chunk(uint32_t (&T)[kNet], const uint32_t*
   clean32_desc(T, std::make_index_sequence<80>{});
 }
 // Merge slots [J0, J0 + 32) with the narrower chunk when no lane of the wave
-// holds a count past J0 + 16.
+// holds a count past J0 + 16 (or the slots end there).
 template <int J0>
 __device__ __forceinline__ void merge_span(uint32_t (&T)[kNet], const uint32_t* buf, uint32_t cnt) {
-  if (__builtin_amdgcn_ballot_w64(cnt > (uint32_t)(J0 + 16)) != 0)
-    merge_chunk<J0, 32>(T, buf, cnt);
-  else
+  if constexpr (kBuf - J0 <= 16) {
     merge_chunk<J0, 16>(T, buf, cnt);
+  } else {
+    if (__builtin_amdgcn_ballot_w64(cnt > (uint32_t)(J0 + 16)) != 0)
+      merge_chunk<J0, 32>(T, buf, cnt);
+    else
+      merge_chunk<J0, 16>(T, buf, cnt);
+  }
 }
-// tau of theta = T[knn - 1], the smallest of T[0 .. knn) (T is sorted; a
-// minimum rather than an indexed pick keeps T in registers)
-__device__ __forceinline__ float tau_of(const uint32_t (&T)[kNet], int knn) {
-  uint32_t th = T[0];
+// theta: the larger of the lane's T[31] and the pair bound
+// max_a min(T_lo[a - 1], T_hi[31 - a]) over both lanes of the token
+// (v_permlane32_swap of a register with itself gives every lane the lower
+// lanes' value as its first result and the upper lanes' as its second). Both
+// are at most the token's 32nd best value, so at most its knn-th for every
+// knn <= 32. Only theta's value is used (by raw_floor), so the lanes' index'
+// encodings do not matter here.
+__device__ __forceinline__ float tau_of(const uint32_t (&T)[kNet]) {
+  uint32_t th = T[kNet - 1];
+  constexpr int kSplit[3] = {12, 16, 20};
 #pragma unroll
-  for (int j = 1; j < kNet; ++j) {
-    const uint32_t v = j < knn ? T[j] : 0xFFFFFFFFu;
-    th = th < v ? th : v;
+  for (int s = 0; s < 3; ++s) {
+    const int a = kSplit[s];
+    const uint32_t lo = __builtin_amdgcn_permlane32_swap(T[a - 1], T[a - 1], false, false)[0];
+    const uint32_t hi = __builtin_amdgcn_permlane32_swap(T[31 - a], T[31 - a], false, false)[1];
+    const uint32_t m = lo < hi ? lo : hi;
+    th = th > m ? th : m;
   }
   return raw_floor(th);
 }
@@ -1256,20 +1289,17 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Slot budget. Merges are decided once per 64-key block for the whole
-// workgroup. At the start of a block every lane holds at most kTrigger - 1
-// unmerged slots (a merge takes slots [0, 64) and leaves max(cnt - 64, 0)),
-// and a block appends at most 64, so kTrigger + 63 slots suffice (the
-// paired append writes one slot past the count, still inside them); the merge
-// moves slots [64, kBuf) to the front.
-constexpr int kTrigger = 28;
-static_assert(kTrigger + 63 <= kBuf && kBuf - 64 >= kTrigger - 1, "slot budget");
+// workgroup, and a merge takes every slot (two chunks: [0, 32) and
+// [32, kBuf)). At the start of a block every lane holds at most kTrigger - 1
+// slots, and a block appends at most 32, the last pair's second write one
+// slot past its count: kTrigger + 31 slots suffice.
+constexpr int kTrigger = 16;
+static_assert(kTrigger + 31 <= kBuf && kBuf <= 64, "slot budget");
 
-// A block's 64 scores of a lane are 32 words of two bf16: word w = 16 kt + 2 j
-// + v holds keys word_key(w) and word_key(w) + 1 of the block (tile kt,
-// elements 2j and 2j + 1 of the MFMA output, swap half v).
-__host__ __device__ constexpr int word_key(int w) {
-  return 32 * (w >> 4) + 8 * ((w >> 2) & 3) + 4 * (w & 1) + 2 * ((w >> 1) & 1);
-}
+// A block's 32 scores of a lane are 16 words of two bf16: word w = 8 kt + j
+// holds the scores of elements 2j and 2j + 1 of tile kt's accumulators, keys
+// word_key(w) + 4 (lane / 32) and the next one of the block.
+__host__ __device__ constexpr int word_key(int w) { return 32 * (w >> 3) + 8 * ((w & 7) >> 1) + 2 * (w & 1); }
 
 // Append the two scores of word p (keys key, key + 1) that can reach theta;
 // cb is the lane's slot count times the slot stride (kThreads words). Both
@@ -1289,19 +1319,6 @@ __device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* 
   s[kThreads] = r1;
   cb += (p0 ? kThreads * 4u : 0u) + (p1 ? kThreads * 4u : 0u);
 }
-
-// Words 16 KT + 2 J + {0, 1} from elements 2J, 2J + 1 of the token-set
-// accumulators A0, A1: the swap gives lane l token l's scores (element e of
-// A0 for swap half 0, of A1 for half 1).
-#define PKM_STREAM_WORDS(A0, A1, KT, J)                                                                      \
-  {                                                                                                          \
-    const auto s0_ = __builtin_amdgcn_permlane32_swap(__float_as_uint((A0)[2 * (J)]),                        \
-                                                      __float_as_uint((A1)[2 * (J)]), false, false);         \
-    const auto s1_ = __builtin_amdgcn_permlane32_swap(__float_as_uint((A0)[2 * (J) + 1]),                    \
-                                                      __float_as_uint((A1)[2 * (J) + 1]), false, false);     \
-    P[16 * (KT) + 2 * (J)] = pack2_bf16(__uint_as_float(s0_[0]), __uint_as_float(s1_[0]));                   \
-    P[16 * (KT) + 2 * (J) + 1] = pack2_bf16(__uint_as_float(s0_[1]), __uint_as_float(s1_[1]));               \
-  }
 
 // global_load_lds_dwordx4: lane i's 16 bytes at src go to LDS at dst + 16 i
 // (dst wave-uniform). Issued as inline assembly, so that the compiler's
@@ -1353,9 +1370,8 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   constexpr int BLK = kKB * HALF * 2;         // bytes per staged block
   constexpr int LOADS = BLK / 1024 / kWaves;  // 1 KB global->LDS loads per wave per block
   constexpr int STEPS = 2 * KS;               // MFMA steps per block: tile 0's k-steps, then tile 1's
-  constexpr int WPS = 32 / STEPS;             // words appended per step
   constexpr int LOOK = 4;                     // A fragments read this many steps ahead
-  static_assert(LOADS * 1024 * kWaves == BLK && CPR >= 16 && WPS * STEPS == 32, "block layout");
+  static_assert(LOADS * 1024 * kWaves == BLK && CPR >= 16 && STEPS >= kWpb, "block layout");
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* kst = smem;                                  // [2][kKB][CPR] 16-byte chunks
   uint32_t* buf = (uint32_t*)(smem + 2 * BLK) + threadIdx.x;  // slot j at buf[j * kThreads]
@@ -1371,27 +1387,25 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   const int64_t tile = blockIdx.x / (unsigned)H2;
   const int h = hc % H, c = hc / H;
   const int hk = 2 * h + c;                 // key rows (2h + c) n .. of this head-half
-  const int64_t tw = tile * kTok + 64 * w;  // first token of this wave
+  const int64_t tw = tile * kTok + 32 * w;  // first token of this wave
+  const int64_t tok = tw + (lane & 31);     // this lane's token
+  const bool live = tok < Ntok;
 
-  // B fragments: token set u is tokens tw + 32 u + lane % 32; k = 16 s + 8 (lane / 32)
-  u32x4_t bq[2][KS];
+  // B fragments: token tok; k = 16 s + 8 (lane / 32)
+  u32x4_t bq[KS];
+  {
+    const uint16_t* qr = Q + ((live ? tok : 0) * H + h) * (2 * HALF) + c * HALF + 8 * (lane >> 5);
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int64_t t = tw + 32 * u + (lane & 31);
-    const uint16_t* qr = Q + ((t < Ntok ? t : 0) * H + h) * (2 * HALF) + c * HALF + 8 * (lane >> 5);
+    for (int s = 0; s < KS; ++s) bq[s] = *(const u32x4_t*)(qr + 16 * s);
+    if (!live) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) bq[u][s] = *(const u32x4_t*)(qr + 16 * s);
-    if (t >= Ntok) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) bq[u][s] = u32x4_t{0u, 0u, 0u, 0u};
+      for (int s = 0; s < KS; ++s) bq[s] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
   // the B fragments live in accumulation registers (MFMA reads them there),
   // leaving the arch VGPRs to the selection and the A fragments
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int s = 0; s < KS; ++s) asm volatile("" : "+a"(bq[u][s]));
+  for (int s = 0; s < KS; ++s) asm volatile("" : "+a"(bq[s]));
   // byte offset of A chunk 2 s + lane / 32 in the lane's (swizzled) row, s < 8;
   // s >= 8 adds 256 (the row's second 16 chunks)
   int aoff[8];
@@ -1404,24 +1418,23 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   uint32_t T[kNet];
 #pragma unroll
   for (int i = 0; i < kNet; ++i) T[i] = 0u;
-  uint32_t P[32];
+  uint32_t P[kWpb];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) P[i] = 0u;
+  for (int i = 0; i < kWpb; ++i) P[i] = 0u;
   uint32_t cb = 0;  // slot count x slot stride in bytes
   constexpr uint32_t SB = kThreads * 4u;
-  // +inf while P holds no scores (its zero words stay below it), NaN (every
-  // score passes) from the first block's words until the first merge
-  float tau = __uint_as_float(0x7F800000u);
-  const int64_t tok = tw + lane;  // this lane's token once the scores are swapped
-  const bool live = tok < Ntok;
-  // this half's sub-score row; a NULL output (the caller asked for the other
-  // half only) writes nothing
+  // +inf until the second block's words are appended (P holds no scores, then
+  // the first block's, which are in T already); tau_first once they are
+  float tau = __uint_as_float(0x7F800000u), tau_first = 0.f;
+  // this lane's half of the sub-score row (pairs of bf16: the lane's keys
+  // 4 (lane / 32) + ... are at word 2 (lane / 32) + ...); a NULL output (the
+  // caller asked for the other half only) writes nothing
   uint32_t* srow = nullptr;
   bool write_sub = false;
   if constexpr (SUB) {
     uint32_t* out_s = c == 0 ? out_s1 : out_s2;
     write_sub = live && out_s != nullptr;
-    if (write_sub) srow = out_s + (tok * H + h) * (n / 2);
+    if (write_sub) srow = out_s + (tok * H + h) * (n / 2) + 2 * (lane >> 5);
   }
   // 0xFFFF0000 in a register: v_and_or_b32 takes it beside the scalar index
   uint32_t hi_mask = 0xFFFF0000u;
@@ -1436,8 +1449,8 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   // complete; block j + 1 is staged meanwhile. Iteration nb appends block
   // nb - 1's words. After each iteration the workgroup merges if any of its
   // lanes holds kTrigger slots (the waves decide together at the barrier, so
-  // that they merge at the same time); after the last, each wave merges until
-  // its slots are empty.
+  // that they merge at the same time); after the last, each wave merges its
+  // remaining slots.
 #pragma unroll 1
   for (int j = 0; j <= nb; ++j) {
     if (j < nb) {
@@ -1447,11 +1460,9 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
       }
       const uint32_t kprev = (uint32_t)(j - 1) * kKB;  // key base of the words being appended
       const unsigned char* ar = kcur + (lane & 31) * (CPR * 16);
-      f32x16_t X[2][2];
+      f32x16_t X[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) X[kt][u] = f32x16_t{};
+      for (int kt = 0; kt < 2; ++kt) X[kt] = f32x16_t{};
       u32x4_t A[STEPS];
 #pragma unroll
       for (int t = 0; t < LOOK; ++t)
@@ -1463,33 +1474,46 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
           const int t2 = t + LOOK;
           A[t2] = *(const u32x4_t*)(ar + (t2 / KS) * 32 * CPR * 16 + aoff[(t2 % KS) & 7] + ((t2 % KS) >> 3) * 256);
         }
-        X[kt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, A[t]),
-                                                           __builtin_bit_cast(bf16x8_t, bq[0][st]), X[kt][0], 0, 0, 0);
+        X[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, A[t]),
+                                                        __builtin_bit_cast(bf16x8_t, bq[st]), X[kt], 0, 0, 0);
 #pragma unroll
-        for (int q = 0; q < WPS; ++q)
-          append_pair(P[t * WPS + q], kprev + word_key(t * WPS + q), buf, cb, tau, hi_mask);
-        X[kt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, A[t]),
-                                                           __builtin_bit_cast(bf16x8_t, bq[1][st]), X[kt][1], 0, 0, 0);
+        for (int q = (t * kWpb) / STEPS; q < ((t + 1) * kWpb) / STEPS; ++q)
+          append_pair(P[q], kprev + word_key(q), buf, cb, tau, hi_mask);
         if (t >= KS) {
           // tile 0 is complete: its words replace the appended ones
 #pragma unroll
-          for (int jj = ((t - KS) * 8) / KS; jj < ((t - KS + 1) * 8) / KS; ++jj) PKM_STREAM_WORDS(X[0][0], X[0][1], 0, jj);
+          for (int jj = ((t - KS) * 8) / KS; jj < ((t - KS + 1) * 8) / KS; ++jj)
+            P[jj] = pack2_bf16(X[0][2 * jj], X[0][2 * jj + 1]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) PKM_STREAM_WORDS(X[1][0], X[1][1], 1, jj);
+      for (int jj = 0; jj < 8; ++jj) P[8 + jj] = pack2_bf16(X[1][2 * jj], X[1][2 * jj + 1]);
       if constexpr (SUB) {
         if (write_sub) {
 #pragma unroll
-          for (int q = 0; q < 32; ++q) srow[(j * kKB + word_key(q)) >> 1] = canon_pair(P[q]);
+          for (int q = 0; q < kWpb; ++q) srow[(j * kKB + word_key(q)) >> 1] = canon_pair(P[q]);
         }
       }
-      if (j == 0) tau = __uint_as_float(0xFFFFFFFFu);
+      if (j == 0) {
+        // the first block's 32 scores of the lane, sorted, are T
+#pragma unroll
+        for (int q = 0; q < kWpb; ++q) {
+          T[2 * q] = raw_key((P[q] << 16) | (0xFFFFu - (uint32_t)word_key(q)));
+          T[2 * q + 1] = raw_key((P[q] & hi_mask) | (0xFFFEu - (uint32_t)word_key(q)));
+        }
+        sort32_desc(T, std::make_index_sequence<191>{});
+        tau_first = tau_of(T);
+        // zero words (tiny positive raw words) stay below tau = +inf, where a
+        // word holding an infinity (a NaN raw word) would pass again
+#pragma unroll
+        for (int q = 0; q < kWpb; ++q) P[q] = 0u;
+      }
     } else {
 #pragma unroll
-      for (int q = 0; q < 32; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, cb, tau, hi_mask);
+      for (int q = 0; q < kWpb; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, cb, tau, hi_mask);
     }
+    if (j == 1) tau = tau_first;
     bool need;
     if (j < nb) {
       const bool mine = __builtin_amdgcn_ballot_w64(cb >= kTrigger * SB) != 0;
@@ -1503,30 +1527,45 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
     } else {
       need = __builtin_amdgcn_ballot_w64(cb > 0u) != 0;
     }
-    while (need) {
+    if (need) {
+      // every slot: [0, 32), then [32, kBuf) where a lane holds more than 32
       const uint32_t cnt = cb / SB;
       merge_span<0>(T, buf, cnt);
       if (__builtin_amdgcn_ballot_w64(cnt > 32u) != 0) merge_span<32>(T, buf, cnt);
-#pragma unroll
-      for (int q = 0; q < kBuf - 64; ++q) buf[q * kThreads] = buf[(64 + q) * kThreads];
-      cb = cnt > 64u ? cb - 64u * SB : 0u;
-      tau = tau_of(T, knn);
-      need = j == nb && __builtin_amdgcn_ballot_w64(cb > 0u) != 0;
+      cb = 0u;
+      if (j < nb) tau = tau_of(T);
     }
   }
 
-  // Outputs through a [64][33] word tile per wave (LDS is idle once every wave
+  // The token's list: the upper lane's keys get their true index (0xFFFF -
+  // index is 4 lower), then both lanes merge the pair's lists,
+  // max(T_lo[i], T_hi[31 - i]) sorted by the cleaner (the same in both).
+  const uint32_t fix = (lane >> 5) ? 4u : 0u;
+#pragma unroll
+  for (int i = 0; i < kNet; ++i) T[i] = T[i] != 0u ? T[i] - fix : 0u;
+#pragma unroll
+  for (int i = 0; i < kNet / 2; ++i) {
+    const auto a = __builtin_amdgcn_permlane32_swap(T[i], T[i], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(T[31 - i], T[31 - i], false, false);
+    T[i] = a[0] > b[1] ? a[0] : b[1];       // max(T_lo[i], T_hi[31 - i])
+    T[31 - i] = b[0] > a[1] ? b[0] : a[1];  // max(T_lo[31 - i], T_hi[i])
+  }
+  clean32_desc(T, std::make_index_sequence<80>{});
+
+  // Outputs through a [32][33] word tile per wave (LDS is idle once every wave
   // has merged), so that a store covers two tokens' contiguous rows: lane i
   // writes word i % 32 of token 2 m + i / 32 of the wave.
   __syncthreads();
-  uint32_t* tp = (uint32_t*)smem + w * (64 * 33);
+  uint32_t* tp = (uint32_t*)smem + w * (32 * 33);
+  if (lane < 32) {
 #pragma unroll
-  for (int q = 0; q < kNet; ++q) tp[lane * 33 + q] = key_to_okey16(T[q]);
+    for (int q = 0; q < kNet; ++q) tp[lane * 33 + q] = key_to_okey16(T[q]);
+  }
   __builtin_amdgcn_wave_barrier();
   int64_t* oi = c == 0 ? out_i1 : out_i2;
   const int q = lane & 31;
 #pragma unroll 4
-  for (int m = 0; m < 32; ++m) {
+  for (int m = 0; m < 16; ++m) {
     const int tl = 2 * m + (lane >> 5);
     const int64_t t = tw + tl;
     const uint32_t k = tp[tl * 33 + q];
@@ -1537,7 +1576,6 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   }
 }
 #undef PKM_STREAM_STAGE
-#undef PKM_STREAM_WORDS
 
 __host__ inline size_t lds_bytes(int half) {
   return (size_t)2 * kKB * half * 2 + (size_t)kBuf * kThreads * 4 + 2 * kWaves * 4;

@@ -233,69 +233,91 @@ def test_merge_step_keeps_the_best_32_sorted():
 # --- the per-token stream ------------------------------------------------------
 
 def word_key(w: int) -> int:
-    return 32 * (w >> 4) + 8 * ((w >> 2) & 3) + 4 * (w & 1) + 2 * ((w >> 1) & 1)
+    return 32 * (w >> 3) + 8 * ((w & 7) >> 1) + 2 * (w & 1)
 
 
-# a block's key order: words in order, each its two keys
-BLOCK_ORDER = [word_key(w) + v for w in range(K_KB // 2) for v in range(2)]
+K_WPB = K_KB // 4  # words per block and lane
+K_SPLITS = (12, 16, 20)
+# a block's keys of each lane of a token (lane half hl = lane / 32), in append
+# order: words in order, each its two keys; the raw words carry index' = key - 4 hl
+BLOCK_KEYS = [[word_key(w) + 4 * hl + v for w in range(K_WPB) for v in range(2)] for hl in (0, 1)]
 
 
 def stream_select(bits: np.ndarray, knn: int, stats: dict | None = None) -> np.ndarray:
     """The kernel's selection for the tokens of one workgroup (rows of bits
     [tokens <= 256, n], bf16 scores of one half): returns the okey16-form
-    lists [tokens, knn] (okey16 << 16 | 0xFFFF - index)."""
+    lists [tokens, knn] (okey16 << 16 | 0xFFFF - index). Lane t * 2 + hl here
+    is lane t % 32 + 32 hl of wave t // 32 in the kernel."""
     L, n = bits.shape
-    assert L <= K_TOK and n % K_KB == 0 and set(BLOCK_ORDER) == set(range(K_KB))
+    assert L <= K_TOK and n % K_KB == 0
+    assert sorted(BLOCK_KEYS[0] + BLOCK_KEYS[1]) == list(range(K_KB))
     nb = n // K_KB
-    T = np.zeros((L, K_NET), dtype=U32)
-    buf = np.zeros((L, K_BUF), dtype=U32)
-    cnt = np.zeros(L, dtype=np.int64)
-    lanes = np.arange(L)
-    tau = np.full(L, np.inf, dtype=np.float32)
+    NL = 2 * L
+    hl = np.arange(NL) % 2
+    tok = np.arange(NL) // 2
+    T = np.zeros((NL, K_NET), dtype=U32)
+    buf = np.zeros((NL, K_BUF), dtype=U32)
+    cnt = np.zeros(NL, dtype=np.int64)
+    lanes = np.arange(NL)
+    tau = np.full(NL, np.inf, dtype=np.float32)
 
-    def merge_chunk(j0):
-        C = raw_key(buf[:, j0:j0 + 32])
+    def merge_chunk(j0, rows, width_rule):
+        C = np.zeros((NL, 32), dtype=U32)
+        hi = min(j0 + 32, K_BUF)
+        C[:, :hi - j0] = raw_key(buf[:, j0:hi])
         C = np.where(np.arange(j0, j0 + 32)[None, :] < cnt[:, None], C, U32(0)).astype(U32)
-        for w0 in range(0, L, 64):  # each wave picks its chunk width
-            r = slice(w0, w0 + 64)
-            if np.any(cnt[r] > j0 + 16):
+        for w0 in range(0, NL, 64):  # each wave picks its chunk width
+            r = np.intersect1d(np.arange(w0, min(w0 + 64, NL)), rows)
+            if r.size == 0:
+                continue
+            if width_rule(r):
                 T[r] = run_net(np.maximum(T[r], run_net(C[r], SORT32)[:, ::-1]), CLEAN32)
-            else:  # 16 wide: slots j0 + 16 .. are past every count of the wave
+            else:  # 16 wide: slots j0 + 16 .. are past every count of the wave (or the buffer)
+                assert np.all(cnt[r] <= j0 + 16)
                 C16 = run_net(C[r, :16], SORT16)
                 M = T[r].copy()
                 M[:, 16:] = np.maximum(M[:, 16:], C16[:, ::-1])
                 T[r] = run_net(M, CLEAN32)
             if stats is not None:
-                key = "w32" if np.any(cnt[r] > j0 + 16) else "w16"
+                key = "w32" if width_rule(r) else "w16"
                 stats[key] = stats.get(key, 0) + 1
 
     def tau_of():
-        th = np.min(np.where(np.arange(K_NET)[None, :] < knn, T, U32(M32)), axis=1)
+        th = T[:, K_NET - 1].astype(np.int64)
+        lo, hi_ = T[0::2].astype(np.int64), T[1::2].astype(np.int64)  # the token's two lanes
+        bound = np.max(np.stack([np.minimum(lo[:, a - 1], hi_[:, 31 - a]) for a in K_SPLITS]), axis=0)
+        th = np.maximum(th, np.repeat(bound, 2))
         return raw_floor(th)
 
     def merge(rows):
-        nonlocal T, cnt
-        keep_T = T.copy()
-        merge_chunk(0)
-        if np.any(cnt[rows] > 32):
-            merge_chunk(32)
-        buf[rows, :K_BUF - 64] = buf[rows, 64:]
-        sel = np.zeros(L, dtype=bool)
-        sel[rows] = True
-        T = np.where(sel[:, None], T, keep_T)
-        cnt = np.where(sel, np.maximum(cnt - 64, 0), cnt)
-        tau[sel] = tau_of()[sel]
+        # every slot: [0, 32), then [32, kBuf) in the waves where a lane holds more than 32
+        merge_chunk(0, rows, lambda r: np.any(cnt[r] > 16))
+        second = np.array([w for w in rows if np.any(cnt[(w // 64) * 64:(w // 64) * 64 + 64] > 32)], dtype=np.int64)
+        if second.size:
+            merge_chunk(32, second, lambda r: False)
+        cnt[rows] = 0
 
+    tau_first = None
     for j in range(nb + 1):
+        if j == 0:
+            # the first block's 32 scores of a lane, sorted, are T
+            keys = np.array(BLOCK_KEYS[0])  # index' of the lane's append positions
+            tk = keys[None, :] + 4 * hl[:, None]
+            r = raw_words(bits[tok[:, None], tk], np.broadcast_to(keys, tk.shape))
+            T[:] = run_net(raw_key(r), SORT32)
+            tau_first = tau_of()
         if j >= 1:
             # the appends of block j - 1's words, during block j (or the drain)
-            for key0, key1 in zip(BLOCK_ORDER[0::2], BLOCK_ORDER[1::2]):
+            for q in range(K_WPB):
+                k0 = (j - 1) * K_KB + word_key(q)  # index' of the word's first score
                 # a word's two scores: slot cnt takes the first if it passes,
                 # else the second; slot cnt + 1 takes the second (both are
                 # written whether or not they count)
-                k0, k1 = (j - 1) * K_KB + key0, (j - 1) * K_KB + key1
-                r0 = raw_words(bits[:, k0], np.full(L, k0))
-                r1 = raw_words(bits[:, k1], np.full(L, k1))
+                # (block 0's words are zeroed once sorted into T)
+                w0_ = np.zeros(NL, np.int64) if j == 1 else bits[tok, k0 + 4 * hl]
+                w1_ = np.zeros(NL, np.int64) if j == 1 else bits[tok, k0 + 4 * hl + 1]
+                r0 = raw_words(w0_, np.full(NL, k0))
+                r1 = raw_words(w1_, np.full(NL, k0 + 1))
                 p0 = ~(r0.view(np.float32) < tau)
                 p1 = ~(r1.view(np.float32) < tau)
                 assert cnt.max() + 2 <= K_BUF, "both slots of a word inside the buffer"
@@ -304,19 +326,25 @@ def stream_select(bits: np.ndarray, knn: int, stats: dict | None = None) -> np.n
                 cnt += p0.astype(np.int64) + p1.astype(np.int64)
                 if stats is not None:
                     stats["max_cnt"] = max(stats.get("max_cnt", 0), int(cnt.max()))
-        if j == 0:
-            tau[:] = np.nan  # from the first block's words until the first merge
+        if j == 1:
+            tau[:] = tau_first  # block 0's words (in T, then zeroed) were appended against +inf
         if j < nb:
             if np.any(cnt >= K_TRIGGER):  # the workgroup merges together
                 merge(lanes)
+                tau[:] = tau_of()
             assert cnt.max() <= K_TRIGGER - 1, "slot budget: a block starts with <= kTrigger - 1 slots"
         else:
-            for w0 in range(0, L, 64):  # each wave drains its own slots
+            for w0 in range(0, NL, 64):  # each wave drains its own slots
                 rows = lanes[w0:w0 + 64]
-                while np.any(cnt[rows] > 0):
+                if np.any(cnt[rows] > 0):
                     merge(rows)
-    out = key_to_okey16(T[:, :knn])
-    return out
+            assert cnt.max() == 0
+    # the token's list: true indices (0xFFFF - index is 4 lower in the upper
+    # lane), then the pair merge max(T_lo[i], T_hi[31 - i]) and the cleaner
+    Tt = np.where((hl[:, None] == 1) & (T != 0), T.astype(np.int64) - 4, T.astype(np.int64)).astype(U32)
+    lo, hi_ = Tt[0::2], Tt[1::2]
+    M = run_net(np.maximum(lo, hi_[:, ::-1]), CLEAN32)
+    return key_to_okey16(M[:, :knn])
 
 
 def check_rows(bits: np.ndarray, knn: int):
@@ -382,36 +410,38 @@ def test_stream_key_orders_that_fill_slots_fastest():
 def test_stream_slot_budget_worst_case():
     # Lanes that reach kTrigger - 1 unmerged slots at the start of a block
     # (too few for a merge) and then append a whole block: the most slots a
-    # lane can hold. Scores are bf16 bits: 0x3F80 + rank is an increasing run
-    # of positive values, so a key at a higher rank than every earlier one
-    # passes; 0xBF80 (-1.0) is below everything, so once a merge has set
-    # theta it never passes (before the first merge every score passes).
-    rng = np.random.default_rng(40)
-    first = -(-K_TRIGGER // K_KB)  # blocks of all-passing scores until the first merge
-    left = first * K_KB - 64  # slots the first merge leaves
-    assert 0 <= left < K_TRIGGER
+    # lane can hold. Scores are bf16 bits: 0x3F80 + 2 rank + lane half is an
+    # increasing run of positive values over both lanes of a token, so a
+    # passing position's score is above every earlier score of the token and
+    # passes whatever theta is; 0xBF80 (-1.0) is below everything, so once a
+    # merge has set theta it never passes (before the first merge every score
+    # passes).
+    per_blk = 2 * K_WPB  # scores of a block per lane
+    first = -(-K_TRIGGER // per_blk)  # blocks of all-passing scores until the first merge
+    assert first * per_blk >= K_TRIGGER
     fill = []  # passing counts of the following blocks up to kTrigger - 1 slots
-    while left + sum(fill) < K_TRIGGER - 1:
-        fill.append(min(K_KB, K_TRIGGER - 1 - left - sum(fill)))
-    nblk = first + len(fill) + 3
+    while sum(fill) < K_TRIGGER - 1:
+        fill.append(min(per_blk, K_TRIGGER - 1 - sum(fill)))
+    nblk = first + len(fill) + 4
     n, L = K_KB * nblk, 256
+    rng = np.random.default_rng(40)
     for knn in (1, 32):
-        bits = np.empty((L, n), dtype=np.int64)
+        bits = np.full((L, n), 0xBF80, dtype=np.int64)
         for t in range(L):
             rank = 0
             for b in range(nblk):
-                seg = np.full(K_KB, 0xBF80, dtype=np.int64)
-                cnt_b = K_KB if (b < first or b >= first + len(fill)) else fill[b - first]
-                pos = np.sort(rng.choice(K_KB, cnt_b, replace=False))
-                seg[pos] = 0x3F80 + rank + np.arange(cnt_b)
-                rank += cnt_b
-                bits[t, b * K_KB:(b + 1) * K_KB] = seg
-            if t % 2:  # half of the lanes: the full blocks after the fill reversed
-                tail = bits[t, (first + len(fill)) * K_KB:]
-                bits[t, (first + len(fill)) * K_KB:] = tail[::-1]
+                if b < first or b >= first + len(fill):
+                    cnt_b = per_blk if (b < first + len(fill) + 1 or t % 2 == 0) else 0
+                else:
+                    cnt_b = fill[b - first]
+                pos = np.sort(rng.choice(per_blk, cnt_b, replace=False))
+                for p_ in pos:
+                    for h in (0, 1):
+                        bits[t, b * K_KB + BLOCK_KEYS[h][p_]] = 0x3F80 + 2 * (rank + p_) + h
+                rank += per_blk
         stats = {}
         lists = stream_select(bits, knn, stats)
-        assert stats["max_cnt"] == K_TRIGGER - 1 + K_KB <= K_BUF, stats
+        assert stats["max_cnt"] == K_TRIGGER - 1 + per_blk <= K_BUF, stats
         check_rows(bits, knn)
         assert lists.shape == (L, knn)
 
