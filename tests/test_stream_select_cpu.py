@@ -3,8 +3,10 @@ checked against the oracle's stable top-k.
 
 pkm_score_topk's streaming kernel (modelos_amd/csrc/score_topk.hip, namespace
 stream) selects each token's per-half top-knn of bfloat16 scores without
-sorting a row: a sorted running list T of 32 unique keys per token, an
-admission test of every score against a float threshold, LDS slots for the
+sorting a row: each token's keys are split between two lanes, each with a
+sorted running list T of 32 unique keys, a threshold bound shared by the two
+lanes and a final merge of their lists; an admission test of every score
+against a float threshold, LDS slots for the
 admitted scores, merges of 32-slot chunks through Batcher's odd-even merge
 sort and a half-cleaner cascade, decided for 256 tokens at a time. The GPU
 tests check the kernel's outputs; this file checks the scheme itself, on many
