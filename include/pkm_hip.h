@@ -314,10 +314,10 @@ int pkm_fw_sgd_update_bwd(const void* d_new_values, const void* d_scaled_grad, c
  *   c                 = grad_clip ? clamp(scaled_grad, -1, 1) : scaled_grad
  *   new_values[r, :]  = dtype(values - dtype(lr * dtype(c + dtype(weight_decay * values))))
  * with pkm_fw_sgd_update's rounding steps. Every row is written (untouched
- * rows: g = 0). Optional outputs (NULL = not written): grad_psw as in
- * pkm_eb_bwd; counts [num_rows] int32 = cnt; row_sumsq [num_rows] float32 =
- * sum over the row of scaled_grad^2 (the squared norm of the scaled gradient
- * is their sum).
+ * rows: g = 0). new_values must not overlap values. Optional outputs (NULL =
+ * not written): scaled_grad; grad_psw as in pkm_eb_bwd; counts [num_rows]
+ * int32 = cnt; row_sumsq [num_rows] float32 = sum over the row of
+ * scaled_grad^2 (the squared norm of the scaled gradient is their sum).
  *
  * Replaces, for the values (fwpkm/fwpkm.py:333-365 with update_fw_param,
  * 266-272), the table gradient of autograd.grad(mem_loss, values) through

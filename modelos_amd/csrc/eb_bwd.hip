@@ -91,8 +91,8 @@ __device__ __forceinline__ float sgd_step(const float* acc, const float* p, uint
 #pragma clang fp contract(on)
 
 // The SGD epilogue of one row held by LPG lanes (the lane's VPL vectors at
-// element col0 + v * LPG * EPV): stores gs and p', and from the group's first
-// lane the row's count and sum of gs^2.
+// element col0 + v * LPG * EPV): stores gs (unless S.scaled_grad is NULL) and
+// p', and from the group's first lane the row's count and sum of gs^2.
 template <typename TW, int LPG, int VPL>
 __device__ __forceinline__ void sgd_store_row(const float* acc, const float* p, uint32_t cnt, int64_t row, int64_t D,
                                               int64_t col0, int glane, const SgdArgs& S) {
@@ -104,7 +104,7 @@ __device__ __forceinline__ void sgd_store_row(const float* acc, const float* p, 
   TW* prow = (TW*)S.new_values + row * D + col0;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
-    st16_nt(grow + v * LPG * EPV, VecTraits<TW>::pack(o_g + v * EPV));
+    if (S.scaled_grad != nullptr) st16_nt(grow + v * LPG * EPV, VecTraits<TW>::pack(o_g + v * EPV));
     st16_nt(prow + v * LPG * EPV, VecTraits<TW>::pack(o_p + v * EPV));
   }
   ss = group_sum<LPG>(ss);
@@ -1597,8 +1597,14 @@ extern "C" int pkm_eb_bwd_sgd(const void* values, int64_t num_rows, int64_t dim,
                         workspace_bytes, &c, &l);
   if (rc != PKM_OK) return rc;
   const int64_t N = bags * bag_size;
-  PKM_REQUIRE(num_rows == 0 || (values != nullptr && new_values != nullptr && scaled_grad != nullptr),
-              PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd_sgd: null values / new_values / scaled_grad");
+  PKM_REQUIRE(num_rows == 0 || (values != nullptr && new_values != nullptr), PKM_ERR_INVALID_ARGUMENT,
+              "pkm_eb_bwd_sgd: null values / new_values");
+  {
+    const uintptr_t tb = (uintptr_t)num_rows * (uintptr_t)dim * (dtype == PKM_DTYPE_F32 ? 4u : 2u);
+    const uintptr_t v0 = (uintptr_t)values, n0 = (uintptr_t)new_values;
+    PKM_REQUIRE(num_rows == 0 || n0 + tb <= v0 || v0 + tb <= n0, PKM_ERR_INVALID_ARGUMENT,
+                "pkm_eb_bwd_sgd: new_values overlaps values");
+  }
   PKM_REQUIRE(N == 0 || grad_out != nullptr, PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd_sgd: null grad_out");
   PKM_REQUIRE(grad_psw == nullptr || psw != nullptr, PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd_sgd: grad_psw given without psw");

@@ -107,6 +107,8 @@ class _SgdValueUpdate(torch.autograd.Function):
                   _lib.stream_of(p2.device))
         ctx.save_for_backward(gs, counts)
         ctx.scale, ctx.lr, ctx.wd, ctx.clip = scale, lr, wd, clip
+        # an output no loss reaches gets None, not a [K, D] tensor of zeros
+        ctx.set_materialize_grads(False)
         return new, gs
 
     @staticmethod
@@ -167,6 +169,9 @@ class _FusedValueStep(torch.autograd.Function):
         ctx.save_for_backward(gs, counts, idx, w, g)
         ctx.scale, ctx.lr, ctx.wd, ctx.clip = scale, lr, wd, clip
         ctx.mark_non_differentiable(sumsq)
+        # the scaled gradient usually reaches no loss: None, not a [K, D] of zeros
+        # (which the double backward would also read)
+        ctx.set_materialize_grads(False)
         return new, gs, sumsq
 
     @staticmethod
@@ -198,6 +203,45 @@ class _FusedValueStep(torch.autograd.Function):
                       _lib.stream_of(gs.device))
         return (d_values, None, d_psw if ctx.needs_input_grad[2] else None,
                 d_hyp if ctx.needs_input_grad[3] else None, None, None, None, None)
+
+
+def _final_values_step(values, indices, psw, d_hyp, scale, lr, wd, clip, out):
+    """The values step of an update whose result is only stored (the last
+    chunk's: no loss differentiates through it): pkm_eb_bwd_sgd writing the
+    new table straight into `out` (the values parameter, which must not share
+    storage with `values`), without the scaled gradient. Returns the per-row
+    sums of the scaled gradient's squares."""
+    from ..embedding_bag import eb_backward_workspace_bytes
+
+    with torch.no_grad():
+        V = _aligned(values.detach())
+        idx = indices.contiguous()
+        w = psw.detach().contiguous()
+        g = _aligned(d_hyp.detach().to(V.dtype))
+        K, D = V.shape
+        B, L = idx.shape
+        sumsq = torch.empty(K, dtype=torch.float32, device=V.device)
+        ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=V.device)
+        _lib.call("pkm_eb_bwd_sgd", _lib.ptr(V), K, D, _lib.dtype_code(V), _lib.ptr(idx), _lib.ptr(w),
+                  _lib.dtype_code(w), _lib.ptr(g), B, L, float(scale), float(lr), float(wd), int(bool(clip)),
+                  _lib.ptr(out), None, None, None, _lib.ptr(sumsq), _lib.ptr(ws), ws_bytes,
+                  _lib.stream_of(V.device))
+    return sumsq
+
+
+def _storable_into(values: torch.Tensor, param: torch.Tensor) -> bool:
+    """Whether the last values step can write the parameter directly: same
+    shape and dtype, a 16-byte aligned contiguous parameter, no shared storage
+    with the table the step reads."""
+    if param.shape != values.shape or param.dtype != values.dtype or not param.is_contiguous():
+        return False
+    if param.data_ptr() % 16 or param.device != values.device:
+        return False
+    a0, a1 = param.data_ptr(), param.data_ptr() + param.numel() * param.element_size()
+    b0 = values.untyped_storage().data_ptr()
+    b1 = b0 + values.untyped_storage().nbytes()
+    return a1 <= b0 or b1 <= a0
 
 
 def sgd_value_update(p: torch.Tensor, g: torch.Tensor, indices: torch.Tensor, scale: float, lr: float,
@@ -452,12 +496,18 @@ class FastWeightProductKeyMemory(nn.Module):
         return nvec <= 64 and (nvec & (nvec - 1)) == 0 or (nvec % 64 == 0 and nvec // 64 in (1, 2, 4, 8))
 
     def _update_fw_fused(self, fw_named_params: OrderedDict, num_samples: int, retrieval: dict,
-                         mem_loss: torch.Tensor, addr_loss: Optional[torch.Tensor] = None):
+                         mem_loss: torch.Tensor, addr_loss: Optional[torch.Tensor] = None,
+                         store_into: Optional[torch.Tensor] = None):
         """update_fw with the values step fused into the value backward: the
         same step (fwpkm.py:333-365) and outer gradients, the table gradient
         and the dense normalisation / SGD passes replaced by one kernel.
         Returns (updated params, [scaled gradient of each param], [squared
-        norm of each]: the values' from the kernel's row sums)."""
+        norm of each]: the values' from the kernel's row sums).
+
+        store_into: the values parameter, for the last chunk's step, whose
+        result is only stored (fwpkm.py:540-545) and never differentiated: the
+        new table is written into it directly, with no graph and no scaled
+        gradient (its entry in the returned gradients is None)."""
         mem_loss = mem_loss * 0.5
         names = list(fw_named_params.keys())
         params = list(fw_named_params.values())
@@ -466,12 +516,22 @@ class FastWeightProductKeyMemory(nn.Module):
         else:
             addr_grads = [None] * len(params)
         hyp = retrieval["retireved_values"]
-        (d_hyp,) = torch.autograd.grad(mem_loss, hyp, create_graph=self.training)
+        if store_into is None:
+            (d_hyp,) = torch.autograd.grad(mem_loss, hyp, create_graph=self.training)
+        else:
+            (d_hyp,) = torch.autograd.grad(mem_loss, hyp, retain_graph=True)
         scale = num_samples * self.v_dim * self.topk * self.heads
         flat = retrieval["indices"].reshape(hyp.shape[0], -1)
         psw = retrieval["normed_scores"].reshape(hyp.shape[0], -1)
         scaled, updated, norms2 = [], [], []
         for i, (n, p) in enumerate(zip(names, params)):
+            if n == "values" and store_into is not None:
+                sumsq = _final_values_step(p, flat, psw, d_hyp, scale, self.learning_rate, self.weight_decay,
+                                           self.grad_clip, store_into)
+                scaled.append(None)
+                updated.append(store_into)
+                norms2.append(sumsq.sum())
+                continue
             if n == "values":
                 new_p, g_scaled, sumsq = _FusedValueStep.apply(p, flat, psw, d_hyp, scale, self.learning_rate,
                                                                self.weight_decay, self.grad_clip)
@@ -526,7 +586,7 @@ class FastWeightProductKeyMemory(nn.Module):
     def _store_fast_weights(self, fw_named_params):
         with torch.no_grad():
             for n, p in self.named_parameters():
-                if n in fw_named_params:
+                if n in fw_named_params and fw_named_params[n] is not p:  # (the last step may have written p)
                     p.data.copy_(fw_named_params[n].data.to(p.dtype))
 
     # ---- chunked forward --------------------------------------------------------------------
@@ -544,7 +604,8 @@ class FastWeightProductKeyMemory(nn.Module):
             params = self.get_fw_named_params()
             n_params = len(params)
             fused = self._fused_values_step(params["values"])
-            for start, end in _chunks(T, chunk_size, chunk_size):
+            bounds = _chunks(T, chunk_size, chunk_size)
+            for ci, (start, end) in enumerate(bounds):
                 cT = end - start
                 cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
                 r = self.retrieve_values(q[:, start:end, :].contiguous(), params)
@@ -558,8 +619,10 @@ class FastWeightProductKeyMemory(nn.Module):
                 mem_losses, addr_loss = self._losses(u_hyp, u_ref, u_w, u_mask, r)
                 num_samples = (u_mask > 0).sum().item() if u_mask is not None else B * cT
                 if fused:
+                    # the last step's table is only stored: written into the parameter when it can be
+                    last = ci == len(bounds) - 1 and _storable_into(params["values"], self.values)
                     params, grads, norms2 = self._update_fw_fused(params, num_samples, r, mem_losses.mean(),
-                                                                  addr_loss)
+                                                                  addr_loss, self.values if last else None)
                 else:
                     params, grads = self.update_fw(params, num_samples, r["indices"], mem_losses.mean(), addr_loss)
                     norms2 = [None] * len(grads)
@@ -568,8 +631,8 @@ class FastWeightProductKeyMemory(nn.Module):
                                       scores=cgates.view(B, cT, -1))
                 with torch.no_grad():
                     # each param's gradient norm (the values' from the kernel's row sums when fused)
-                    step_norms.append([torch.sqrt(n2).to(g.dtype) if n2 is not None else g.detach().norm()
-                                       for g, n2 in zip(grads, norms2)])
+                    step_norms.append([torch.sqrt(n2).to(p.dtype) if n2 is not None else g.detach().norm()
+                                       for g, n2, p in zip(grads, norms2, params.values())])
                 losses.append(mem_losses.view(B, -1).detach())
                 if self.addr_loss is not None:
                     addr_losses.append(addr_loss.detach())
