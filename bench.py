@@ -633,6 +633,55 @@ FWPKM = dict(mem_k_dim=256, mem_v_dim=1024, mem_heads=4, mem_topk=16, mem_n_subk
              qk_score_type="idw", learning_rate=0.1, addr_loss="me")
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X fp32 matrix
+
+
+def fwpkm_rooflines(kern, dtype_bytes, distinct_rows, bags=4096, bag_size=64, K=1 << 18, D=1024, H=4, n=512,
+                    k_dim=256, chunks=2, clip=False):
+    """Per-call algorithmic work of the fast-weight step's library kernels,
+    achieved / peak from their measured per-step times, and the step's floor
+    (every library call at its roofline, the torch glue at zero: a lower
+    bound). Per chunk: bags = 8 sequences x 512 tokens, bag_size = heads x
+    knn lookups into K x D; psw in the table dtype.
+      pkm_eb_fwd (gather):     N*D*s + N*(8 + s) + B*D*s
+      pkm_eb_bwd (outer):      B*D*s + U*D*s + K*D*s + N*(8 + s) + N*s
+      pkm_eb_bwd_sgd (step):   every table row read and the new one written
+                               (2*K*D*s), the scaled gradient for every step
+                               but the last (K*D*s), B*D*s + N*(8 + s), 8*K
+      pkm_eb_bwd2_sgd:         the double backward's A_bwd2, N*D*s + 2*B*D*s
+                               + N*(8 + 2*s), plus N*D*s of scaled-gradient
+                               rows under grad_clip
+      pkm_score_topk:          2 * tokens * heads * 2 * n * k_dim/2 flops on
+                               the matrix peak of the dtype"""
+    s = dtype_bytes
+    N, B = bags * bag_size, bags
+    U = distinct_rows
+    per_call = {
+        "pkm_eb_fwd": N * D * s + N * (8 + s) + B * D * s,
+        "pkm_eb_bwd": B * D * s + U * D * s + K * D * s + N * (8 + s) + N * s,
+        "pkm_eb_bwd2_sgd": N * D * s * (2 if clip else 1) + 2 * B * D * s + N * (8 + 2 * s),
+    }
+    sgd_total = chunks * (2 * K * D * s + B * D * s + N * (8 + s) + 8 * K) + (chunks - 1) * K * D * s
+    flops = score_flops(bags, H, n, k_dim)
+    peak_tf = MFMA_F32_PEAK_TFLOPS if s == 4 else MFMA_BF16_PEAK_TFLOPS
+    out, floor = {}, 0.0
+    for name, v in kern.items():
+        calls, ms = v["calls_per_step"], v["ms_per_step"]
+        if name in per_call:
+            work, unit, peak = per_call[name] * calls, "GB/s", HBM_PEAK_GBS
+        elif name == "pkm_eb_bwd_sgd":
+            work, unit, peak = sgd_total, "GB/s", HBM_PEAK_GBS
+        elif name == "pkm_score_topk":
+            work, unit, peak = flops * calls, "TFLOP/s", peak_tf
+        else:
+            continue
+        achieved = work / (ms * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
+        floor += work / (peak * (1e9 if unit == "GB/s" else 1e12)) * 1e3
+        out[name] = {"ms_per_step": ms, "work_per_step": work, "achieved": round(achieved, 2), "unit": unit,
+                     "peak": peak, "frac": round(achieved / peak, 4)}
+    return out, floor
+
+
 def cpu_baseline_fwpkm(mem, x, target, budget_s=25.0):
     """The reference's fast-weight chain as torch CPU ops (oracle.fwpkm, pinned
     to the reference's own outputs): one sequence of 1024 tokens (two chunks
@@ -705,9 +754,19 @@ def run_fwpkm(args, dev, with_cpu=None):
         lib_ms = sum(v["ms_per_step"] for v in kern.values())
         tag = "f32" if dtype == torch.float32 else "bf16"
         log(f"fwpkm {tag}: {ms:.3f} ms/step, library entry points {lib_ms:.3f} ms")
+        # distinct rows per chunk (the outer value backward reads each once), from one more forward
+        with torch.no_grad():
+            idx = mem(q=x, ref_v=target, gates=None, chunk_size=512)["indices"]
+        U = sum(int(torch.unique(idx[:, c:c + 512]).numel()) for c in (0, 512)) // 2
+        roof, floor_ms = fwpkm_rooflines(kern, 4 if dtype == torch.float32 else 2, U)
         results[tag] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(8192 / (ms * 1e-3), 1), "kernels": kern,
                         "library_ms_per_step": round(lib_ms, 4),
                         "library_frac": round(lib_ms / ms, 4),
+                        "rooflines": roof,
+                        "distinct_rows_per_chunk": U,
+                        "floor": {"ms": round(floor_ms, 4), "frac": round(floor_ms / ms, 4),
+                                  "note": "every library call at its roofline (HBM 8 TB/s on algorithmic bytes, "
+                                          "scoring at the dtype's matrix peak), the torch glue at zero"},
                         "note": "library_ms_per_step: HIP-event time of every libpkm_hip entry point per step "
                                 "(instrumented pass); the rest is the module's torch glue (losses, transforms, "
                                 "autograd bookkeeping) and hipBLASLt products"}
