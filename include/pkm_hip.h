@@ -160,6 +160,58 @@ int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int gbar_dtype,
                 const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
                 void* d_grad_out, void* d_a, void* stream);
 
+/*
+ * Marginal-entropy address loss of the fast-weight memory and the key
+ * table's gradient of it (compute_marginal_entropy / compute_addr_loss,
+ * fwpkm/fwpkm.py:117-147, 233-264, differentiated by update_fw with
+ * create_graph, fwpkm/fwpkm.py:274-367), and that gradient's derivative
+ * along a direction (its double backward).
+ *   s1, s2   [num_tokens, heads, n_keys] sub-score matrices (dtype), rows
+ *            r = t * heads + h; sel1, sel2 [num_tokens, heads, topk] int64 the
+ *            per-half top-k lists of the same retrieval, best first (row r
+ *            keeps its entries >= s[r, sel[r, topk - 1]]);
+ *   weight   addr_loss_weight: loss = weight * (-H_1 - H_2), H_c = -sum_j
+ *            pbar_j log(pbar_j + 1e-8), pbar = mean over rows of the masked
+ *            float32 softmax;
+ *   batch b = 2h + c (head h, half c), q_t the token's c-th half-query of
+ *   head h, k_j key (h, c, j), float32 products (idw only, NULL for dot):
+ *     qq [2 heads, num_tokens] |q_t|^2, kk [2 heads, n_keys] |k_j|^2,
+ *     dots [2 heads, num_tokens, n_keys] <q_t, k_j>.
+ * pkm_me_grad_fwd writes entropy[2] = (H_1, H_2), avec [2, n_keys] (d loss /
+ * d P_rj), pbar [2, n_keys], and coef [2 heads, num_tokens, n_keys] float32:
+ * idw U_tj = dS_tj / (1e-3 + d2_tj) where d2 = (qq + kk) - 2 dots > 0 (else
+ * 0), dot dS_tj, with dS the sub-scores' gradient rounded to dtype. The key
+ * gradient is then
+ *   idw: g[b, j] = 2 (sum_t coef[b, t, j] q_t - k_j sum_t coef[b, t, j]);
+ *   dot: g[b, j] = sum_t coef[b, t, j] q_t.
+ * pkm_me_grad_hvp takes, for a direction gbar [2 heads, n_keys, half] (the
+ * outer gradient of g), qg [2 heads, num_tokens, n_keys] = <q_t, gbar_j> and
+ * (idw) kg [2 heads, n_keys] = <k_j, gbar_j>, with avec and pbar from the
+ * forward, and writes the derivative of <gbar, g>: through the sub-scores as
+ * d_s1, d_s2 (dtype, every entry); with the sub-scores held fixed as the
+ * rows of ul (float32; idw [2 heads, num_tokens, 2 n_keys] = [U | lam] and
+ * lsum [2 heads, num_tokens] the row sums of lam; dot [2 heads, num_tokens,
+ * n_keys] = dS), from which
+ *   idw: d q_t = 2 (sum_j U_tj gbar_j + sum_j lam_tj k_j - lsum_t q_t),
+ *        d k_j = 2 (sum_t lam_tj q_t - k_j sum_t lam_tj - gbar_j sum_t U_tj);
+ *   dot: d q_t = sum_j dS_tj gbar_j.
+ * adot [2, n_keys] float32 is scratch. Deterministic.
+ * Limits: n_keys <= 1024, topk <= n_keys, num_tokens >= 1.
+ * workspace: pkm_me_grad_workspace_size(num_tokens, heads, n_keys) bytes.
+ */
+size_t pkm_me_grad_workspace_size(int64_t num_tokens, int64_t heads, int64_t n_keys);
+int pkm_me_grad_fwd(const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2, int dtype,
+                    int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
+                    float weight, const float* qq, const float* kk, const float* dots, float* entropy,
+                    float* coef, float* avec, float* pbar, void* workspace, size_t workspace_bytes,
+                    void* stream);
+int pkm_me_grad_hvp(const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2, int dtype,
+                    int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
+                    float weight, const float* qq, const float* kk, const float* kg, const float* dots,
+                    const float* qg, const float* avec, const float* pbar, float* adot, void* d_s1,
+                    void* d_s2, float* ul, float* lsum, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* Sub-key score of pkm_score_topk. */
 enum pkm_score_t {
   PKM_SCORE_DOT = 0, /* <q, k> */

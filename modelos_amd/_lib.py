@@ -146,6 +146,30 @@ SIGNATURES = {
             c_void_p, c_void_p, c_void_p,  # d_grad_out, d_a, stream
         ],
     ),
+    "pkm_me_grad_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "pkm_me_grad_fwd": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_void_p, c_int,  # s1, s2, sel1, sel2, dtype
+            c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, topk
+            c_int, c_float,  # score_type, weight
+            c_void_p, c_void_p, c_void_p,  # qq, kk, dots
+            c_void_p, c_void_p, c_void_p, c_void_p,  # entropy, coef, avec, pbar
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+    "pkm_me_grad_hvp": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_void_p, c_int,  # s1, s2, sel1, sel2, dtype
+            c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, topk
+            c_int, c_float,  # score_type, weight
+            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # qq, kk, kg, dots, qg
+            c_void_p, c_void_p, c_void_p,  # avec, pbar, adot
+            c_void_p, c_void_p, c_void_p, c_void_p,  # d_s1, d_s2, ul, lsum
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
     "pkm_softmax_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_softmax_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "pkm_column_sum_workspace_size": (c_size_t, [c_int64, c_int64]),
@@ -302,6 +326,8 @@ _SIZE_ARGS = {
     "pkm_score_grad_sparse": (3, 4, 5, 6),  # num_tokens, heads, n_keys, half
     "pkm_rmsnorm_fwd": (2, 3),  # rows, dim
     "pkm_rmsnorm_bwd": (4, 5),
+    "pkm_me_grad_fwd": (5, 6, 7),  # num_tokens, heads, n_keys
+    "pkm_me_grad_hvp": (5, 6, 7),
 }
 
 

@@ -16,10 +16,13 @@ update runs on gfx950 HIP kernels:
     outer loss takes through the inner gradient step);
   * update_fw: the values' SGD step (sample-count scaling, division by the
     slot access counts, optional clipping, weight decay) in one pass over the
-    table, differentiable for the outer loss.
+    table, differentiable for the outer loss;
+  * the marginal-entropy address loss and the keys' gradient of it, with its
+    own double backward (marginal_entropy), over the top-k entries of each
+    sub-score row.
 
-The losses (mean squared error, marginal entropy of the sub-key addressing)
-and the chunk loop are torch code around these kernels, with the reference's
+The mean squared error and the chunk loop are torch code around these
+kernels, with the reference's
 semantics, including its quirks: the output of a chunk is read before that
 chunk's update; the streaming path normalises the update with the forward
 chunk's indices and counts samples as B * chunk length; addr_loss=None with
@@ -42,6 +45,7 @@ from torch.nn import functional as F
 from .. import _lib
 from ..embedding_bag import _aligned, _require_device
 from ..product_keys import check_supported, product_key_topk, score_softmax
+from .marginal_entropy import addr_loss_and_key_grad, supported as _me_supported
 from .xformer_embeddingbag_grad_wrapper import xformers_embedding_bag
 
 logger = getLogger()
@@ -447,11 +451,20 @@ class FastWeightProductKeyMemory(nn.Module):
         (fwpkm.py:274-367). Returns (updated params, unclipped gradients with
         the values' one scaled). The values' step runs as one kernel pass
         (sgd_value_update); create_graph follows self.training."""
+        return self._update_fw(fw_named_params, num_samples, indices, mem_loss, addr_loss)
+
+    def _update_fw(self, fw_named_params: OrderedDict, num_samples: int, indices: torch.Tensor,
+                   mem_loss: torch.Tensor, addr_loss: Optional[torch.Tensor] = None, addr_grads=None):
+        """update_fw; addr_grads: the address loss's gradient of each param,
+        when the caller has it already (the marginal-entropy kernels): with
+        mem_grad_to_values_only it replaces the autograd pass over addr_loss."""
         mem_loss = mem_loss * 0.5
         names = list(fw_named_params.keys())
         params = list(fw_named_params.values())
         if self.mem_grad_to_values_only:
-            if addr_loss is not None:
+            if addr_grads is not None:
+                pass
+            elif addr_loss is not None:
                 addr_grads = torch.autograd.grad(addr_loss, params, create_graph=self.training, allow_unused=True)
             else:
                 addr_grads = [None] * len(params)
@@ -497,7 +510,7 @@ class FastWeightProductKeyMemory(nn.Module):
 
     def _update_fw_fused(self, fw_named_params: OrderedDict, num_samples: int, retrieval: dict,
                          mem_loss: torch.Tensor, addr_loss: Optional[torch.Tensor] = None,
-                         store_into: Optional[torch.Tensor] = None):
+                         store_into: Optional[torch.Tensor] = None, addr_grads=None):
         """update_fw with the values step fused into the value backward: the
         same step (fwpkm.py:333-365) and outer gradients, the table gradient
         and the dense normalisation / SGD passes replaced by one kernel.
@@ -507,11 +520,15 @@ class FastWeightProductKeyMemory(nn.Module):
         store_into: the values parameter, for the last chunk's step, whose
         result is only stored (fwpkm.py:540-545) and never differentiated: the
         new table is written into it directly, with no graph and no scaled
-        gradient (its entry in the returned gradients is None)."""
+        gradient (its entry in the returned gradients is None).
+
+        addr_grads: as in update_fw."""
         mem_loss = mem_loss * 0.5
         names = list(fw_named_params.keys())
         params = list(fw_named_params.values())
-        if addr_loss is not None:
+        if addr_grads is not None:
+            pass
+        elif addr_loss is not None:
             addr_grads = torch.autograd.grad(addr_loss, params, create_graph=self.training, allow_unused=True)
         else:
             addr_grads = [None] * len(params)
@@ -571,7 +588,12 @@ class FastWeightProductKeyMemory(nn.Module):
                 gates[:, :stop].contiguous() if gates is not None else None,
                 mask[:, :stop].contiguous() if mask is not None else None)
 
-    def _losses(self, hyp, ref, weights, mask, retrieval):
+    def _losses(self, hyp, ref, weights, mask, retrieval, query=None, params=None, create_graph=False):
+        """(per-example memory losses, address loss, the address loss's
+        gradient of each param or None). The gradient comes with the loss from
+        the marginal-entropy kernels when they apply (query and params given:
+        the retrieval's query and the params it read); otherwise the caller
+        differentiates the loss."""
         D = hyp.size(-1)
         mem_losses = self.compute_mem_loss(
             hyp_values=hyp.view(-1, D),
@@ -579,9 +601,29 @@ class FastWeightProductKeyMemory(nn.Module):
             loss_mask=mask.view(-1) if mask is not None else None,
             loss_weights=weights.view(-1) if weights is not None else None,
         )
+        if self._addr_kernels(retrieval, query, params):
+            addr_loss, g_keys = addr_loss_and_key_grad(
+                query, params["keys"], retrieval["all_sub_scores1"], retrieval["all_sub_scores2"],
+                retrieval["sub_indices1"], retrieval["sub_indices2"], self.heads, self.topk, self.addr_loss_weight,
+                _score_type(self.qk_score_type), create_graph)
+            return mem_losses, addr_loss, [g_keys if n == "keys" else None for n in params]
         addr_loss = self.compute_addr_loss(retrieval["sub_indices1"], retrieval["sub_indices2"],
                                            retrieval["all_sub_scores1"], retrieval["all_sub_scores2"])
-        return mem_losses, addr_loss
+        return mem_losses, addr_loss, None
+
+    def _addr_kernels(self, retrieval, query, params) -> bool:
+        """Whether the address loss and its gradient run on the
+        marginal-entropy kernels: the "me" loss with a nonzero weight, the
+        keys' gradient from it alone (mem_grad_to_values_only), one dtype for
+        the query, keys and sub-scores, sizes the kernels take."""
+        if query is None or params is None or "keys" not in params:
+            return False
+        if self.addr_loss != "me" or self.addr_loss_weight == 0.0 or not self.mem_grad_to_values_only:
+            return False
+        s1 = retrieval["all_sub_scores1"]
+        keys = params["keys"]
+        return (s1.dtype == keys.dtype == query.dtype
+                and _me_supported(self.subsize, s1.dtype, _score_type(self.qk_score_type)))
 
     def _store_fast_weights(self, fw_named_params):
         with torch.no_grad():
@@ -608,7 +650,8 @@ class FastWeightProductKeyMemory(nn.Module):
             for ci, (start, end) in enumerate(bounds):
                 cT = end - start
                 cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
-                r = self.retrieve_values(q[:, start:end, :].contiguous(), params)
+                cq = q[:, start:end, :].contiguous()
+                r = self.retrieve_values(cq, params)
                 hyp = r["retireved_values"].view(B, cT, -1)
                 # the chunk's output is read before its own update
                 outputs.append(hyp)
@@ -616,15 +659,21 @@ class FastWeightProductKeyMemory(nn.Module):
                 scores.append(r["normed_scores"].view(B, cT, -1))
                 u_hyp, u_ref, u_w, u_mask = self._update_targets(hyp, ref_v[:, start:end, :].contiguous(), cgates,
                                                                  cmask)
-                mem_losses, addr_loss = self._losses(u_hyp, u_ref, u_w, u_mask, r)
+                # the last step's result is only stored, never differentiated
+                final = ci == len(bounds) - 1
+                mem_losses, addr_loss, addr_grads = self._losses(u_hyp, u_ref, u_w, u_mask, r, query=cq,
+                                                                 params=params,
+                                                                 create_graph=self.training and not final)
                 num_samples = (u_mask > 0).sum().item() if u_mask is not None else B * cT
                 if fused:
-                    # the last step's table is only stored: written into the parameter when it can be
-                    last = ci == len(bounds) - 1 and _storable_into(params["values"], self.values)
+                    # the last step's table is written into the parameter when it can be
+                    last = final and _storable_into(params["values"], self.values)
                     params, grads, norms2 = self._update_fw_fused(params, num_samples, r, mem_losses.mean(),
-                                                                  addr_loss, self.values if last else None)
+                                                                  addr_loss, self.values if last else None,
+                                                                  addr_grads=addr_grads)
                 else:
-                    params, grads = self.update_fw(params, num_samples, r["indices"], mem_losses.mean(), addr_loss)
+                    params, grads = self._update_fw(params, num_samples, r["indices"], mem_losses.mean(), addr_loss,
+                                                    addr_grads=addr_grads)
                     norms2 = [None] * len(grads)
                 if self.ob_mode:
                     self.write_ob_log(token_ids=cids.view(B, cT), indices=r["indices"].view(B, cT, -1),
@@ -703,14 +752,17 @@ class FastWeightProductKeyMemory(nn.Module):
             updated = True
             with torch.enable_grad():
                 params = {n: p.detach().requires_grad_(True) for n, p in params.items()}
-                ru = self.retrieve_values(qq[:, :stop].contiguous(), params)
+                uq = qq[:, :stop].contiguous()
+                ru = self.retrieve_values(uq, params)
                 u_w = gq[:, :stop].contiguous() if gq is not None else None
                 u_mask = mq[:, :stop].contiguous() if mq is not None else None
-                mem_losses, addr_loss = self._losses(ru["retireved_values"], rq[:, la:].contiguous(), u_w, u_mask,
-                                                     ru)
+                mem_losses, addr_loss, addr_grads = self._losses(ru["retireved_values"], rq[:, la:].contiguous(),
+                                                                 u_w, u_mask, ru, query=uq, params=params,
+                                                                 create_graph=self.training)
                 # as the reference: samples counted as B * chunk length, slots from the forward chunk
                 num_samples = (u_mask > 0).sum().item() if u_mask is not None else B * cT
-                params, _ = self.update_fw(params, num_samples, chunk_indices, mem_losses.mean(), addr_loss)
+                params, _ = self._update_fw(params, num_samples, chunk_indices, mem_losses.mean(), addr_loss,
+                                            addr_grads=addr_grads)
                 if self.ob_mode:
                     pad = torch.zeros(iq.size(0), la, self.heads * self.topk, device=iq.device)
                     n_u = iq.size(1) - la
