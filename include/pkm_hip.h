@@ -267,6 +267,23 @@ int pkm_score_grad_dense(const int64_t* indices, const void* d_scores, int dtype
                          const void* d_sub_scores1, const void* d_sub_scores2,
                          void* d_sub_dense, void* stream);
 
+/*
+ * The idw (distance) factor of a dense sub-score gradient, for the products
+ *   dq_b = 2 (U_b @ keys_b - q_b * rowsum_b),  dkeys_b = 2 (U_b^T @ q_b - keys_b * colsum(U_b)):
+ *   U[b, t, j]   = dS[b, t, j] / (1e-3 + d2) where d2 = (qq[b, t] + kk[b, j]) - 2 dots[b, t, j] > 0, else 0
+ *   rowsum[b, t] = sum_j U[b, t, j]
+ * dS [batches, tokens, n_keys] in dtype (pkm_score_grad_dense's output, batch
+ * b = 2h + c); qq [batches, tokens] = |q_t|^2, kk [batches, n_keys] = |k_j|^2,
+ * dots [batches, tokens, n_keys] = <q_t, k_j>, float32 (the operands of the
+ * mm-based distance); U, rowsum float32, fully written.
+ *
+ * Replaces the elementwise part of cdist's autograd backward (compute_mode
+ * use_mm_for_euclid_dist) under the idw scores of
+ * FastWeightProductKeyMemory.compute_qk_scores (fwpkm/fwpkm.py:863-866).
+ */
+int pkm_idw_grad_coef(const void* dS, int dtype, const float* qq, const float* kk, const float* dots,
+                      int64_t batches, int64_t tokens, int64_t n_keys, float* U, float* rowsum, void* stream);
+
 /* Workspace bytes pkm_score_grad_sparse needs for these sizes (0 when unsupported). */
 size_t pkm_score_grad_sparse_workspace_size(int64_t num_tokens, int64_t heads, int64_t n_keys,
                                             int64_t half, int64_t knn);

@@ -97,6 +97,14 @@ SIGNATURES = {
             c_void_p, c_void_p,  # d_sub_dense, stream
         ],
     ),
+    "pkm_idw_grad_coef": (
+        c_int,
+        [
+            c_void_p, c_int, c_void_p, c_void_p, c_void_p,  # dS, dtype, qq, kk, dots
+            c_int64, c_int64, c_int64,  # batches, tokens, n_keys
+            c_void_p, c_void_p, c_void_p,  # U, rowsum, stream
+        ],
+    ),
     "pkm_score_grad_sparse_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "pkm_score_grad_sparse": (
         c_int,

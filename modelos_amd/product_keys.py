@@ -199,6 +199,19 @@ class _DenseScoreGrad(torch.autograd.Function):
         return (None, d_scores, g0 if ctx.has_sub[0] else None, g1 if ctx.has_sub[1] else None, None, None)
 
 
+def _idw_grad_coef(dS, qq, kk, dots):
+    """(U, rowsum) of pkm_idw_grad_coef: U = dS / (1e-3 + d2) where d2 =
+    (qq + kk) - 2 dots > 0, else 0, float32 [batches, tokens, n]."""
+    B, T, n = dots.shape
+    dS = dS.contiguous()
+    qq, kk, dots = qq.float().contiguous(), kk.float().contiguous(), dots.contiguous()
+    U = torch.empty((B, T, n), device=dots.device, dtype=torch.float32)
+    rs = torch.empty((B, T), device=dots.device, dtype=torch.float32)
+    _lib.call("pkm_idw_grad_coef", _lib.ptr(dS), _lib.dtype_code(dS), _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(dots), B, T,
+              n, _lib.ptr(U), _lib.ptr(rs), _lib.stream_of(dots.device))
+    return U, rs
+
+
 def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
     """dq [tokens, heads, k_dim] and dkeys [2*heads*n, half] from the dense
     sub-score gradient dS [heads, 2, tokens, n] with one pair of batched GEMMs
@@ -234,10 +247,17 @@ def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
             if torch.is_grad_enabled():
                 kf = kf + (k32 - k32.detach())
         dots = torch.bmm(q32, kf.transpose(1, 2).contiguous())
-        d2 = (q32 * q32).sum(-1)[:, :, None] + (kf * kf).sum(-1)[:, None, :] - 2.0 * dots
-        U = torch.where(d2 > 0, D.float() / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
-        dqh = 2.0 * (torch.bmm(U, kf) - q32 * U.sum(-1, keepdim=True))
-        dk = 2.0 * (torch.bmm(U.transpose(1, 2).contiguous(), q32) - kf * U.sum(1)[:, :, None])
+        if torch.is_grad_enabled():
+            d2 = (q32 * q32).sum(-1)[:, :, None] + (kf * kf).sum(-1)[:, None, :] - 2.0 * dots
+            U = torch.where(d2 > 0, D.float() / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
+            rs = U.sum(-1, keepdim=True)
+        else:
+            # the same U (and its row sums) in one pass (pkm_idw_grad_coef)
+            U, rs = _idw_grad_coef(D, (q32 * q32).sum(-1), (kf * kf).sum(-1), dots)
+            rs = rs[:, :, None]
+        dqh = 2.0 * (torch.bmm(U, kf) - q32 * rs)
+        # float32 operands: the transposed view goes to the GEMM as it is
+        dk = 2.0 * (torch.bmm(U.transpose(1, 2), q32) - kf * U.sum(1)[:, :, None])
     dq = dqh.view(heads, 2, N, half).permute(2, 0, 1, 3).reshape(N, heads, 2 * half)
     return dq, dk.reshape(keys.shape)
 
