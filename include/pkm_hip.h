@@ -121,6 +121,30 @@ int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t dim, int w
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * pkm_eb_bwd that adds into a gradient already in grad_weight instead of
+ * overwriting it:
+ *   grad_weight[r, :] = grad_weight[r, :] + T(sum_{(b,j): indices[b,j] == r} psw[b, j] * grad_out[b, :])
+ * (rounded to the table dtype T once more), rows without lookups unchanged;
+ * grad_psw as pkm_eb_bwd. The result equals pkm_eb_bwd into a separate
+ * buffer followed by an elementwise add of the two gradients, bit for bit
+ * (the sum autograd forms for a table read by two operations), without
+ * that add's pass over the table or the zero rows. Needs grad_dtype ==
+ * weight_dtype and a row split of 64 lanes (dim >= 256 float32 / 512 16-bit
+ * elements, as pkm_eb_bwd's row kernels take it); otherwise
+ * PKM_ERR_UNSUPPORTED, nothing enqueued.
+ *
+ * Replaces the reference's pair of embedding_bag_bw_rev_indices
+ * (pkm/xformer_embeddingbag.py:331-386) and autograd's accumulation of the
+ * table gradient when the fast-weight module reads a table twice (its
+ * retrieval and its update step, fwpkm/fwpkm.py:448, 503-509).
+ */
+int pkm_eb_bwd_accumulate(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                          const int64_t* indices, const void* psw, int psw_dtype,
+                          const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size,
+                          void* grad_weight, void* grad_psw,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * pkm_eb_bwd without a workspace argument: the same kernels and results
  * (bit-identical outputs), with their workspace in a fixed scratch array of
  * 64 MiB that the library holds on each GPU it runs on until the process ends.

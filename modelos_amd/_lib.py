@@ -55,6 +55,17 @@ SIGNATURES = {
             c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),
+    "pkm_eb_bwd_accumulate": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64, c_int,  # weight, num_rows, dim, weight_dtype
+            c_void_p, c_void_p, c_int,  # indices, psw, psw_dtype
+            c_void_p, c_int,  # grad_out, grad_dtype
+            c_int64, c_int64,  # bags, bag_size
+            c_void_p, c_void_p,  # grad_weight (in / out), grad_psw
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
+        ],
+    ),
     "pkm_eb_bwd_noalloc": (
         c_int,
         [
@@ -327,6 +338,7 @@ _SIZE_ARGS = {
     "pkm_eb_bwd_noalloc": (1, 2),
     "pkm_eb_bwd_prepare": (0, 1),
     "pkm_eb_bwd_prepared": (1, 2),
+    "pkm_eb_bwd_accumulate": (1, 2),
     "pkm_eb_bwd2": (1, 2),
     "pkm_eb_bwd_sgd": (1, 2),
     "pkm_eb_bwd2_sgd": (4, 5),

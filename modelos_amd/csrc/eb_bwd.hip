@@ -751,12 +751,34 @@ __device__ __forceinline__ float accumulate_slots(const RowData<VPL, U, GradTrai
   return mydot;
 }
 
+// Accumulating reduction (pkm_eb_bwd_accumulate): the row's gradient is added
+// to the one already in gW, as autograd adds two gradients of one tensor:
+// acc = pending + T(sum), rounded to T once more by the store.
+template <typename TW, int VPL>
+__device__ __forceinline__ void unpack_add_pending(const uint4* P, float* acc) {
+  constexpr int EPV = VecTraits<TW>::EPV;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    float pv[EPV];
+    VecTraits<TW>::unpack(P[v], pv);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[v * EPV + e] = pv[e] + round_to<TW>(acc[v * EPV + e]);
+  }
+}
+template <typename TW, int VPL>
+__device__ __forceinline__ void add_pending_row(const char* orow, uint32_t lane_byte, float* acc) {
+  uint4 P[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) P[v] = ld16(orow + lane_byte + v * 1024u);
+  unpack_add_pending<TW, VPL>(P, acc);
+}
+
 // The long light rows list_long_rows_kernel listed: each wave takes one row at a time
 // (grid-stride over the list, whose length every wave reads, so every wave
 // ends) and reduces it U occurrences at a time, in order, the next chunk's
 // metadata and gradient rows in flight while the current chunk is reduced.
 // One wave per row keeps each row's sums in position order.
-template <typename TW, typename TG, int VPL, int U, bool SGD>
+template <typename TW, typename TG, int VPL, int U, bool SGD, bool ACC>
 __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
     const TW* __restrict__ W, int64_t D, int want_dot, const TG* __restrict__ g, const uint32_t* __restrict__ offs,
     const uint2* __restrict__ meta, const TW* __restrict__ zrow, TW* __restrict__ gW, float* __restrict__ dsorted,
@@ -824,6 +846,7 @@ __global__ __launch_bounds__(256) void eb_bwd_long_rows_kernel(
       sgd_store_row<TW, 64, VPL>(acc, p, end - beg, r, D, (int64_t)lane * EPV, lane, S);
     } else {
       char* orow = (char*)gW + (uint64_t)r * rowbytes;
+      if constexpr (ACC) add_pending_row<TW, VPL>(orow, lane_byte, acc);
 #pragma unroll
       for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
     }
@@ -915,7 +938,7 @@ __global__ __launch_bounds__(256) void list_long_rows_kernel(const uint32_t* __r
 template <typename TW, typename TG, int VPL>
 constexpr int kRowVecs = VPL * GradTraits<TW, TG>::NV;
 
-template <typename TW, typename TG, int VPL, int U, bool SGD>
+template <typename TW, typename TG, int VPL, int U, bool SGD, bool ACC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<TW, TG, VPL> == 1 && U <= 4) ? 5 : ((kRowVecs<TW, TG, VPL> == 1 || (kRowVecs<TW, TG, VPL> == 2 && U <= 4)) ? 3 : 2)))) void eb_bwd_rows_dyn_kernel(
     const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TG* __restrict__ g,
     const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
@@ -975,12 +998,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
       M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readlane((int)C.mw, i * U + u)) : 0.f;
     }
   };
-  auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R) {
+  auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R, uint4* P) {
     // the SGD epilogue reads every table row (empty ones included); tail rows past K read the zero row
     const bool read_w = SGD ? row < K32 : (want_dot && M.nh);
     const char* wrow = read_w ? Wb + (uint64_t)row * rowbytes : zb;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);  // read once: keep L2 for g
+    if constexpr (ACC) {
+      // the pending gradient of a row this kernel writes (one with lookups, not left to the long-row kernel)
+      const uint32_t cnt = M.end - M.beg;
+      const bool mine = row < K32 && cnt > 0 && !(cnt > long_min && cnt <= (uint32_t)kHeavyT);
+      const char* prow = mine ? (const char*)gW + (uint64_t)row * rowbytes : zb;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) P[v] = ld16(prow + lane_byte + v * 1024u);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * growbytes : zb;
@@ -1015,7 +1046,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
       if (want_dot && dot_store) dsorted[(uint32_t)dot_slot < nh ? s + dot_slot : dummy_slot] = d;
     }
   };
-  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, RowData<VPL, U, NV>& R) {
+  auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, RowData<VPL, U, NV>& R, const uint4* P) {
     if (skip) return;  // longer than 2 U (and light): reduced by the long-row kernel
     float acc[NE];
 #pragma unroll
@@ -1036,6 +1067,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
         sgd_store_row<TW, 64, VPL>(acc, p, cnt, row, D, col0, lane, S);
       }
     } else {
+      if constexpr (ACC) {
+        if (cnt == 0) return;  // no lookups: the row keeps its pending gradient
+        unpack_add_pending<TW, VPL>(P, acc);
+      }
       char* orow = row < K32 ? (char*)gW + (uint64_t)row * rowbytes : (char*)dummy_row;
 #pragma unroll
       for (int v = 0; v < VPL; ++v) st16_nt(orow + lane_byte + v * 1024u, VecTraits<TW>::pack(acc + v * EPV));
@@ -1054,10 +1089,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
 
   RowMeta<U> MA, MB;
   RowData<VPL, U, NV> DA, DB;
+  uint4 PA[ACC ? VPL : 1], PB[ACC ? VPL : 1];  // pending gradient rows (accumulating reduction)
   uint32_t rowA, rowB;
   bool skA, skB;
   get_meta(cur, 0, MA, rowA, skA);
-  issue(MA, rowA, DA);
+  issue(MA, rowA, DA, PA);
   get_meta(cur, 1, MB, rowB, skB);
   // One chunk's 4 rows per trip, rows i and i + 1 in flight across chunk
   // boundaries. The order keeps every wait partial: each load is first used
@@ -1068,21 +1104,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
   while (true) {
     fetch_offs(tk, nn);   // the chunk after next (its ticket was taken one trip ago)
     tk = take_ticket();
-    issue(MB, rowB, DB);  // row 1
-    fetch_meta(nxt);      // its offsets were loaded one trip ago
-    process(MA, rowA, skA, DA);  // row 0
+    issue(MB, rowB, DB, PB);  // row 1
+    fetch_meta(nxt);          // its offsets were loaded one trip ago
+    process(MA, rowA, skA, DA, PA);  // row 0
     get_meta(cur, 2, MA, rowA, skA);
-    issue(MA, rowA, DA);  // row 2
-    process(MB, rowB, skB, DB);  // row 1
+    issue(MA, rowA, DA, PA);  // row 2
+    process(MB, rowB, skB, DB, PB);  // row 1
     get_meta(cur, 3, MB, rowB, skB);
-    issue(MB, rowB, DB);  // row 3
-    process(MA, rowA, skA, DA);  // row 2 (its wait covers nxt's metadata)
+    issue(MB, rowB, DB, PB);  // row 3
+    process(MA, rowA, skA, DA, PA);  // row 2 (its wait covers nxt's metadata)
     const bool more = nxt.row0 < K32;
     if (more) {
       get_meta(nxt, 0, MA, rowA, skA);
-      issue(MA, rowA, DA);  // next chunk's row 0
+      issue(MA, rowA, DA, PA);  // next chunk's row 0
     }
-    process(MB, rowB, skB, DB);  // row 3
+    process(MB, rowB, skB, DB, PB);  // row 3
     if (!more) break;
     get_meta(nxt, 1, MB, rowB, skB);
     cur = nxt;
@@ -1265,7 +1301,7 @@ static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* l
 // The row reduction on the ticket schedule: the rows kernel, then the long
 // rows listed by prepare_rows_dyn. Each reduction clears its own ticket
 // counters first, so a prepared workspace can serve any number of reductions.
-template <typename TW, typename TG, int VPL, int U, bool SGD>
+template <typename TW, typename TG, int VPL, int U, bool SGD, bool ACC>
 static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
                             const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                             float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, uint32_t* tickets,
@@ -1280,12 +1316,12 @@ static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, c
   wgs = wgs < 1280 ? wgs : 1280;
   wgs = cdiv(wgs, kDynGroups * kDynSub) * kDynGroups * kDynSub;  // every counter gets workgroups
   KernelSpan span("eb_bwd_rows", st);
-  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, TG, VPL, U, SGD>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W,
+  hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, TG, VPL, U, SGD, ACC>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W,
                      K, D, want_dot, (const TG*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW,
                      dsorted, dummy_slot, tickets, blk, long_min, S);
   const int64_t rb = cdiv(K, 4 * 64);
   const unsigned lb = (unsigned)(rb < 1024 ? rb : 1024);
-  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, TG, VPL, U, SGD>), dim3(lb), dim3(256), 0, st, (const TW*)W, D,
+  hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, TG, VPL, U, SGD, ACC>), dim3(lb), dim3(256), 0, st, (const TW*)W, D,
                      want_dot, (const TG*)g, offs, meta, (const TW*)zrow, (TW*)gW, dsorted, dummy_slot,
                      (const uint32_t*)long_rows, long_count, S);
 }
@@ -1311,7 +1347,7 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
   }
 }
 
-template <typename TW, typename TG, int LPG, int VPL, bool SGD>
+template <typename TW, typename TG, int LPG, int VPL, bool SGD, bool ACC = false>
 static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, int pdt, const void* g, int64_t L,
                           const uint32_t* offs, const uint32_t* skeys, const uint32_t* svals, const uint32_t* nvalid,
                           int64_t N, const BwdLayout& l, char* ws, void* gW, void* gpsw, const SgdArgs& S,
@@ -1340,7 +1376,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       uint32_t* long_rows = (uint32_t*)(ws + l.long_rows);
       uint32_t* tickets = (uint32_t*)(ws + l.tickets);
 #define PKM_ROWS(U_) \
-  launch_rows_dyn<TW, TG, VPL, U_, SGD>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, S, st)
+  launch_rows_dyn<TW, TG, VPL, U_, SGD, ACC>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, S, st)
       if constexpr (VPL <= 2 && NV == 1) {
         if (u0 == 8) PKM_ROWS(8); else PKM_ROWS(4);
       } else if constexpr (VPL <= 2) {
@@ -1356,6 +1392,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, svals,
                          (const float*)dsorted, nvalid, N, gpsw, pdt);
   } else {
+    static_assert(!ACC, "the accumulating reduction runs on 64-lane rows");
     if (N > 0)
       hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, TG, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D,
                          psw, pdt, (const TG*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
@@ -1377,12 +1414,19 @@ template <typename TW, typename TG = TW>
 static bool dispatch_reduce(bool prepare, const GroupCfg& c, const void* W, int64_t K, int64_t D, const void* psw, int pdt,
                             const void* g, int64_t L, const uint32_t* offs, const uint32_t* skeys,
                             const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l,
-                            char* ws, void* gW, void* gpsw, hipStream_t st, const SgdArgs* sgd = nullptr) {
+                            char* ws, void* gW, void* gpsw, hipStream_t st, const SgdArgs* sgd = nullptr,
+                            bool acc = false) {
   static const SgdArgs no_sgd = {};
 #define PKM_RED_CASE(LPG_, VPL_)                                                                                  \
   if (c.lpg == LPG_ && c.vpl == VPL_) {                                                                           \
     if (prepare) {                                                                                                \
       launch_prepare<TW, LPG_, VPL_>(K, D, psw, pdt, L, offs, svals, nvalid, N, l, ws, st);                       \
+    } else if (sgd == nullptr && acc) {                                                                         \
+      if constexpr (LPG_ == 64 && std::is_same<TW, TG>::value)                                                    \
+        launch_reduce<TW, TG, LPG_, VPL_, false, true>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, \
+                                                       ws, gW, gpsw, no_sgd, st);                                 \
+      else                                                                                                        \
+        return false;                                                                                             \
     } else if (sgd == nullptr) {                                                                                  \
       launch_reduce<TW, TG, LPG_, VPL_, false>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, ws, gW, \
                                                gpsw, no_sgd, st);                                                 \
@@ -1525,14 +1569,17 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
   return pkm_check_launch("pkm_eb_bwd_prepare");
 }
 
-extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
-                                   const int64_t* indices, const void* psw, int psw_dtype, const void* grad_out,
-                                   int grad_dtype, int64_t bags, int64_t bag_size, void* grad_weight, void* grad_psw,
-                                   void* workspace, size_t workspace_bytes, void* stream) {
+namespace pkm {
+// The reduction on a prepared workspace; acc: grad_weight holds a gradient
+// that the rows' sums are added to (rows without lookups keep it).
+static int eb_bwd_reduce(const char* fn, bool acc, const void* weight, int64_t num_rows, int64_t dim,
+                         int weight_dtype, const int64_t* indices, const void* psw, int psw_dtype,
+                         const void* grad_out, int grad_dtype, int64_t bags, int64_t bag_size, void* grad_weight,
+                         void* grad_psw, void* workspace, size_t workspace_bytes, void* stream) {
   GroupCfg c;
   BwdLayout l;
-  const int rc = eb_bwd_check("pkm_eb_bwd_prepared", num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags,
-                              bag_size, workspace, workspace_bytes, &c, &l);
+  const int rc = eb_bwd_check(fn, num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags, bag_size, workspace,
+                              workspace_bytes, &c, &l);
   if (rc != PKM_OK) return rc;
   const int64_t N = bags * bag_size;
   const bool wide_grad = grad_dtype == PKM_DTYPE_F32 && weight_dtype != PKM_DTYPE_F32;
@@ -1554,7 +1601,7 @@ extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t
   bool ok;
 #define PKM_REDUCE(TW_, TG_)                                                                                    \
   dispatch_reduce<TW_, TG_>(false, c, weight, K, dim, psw, psw_dtype, grad_out, bag_size, v.offs, v.keys, v.vals, \
-                            v.nvalid, N, l, ws, grad_weight, gpsw, st)
+                            v.nvalid, N, l, ws, grad_weight, gpsw, st, nullptr, acc)
   if (weight_dtype == PKM_DTYPE_F32)
     ok = PKM_REDUCE(float, float);
   else if (weight_dtype == PKM_DTYPE_BF16)
@@ -1562,11 +1609,45 @@ extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t
   else
     ok = wide_grad ? PKM_REDUCE(f16_t, float) : PKM_REDUCE(f16_t, f16_t);
 #undef PKM_REDUCE
-  PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
+  PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "%s: no kernel for lpg=%d vpl=%d%s", fn, c.lpg, c.vpl,
+              acc ? " (accumulating: 64-lane rows, gradient in the table's dtype)" : "");
   if (N > 0 && gpsw != nullptr)
     hipLaunchKernelGGL(zero_invalid_gpsw_kernel, dim3(64), dim3(256), 0, st, (const uint32_t*)v.invalid, gpsw,
                        psw_dtype);
-  return pkm_check_launch("pkm_eb_bwd_prepared");
+  return pkm_check_launch(fn);
+}
+
+// Whether the accumulating reduction has a kernel for these sizes and dtypes.
+static bool eb_bwd_acc_supported(int64_t dim, int weight_dtype, int grad_dtype) {
+  GroupCfg c;
+  const int epv = weight_dtype == PKM_DTYPE_F32 ? 4 : 8;
+  return grad_dtype == weight_dtype && valid_dt(weight_dtype) && choose_group_cfg(dim, epv, true, &c) && c.lpg == 64;
+}
+}  // namespace pkm
+
+extern "C" int pkm_eb_bwd_prepared(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                                   const int64_t* indices, const void* psw, int psw_dtype, const void* grad_out,
+                                   int grad_dtype, int64_t bags, int64_t bag_size, void* grad_weight, void* grad_psw,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  return eb_bwd_reduce("pkm_eb_bwd_prepared", false, weight, num_rows, dim, weight_dtype, indices, psw, psw_dtype,
+                       grad_out, grad_dtype, bags, bag_size, grad_weight, grad_psw, workspace, workspace_bytes,
+                       stream);
+}
+
+extern "C" int pkm_eb_bwd_accumulate(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype,
+                                     const int64_t* indices, const void* psw, int psw_dtype, const void* grad_out,
+                                     int grad_dtype, int64_t bags, int64_t bag_size, void* grad_weight,
+                                     void* grad_psw, void* workspace, size_t workspace_bytes, void* stream) {
+  PKM_REQUIRE(eb_bwd_acc_supported(dim, weight_dtype, grad_dtype), PKM_ERR_UNSUPPORTED,
+              "pkm_eb_bwd_accumulate: dim %lld, weight dtype %d, grad dtype %d not supported (grad_out in the "
+              "table's dtype, rows of 64 16-byte vectors or more)",
+              (long long)dim, weight_dtype, grad_dtype);
+  const int rc = pkm_eb_bwd_prepare(num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags, bag_size, workspace,
+                                    workspace_bytes, stream);
+  if (rc != PKM_OK) return rc;
+  return eb_bwd_reduce("pkm_eb_bwd_accumulate", true, weight, num_rows, dim, weight_dtype, indices, psw, psw_dtype,
+                       grad_out, grad_dtype, bags, bag_size, grad_weight, grad_psw, workspace, workspace_bytes,
+                       stream);
 }
 
 extern "C" int pkm_eb_bwd(const void* weight, int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,

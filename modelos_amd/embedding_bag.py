@@ -210,6 +210,46 @@ def eb_backward(
     return grad_weight, grad_psw
 
 
+def eb_backward_into(
+    indices: torch.Tensor,
+    weight: torch.Tensor,
+    per_sample_weights: Optional[torch.Tensor],
+    grad_output: torch.Tensor,
+    grad_weight: torch.Tensor,
+) -> Optional[Tuple[torch.Tensor, Optional[torch.Tensor]]]:
+    """eb_backward adding the table gradient into `grad_weight` in place
+    (pkm_eb_bwd_accumulate): grad_weight + eb_backward(...)[0], bit for bit,
+    without a separate add over the table. Returns (grad_weight, grad_psw),
+    or None, with nothing done, where the kernels have no accumulating path
+    (a gradient dtype other than the table's, rows narrower than 64 lanes, a
+    grad_weight that is not a contiguous aligned [K, D] of the table's dtype)."""
+    _check_bag_inputs(indices, weight, per_sample_weights, "eb_backward_into")
+    dev = _require_device(indices, weight, per_sample_weights, grad_output, grad_weight)
+    B, L = indices.shape
+    K, D = weight.shape
+    if grad_output.shape != (B, D):
+        raise ValueError(f"eb_backward_into: grad_output shape {tuple(grad_output.shape)} != {(B, D)}")
+    if (grad_weight.shape != weight.shape or grad_weight.dtype != weight.dtype or not grad_weight.is_contiguous()
+            or grad_weight.data_ptr() % 16 or grad_output.dtype != weight.dtype):
+        return None
+    indices = indices.contiguous()
+    weight = _aligned(weight)
+    psw = per_sample_weights.contiguous() if per_sample_weights is not None else None
+    grad_output = _aligned(grad_output)
+    grad_psw = torch.empty_like(psw, memory_format=torch.contiguous_format) if psw is not None else None
+    ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
+    workspace = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    try:
+        _lib.call("pkm_eb_bwd_accumulate", _lib.ptr(weight), K, D, _lib.dtype_code(weight), _lib.ptr(indices),
+                  _lib.ptr(psw), _lib.dtype_code(psw), _lib.ptr(grad_output), _lib.dtype_code(grad_output), B, L,
+                  _lib.ptr(grad_weight), _lib.ptr(grad_psw), _lib.ptr(workspace), ws_bytes, _lib.stream_of(dev))
+    except _lib.PkmError as e:
+        if e.status == 2:  # PKM_ERR_UNSUPPORTED: checked before anything is enqueued
+            return None
+        raise
+    return grad_weight, grad_psw
+
+
 def eb_double_backward(
     indices: torch.Tensor,
     a: Optional[torch.Tensor],

@@ -138,6 +138,54 @@ class _SgdValueUpdate(torch.autograd.Function):
             None, None, None, None, None
 
 
+class _GradSink:
+    """A table gradient parked by one consumer's backward for another's to
+    add its own into (_TableFanout)."""
+
+    __slots__ = ("pending",)
+
+    def __init__(self):
+        self.pending = None
+
+    def take(self):
+        p, self.pending = self.pending, None
+        return p
+
+
+class _TableFanout(torch.autograd.Function):
+    """Two handles on one fast-weight table, its chunk's retrieval's and its
+    update step's. Their gradients meet in a sink: the step's backward parks
+    its table gradient there and the retrieval's bag backward adds its own
+    into it in place (pkm_eb_bwd_accumulate), instead of autograd adding two
+    dense [K, D] gradients in a pass of its own. Whatever is still parked or
+    arrives separately is added here (any order of the two backward passes)."""
+
+    @staticmethod
+    def forward(ctx, table, sink):
+        ctx.sink = sink
+        ctx.set_materialize_grads(False)  # a handle without a gradient arrives as None, not a [K, D] of zeros
+        return table.view_as(table), table.view_as(table)
+
+    @staticmethod
+    def backward(ctx, g_read, g_step):
+        parts = [g for g in (g_read, g_step, ctx.sink.take()) if g is not None]
+        if not parts:
+            return None, None
+        out = parts[0]
+        for g in parts[1:]:
+            out = out + g
+        return out, None
+
+
+def _fan_out(table: torch.Tensor):
+    """(handle for the retrieval, handle for the update step) of `table`."""
+    sink = _GradSink()
+    read, step = _TableFanout.apply(table, sink)
+    read._pkm_grad_sink = sink
+    step._pkm_grad_sink = sink
+    return read, step
+
+
 class _FusedValueStep(torch.autograd.Function):
     """FwPKM's values step taken straight from the gradient of the memory loss
     w.r.t. the bag output: the table gradient EB^T(indices, psw, d_hyp) and the
@@ -172,6 +220,7 @@ class _FusedValueStep(torch.autograd.Function):
                   _lib.stream_of(V.device))
         ctx.save_for_backward(gs, counts, idx, w, g)
         ctx.scale, ctx.lr, ctx.wd, ctx.clip = scale, lr, wd, clip
+        ctx.sink = getattr(values, "_pkm_grad_sink", None)
         ctx.mark_non_differentiable(sumsq)
         # the scaled gradient usually reaches no loss: None, not a [K, D] of zeros
         # (which the double backward would also read)
@@ -205,6 +254,10 @@ class _FusedValueStep(torch.autograd.Function):
                       _lib.dtype_code(gs), float(ctx.scale), float(ctx.lr), int(bool(ctx.clip)), _lib.ptr(idx),
                       _lib.ptr(w), _lib.dtype_code(w), _lib.ptr(g), B, L, _lib.ptr(d_hyp), _lib.ptr(d_psw),
                       _lib.stream_of(gs.device))
+        if d_values is not None and ctx.sink is not None and not torch.is_grad_enabled():
+            # parked for the retrieval's bag backward to add its gradient into (_TableFanout)
+            ctx.sink.pending = d_values if ctx.sink.pending is None else ctx.sink.pending + d_values
+            d_values = None
         return (d_values, None, d_psw if ctx.needs_input_grad[2] else None,
                 d_hyp if ctx.needs_input_grad[3] else None, None, None, None, None)
 
@@ -651,7 +704,14 @@ class FastWeightProductKeyMemory(nn.Module):
                 cT = end - start
                 cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
                 cq = q[:, start:end, :].contiguous()
-                r = self.retrieve_values(cq, params)
+                final = ci == len(bounds) - 1
+                read_params = step_params = params
+                if fused and not final and params["values"].requires_grad:
+                    # the table's retrieval and update step meet in one gradient buffer
+                    v_read, v_step = _fan_out(params["values"])
+                    read_params = OrderedDict((n, v_read if n == "values" else p) for n, p in params.items())
+                    step_params = OrderedDict((n, v_step if n == "values" else p) for n, p in params.items())
+                r = self.retrieve_values(cq, read_params)
                 hyp = r["retireved_values"].view(B, cT, -1)
                 # the chunk's output is read before its own update
                 outputs.append(hyp)
@@ -660,7 +720,6 @@ class FastWeightProductKeyMemory(nn.Module):
                 u_hyp, u_ref, u_w, u_mask = self._update_targets(hyp, ref_v[:, start:end, :].contiguous(), cgates,
                                                                  cmask)
                 # the last step's result is only stored, never differentiated
-                final = ci == len(bounds) - 1
                 mem_losses, addr_loss, addr_grads = self._losses(u_hyp, u_ref, u_w, u_mask, r, query=cq,
                                                                  params=params,
                                                                  create_graph=self.training and not final)
@@ -668,7 +727,7 @@ class FastWeightProductKeyMemory(nn.Module):
                 if fused:
                     # the last step's table is written into the parameter when it can be
                     last = final and _storable_into(params["values"], self.values)
-                    params, grads, norms2 = self._update_fw_fused(params, num_samples, r, mem_losses.mean(),
+                    params, grads, norms2 = self._update_fw_fused(step_params, num_samples, r, mem_losses.mean(),
                                                                   addr_loss, self.values if last else None,
                                                                   addr_grads=addr_grads)
                 else:

@@ -82,6 +82,8 @@ class _XEmbeddingBagFn(Function):
         ctx.has_psw = per_sample_weights is not None
         ctx.K, ctx.D = K, D
         ctx.bw_kernel = bw_kernel
+        # a table handle whose other consumer parks its gradient for this backward to add into
+        ctx.sink = getattr(weight, "_pkm_grad_sink", None)
         return out
 
     @staticmethod
@@ -89,9 +91,17 @@ class _XEmbeddingBagFn(Function):
         weight, indices, a_saved = ctx.saved_tensors
         K, D = ctx.K, ctx.D
         a = a_saved if ctx.has_psw else None
+        res = None
+        if ctx.sink is not None and ctx.bw_kernel is _bw_kernel and not torch.is_grad_enabled():
+            pending = ctx.sink.take()
+            if pending is not None:
+                res = _eb.eb_backward_into(indices, weight, a, grad_output, pending)
+                if res is None:
+                    ctx.sink.pending = pending  # no accumulating kernel here: the fan-out node adds it
         # first-order kernel: not differentiable; EmbeddingBagBW carries the VJP
         with torch.no_grad():
-            weight_grad_fast, psw_grad_fast = ctx.bw_kernel(indices, weight, a, grad_output)
+            weight_grad_fast, psw_grad_fast = res if res is not None else ctx.bw_kernel(indices, weight, a,
+                                                                                          grad_output)
         grad_weight = EmbeddingBagBW.apply(indices, a if ctx.has_psw else None, grad_output, K, D, weight_grad_fast)
         grad_psw = psw_grad_fast if ctx.has_psw else None
         return grad_weight, None, grad_psw, None

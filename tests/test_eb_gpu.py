@@ -592,3 +592,53 @@ def test_backward_prepared_rejects_in_place_changes(device):
     didx[0, 0] = 3
     with pytest.raises(ValueError):
         eb.eb_backward(didx, dW, dp, dg, prepared=prep)
+
+
+# pkm_eb_bwd_accumulate: grad_weight + (the backward's table gradient), bit for
+# bit the same as the backward into its own buffer followed by an add (what
+# autograd forms for a table read twice), rows without lookups unchanged; on
+# uniform lookups, hot rows (chunked partial sums) and clustered long rows
+# (the long-row kernel). Shapes without an accumulating kernel return None.
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("pattern", ["uniform", "hot", "clustered"])
+def test_backward_accumulate_equals_backward_plus_add(pattern, dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K, D = 512, 64, 40000, 1024
+    W, idx, p, gr = eb_inputs(B, L, K, D, dtype, seed=71)
+    if pattern == "hot":
+        idx = _hot_indices(B, L, K, seed=72)
+    elif pattern == "clustered":
+        g = torch.Generator().manual_seed(73)
+        ids = torch.cat([torch.full((int(c),), r) for r, c in enumerate(torch.randint(5, 200, (60,), generator=g))])
+        rest = torch.randint(0, K, (B * L - ids.numel(),), generator=g)
+        idx = torch.cat([ids, rest])[torch.randperm(B * L, generator=g)].view(B, L)
+    pending = torch.randn((K, D), generator=torch.Generator().manual_seed(74)).to(dtype)
+    args = _dev(idx, W, p, gr, device=device)
+    gW, gp = eb.eb_backward(*args)
+    want = gW + pending.to(device)
+    buf = pending.to(device)
+    res = eb.eb_backward_into(*args, buf)
+    assert res is not None
+    got, gp2 = res
+    assert got.data_ptr() == buf.data_ptr()
+    assert torch.equal(got, want)
+    assert torch.equal(gp2, gp)
+    untouched = torch.ones(K, dtype=torch.bool)
+    untouched[idx[idx >= 0].unique()] = False
+    assert torch.equal(got.cpu()[untouched], pending[untouched])
+
+
+def test_backward_accumulate_unsupported_returns_none(device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K = 64, 16, 3000
+    W, idx, p, gr = eb_inputs(B, L, K, 64, torch.float32, seed=75)  # 16 vectors a row: no 64-lane rows
+    buf = torch.zeros((K, 64), device=device)
+    assert eb.eb_backward_into(*_dev(idx, W, p, gr, device=device), buf) is None
+    assert torch.count_nonzero(buf) == 0
+    W, idx, p, gr = eb_inputs(B, L, K, 1024, torch.bfloat16, seed=76)
+    idd, Wd, pd, gd = _dev(idx, W, p, gr, device=device)
+    buf = torch.zeros((K, 1024), device=device, dtype=torch.bfloat16)
+    assert eb.eb_backward_into(idd, Wd, pd, gd.float(), buf) is None  # float32 gradient of a bf16 table
+    assert torch.count_nonzero(buf) == 0

@@ -266,3 +266,36 @@ def test_addr_loss_threshold_from_retrieval_lists(dtype, score_type, device):
     want = mem.addr_loss_weight * (-1.0 * mem.compute_marginal_entropy(s1.view(-1, mem.subsize))
                                    + -1.0 * mem.compute_marginal_entropy(s2.view(-1, mem.subsize)))
     assert torch.equal(got, want), (got.item(), want.item())
+
+
+@pytest.mark.parametrize("chunks", [2, 3])
+def test_table_gradient_summed_in_place(chunks, device, monkeypatch):
+    """The values table read by a chunk's retrieval and its update step: the
+    step's gradient parked and the retrieval's bag backward adding into it
+    (pkm_eb_bwd_accumulate) gives the gradients autograd's own sum gives, bit
+    for bit."""
+    from modelos_amd.fwpkm import fwpkm as fw
+    from modelos_amd.fwpkm.fwpkm import FastWeightProductKeyMemory
+
+    kw = dict(mem_k_dim=64, mem_v_dim=1024, mem_heads=2, mem_topk=8, mem_n_subkeys=64, lookahead=0,
+              qk_score_type="idw", learning_rate=0.3)
+    g = gen(81)
+    x = torch.randn((2, 32 * chunks, 128), generator=g) * 0.3
+    ref_v = torch.randn((2, 32 * chunks, 1024), generator=g)
+    dout = torch.randn((2, 32 * chunks, 1024), generator=g)
+    torch.manual_seed(0)
+    base = FastWeightProductKeyMemory(**kw)
+    base.reset_parameters()
+
+    def run():
+        mem = module(kw, base.keys.detach(), base.values.detach(), device)
+        xd = x.to(device).requires_grad_(True)
+        out = mem(q=xd, ref_v=ref_v.to(device), gates=None, chunk_size=32)
+        out["output"].backward(dout.to(device))
+        return xd.grad, mem.keys.grad, mem.values.grad
+
+    a = run()
+    monkeypatch.setattr(fw, "_fan_out", lambda t: (t, t))  # autograd sums the table's two gradients
+    b = run()
+    for u, v, what in zip(a, b, ("dx", "dkeys", "dvalues")):
+        assert torch.equal(u, v), what
