@@ -637,7 +637,7 @@ MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X fp32 matrix
 
 
 def fwpkm_rooflines(kern, dtype_bytes, distinct_rows, bags=4096, bag_size=64, K=1 << 18, D=1024, H=4, n=512,
-                    k_dim=256, chunks=2, clip=False):
+                    k_dim=256, chunks=2, clip=False, wd=0.0):
     """Per-call algorithmic work of the fast-weight step's library kernels,
     achieved / peak from their measured per-step times, and the step's floor
     (every library call at its roofline, the torch glue at zero: a lower
@@ -646,22 +646,43 @@ def fwpkm_rooflines(kern, dtype_bytes, distinct_rows, bags=4096, bag_size=64, K=
       pkm_eb_fwd (gather):     N*D*s + N*(8 + s) + B*D*s
       pkm_eb_bwd (outer):      B*D*s + U*D*s + K*D*s + N*(8 + s) + N*s
       pkm_eb_bwd_sgd (step):   every table row read and the new one written
-                               (2*K*D*s), the scaled gradient for every step
-                               but the last (K*D*s), B*D*s + N*(8 + s), 8*K
+                               (2*K*D*s), B*D*s + N*(8 + s), 8*K; the scaled
+                               gradient (K*D*s) for every step but the last
+                               only under grad_clip or weight decay (the only
+                               cases whose backward reads it again)
       pkm_eb_bwd2_sgd:         the double backward's A_bwd2, N*D*s + 2*B*D*s
                                + N*(8 + 2*s), plus N*D*s of scaled-gradient
                                rows under grad_clip
+      pkm_eb_bwd_accumulate:   as pkm_eb_bwd, the table gradient's touched
+                               rows read and written (2*U*D*s) instead of
+                               every row written
+      pkm_me_grad_fwd:         the sub-score matrices read twice (2 * 2*R*n*s,
+                               R = tokens x heads), the <q, k> products read
+                               and the coefficient rows written (2 * 2H*T*n*4)
+      pkm_me_grad_hvp:         the sub-scores read twice and their gradient
+                               written (3 * 2*R*n*s), <q, k> and <q, gbar>
+                               read twice (4 * 2H*T*n*4), [U | lam] rows
+                               written (2H*T*2n*4)
+      pkm_idw_grad_coef:       the dense sub-score gradient read (2H*T*n*s),
+                               <q, k> read and U written (2 * 2H*T*n*4)
       pkm_score_topk:          2 * tokens * heads * 2 * n * k_dim/2 flops on
                                the matrix peak of the dtype"""
     s = dtype_bytes
     N, B = bags * bag_size, bags
     U = distinct_rows
+    T, R = bags, bags * H  # tokens per chunk, sub-score rows per half
+    dense = 2 * H * T * n  # entries of a [2 heads, tokens, n] operand
     per_call = {
         "pkm_eb_fwd": N * D * s + N * (8 + s) + B * D * s,
         "pkm_eb_bwd": B * D * s + U * D * s + K * D * s + N * (8 + s) + N * s,
+        "pkm_eb_bwd_accumulate": B * D * s + U * D * s + 2 * U * D * s + N * (8 + s) + N * s,
         "pkm_eb_bwd2_sgd": N * D * s * (2 if clip else 1) + 2 * B * D * s + N * (8 + 2 * s),
+        "pkm_me_grad_fwd": 2 * 2 * R * n * s + 2 * dense * 4,
+        "pkm_me_grad_hvp": 3 * 2 * R * n * s + 4 * dense * 4 + 2 * dense * 4,
+        "pkm_idw_grad_coef": dense * s + 2 * dense * 4,
     }
-    sgd_total = chunks * (2 * K * D * s + B * D * s + N * (8 + s) + 8 * K) + (chunks - 1) * K * D * s
+    sgd_total = chunks * (2 * K * D * s + B * D * s + N * (8 + s) + 8 * K) + (chunks - 1) * K * D * s * (
+        1 if (clip or wd) else 0)
     flops = score_flops(bags, H, n, k_dim)
     peak_tf = MFMA_F32_PEAK_TFLOPS if s == 4 else MFMA_BF16_PEAK_TFLOPS
     out, floor = {}, 0.0

@@ -190,7 +190,9 @@ class _FusedValueStep(torch.autograd.Function):
     """FwPKM's values step taken straight from the gradient of the memory loss
     w.r.t. the bag output: the table gradient EB^T(indices, psw, d_hyp) and the
     bincount-normalised SGD step in one pass over the table (pkm_eb_bwd_sgd).
-    Returns (new values, scaled gradient, per-row sums of its squares).
+    Returns (new values, scaled gradient, per-row sums of its squares); with
+    want_scaled False the scaled gradient is None (not written) unless the
+    backward of a clipped or weight-decayed step needs it.
 
     Its backward is the reference's through EmbeddingBagBW and the step
     (fwpkm/xformer_embeddingbag_grad_wrapper.py:42-74, fwpkm.py:351-365):
@@ -199,7 +201,7 @@ class _FusedValueStep(torch.autograd.Function):
     pkm_eb_bwd2_sgd forms row by row as it gathers (never a dense [K, D])."""
 
     @staticmethod
-    def forward(ctx, values, indices, psw, d_hyp, scale, lr, wd, clip):
+    def forward(ctx, values, indices, psw, d_hyp, scale, lr, wd, clip, want_scaled=True):
         from ..embedding_bag import eb_backward_workspace_bytes
 
         V = _aligned(values)
@@ -209,7 +211,9 @@ class _FusedValueStep(torch.autograd.Function):
         K, D = V.shape
         B, L = idx.shape
         new = torch.empty_like(V)
-        gs = torch.empty_like(V)
+        # the scaled gradient: when asked for, or when the backward of a clipped or weight-decayed
+        # step reads it (otherwise None, and no [K, D] write)
+        gs = torch.empty_like(V) if (want_scaled or clip or wd != 0.0) else None
         counts = torch.empty(K, dtype=torch.int32, device=V.device)
         sumsq = torch.empty(K, dtype=torch.float32, device=V.device)
         ws_bytes = eb_backward_workspace_bytes(K, D, B, L)
@@ -220,6 +224,7 @@ class _FusedValueStep(torch.autograd.Function):
                   _lib.stream_of(V.device))
         ctx.save_for_backward(gs, counts, idx, w, g)
         ctx.scale, ctx.lr, ctx.wd, ctx.clip = scale, lr, wd, clip
+        ctx.table = (K, D, V.dtype)
         ctx.sink = getattr(values, "_pkm_grad_sink", None)
         ctx.mark_non_differentiable(sumsq)
         # the scaled gradient usually reaches no loss: None, not a [K, D] of zeros
@@ -231,35 +236,35 @@ class _FusedValueStep(torch.autograd.Function):
     def backward(ctx, d_new, d_gs, _d_sumsq):
         gs, counts, idx, w, g = ctx.saved_tensors
         if d_new is None and d_gs is None:
-            return (None,) * 8
-        K, D = gs.shape
+            return (None,) * 9
+        K, D, dt = ctx.table
         B, L = idx.shape
-        dn = _aligned(d_new.to(gs.dtype)) if d_new is not None else torch.zeros_like(gs)
-        dgi = _aligned(d_gs.to(gs.dtype)) if d_gs is not None else None
+        dn = _aligned(d_new.to(dt)) if d_new is not None else torch.zeros((K, D), dtype=dt, device=idx.device)
+        dgi = _aligned(d_gs.to(dt)) if d_gs is not None else None
         d_values = None
         if ctx.needs_input_grad[0]:
             if ctx.wd == 0.0:
                 d_values = dn  # p - lr * (step + 0 * p): the identity path alone
             else:
-                d_values = torch.empty_like(gs)
+                d_values = torch.empty_like(dn)
                 cnt64 = counts.to(torch.int64)
                 _lib.call("pkm_fw_sgd_update_bwd", _lib.ptr(dn), None, _lib.ptr(gs), _lib.ptr(cnt64), K, D,
                           _lib.dtype_code(gs), float(ctx.scale), float(ctx.lr), float(ctx.wd), int(bool(ctx.clip)),
                           _lib.ptr(d_values), None, _lib.stream_of(gs.device))
         d_hyp = d_psw = None
         if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
-            d_hyp = torch.empty((B, D), dtype=gs.dtype, device=gs.device)
+            d_hyp = torch.empty((B, D), dtype=dt, device=dn.device)
             d_psw = torch.empty_like(w)
             _lib.call("pkm_eb_bwd2_sgd", _lib.ptr(dn), _lib.ptr(dgi), _lib.ptr(gs), _lib.ptr(counts), K, D,
-                      _lib.dtype_code(gs), float(ctx.scale), float(ctx.lr), int(bool(ctx.clip)), _lib.ptr(idx),
+                      _lib.dtype_code(dn), float(ctx.scale), float(ctx.lr), int(bool(ctx.clip)), _lib.ptr(idx),
                       _lib.ptr(w), _lib.dtype_code(w), _lib.ptr(g), B, L, _lib.ptr(d_hyp), _lib.ptr(d_psw),
-                      _lib.stream_of(gs.device))
+                      _lib.stream_of(dn.device))
         if d_values is not None and ctx.sink is not None and not torch.is_grad_enabled():
             # parked for the retrieval's bag backward to add its gradient into (_TableFanout)
             ctx.sink.pending = d_values if ctx.sink.pending is None else ctx.sink.pending + d_values
             d_values = None
         return (d_values, None, d_psw if ctx.needs_input_grad[2] else None,
-                d_hyp if ctx.needs_input_grad[3] else None, None, None, None, None)
+                d_hyp if ctx.needs_input_grad[3] else None, None, None, None, None, None)
 
 
 def _final_values_step(values, indices, psw, d_hyp, scale, lr, wd, clip, out):
@@ -568,7 +573,8 @@ class FastWeightProductKeyMemory(nn.Module):
         same step (fwpkm.py:333-365) and outer gradients, the table gradient
         and the dense normalisation / SGD passes replaced by one kernel.
         Returns (updated params, [scaled gradient of each param], [squared
-        norm of each]: the values' from the kernel's row sums).
+        norm of each]: the values' from the kernel's row sums; the values'
+        scaled gradient itself is None, its norm being all the caller reads).
 
         store_into: the values parameter, for the last chunk's step, whose
         result is only stored (fwpkm.py:540-545) and never differentiated: the
@@ -603,8 +609,9 @@ class FastWeightProductKeyMemory(nn.Module):
                 norms2.append(sumsq.sum())
                 continue
             if n == "values":
+                # the scaled gradient is not needed here: its norm comes from the row sums
                 new_p, g_scaled, sumsq = _FusedValueStep.apply(p, flat, psw, d_hyp, scale, self.learning_rate,
-                                                               self.weight_decay, self.grad_clip)
+                                                               self.weight_decay, self.grad_clip, False)
                 scaled.append(g_scaled)
                 updated.append(new_p)
                 norms2.append(sumsq.sum())
