@@ -204,20 +204,22 @@ int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int gbar_dtype,
  * pkm_me_grad_fwd writes entropy[2] = (H_1, H_2), avec [2, n_keys] (d loss /
  * d P_rj), pbar [2, n_keys], and coef [2 heads, num_tokens, n_keys] float32:
  * idw U_tj = dS_tj / (1e-3 + d2_tj) where d2 = (qq + kk) - 2 dots > 0 (else
- * 0), dot dS_tj, with dS the sub-scores' gradient rounded to dtype. The key
+ * 0), dot dS_tj, with dS the sub-scores' gradient rounded to dtype; for idw
+ * also colsum [2 heads, n_keys] = sum_t U_tj (NULL = not written). The key
  * gradient is then
- *   idw: g[b, j] = 2 (sum_t coef[b, t, j] q_t - k_j sum_t coef[b, t, j]);
+ *   idw: g[b, j] = 2 (sum_t coef[b, t, j] q_t - k_j colsum[b, j]);
  *   dot: g[b, j] = sum_t coef[b, t, j] q_t.
  * pkm_me_grad_hvp takes, for a direction gbar [2 heads, n_keys, half] (the
  * outer gradient of g), qg [2 heads, num_tokens, n_keys] = <q_t, gbar_j> and
  * (idw) kg [2 heads, n_keys] = <k_j, gbar_j>, with avec and pbar from the
  * forward, and writes the derivative of <gbar, g>: through the sub-scores as
  * d_s1, d_s2 (dtype, every entry); with the sub-scores held fixed as the
- * rows of ul (float32; idw [2 heads, num_tokens, 2 n_keys] = [U | lam] and
- * lsum [2 heads, num_tokens] the row sums of lam; dot [2 heads, num_tokens,
+ * rows of ul (float32; idw [2 heads, num_tokens, 2 n_keys] = [U | lam],
+ * lsum [2 heads, num_tokens] the row sums of lam and lam_colsum [2 heads,
+ * n_keys] its column sums (NULL = not written); dot [2 heads, num_tokens,
  * n_keys] = dS), from which
  *   idw: d q_t = 2 (sum_j U_tj gbar_j + sum_j lam_tj k_j - lsum_t q_t),
- *        d k_j = 2 (sum_t lam_tj q_t - k_j sum_t lam_tj - gbar_j sum_t U_tj);
+ *        d k_j = 2 (sum_t lam_tj q_t - k_j lam_colsum_j - gbar_j colsum_j);
  *   dot: d q_t = sum_j dS_tj gbar_j.
  * adot [2, n_keys] float32 is scratch. Deterministic.
  * Limits: n_keys <= 1024, topk <= n_keys, num_tokens >= 1.
@@ -227,14 +229,14 @@ size_t pkm_me_grad_workspace_size(int64_t num_tokens, int64_t heads, int64_t n_k
 int pkm_me_grad_fwd(const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2, int dtype,
                     int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
                     float weight, const float* qq, const float* kk, const float* dots, float* entropy,
-                    float* coef, float* avec, float* pbar, void* workspace, size_t workspace_bytes,
-                    void* stream);
+                    float* coef, float* avec, float* pbar, float* colsum, void* workspace,
+                    size_t workspace_bytes, void* stream);
 int pkm_me_grad_hvp(const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2, int dtype,
                     int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
                     float weight, const float* qq, const float* kk, const float* kg, const float* dots,
                     const float* qg, const float* avec, const float* pbar, float* adot, void* d_s1,
-                    void* d_s2, float* ul, float* lsum, void* workspace, size_t workspace_bytes,
-                    void* stream);
+                    void* d_s2, float* ul, float* lsum, float* lam_colsum, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /* Sub-key score of pkm_score_topk. */
 enum pkm_score_t {
@@ -293,20 +295,24 @@ int pkm_score_grad_dense(const int64_t* indices, const void* d_scores, int dtype
 
 /*
  * The idw (distance) factor of a dense sub-score gradient, for the products
- *   dq_b = 2 (U_b @ keys_b - q_b * rowsum_b),  dkeys_b = 2 (U_b^T @ q_b - keys_b * colsum(U_b)):
+ *   dq_b = 2 (U_b @ keys_b - q_b * rowsum_b),  dkeys_b = 2 (U_b^T @ q_b - keys_b * colsum_b):
  *   U[b, t, j]   = dS[b, t, j] / (1e-3 + d2) where d2 = (qq[b, t] + kk[b, j]) - 2 dots[b, t, j] > 0, else 0
- *   rowsum[b, t] = sum_j U[b, t, j]
+ *   rowsum[b, t] = sum_j U[b, t, j],  colsum[b, j] = sum_t U[b, t, j]   (fixed order)
  * dS [batches, tokens, n_keys] in dtype (pkm_score_grad_dense's output, batch
- * b = 2h + c); qq [batches, tokens] = |q_t|^2, kk [batches, n_keys] = |k_j|^2,
- * dots [batches, tokens, n_keys] = <q_t, k_j>, float32 (the operands of the
- * mm-based distance); U, rowsum float32, fully written.
+ * b = 2h + c, batches even); qq [batches, tokens] = |q_t|^2, kk [batches,
+ * n_keys] = |k_j|^2, dots [batches, tokens, n_keys] = <q_t, k_j>, float32 (the
+ * operands of the mm-based distance); U, rowsum, colsum float32, fully
+ * written. Limits: n_keys <= 1024, tokens >= 1.
+ * workspace: pkm_idw_grad_coef_workspace_size(batches, tokens, n_keys) bytes.
  *
  * Replaces the elementwise part of cdist's autograd backward (compute_mode
  * use_mm_for_euclid_dist) under the idw scores of
  * FastWeightProductKeyMemory.compute_qk_scores (fwpkm/fwpkm.py:863-866).
  */
+size_t pkm_idw_grad_coef_workspace_size(int64_t batches, int64_t tokens, int64_t n_keys);
 int pkm_idw_grad_coef(const void* dS, int dtype, const float* qq, const float* kk, const float* dots,
-                      int64_t batches, int64_t tokens, int64_t n_keys, float* U, float* rowsum, void* stream);
+                      int64_t batches, int64_t tokens, int64_t n_keys, float* U, float* rowsum, float* colsum,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes pkm_score_grad_sparse needs for these sizes (0 when unsupported). */
 size_t pkm_score_grad_sparse_workspace_size(int64_t num_tokens, int64_t heads, int64_t n_keys,

@@ -108,12 +108,14 @@ SIGNATURES = {
             c_void_p, c_void_p,  # d_sub_dense, stream
         ],
     ),
+    "pkm_idw_grad_coef_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
     "pkm_idw_grad_coef": (
         c_int,
         [
             c_void_p, c_int, c_void_p, c_void_p, c_void_p,  # dS, dtype, qq, kk, dots
             c_int64, c_int64, c_int64,  # batches, tokens, n_keys
-            c_void_p, c_void_p, c_void_p,  # U, rowsum, stream
+            c_void_p, c_void_p, c_void_p,  # U, rowsum, colsum
+            c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),
     "pkm_score_grad_sparse_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
@@ -173,7 +175,7 @@ SIGNATURES = {
             c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, topk
             c_int, c_float,  # score_type, weight
             c_void_p, c_void_p, c_void_p,  # qq, kk, dots
-            c_void_p, c_void_p, c_void_p, c_void_p,  # entropy, coef, avec, pbar
+            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # entropy, coef, avec, pbar, colsum
             c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),
@@ -185,7 +187,7 @@ SIGNATURES = {
             c_int, c_float,  # score_type, weight
             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # qq, kk, kg, dots, qg
             c_void_p, c_void_p, c_void_p,  # avec, pbar, adot
-            c_void_p, c_void_p, c_void_p, c_void_p,  # d_s1, d_s2, ul, lsum
+            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # d_s1, d_s2, ul, lsum, lam_colsum
             c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),

@@ -47,18 +47,30 @@
 //
 // Every (t, j) entry is handled independently, so the cost does not depend
 // on how many entries tie at a row's threshold (16-bit idw scores tie for
-// most of a row). Work split: a wave takes kTokPerWave tokens of one batch b,
+// most of a row). Work split: a wave takes G.rpw tokens of one batch b (1-8,
+// chosen for about 16 K waves: the row loop is latency-bound),
 // a row at a time; lane l holds the row's entries l, l + 64, ... (NPL of
 // them, n <= 64 NPL). Column sums over rows (pbar, the Pdot sums) are
 // per-wave register partials, added in wave order within a workgroup and in
-// workgroup order by a finalize kernel: every result is deterministic.
+// workgroup order by a finalize kernel: every result is deterministic. The
+// column sums the key-side products need (sum_t U_tj, sum_t lam_tj) leave the
+// row kernels the same way, as per-workgroup partials reduced in order.
+//
+// The same row layout serves the idw factor of the retrieval's dense
+// backward (pkm_idw_grad_coef): with s = -log(1e-3 + d2) the products
+// dq = 2 (U K - q rowsum U) and dK = 2 (U^T q - K colsum U) take
+// U = dS / (1e-3 + d2) where d2 > 0 (cdist's autograd under
+// compute_mode use_mm_for_euclid_dist, fwpkm/fwpkm.py:863-866).
+#include <initializer_list>
+
 #include "pkm_common.h"
 
 namespace pkm {
 namespace me {
 
 constexpr int kWaves = 8;
-constexpr int kTokPerWave = 8;
+constexpr int kMaxRowsPerWave = 8;
+constexpr int64_t kTargetWaves = 16384;
 constexpr float kEntEps = 1e-8f;
 constexpr float kIdwEps = 1e-3f;
 
@@ -102,7 +114,8 @@ __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 struct Geo {
   int64_t tokens;
-  int heads, n, topk, wgb;
+  int heads, n, topk, wgb, rpw;  // rpw: tokens per wave
+  int vec;  // rows read and written as 16-byte vectors (n % 8 == 0, aligned rows)
 };
 
 // The wave's batch and first token; workgroup g covers batch g / wgb.
@@ -116,33 +129,129 @@ __device__ __forceinline__ WaveJob wave_job(const Geo& G) {
   J.b = g / G.wgb;
   J.c = J.b & 1;
   J.h = J.b >> 1;
-  J.t0 = ((int64_t)(g % G.wgb) * kWaves + (threadIdx.x >> 6)) * kTokPerWave;
-  J.t1 = J.t0 + kTokPerWave < G.tokens ? J.t0 + kTokPerWave : G.tokens;
+  J.t0 = ((int64_t)(g % G.wgb) * kWaves + (threadIdx.x >> 6)) * G.rpw;
+  J.t1 = J.t0 + G.rpw < G.tokens ? J.t0 + G.rpw : G.tokens;
   return J;
 }
 
-// P of one row (0 outside its mask) and the mask as one ballot per register.
+// Column of lane l's i-th entry of a row: 4 consecutive columns per 16-byte
+// vector (entry 4v + e is column 256v + 4l + e) when the rows allow it, else
+// column 64i + l.
+template <int NPL>
+__device__ __forceinline__ int col_of(const Geo& G, int lane, int i) {
+  if constexpr (NPL >= 4) {
+    if (G.vec) return 256 * (i >> 2) + 4 * lane + (i & 3);
+  }
+  return 64 * i + lane;
+}
+
+template <typename T>
+__device__ __forceinline__ void ld4(const T* p, float* f);
+template <>
+__device__ __forceinline__ void ld4<float>(const float* p, float* f) {
+  const float4 v = *(const float4*)p;
+  f[0] = v.x;
+  f[1] = v.y;
+  f[2] = v.z;
+  f[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void ld4<bf16_t>(const bf16_t* p, float* f) {
+  const uint2 w = *(const uint2*)p;
+  f[0] = __uint_as_float(w.x << 16);
+  f[1] = __uint_as_float(w.x & 0xffff0000u);
+  f[2] = __uint_as_float(w.y << 16);
+  f[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ void ld4<f16_t>(const f16_t* p, float* f) {
+  const uint2 w = *(const uint2*)p;
+  f[0] = f16_bits_to_f32(w.x & 0xffffu);
+  f[1] = f16_bits_to_f32(w.x >> 16);
+  f[2] = f16_bits_to_f32(w.y & 0xffffu);
+  f[3] = f16_bits_to_f32(w.y >> 16);
+}
+
+template <typename T>
+__device__ __forceinline__ void st4(T* p, const float* f);
+template <>
+__device__ __forceinline__ void st4<float>(float* p, const float* f) {
+  *(float4*)p = make_float4(f[0], f[1], f[2], f[3]);
+}
+template <>
+__device__ __forceinline__ void st4<bf16_t>(bf16_t* p, const float* f) {
+  *(uint2*)p = make_uint2(pack2_bf16(f[0], f[1]), pack2_bf16(f[2], f[3]));
+}
+template <>
+__device__ __forceinline__ void st4<f16_t>(f16_t* p, const float* f) {
+  *(uint2*)p = make_uint2(pack2_f16(f[0], f[1]), pack2_f16(f[2], f[3]));
+}
+
+// A lane's entries of a row of n (fill outside [0, n)).
 template <typename T, int NPL>
-__device__ __forceinline__ void row_probs(const T* __restrict__ srow, const int64_t* __restrict__ selrow, int n,
-                                          int topk, int lane, float (&p)[NPL], uint64_t (&in)[NPL]) {
-  int64_t kj = selrow[topk - 1];
-  kj = kj < 0 ? 0 : (kj >= n ? n - 1 : kj);  // a list entry outside the row reads inside it
+__device__ __forceinline__ void load_row(const T* __restrict__ row, const Geo& G, int lane, float fill,
+                                         float (&v)[NPL]) {
+  if constexpr (NPL >= 4) {
+    if (G.vec) {
+#pragma unroll
+      for (int q = 0; q < NPL / 4; ++q) {
+        const int c0 = 256 * q + 4 * lane;
+        if (c0 < G.n) {
+          ld4<T>(row + c0, v + 4 * q);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * q + e] = fill;
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = 64 * i + lane;
+    v[i] = j < G.n ? ldf<T>(row, j) : fill;
+  }
+}
+
+template <typename T, int NPL>
+__device__ __forceinline__ void store_row(T* __restrict__ row, const Geo& G, int lane, const float (&v)[NPL]) {
+  if constexpr (NPL >= 4) {
+    if (G.vec) {
+#pragma unroll
+      for (int q = 0; q < NPL / 4; ++q) {
+        const int c0 = 256 * q + 4 * lane;
+        if (c0 < G.n) st4<T>(row + c0, v + 4 * q);
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = 64 * i + lane;
+    if (j < G.n) stf<T>(row, j, v[i]);
+  }
+}
+
+// P of one row (0 outside its mask) and the mask.
+template <typename T, int NPL>
+__device__ __forceinline__ void row_probs(const T* __restrict__ srow, const int64_t* __restrict__ selrow,
+                                          const Geo& G, int lane, float (&p)[NPL], bool (&on)[NPL]) {
+  int64_t kj = selrow[G.topk - 1];
+  kj = kj < 0 ? 0 : (kj >= G.n ? G.n - 1 : kj);  // a list entry outside the row reads inside it
   const float kth = ldf<T>(srow, kj);
   float v[NPL];
+  load_row<T, NPL>(srow, G, lane, -__builtin_inff(), v);
   float mx = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    const int j = lane + 64 * i;
-    v[i] = j < n ? ldf<T>(srow, j) : -__builtin_inff();
-    const bool on = j < n && v[i] >= kth;
-    in[i] = __ballot(on);
-    if (on) mx = fmaxf(mx, v[i]);
+    on[i] = col_of<NPL>(G, lane, i) < G.n && v[i] >= kth;
+    if (on[i]) mx = fmaxf(mx, v[i]);
   }
   mx = wave_max(mx);
   float z = 0.f;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    p[i] = ((in[i] >> lane) & 1) ? expf(v[i] - mx) : 0.f;
+    p[i] = on[i] ? expf(v[i] - mx) : 0.f;
     z += p[i];
   }
   z = wave_sum(z);
@@ -153,26 +262,26 @@ __device__ __forceinline__ void row_probs(const T* __restrict__ srow, const int6
 // Per-lane column partials of the wave's rows, added in wave order, one row
 // of `partial` per workgroup.
 template <int NPL>
-__device__ __forceinline__ void store_partial(const float (&acc)[NPL], int n, float* __restrict__ partial) {
+__device__ __forceinline__ void store_partial(const float (&acc)[NPL], const Geo& G, float* __restrict__ partial) {
   __shared__ float red[kWaves][64 * NPL];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) red[wv][lane + 64 * i] = acc[i];
+  for (int i = 0; i < NPL; ++i) red[wv][col_of<NPL>(G, lane, i)] = acc[i];
   __syncthreads();
-  for (int j = threadIdx.x; j < n; j += 64 * kWaves) {
+  for (int j = threadIdx.x; j < G.n; j += 64 * kWaves) {
     float s = red[0][j];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) s += red[w][j];
-    partial[(int64_t)blockIdx.x * n + j] = s;
+    partial[(int64_t)blockIdx.x * G.n + j] = s;
   }
 }
 
 // Pass 1 of the loss: column partials of P.
 template <typename T, int NPL>
 __global__ __launch_bounds__(64 * kWaves) void me_pbar_kernel(const T* __restrict__ s1, const T* __restrict__ s2,
-                                                      const int64_t* __restrict__ sel1,
-                                                      const int64_t* __restrict__ sel2, Geo G,
-                                                      float* __restrict__ partial) {
+                                                              const int64_t* __restrict__ sel1,
+                                                              const int64_t* __restrict__ sel2, Geo G,
+                                                              float* __restrict__ partial) {
   const int lane = threadIdx.x & 63;
   const WaveJob J = wave_job(G);
   const T* s = J.c ? s2 : s1;
@@ -183,30 +292,31 @@ __global__ __launch_bounds__(64 * kWaves) void me_pbar_kernel(const T* __restric
   for (int64_t t = J.t0; t < J.t1; ++t) {
     const int64_t r = t * G.heads + J.h;
     float p[NPL];
-    uint64_t in[NPL];
-    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G.n, G.topk, lane, p, in);
+    bool on[NPL];
+    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G, lane, p, on);
 #pragma unroll
     for (int i = 0; i < NPL; ++i) acc[i] += p[i];
   }
-  store_partial<NPL>(acc, G.n, partial);
+  store_partial<NPL>(acc, G, partial);
 }
 
-// Sums the partials of each half: workgroup (column block, half c), 64
-// columns x kFinGroups row groups; row group rg adds partial rows rg,
+// Sums the partials of each half: workgroup (column block, half c) of
+// kFinCols columns x kFinGroups row groups; row group rg adds partial rows rg,
 // rg + kFinGroups, ... (heads, then workgroups) and the groups are added in
 // order.
 //   mode 0: pbar, a, and the block's share of sum_j pbar_j log(pbar_j + eps)
 //           (ent_part [2, column blocks]; me_coef_kernel adds the shares);
 //   mode 1: adot from the Pdot partials.
-constexpr int kFinGroups = 16;
-__global__ __launch_bounds__(64 * kFinGroups) void me_finalize_kernel(const float* __restrict__ partial, Geo G,
-                                                                      float weight, int mode,
-                                                                      float* __restrict__ pbar,
-                                                                      float* __restrict__ avec,
-                                                                      float* __restrict__ ent_part) {
+constexpr int kFinCols = 16;
+constexpr int kFinGroups = 64;
+__global__ __launch_bounds__(kFinCols * kFinGroups) void me_finalize_kernel(const float* __restrict__ partial, Geo G,
+                                                                            float weight, int mode,
+                                                                            float* __restrict__ pbar,
+                                                                            float* __restrict__ avec,
+                                                                            float* __restrict__ ent_part) {
   const int c = blockIdx.y;
-  const int col = threadIdx.x & 63, rg = threadIdx.x >> 6;
-  const int j = blockIdx.x * 64 + col;
+  const int col = threadIdx.x % kFinCols, rg = threadIdx.x / kFinCols;
+  const int j = blockIdx.x * kFinCols + col;
   const int rows = G.heads * G.wgb;
   float S = 0.f;
   if (j < G.n) {
@@ -216,14 +326,14 @@ __global__ __launch_bounds__(64 * kFinGroups) void me_finalize_kernel(const floa
       S += partial[((int64_t)(2 * h + c) * G.wgb + g) * G.n + j];
     }
   }
-  __shared__ float red[kFinGroups][64];
+  __shared__ float red[kFinGroups][kFinCols];
   red[rg][col] = S;
   __syncthreads();
-  if (rg != 0) return;
+  if (threadIdx.x >= 64) return;  // wave 0 finishes (its first kFinCols lanes own the columns)
   float hs = 0.f;
-  if (j < G.n) {
+  if (rg == 0 && j < G.n) {
     float T = red[0][col];
-#pragma unroll
+#pragma unroll 8
     for (int k = 1; k < kFinGroups; ++k) T += red[k][col];
     const float R = (float)(G.tokens * G.heads);
     if (mode == 0) {
@@ -238,8 +348,31 @@ __global__ __launch_bounds__(64 * kFinGroups) void me_finalize_kernel(const floa
     }
   }
   if (mode == 0) {
-    hs = wave_sum(hs);  // rg == 0 is wave 0
-    if (col == 0) ent_part[c * gridDim.x + blockIdx.x] = hs;
+    hs = wave_sum(hs);
+    if (threadIdx.x == 0) ent_part[c * gridDim.x + blockIdx.x] = hs;
+  }
+}
+
+// out[b, j] = sum over the batch's workgroups g, in order, of partial[b * wgb + g][j]
+// (row groups rg, rg + kFinGroups, ... summed per thread, the groups added in order).
+__global__ __launch_bounds__(kFinCols * kFinGroups) void me_colsum_kernel(const float* __restrict__ partial, Geo G,
+                                                                          float* __restrict__ out) {
+  const int b = blockIdx.y;
+  const int col = threadIdx.x % kFinCols, rg = threadIdx.x / kFinCols;
+  const int j = blockIdx.x * kFinCols + col;
+  float S = 0.f;
+  if (j < G.n) {
+#pragma unroll 4
+    for (int g = rg; g < G.wgb; g += kFinGroups) S += partial[((int64_t)b * G.wgb + g) * G.n + j];
+  }
+  __shared__ float red[kFinGroups][kFinCols];
+  red[rg][col] = S;
+  __syncthreads();
+  if (rg == 0 && j < G.n) {
+    float T = red[0][col];
+#pragma unroll 8
+    for (int k = 1; k < kFinGroups; ++k) T += red[k][col];
+    out[(int64_t)b * G.n + j] = T;
   }
 }
 
@@ -254,31 +387,26 @@ __device__ __forceinline__ void row_dS(const float (&p)[NPL], const float (&av)[
   *pa_out = pa;
 }
 
-template <int NPL>
-__device__ __forceinline__ void load_cols(const float* __restrict__ v, int n, int lane, float (&x)[NPL]) {
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int j = lane + 64 * i;
-    x[i] = j < n ? v[j] : 0.f;
-  }
-}
-
-// Pass 2 of the loss: dense coefficient rows (U for idw, dS for dot).
-// idw: d2_tj = (|q_t|^2 + |k_j|^2) - 2 dots_tj from qq [2 heads, tokens],
-// kk [2 heads, n] and dots [2 heads, tokens, n] (the same expression and
-// operands as the reference path's mm-based distances).
+// Pass 2 of the loss: dense coefficient rows (U for idw, dS for dot) and, for
+// idw, per-workgroup column partials of U. d2_tj = (|q_t|^2 + |k_j|^2) - 2
+// dots_tj from qq [2 heads, tokens], kk [2 heads, n] and dots [2 heads,
+// tokens, n] (the same expression and operands as the reference path's
+// mm-based distances).
 template <typename T, int NPL, bool IDW>
 __global__ __launch_bounds__(64 * kWaves) void me_coef_kernel(const T* __restrict__ s1, const T* __restrict__ s2,
-                                                      const int64_t* __restrict__ sel1,
-                                                      const int64_t* __restrict__ sel2, const float* __restrict__ qq,
-                                                      const float* __restrict__ kk, const float* __restrict__ dots,
-                                                      Geo G, const float* __restrict__ avec,
-                                                      const float* __restrict__ ent_part,
-                                                      float* __restrict__ entropy, float* __restrict__ coef) {
+                                                              const int64_t* __restrict__ sel1,
+                                                              const int64_t* __restrict__ sel2,
+                                                              const float* __restrict__ qq,
+                                                              const float* __restrict__ kk,
+                                                              const float* __restrict__ dots, Geo G,
+                                                              const float* __restrict__ avec,
+                                                              const float* __restrict__ ent_part,
+                                                              float* __restrict__ entropy, float* __restrict__ coef,
+                                                              float* __restrict__ partial) {
   const int lane = threadIdx.x & 63;
   if (blockIdx.x == 0 && threadIdx.x < 2) {
     // H_c from the finalize kernel's column-block shares, in block order
-    const int nb = (G.n + 63) / 64;
+    const int nb = (G.n + kFinCols - 1) / kFinCols;
     float h = 0.f;
     for (int k = 0; k < nb; ++k) h += ent_part[threadIdx.x * nb + k];
     entropy[threadIdx.x] = -h;
@@ -286,58 +414,57 @@ __global__ __launch_bounds__(64 * kWaves) void me_coef_kernel(const T* __restric
   const WaveJob J = wave_job(G);
   const T* s = J.c ? s2 : s1;
   const int64_t* sel = J.c ? sel2 : sel1;
-  float av[NPL], kv[NPL];
-  load_cols<NPL>(avec + J.c * G.n, G.n, lane, av);
-  if constexpr (IDW) load_cols<NPL>(kk + (int64_t)J.b * G.n, G.n, lane, kv);
+  float av[NPL], kv[NPL], csum[NPL];
+  load_row<float, NPL>(avec + J.c * G.n, G, lane, 0.f, av);
+  if constexpr (IDW) load_row<float, NPL>(kk + (int64_t)J.b * G.n, G, lane, 0.f, kv);
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) csum[i] = 0.f;
   for (int64_t t = J.t0; t < J.t1; ++t) {
     const int64_t r = t * G.heads + J.h;
     const int64_t bt = (int64_t)J.b * G.tokens + t;
-    float p[NPL], ds[NPL], pa;
-    uint64_t in[NPL];
-    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G.n, G.topk, lane, p, in);
+    float p[NPL], ds[NPL], cf[NPL], pa;
+    bool on[NPL];
+    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G, lane, p, on);
     row_dS<T, NPL>(p, av, ds, &pa);
-    float* crow = coef + bt * G.n;
     if constexpr (IDW) {
       const float q2 = qq[bt];
-      const float* drow = dots + bt * G.n;
+      float dv[NPL];
+      load_row<float, NPL>(dots + bt * G.n, G, lane, 0.f, dv);
 #pragma unroll
       for (int i = 0; i < NPL; ++i) {
-        const int j = lane + 64 * i;
-        if (j < G.n) {
-          const float d2 = (q2 + kv[i]) - 2.f * drow[j];
-          crow[j] = ((in[i] >> lane) & 1) && d2 > 0.f ? ds[i] / (kIdwEps + d2) : 0.f;
-        }
+        const float d2 = (q2 + kv[i]) - 2.f * dv[i];
+        cf[i] = on[i] && d2 > 0.f ? ds[i] / (kIdwEps + d2) : 0.f;
+        csum[i] += cf[i];
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        const int j = lane + 64 * i;
-        if (j < G.n) crow[j] = ds[i];
-      }
+      for (int i = 0; i < NPL; ++i) cf[i] = ds[i];
     }
+    store_row<float, NPL>(coef + bt * G.n, G, lane, cf);
   }
+  // idw: column sums of U (the key gradient's k_j sum_t U_tj term), per workgroup
+  if constexpr (IDW) store_partial<NPL>(csum, G, partial);
 }
 
-// sigma and u of a row's entries (0 outside the mask). idw: e = qg_tj - kg_j
-// (qg = <q_t, gbar_j> [2 heads, tokens, n], kg = <k_j, gbar_j> [2 heads, n]).
+// sigma and u of a row's entries (0 outside the mask): idw sigma = 2 u e with
+// e = qg_tj - kg_j (qg = <q_t, gbar_j>, kg = <k_j, gbar_j>); dot sigma = qg_tj.
 template <int NPL, bool IDW>
-__device__ __forceinline__ void row_sigma(const uint64_t (&in)[NPL], int lane, int n, float q2, const float (&kv)[NPL],
-                                          const float (&kg)[NPL], const float* __restrict__ drow,
-                                          const float* __restrict__ erow, float (&sg)[NPL], float (&uu)[NPL]) {
+__device__ __forceinline__ void row_sigma(const bool (&on)[NPL], float q2, const float (&kv)[NPL],
+                                          const float (&kg)[NPL], const float (&dv)[NPL], const float (&ev)[NPL],
+                                          float (&sg)[NPL], float (&uu)[NPL], float (&d2v)[NPL]) {
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    const int j = lane + 64 * i;
-    const bool on = j < n && ((in[i] >> lane) & 1);
-    sg[i] = uu[i] = 0.f;
-    if (!on) continue;
+    sg[i] = uu[i] = d2v[i] = 0.f;
+    if (!on[i]) continue;
     if constexpr (IDW) {
-      const float d2 = (q2 + kv[i]) - 2.f * drow[j];
+      const float d2 = (q2 + kv[i]) - 2.f * dv[i];
+      d2v[i] = d2;
       if (d2 > 0.f) {
         uu[i] = 1.f / (kIdwEps + d2);
-        sg[i] = 2.f * uu[i] * (erow[j] - kg[i]);
+        sg[i] = 2.f * uu[i] * (ev[i] - kg[i]);
       }
     } else {
-      sg[i] = erow[j];
+      sg[i] = ev[i];
     }
   }
 }
@@ -345,19 +472,22 @@ __device__ __forceinline__ void row_sigma(const uint64_t (&in)[NPL], int lane, i
 // Pass 1 of the derivative: column partials of Pdot.
 template <typename T, int NPL, bool IDW>
 __global__ __launch_bounds__(64 * kWaves) void me_hvp1_kernel(const T* __restrict__ s1, const T* __restrict__ s2,
-                                                      const int64_t* __restrict__ sel1,
-                                                      const int64_t* __restrict__ sel2, const float* __restrict__ qq,
-                                                      const float* __restrict__ kk, const float* __restrict__ kg,
-                                                      const float* __restrict__ dots, const float* __restrict__ qg,
-                                                      Geo G, float* __restrict__ partial) {
+                                                              const int64_t* __restrict__ sel1,
+                                                              const int64_t* __restrict__ sel2,
+                                                              const float* __restrict__ qq,
+                                                              const float* __restrict__ kk,
+                                                              const float* __restrict__ kg,
+                                                              const float* __restrict__ dots,
+                                                              const float* __restrict__ qg, Geo G,
+                                                              float* __restrict__ partial) {
   const int lane = threadIdx.x & 63;
   const WaveJob J = wave_job(G);
   const T* s = J.c ? s2 : s1;
   const int64_t* sel = J.c ? sel2 : sel1;
   float kv[NPL], kgv[NPL];
   if constexpr (IDW) {
-    load_cols<NPL>(kk + (int64_t)J.b * G.n, G.n, lane, kv);
-    load_cols<NPL>(kg + (int64_t)J.b * G.n, G.n, lane, kgv);
+    load_row<float, NPL>(kk + (int64_t)J.b * G.n, G, lane, 0.f, kv);
+    load_row<float, NPL>(kg + (int64_t)J.b * G.n, G, lane, 0.f, kgv);
   }
   float acc[NPL];
 #pragma unroll
@@ -365,11 +495,12 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp1_kernel(const T* __restric
   for (int64_t t = J.t0; t < J.t1; ++t) {
     const int64_t r = t * G.heads + J.h;
     const int64_t bt = (int64_t)J.b * G.tokens + t;
-    float p[NPL], sg[NPL], uu[NPL];
-    uint64_t in[NPL];
-    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G.n, G.topk, lane, p, in);
-    row_sigma<NPL, IDW>(in, lane, G.n, IDW ? qq[bt] : 0.f, kv, kgv, IDW ? dots + bt * G.n : nullptr,
-                        qg + bt * G.n, sg, uu);
+    float p[NPL], sg[NPL], uu[NPL], d2v[NPL], dv[NPL], ev[NPL];
+    bool on[NPL];
+    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G, lane, p, on);
+    if constexpr (IDW) load_row<float, NPL>(dots + bt * G.n, G, lane, 0.f, dv);
+    load_row<float, NPL>(qg + bt * G.n, G, lane, 0.f, ev);
+    row_sigma<NPL, IDW>(on, IDW ? qq[bt] : 0.f, kv, kgv, dv, ev, sg, uu, d2v);
     float tau = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) tau += p[i] * sg[i];
@@ -377,49 +508,56 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp1_kernel(const T* __restric
 #pragma unroll
     for (int i = 0; i < NPL; ++i) acc[i] += p[i] * (sg[i] - tau);
   }
-  store_partial<NPL>(acc, G.n, partial);
+  store_partial<NPL>(acc, G, partial);
 }
 
 // Pass 2 of the derivative: the sub-scores' gradient rho, and the direct
-// terms' coefficients: idw rows [U | lam] of 2n entries and the row sums of
-// lam, dot rows dS of n entries.
+// terms' coefficients: idw rows [U | lam] of 2n entries, the row sums of lam
+// and per-workgroup column partials of lam; dot rows dS of n entries.
 template <typename T, int NPL, bool IDW>
 __global__ __launch_bounds__(64 * kWaves) void me_hvp2_kernel(const T* __restrict__ s1, const T* __restrict__ s2,
-                                                      const int64_t* __restrict__ sel1,
-                                                      const int64_t* __restrict__ sel2, const float* __restrict__ qq,
-                                                      const float* __restrict__ kk, const float* __restrict__ kg,
-                                                      const float* __restrict__ dots, const float* __restrict__ qg,
-                                                      Geo G, const float* __restrict__ avec,
-                                                      const float* __restrict__ adot, T* __restrict__ d_s1,
-                                                      T* __restrict__ d_s2, float* __restrict__ ul,
-                                                      float* __restrict__ lsum) {
+                                                              const int64_t* __restrict__ sel1,
+                                                              const int64_t* __restrict__ sel2,
+                                                              const float* __restrict__ qq,
+                                                              const float* __restrict__ kk,
+                                                              const float* __restrict__ kg,
+                                                              const float* __restrict__ dots,
+                                                              const float* __restrict__ qg, Geo G,
+                                                              const float* __restrict__ avec,
+                                                              const float* __restrict__ adot, T* __restrict__ d_s1,
+                                                              T* __restrict__ d_s2, float* __restrict__ ul,
+                                                              float* __restrict__ lsum, float* __restrict__ partial) {
   const int lane = threadIdx.x & 63;
   const WaveJob J = wave_job(G);
   const T* s = J.c ? s2 : s1;
   const int64_t* sel = J.c ? sel2 : sel1;
   T* d_s = J.c ? d_s2 : d_s1;
   float av[NPL], ad[NPL], kv[NPL], kgv[NPL];
-  load_cols<NPL>(avec + J.c * G.n, G.n, lane, av);
-  load_cols<NPL>(adot + J.c * G.n, G.n, lane, ad);
+  load_row<float, NPL>(avec + J.c * G.n, G, lane, 0.f, av);
+  load_row<float, NPL>(adot + J.c * G.n, G, lane, 0.f, ad);
   if constexpr (IDW) {
-    load_cols<NPL>(kk + (int64_t)J.b * G.n, G.n, lane, kv);
-    load_cols<NPL>(kg + (int64_t)J.b * G.n, G.n, lane, kgv);
+    load_row<float, NPL>(kk + (int64_t)J.b * G.n, G, lane, 0.f, kv);
+    load_row<float, NPL>(kg + (int64_t)J.b * G.n, G, lane, 0.f, kgv);
   }
   const int width = IDW ? 2 * G.n : G.n;
+  float lcol[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) lcol[i] = 0.f;
   for (int64_t t = J.t0; t < J.t1; ++t) {
     const int64_t r = t * G.heads + J.h;
     const int64_t bt = (int64_t)J.b * G.tokens + t;
-    float p[NPL], ds[NPL], sg[NPL], uu[NPL], pa;
-    uint64_t in[NPL];
-    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G.n, G.topk, lane, p, in);
+    float p[NPL], ds[NPL], sg[NPL], uu[NPL], d2v[NPL], dv[NPL], ev[NPL], pa;
+    bool on[NPL];
+    row_probs<T, NPL>(s + r * G.n, sel + r * G.topk, G, lane, p, on);
     row_dS<T, NPL>(p, av, ds, &pa);
-    row_sigma<NPL, IDW>(in, lane, G.n, IDW ? qq[bt] : 0.f, kv, kgv, IDW ? dots + bt * G.n : nullptr,
-                        qg + bt * G.n, sg, uu);
+    if constexpr (IDW) load_row<float, NPL>(dots + bt * G.n, G, lane, 0.f, dv);
+    load_row<float, NPL>(qg + bt * G.n, G, lane, 0.f, ev);
+    row_sigma<NPL, IDW>(on, IDW ? qq[bt] : 0.f, kv, kgv, dv, ev, sg, uu, d2v);
     float tau = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) tau += p[i] * sg[i];
     tau = wave_sum(tau);
-    float pd[NPL];
+    float pd[NPL], rho[NPL];
     float beta_dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
@@ -427,31 +565,69 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp2_kernel(const T* __restric
       beta_dot += pd[i] * av[i] + p[i] * ad[i];
     }
     beta_dot = wave_sum(beta_dot);
-    T* drow = d_s + r * G.n;
-    float* urow = ul + bt * width;
-    float lacc = 0.f;
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int j = lane + 64 * i;
-      if (j < G.n) {
-        stf<T>(drow, j, pd[i] * (av[i] - pa) + p[i] * (ad[i] - beta_dot));
-        if constexpr (IDW) {
-          // U as the loss pass writes it (uu = 0 where d2 <= 0 or outside the mask)
-          const float U = uu[i] != 0.f ? ds[i] / (kIdwEps + ((qq[bt] + kv[i]) - 2.f * dots[bt * G.n + j])) : 0.f;
-          const float lm = ds[i] * uu[i] * sg[i];
-          urow[j] = U;
-          urow[G.n + j] = lm;
-          lacc += lm;
-        } else {
-          urow[j] = ds[i];
-        }
-      }
-    }
+    for (int i = 0; i < NPL; ++i) rho[i] = pd[i] * (av[i] - pa) + p[i] * (ad[i] - beta_dot);
+    store_row<T, NPL>(d_s + r * G.n, G, lane, rho);
+    float* urow = ul + bt * width;
     if constexpr (IDW) {
+      // U as the loss pass writes it (uu = 0 where d2 <= 0 or outside the mask)
+      float U[NPL], lm[NPL];
+      float lacc = 0.f;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        U[i] = uu[i] != 0.f ? ds[i] / (kIdwEps + d2v[i]) : 0.f;
+        lm[i] = ds[i] * uu[i] * sg[i];
+        lacc += lm[i];
+        lcol[i] += lm[i];
+      }
+      store_row<float, NPL>(urow, G, lane, U);
+      store_row<float, NPL>(urow + G.n, G, lane, lm);
       lacc = wave_sum(lacc);
       if (lane == 0) lsum[bt] = lacc;
+    } else {
+      store_row<float, NPL>(urow, G, lane, ds);
     }
   }
+  // idw: column sums of lam, per workgroup
+  if constexpr (IDW) store_partial<NPL>(lcol, G, partial);
+}
+
+// The idw factor of a dense sub-score gradient dS [batches, tokens, n]:
+// U = dS / (1e-3 + d2) where d2 = (qq + kk) - 2 dots > 0, else 0; row sums
+// (lane entries in order, then a fixed DPP tree) and per-workgroup column
+// partials.
+template <typename T, int NPL>
+__global__ __launch_bounds__(64 * kWaves) void me_idw_coef_kernel(const T* __restrict__ dS,
+                                                                  const float* __restrict__ qq,
+                                                                  const float* __restrict__ kk,
+                                                                  const float* __restrict__ dots, Geo G,
+                                                                  float* __restrict__ U, float* __restrict__ rowsum,
+                                                                  float* __restrict__ partial) {
+  const int lane = threadIdx.x & 63;
+  const WaveJob J = wave_job(G);
+  float kv[NPL], csum[NPL];
+  load_row<float, NPL>(kk + (int64_t)J.b * G.n, G, lane, 0.f, kv);
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) csum[i] = 0.f;
+  for (int64_t t = J.t0; t < J.t1; ++t) {
+    const int64_t bt = (int64_t)J.b * G.tokens + t;
+    const float q2 = qq[bt];
+    float gv[NPL], dv[NPL], u[NPL];
+    load_row<T, NPL>(dS + bt * G.n, G, lane, 0.f, gv);
+    load_row<float, NPL>(dots + bt * G.n, G, lane, 0.f, dv);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float d2 = (q2 + kv[i]) - 2.f * dv[i];
+      u[i] = col_of<NPL>(G, lane, i) < G.n && d2 > 0.f ? gv[i] / (kIdwEps + d2) : 0.f;
+      acc += u[i];
+      csum[i] += u[i];
+    }
+    store_row<float, NPL>(U + bt * G.n, G, lane, u);
+    acc = wave_sum(acc);
+    if (lane == 0) rowsum[bt] = acc;
+  }
+  store_partial<NPL>(csum, G, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,7 +651,10 @@ static int check(const char* fn, int64_t tokens, int64_t heads, int64_t n, int64
               "%s: score type %d", fn, score_type);
   PKM_REQUIRE(n <= kMaxN && heads <= 4096, PKM_ERR_UNSUPPORTED, "%s: n_keys %lld > %lld or heads %lld > 4096", fn,
               (long long)n, (long long)kMaxN, (long long)heads);
-  const int64_t tblocks = (tokens + kTokPerWave - 1) / kTokPerWave;
+  // tokens per wave: about kTargetWaves waves over the 2 heads x tokens rows
+  int64_t rpw = 2 * heads * tokens / kTargetWaves;
+  rpw = rpw < 1 ? 1 : (rpw > kMaxRowsPerWave ? kMaxRowsPerWave : rpw);
+  const int64_t tblocks = (tokens + rpw - 1) / rpw;
   const int64_t wgb = (tblocks + kWaves - 1) / kWaves;
   PKM_REQUIRE(tokens < ((int64_t)1 << 40) && wgb * 2 * heads < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT,
               "%s: %lld tokens too many", fn, (long long)tokens);
@@ -484,59 +663,94 @@ static int check(const char* fn, int64_t tokens, int64_t heads, int64_t n, int64
   G->n = (int)n;
   G->topk = (int)topk;
   G->wgb = (int)wgb;
+  G->rpw = (int)rpw;
+  G->vec = 0;
   return PKM_OK;
+}
+
+// Rows as 16-byte vectors: 4 entries per lane and vector (NPL >= 4), rows of a
+// multiple of 8 entries (16-byte row starts for float32, 8-byte for 16-bit),
+// every row array 16-byte aligned.
+static int vec_ok(int64_t n, std::initializer_list<const void*> rows) {
+  if (n % 8 != 0 || npl_of(n) < 4) return 0;
+  for (const void* p : rows)
+    if (p != nullptr && (uintptr_t)p % 16 != 0) return 0;
+  return 1;
 }
 
 // partials [2 heads x wgb, n], then the entropy shares [2, column blocks]
 static size_t workspace_bytes(const Geo& G) {
-  return ((size_t)(2 * G.heads) * (size_t)G.wgb * (size_t)G.n + 2 * (size_t)((G.n + 63) / 64)) * sizeof(float);
+  return ((size_t)(2 * G.heads) * (size_t)G.wgb * (size_t)G.n + 2 * (size_t)((G.n + kFinCols - 1) / kFinCols)) *
+         sizeof(float);
 }
 static float* ent_part_of(const Geo& G, float* ws) { return ws + (size_t)(2 * G.heads) * G.wgb * G.n; }
-static dim3 fin_grid(const Geo& G) { return dim3((unsigned)((G.n + 63) / 64), 2); }
+static dim3 fin_grid(const Geo& G) { return dim3((unsigned)((G.n + kFinCols - 1) / kFinCols), 2); }
+
+static dim3 colsum_grid(const Geo& G, int batches) {
+  return dim3((unsigned)((G.n + kFinCols - 1) / kFinCols), (unsigned)batches);
+}
 
 template <typename T, int NPL>
 static void launch_fwd(const Geo& G, int idw, const void* s1, const void* s2, const int64_t* sel1,
                        const int64_t* sel2, const float* qq, const float* kk, const float* dots, float weight,
-                       float* entropy, float* coef, float* avec, float* pbar, float* partial, hipStream_t st) {
+                       float* entropy, float* coef, float* avec, float* pbar, float* colsum, float* partial,
+                       hipStream_t st) {
   const dim3 grid((unsigned)(2 * G.heads * G.wgb)), block(64 * kWaves);
   hipLaunchKernelGGL((me_pbar_kernel<T, NPL>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2, G,
                      partial);
   float* ent = ent_part_of(G, partial);
-  hipLaunchKernelGGL(me_finalize_kernel, fin_grid(G), dim3(64 * kFinGroups), 0, st, (const float*)partial, G, weight,
+  hipLaunchKernelGGL(me_finalize_kernel, fin_grid(G), dim3(kFinCols * kFinGroups), 0, st, (const float*)partial, G, weight,
                      0, pbar, avec, ent);
-  if (idw)
+  // the coefficient kernel's column partials reuse the pbar partials' space (consumed by the finalize kernel)
+  if (idw) {
     hipLaunchKernelGGL((me_coef_kernel<T, NPL, true>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2,
-                       qq, kk, dots, G, (const float*)avec, (const float*)ent, entropy, coef);
-  else
+                       qq, kk, dots, G, (const float*)avec, (const float*)ent, entropy, coef, partial);
+    if (colsum != nullptr)
+      hipLaunchKernelGGL(me_colsum_kernel, colsum_grid(G, 2 * G.heads), dim3(kFinCols * kFinGroups), 0, st,
+                         (const float*)partial, G, colsum);
+  } else {
     hipLaunchKernelGGL((me_coef_kernel<T, NPL, false>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2,
-                       qq, kk, dots, G, (const float*)avec, (const float*)ent, entropy, coef);
+                       qq, kk, dots, G, (const float*)avec, (const float*)ent, entropy, coef, partial);
+  }
 }
 
 template <typename T, int NPL, bool IDW>
 static void launch_hvp_t(const Geo& G, const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2,
                          const float* qq, const float* kk, const float* kg, const float* dots, const float* qg,
                          float weight, const float* avec, float* pbar, float* adot, void* d_s1, void* d_s2,
-                         float* ul, float* lsum, float* partial, hipStream_t st) {
+                         float* ul, float* lsum, float* lam_colsum, float* partial, hipStream_t st) {
   const dim3 grid((unsigned)(2 * G.heads * G.wgb)), block(64 * kWaves);
   hipLaunchKernelGGL((me_hvp1_kernel<T, NPL, IDW>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2, qq,
                      kk, kg, dots, qg, G, partial);
-  hipLaunchKernelGGL(me_finalize_kernel, fin_grid(G), dim3(64 * kFinGroups), 0, st, (const float*)partial, G, weight,
+  hipLaunchKernelGGL(me_finalize_kernel, fin_grid(G), dim3(kFinCols * kFinGroups), 0, st, (const float*)partial, G, weight,
                      1, pbar, adot, (float*)nullptr);
   hipLaunchKernelGGL((me_hvp2_kernel<T, NPL, IDW>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2, qq,
-                     kk, kg, dots, qg, G, avec, (const float*)adot, (T*)d_s1, (T*)d_s2, ul, lsum);
+                     kk, kg, dots, qg, G, avec, (const float*)adot, (T*)d_s1, (T*)d_s2, ul, lsum, partial);
+  if (IDW && lam_colsum != nullptr)
+    hipLaunchKernelGGL(me_colsum_kernel, colsum_grid(G, 2 * G.heads), dim3(kFinCols * kFinGroups), 0, st,
+                       (const float*)partial, G, lam_colsum);
 }
 
 template <typename T, int NPL>
 static void launch_hvp(const Geo& G, int idw, const void* s1, const void* s2, const int64_t* sel1,
                        const int64_t* sel2, const float* qq, const float* kk, const float* kg, const float* dots,
                        const float* qg, float weight, const float* avec, float* pbar, float* adot, void* d_s1,
-                       void* d_s2, float* ul, float* lsum, float* partial, hipStream_t st) {
+                       void* d_s2, float* ul, float* lsum, float* lam_colsum, float* partial, hipStream_t st) {
   if (idw)
     launch_hvp_t<T, NPL, true>(G, s1, s2, sel1, sel2, qq, kk, kg, dots, qg, weight, avec, pbar, adot, d_s1, d_s2, ul,
-                               lsum, partial, st);
+                               lsum, lam_colsum, partial, st);
   else
     launch_hvp_t<T, NPL, false>(G, s1, s2, sel1, sel2, qq, kk, kg, dots, qg, weight, avec, pbar, adot, d_s1, d_s2,
-                                ul, lsum, partial, st);
+                                ul, lsum, lam_colsum, partial, st);
+}
+
+template <typename T, int NPL>
+static void launch_idw(const Geo& G, int batches, const void* dS, const float* qq, const float* kk,
+                       const float* dots, float* U, float* rowsum, float* colsum, float* partial, hipStream_t st) {
+  hipLaunchKernelGGL((me_idw_coef_kernel<T, NPL>), dim3((unsigned)(batches * G.wgb)), dim3(64 * kWaves), 0, st,
+                     (const T*)dS, qq, kk, dots, G, U, rowsum, partial);
+  hipLaunchKernelGGL(me_colsum_kernel, colsum_grid(G, batches), dim3(kFinCols * kFinGroups), 0, st, (const float*)partial,
+                     G, colsum);
 }
 
 #define PKM_ME_DISPATCH(FN, dtype, npl, ...)                                          \
@@ -578,8 +792,8 @@ extern "C" size_t pkm_me_grad_workspace_size(int64_t num_tokens, int64_t heads, 
 extern "C" int pkm_me_grad_fwd(const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2, int dtype,
                                int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
                                float weight, const float* qq, const float* kk, const float* dots, float* entropy,
-                               float* coef, float* avec, float* pbar, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               float* coef, float* avec, float* pbar, float* colsum, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   me::Geo G;
   int rc = me::check("pkm_me_grad_fwd", num_tokens, heads, n_keys, topk, dtype, score_type, &G);
   if (rc != PKM_OK) return rc;
@@ -590,9 +804,10 @@ extern "C" int pkm_me_grad_fwd(const void* s1, const void* s2, const int64_t* se
               "pkm_me_grad_fwd: idw scores need qq, kk and dots");
   PKM_REQUIRE(workspace && workspace_bytes >= me::workspace_bytes(G), PKM_ERR_WORKSPACE,
               "pkm_me_grad_fwd: workspace %zu bytes < %zu", workspace_bytes, me::workspace_bytes(G));
+  G.vec = me::vec_ok(n_keys, {s1, s2, dots, coef, avec, kk});
   const int npl = me::npl_of(n_keys);
   PKM_ME_DISPATCH(me::launch_fwd, dtype, npl, G, idw ? 1 : 0, s1, s2, sel1, sel2, qq, kk, dots, weight, entropy,
-                  coef, avec, pbar, (float*)workspace, (hipStream_t)stream);
+                  coef, avec, pbar, colsum, (float*)workspace, (hipStream_t)stream);
   return pkm_check_launch("pkm_me_grad_fwd");
 }
 
@@ -600,8 +815,8 @@ extern "C" int pkm_me_grad_hvp(const void* s1, const void* s2, const int64_t* se
                                int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
                                float weight, const float* qq, const float* kk, const float* kg, const float* dots,
                                const float* qg, const float* avec, const float* pbar, float* adot, void* d_s1,
-                               void* d_s2, float* ul, float* lsum, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               void* d_s2, float* ul, float* lsum, float* lam_colsum, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   me::Geo G;
   int rc = me::check("pkm_me_grad_hvp", num_tokens, heads, n_keys, topk, dtype, score_type, &G);
   if (rc != PKM_OK) return rc;
@@ -612,8 +827,37 @@ extern "C" int pkm_me_grad_hvp(const void* s1, const void* s2, const int64_t* se
               "pkm_me_grad_hvp: idw scores need qq, kk, kg, dots and lsum");
   PKM_REQUIRE(workspace && workspace_bytes >= me::workspace_bytes(G), PKM_ERR_WORKSPACE,
               "pkm_me_grad_hvp: workspace %zu bytes < %zu", workspace_bytes, me::workspace_bytes(G));
+  G.vec = me::vec_ok(n_keys, {s1, s2, dots, qg, kk, kg, avec, adot, d_s1, d_s2, ul});
   const int npl = me::npl_of(n_keys);
   PKM_ME_DISPATCH(me::launch_hvp, dtype, npl, G, idw ? 1 : 0, s1, s2, sel1, sel2, qq, kk, kg, dots, qg, weight, avec,
-                  (float*)pbar, adot, d_s1, d_s2, ul, lsum, (float*)workspace, (hipStream_t)stream);
+                  (float*)pbar, adot, d_s1, d_s2, ul, lsum, lam_colsum, (float*)workspace, (hipStream_t)stream);
   return pkm_check_launch("pkm_me_grad_hvp");
+}
+
+extern "C" size_t pkm_idw_grad_coef_workspace_size(int64_t batches, int64_t tokens, int64_t n_keys) {
+  me::Geo G;
+  if (batches < 1 || batches % 2 ||
+      me::check("pkm_idw_grad_coef_workspace_size", tokens, batches / 2, n_keys, 1, PKM_DTYPE_F32, PKM_SCORE_IDW,
+                &G) != PKM_OK)
+    return 0;
+  return me::workspace_bytes(G);
+}
+
+extern "C" int pkm_idw_grad_coef(const void* dS, int dtype, const float* qq, const float* kk, const float* dots,
+                                 int64_t batches, int64_t tokens, int64_t n_keys, float* U, float* rowsum,
+                                 float* colsum, void* workspace, size_t workspace_bytes, void* stream) {
+  PKM_REQUIRE(batches >= 2 && batches % 2 == 0, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_idw_grad_coef: batches %lld (2 per head)", (long long)batches);
+  me::Geo G;
+  const int rc = me::check("pkm_idw_grad_coef", tokens, batches / 2, n_keys, 1, dtype, PKM_SCORE_IDW, &G);
+  if (rc != PKM_OK) return rc;
+  PKM_REQUIRE(dS && qq && kk && dots && U && rowsum && colsum, PKM_ERR_INVALID_ARGUMENT,
+              "pkm_idw_grad_coef: null pointer");
+  PKM_REQUIRE(workspace && workspace_bytes >= me::workspace_bytes(G), PKM_ERR_WORKSPACE,
+              "pkm_idw_grad_coef: workspace %zu bytes < %zu", workspace_bytes, me::workspace_bytes(G));
+  G.vec = me::vec_ok(n_keys, {dS, dots, U, kk});
+  const int npl = me::npl_of(n_keys);
+  PKM_ME_DISPATCH(me::launch_idw, dtype, npl, G, (int)batches, dS, qq, kk, dots, U, rowsum, colsum,
+                  (float*)workspace, (hipStream_t)stream);
+  return pkm_check_launch("pkm_idw_grad_coef");
 }

@@ -851,74 +851,3 @@ extern "C" int pkm_score_grad_sparse(const int64_t* indices, const void* d_score
   return pkm_check_launch("pkm_score_grad_sparse");
 }
 
-// ---------------------------------------------------------------------------
-// Distance-score (idw) factor of a dense sub-score gradient: with
-// s = -log(1e-3 + d2), d2 = |q|^2 + |k|^2 - 2 <q, k> clamped at 0, the
-// products dq = 2 (U K - q rowsum(U)) and dK = 2 (U^T q - K colsum(U)) take
-//   U[b, t, j] = dS[b, t, j] / (1e-3 + d2_tj) where d2_tj > 0, else 0,
-//   d2_tj = (qq[b, t] + kk[b, j]) - 2 dots[b, t, j]
-// (the expression and operands of the reference path's mm-based distances,
-// fwpkm/fwpkm.py:863-866 under autograd). One wave per row (b, t), lane l
-// taking entries l, l + 64, ...; rowsum in that order, then a fixed DPP tree.
-// ---------------------------------------------------------------------------
-namespace pkm {
-
-template <typename T>
-__global__ __launch_bounds__(256) void idw_grad_coef_kernel(const T* __restrict__ dS, const float* __restrict__ qq,
-                                                            const float* __restrict__ kk,
-                                                            const float* __restrict__ dots, int64_t rows,
-                                                            int64_t tokens, int n, float* __restrict__ U,
-                                                            float* __restrict__ rowsum) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;  // wave-uniform
-  const int64_t b = row / tokens;
-  const float q2 = qq[row];
-  const float* kb = kk + b * n;
-  const T* drow = dS + row * n;
-  const float* prow = dots + row * n;
-  float* urow = U + row * n;
-  float acc = 0.f;
-  for (int j = lane; j < n; j += 64) {
-    float g;
-    if constexpr (sizeof(T) == 4)
-      g = ((const float*)drow)[j];
-    else if constexpr (__is_same(T, bf16_t))
-      g = bf16_to_f32(((const uint16_t*)drow)[j]);
-    else
-      g = (float)((const f16_t*)drow)[j];
-    const float d2 = (q2 + kb[j]) - 2.f * prow[j];
-    const float u = d2 > 0.f ? g / (1e-3f + d2) : 0.f;
-    urow[j] = u;
-    acc += u;
-  }
-  acc = group_sum<64>(acc);
-  if (lane == 0) rowsum[row] = acc;
-}
-
-}  // namespace pkm
-
-extern "C" int pkm_idw_grad_coef(const void* dS, int dtype, const float* qq, const float* kk, const float* dots,
-                                 int64_t batches, int64_t tokens, int64_t n_keys, float* U, float* rowsum,
-                                 void* stream) {
-  PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
-              "pkm_idw_grad_coef: dtype %d not supported (float32, bfloat16 and float16 are)", dtype);
-  PKM_REQUIRE(batches >= 1 && tokens >= 0 && n_keys >= 1 && n_keys <= (1 << 30), PKM_ERR_INVALID_ARGUMENT,
-              "pkm_idw_grad_coef: bad sizes");
-  if (tokens == 0) return PKM_OK;
-  PKM_REQUIRE(dS && qq && kk && dots && U && rowsum, PKM_ERR_INVALID_ARGUMENT, "pkm_idw_grad_coef: null pointer");
-  const int64_t rows = batches * tokens;
-  const int64_t blocks = (rows + 3) / 4;
-  PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_idw_grad_coef: too many rows");
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == PKM_DTYPE_F32)
-    hipLaunchKernelGGL(idw_grad_coef_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)dS, qq, kk,
-                       dots, rows, tokens, (int)n_keys, U, rowsum);
-  else if (dtype == PKM_DTYPE_BF16)
-    hipLaunchKernelGGL(idw_grad_coef_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, st, (const bf16_t*)dS, qq,
-                       kk, dots, rows, tokens, (int)n_keys, U, rowsum);
-  else
-    hipLaunchKernelGGL(idw_grad_coef_kernel<f16_t>, dim3((unsigned)blocks), dim3(256), 0, st, (const f16_t*)dS, qq,
-                       kk, dots, rows, tokens, (int)n_keys, U, rowsum);
-  return pkm_check_launch("pkm_idw_grad_coef");
-}

@@ -707,10 +707,14 @@ class FastWeightProductKeyMemory(nn.Module):
             n_params = len(params)
             fused = self._fused_values_step(params["values"])
             bounds = _chunks(T, chunk_size, chunk_size)
+            # one split per tensor (its backward is one concatenation, not a zero-filled full-size
+            # gradient per chunk added up)
+            sizes = [e - s for s, e in bounds]
+            q_chunks, ref_chunks = q.split(sizes, dim=1), ref_v.split(sizes, dim=1)
             for ci, (start, end) in enumerate(bounds):
                 cT = end - start
                 cgates, cmask, cids = _sl(gates, start, end), _sl(loss_mask, start, end), _sl(token_ids, start, end)
-                cq = q[:, start:end, :].contiguous()
+                cq = q_chunks[ci].contiguous()
                 final = ci == len(bounds) - 1
                 read_params = step_params = params
                 if fused and not final and params["values"].requires_grad:
@@ -724,8 +728,7 @@ class FastWeightProductKeyMemory(nn.Module):
                 outputs.append(hyp)
                 indices.append(r["indices"].view(B, cT, -1))
                 scores.append(r["normed_scores"].view(B, cT, -1))
-                u_hyp, u_ref, u_w, u_mask = self._update_targets(hyp, ref_v[:, start:end, :].contiguous(), cgates,
-                                                                 cmask)
+                u_hyp, u_ref, u_w, u_mask = self._update_targets(hyp, ref_chunks[ci].contiguous(), cgates, cmask)
                 # the last step's result is only stored, never differentiated
                 mem_losses, addr_loss, addr_grads = self._losses(u_hyp, u_ref, u_w, u_mask, r, query=cq,
                                                                  params=params,

@@ -72,15 +72,14 @@ class _AddrKeyGrad(torch.autograd.Function):
         coef = torch.empty((2 * heads, tokens, n), device=dev, dtype=torch.float32)
         avec = torch.empty((2, n), device=dev, dtype=torch.float32)
         pbar = torch.empty((2, n), device=dev, dtype=torch.float32)
+        cs = torch.empty((2 * heads, n), device=dev, dtype=torch.float32) if idw else None  # sum_t U_tj
         ws = _workspace(tokens, heads, n, dev)
         _lib.call("pkm_me_grad_fwd", _lib.ptr(s1c), _lib.ptr(s2c), _lib.ptr(sel1c), _lib.ptr(sel2c),
                   _lib.dtype_code(s1c), tokens, heads, n, topk, _lib.SCORE_CODES[score_type], float(weight),
                   _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(dots), _lib.ptr(entropy), _lib.ptr(coef), _lib.ptr(avec),
-                  _lib.ptr(pbar), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+                  _lib.ptr(pbar), _lib.ptr(cs), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
         g = torch.bmm(coef.transpose(1, 2), qb)
-        cs = None
         if idw:
-            cs = coef.sum(1)
             g = 2.0 * (g - kf * cs[:, :, None])
         ctx.heads, ctx.topk, ctx.weight, ctx.score_type = heads, topk, float(weight), score_type
         ctx.query_shape, ctx.query_dtype, ctx.keys_dtype = query.shape, query.dtype, keys.dtype
@@ -110,12 +109,13 @@ class _AddrKeyGrad(torch.autograd.Function):
         d_s2 = torch.empty_like(s2)
         ul = torch.empty((2 * heads, tokens, 2 * n if idw else n), device=dev, dtype=torch.float32)
         lsum = torch.empty((2 * heads, tokens), device=dev, dtype=torch.float32) if idw else None
+        lcs = torch.empty((2 * heads, n), device=dev, dtype=torch.float32) if idw else None
         ws = _workspace(tokens, heads, n, dev)
         _lib.call("pkm_me_grad_hvp", _lib.ptr(s1), _lib.ptr(s2), _lib.ptr(sel1), _lib.ptr(sel2),
                   _lib.dtype_code(s1), tokens, heads, n, topk, _lib.SCORE_CODES[score_type], ctx.weight,
                   _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(kg), _lib.ptr(dots), _lib.ptr(qg), _lib.ptr(avec),
                   _lib.ptr(pbar), _lib.ptr(adot), _lib.ptr(d_s1), _lib.ptr(d_s2), _lib.ptr(ul), _lib.ptr(lsum),
-                  _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+                  _lib.ptr(lcs), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
         d_query = d_keys = None
         if ctx.needs_input_grad[0]:
             if idw:
@@ -126,7 +126,7 @@ class _AddrKeyGrad(torch.autograd.Function):
             d_query = dq.transpose(0, 1).reshape(ctx.query_shape).to(ctx.query_dtype)
         if idw and ctx.needs_input_grad[1]:
             lam = ul[:, :, n:]
-            dk = torch.bmm(lam.transpose(1, 2), qb) - kf * lam.sum(1)[:, :, None] - gb * cs[:, :, None]
+            dk = torch.bmm(lam.transpose(1, 2), qb) - kf * lcs[:, :, None] - gb * cs[:, :, None]
             d_keys = (2.0 * dk).reshape(2 * heads * n, half).to(ctx.keys_dtype)
         return (d_query, d_keys, d_s1 if ctx.needs_input_grad[2] else None,
                 d_s2 if ctx.needs_input_grad[3] else None) + nones

@@ -199,17 +199,24 @@ class _DenseScoreGrad(torch.autograd.Function):
         return (None, d_scores, g0 if ctx.has_sub[0] else None, g1 if ctx.has_sub[1] else None, None, None)
 
 
+IDW_COEF_MAX_N = 1024  # pkm_idw_grad_coef's n_keys limit
+
+
 def _idw_grad_coef(dS, qq, kk, dots):
-    """(U, rowsum) of pkm_idw_grad_coef: U = dS / (1e-3 + d2) where d2 =
-    (qq + kk) - 2 dots > 0, else 0, float32 [batches, tokens, n]."""
+    """(U, rowsum, colsum) of pkm_idw_grad_coef: U = dS / (1e-3 + d2) where
+    d2 = (qq + kk) - 2 dots > 0, else 0, float32 [batches, tokens, n]."""
     B, T, n = dots.shape
     dS = dS.contiguous()
     qq, kk, dots = qq.float().contiguous(), kk.float().contiguous(), dots.contiguous()
-    U = torch.empty((B, T, n), device=dots.device, dtype=torch.float32)
-    rs = torch.empty((B, T), device=dots.device, dtype=torch.float32)
+    dev = dots.device
+    U = torch.empty((B, T, n), device=dev, dtype=torch.float32)
+    rs = torch.empty((B, T), device=dev, dtype=torch.float32)
+    cs = torch.empty((B, n), device=dev, dtype=torch.float32)
+    ws_bytes = int(_lib.load().pkm_idw_grad_coef_workspace_size(B, T, n))
+    ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
     _lib.call("pkm_idw_grad_coef", _lib.ptr(dS), _lib.dtype_code(dS), _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(dots), B, T,
-              n, _lib.ptr(U), _lib.ptr(rs), _lib.stream_of(dots.device))
-    return U, rs
+              n, _lib.ptr(U), _lib.ptr(rs), _lib.ptr(cs), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev))
+    return U, rs, cs
 
 
 def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
@@ -247,17 +254,17 @@ def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
             if torch.is_grad_enabled():
                 kf = kf + (k32 - k32.detach())
         dots = torch.bmm(q32, kf.transpose(1, 2).contiguous())
-        if torch.is_grad_enabled():
+        if torch.is_grad_enabled() or n > IDW_COEF_MAX_N:
+            # differentiable in turn (a backward taken with create_graph), or more keys than the kernel takes
             d2 = (q32 * q32).sum(-1)[:, :, None] + (kf * kf).sum(-1)[:, None, :] - 2.0 * dots
             U = torch.where(d2 > 0, D.float() / (1e-3 + d2.clamp_min(0.0)), torch.zeros_like(d2))
-            rs = U.sum(-1, keepdim=True)
+            rs, cs = U.sum(-1), U.sum(1)
         else:
-            # the same U (and its row sums) in one pass (pkm_idw_grad_coef)
-            U, rs = _idw_grad_coef(D, (q32 * q32).sum(-1), (kf * kf).sum(-1), dots)
-            rs = rs[:, :, None]
-        dqh = 2.0 * (torch.bmm(U, kf) - q32 * rs)
+            # the same U and its row and column sums in one pass (pkm_idw_grad_coef)
+            U, rs, cs = _idw_grad_coef(D, (q32 * q32).sum(-1), (kf * kf).sum(-1), dots)
+        dqh = 2.0 * (torch.bmm(U, kf) - q32 * rs[:, :, None])
         # float32 operands: the transposed view goes to the GEMM as it is
-        dk = 2.0 * (torch.bmm(U.transpose(1, 2), q32) - kf * U.sum(1)[:, :, None])
+        dk = 2.0 * (torch.bmm(U.transpose(1, 2), q32) - kf * cs[:, :, None])
     dq = dqh.view(heads, 2, N, half).permute(2, 0, 1, 3).reshape(N, heads, 2 * half)
     return dq, dk.reshape(keys.shape)
 
