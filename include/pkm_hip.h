@@ -212,15 +212,13 @@ int pkm_eb_bwd2(const void* gbar, int64_t num_rows, int64_t dim, int gbar_dtype,
  * pkm_me_grad_hvp takes, for a direction gbar [2 heads, n_keys, half] (the
  * outer gradient of g), qg [2 heads, num_tokens, n_keys] = <q_t, gbar_j> and
  * (idw) kg [2 heads, n_keys] = <k_j, gbar_j>, with avec and pbar from the
- * forward, and writes the derivative of <gbar, g>: through the sub-scores as
- * d_s1, d_s2 (dtype, every entry); with the sub-scores held fixed as the
- * rows of ul (float32; idw [2 heads, num_tokens, 2 n_keys] = [U | lam],
- * lsum [2 heads, num_tokens] the row sums of lam and lam_colsum [2 heads,
- * n_keys] its column sums (NULL = not written); dot [2 heads, num_tokens,
- * n_keys] = dS), from which
- *   idw: d q_t = 2 (sum_j U_tj gbar_j + sum_j lam_tj k_j - lsum_t q_t),
- *        d k_j = 2 (sum_t lam_tj q_t - k_j lam_colsum_j - gbar_j colsum_j);
- *   dot: d q_t = sum_j dS_tj gbar_j.
+ * forward, and writes the derivative of <gbar, g>: as the sub-scores'
+ * gradient d_s1, d_s2 (dtype, every entry; for idw it includes the terms of
+ * the form the retrieval's own backward gives a sub-score gradient), and the
+ * rest as the rows ul [2 heads, num_tokens, n_keys] float32 (idw U, dot dS),
+ * from which
+ *   idw: d q_t = 2 sum_j ul[b, t, j] gbar_j,  d k_j = -2 gbar_j colsum_j;
+ *   dot: d q_t = sum_j ul[b, t, j] gbar_j.
  * adot [2, n_keys] float32 is scratch. Deterministic.
  * Limits: n_keys <= 1024, topk <= n_keys, num_tokens >= 1.
  * workspace: pkm_me_grad_workspace_size(num_tokens, heads, n_keys) bytes.
@@ -235,8 +233,7 @@ int pkm_me_grad_hvp(const void* s1, const void* s2, const int64_t* sel1, const i
                     int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
                     float weight, const float* qq, const float* kk, const float* kg, const float* dots,
                     const float* qg, const float* avec, const float* pbar, float* adot, void* d_s1,
-                    void* d_s2, float* ul, float* lsum, float* lam_colsum, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    void* d_s2, float* ul, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Sub-key score of pkm_score_topk. */
 enum pkm_score_t {

@@ -187,7 +187,7 @@ SIGNATURES = {
             c_int, c_float,  # score_type, weight
             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # qq, kk, kg, dots, qg
             c_void_p, c_void_p, c_void_p,  # avec, pbar, adot
-            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,  # d_s1, d_s2, ul, lsum, lam_colsum
+            c_void_p, c_void_p, c_void_p,  # d_s1, d_s2, ul
             c_void_p, c_size_t, c_void_p,  # workspace, bytes, stream
         ],
     ),

@@ -37,13 +37,15 @@
 //     written as the sub-scores' gradient (the retrieval's backward carries
 //     it on to the query and the keys);
 //   directly, dS held fixed:
-//     idw: d q_t = 2 (sum_j U_tj gbar_j - (sum_j lam_tj) q_t + sum_j lam_tj k_j)
-//          d k_j = 2 (-gbar_j sum_t U_tj + sum_t lam_tj q_t - k_j sum_t lam_tj),  lam = dS u sigma
-//     dot: d q_t = sum_j dS_tj gbar_j,  d k_j = 0
-//   the kernels write the coefficients of both sides as dense rows ([U | lam]
-//   for idw, dS for dot, and the row sums of lam); the caller forms the
-//   products with q, k and gbar as batched GEMMs, from <q_t, gbar_j> handed
-//   in as a GEMM result.
+//     idw: d q_t = 2 (sum_j U_tj gbar_j + sum_j lam_tj (k_j - q_t)),
+//          d k_j = 2 (sum_t lam_tj (q_t - k_j) - gbar_j sum_t U_tj),  lam = dS u sigma;
+//     the lam terms have the form the retrieval's idw backward gives a
+//     sub-score gradient D (2 sum D u (k - q), 2 sum D u (q - k)), so they
+//     travel with rho as D = dS sigma: d_s = rho + dS sigma, and what stays
+//     direct is 2 U gbar (query) and -2 gbar sum_t U (keys);
+//     dot: d q_t = sum_j dS_tj gbar_j,  d k_j = 0;
+//   the kernels write U (idw) or dS (dot) rows for the caller's batched GEMM
+//   with gbar, from <q_t, gbar_j> handed in as a GEMM result.
 //
 // Every (t, j) entry is handled independently, so the cost does not depend
 // on how many entries tie at a row's threshold (16-bit idw scores tie for
@@ -511,9 +513,8 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp1_kernel(const T* __restric
   store_partial<NPL>(acc, G, partial);
 }
 
-// Pass 2 of the derivative: the sub-scores' gradient rho, and the direct
-// terms' coefficients: idw rows [U | lam] of 2n entries, the row sums of lam
-// and per-workgroup column partials of lam; dot rows dS of n entries.
+// Pass 2 of the derivative: the sub-scores' gradient (rho, plus dS sigma for
+// idw) and the direct term's coefficient rows (U for idw, dS for dot).
 template <typename T, int NPL, bool IDW>
 __global__ __launch_bounds__(64 * kWaves) void me_hvp2_kernel(const T* __restrict__ s1, const T* __restrict__ s2,
                                                               const int64_t* __restrict__ sel1,
@@ -525,8 +526,7 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp2_kernel(const T* __restric
                                                               const float* __restrict__ qg, Geo G,
                                                               const float* __restrict__ avec,
                                                               const float* __restrict__ adot, T* __restrict__ d_s1,
-                                                              T* __restrict__ d_s2, float* __restrict__ ul,
-                                                              float* __restrict__ lsum, float* __restrict__ partial) {
+                                                              T* __restrict__ d_s2, float* __restrict__ ul) {
   const int lane = threadIdx.x & 63;
   const WaveJob J = wave_job(G);
   const T* s = J.c ? s2 : s1;
@@ -539,10 +539,6 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp2_kernel(const T* __restric
     load_row<float, NPL>(kk + (int64_t)J.b * G.n, G, lane, 0.f, kv);
     load_row<float, NPL>(kg + (int64_t)J.b * G.n, G, lane, 0.f, kgv);
   }
-  const int width = IDW ? 2 * G.n : G.n;
-  float lcol[NPL];
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) lcol[i] = 0.f;
   for (int64_t t = J.t0; t < J.t1; ++t) {
     const int64_t r = t * G.heads + J.h;
     const int64_t bt = (int64_t)J.b * G.tokens + t;
@@ -566,30 +562,22 @@ __global__ __launch_bounds__(64 * kWaves) void me_hvp2_kernel(const T* __restric
     }
     beta_dot = wave_sum(beta_dot);
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) rho[i] = pd[i] * (av[i] - pa) + p[i] * (ad[i] - beta_dot);
+    for (int i = 0; i < NPL; ++i) {
+      rho[i] = pd[i] * (av[i] - pa) + p[i] * (ad[i] - beta_dot);
+      if constexpr (IDW) rho[i] += ds[i] * sg[i];  // the lam terms, as a sub-score gradient
+    }
     store_row<T, NPL>(d_s + r * G.n, G, lane, rho);
-    float* urow = ul + bt * width;
+    float* urow = ul + bt * G.n;
     if constexpr (IDW) {
       // U as the loss pass writes it (uu = 0 where d2 <= 0 or outside the mask)
-      float U[NPL], lm[NPL];
-      float lacc = 0.f;
+      float U[NPL];
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        U[i] = uu[i] != 0.f ? ds[i] / (kIdwEps + d2v[i]) : 0.f;
-        lm[i] = ds[i] * uu[i] * sg[i];
-        lacc += lm[i];
-        lcol[i] += lm[i];
-      }
+      for (int i = 0; i < NPL; ++i) U[i] = uu[i] != 0.f ? ds[i] / (kIdwEps + d2v[i]) : 0.f;
       store_row<float, NPL>(urow, G, lane, U);
-      store_row<float, NPL>(urow + G.n, G, lane, lm);
-      lacc = wave_sum(lacc);
-      if (lane == 0) lsum[bt] = lacc;
     } else {
       store_row<float, NPL>(urow, G, lane, ds);
     }
   }
-  // idw: column sums of lam, per workgroup
-  if constexpr (IDW) store_partial<NPL>(lcol, G, partial);
 }
 
 // The idw factor of a dense sub-score gradient dS [batches, tokens, n]:
@@ -718,30 +706,27 @@ template <typename T, int NPL, bool IDW>
 static void launch_hvp_t(const Geo& G, const void* s1, const void* s2, const int64_t* sel1, const int64_t* sel2,
                          const float* qq, const float* kk, const float* kg, const float* dots, const float* qg,
                          float weight, const float* avec, float* pbar, float* adot, void* d_s1, void* d_s2,
-                         float* ul, float* lsum, float* lam_colsum, float* partial, hipStream_t st) {
+                         float* ul, float* partial, hipStream_t st) {
   const dim3 grid((unsigned)(2 * G.heads * G.wgb)), block(64 * kWaves);
   hipLaunchKernelGGL((me_hvp1_kernel<T, NPL, IDW>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2, qq,
                      kk, kg, dots, qg, G, partial);
   hipLaunchKernelGGL(me_finalize_kernel, fin_grid(G), dim3(kFinCols * kFinGroups), 0, st, (const float*)partial, G, weight,
                      1, pbar, adot, (float*)nullptr);
   hipLaunchKernelGGL((me_hvp2_kernel<T, NPL, IDW>), grid, block, 0, st, (const T*)s1, (const T*)s2, sel1, sel2, qq,
-                     kk, kg, dots, qg, G, avec, (const float*)adot, (T*)d_s1, (T*)d_s2, ul, lsum, partial);
-  if (IDW && lam_colsum != nullptr)
-    hipLaunchKernelGGL(me_colsum_kernel, colsum_grid(G, 2 * G.heads), dim3(kFinCols * kFinGroups), 0, st,
-                       (const float*)partial, G, lam_colsum);
+                     kk, kg, dots, qg, G, avec, (const float*)adot, (T*)d_s1, (T*)d_s2, ul);
 }
 
 template <typename T, int NPL>
 static void launch_hvp(const Geo& G, int idw, const void* s1, const void* s2, const int64_t* sel1,
                        const int64_t* sel2, const float* qq, const float* kk, const float* kg, const float* dots,
                        const float* qg, float weight, const float* avec, float* pbar, float* adot, void* d_s1,
-                       void* d_s2, float* ul, float* lsum, float* lam_colsum, float* partial, hipStream_t st) {
+                       void* d_s2, float* ul, float* partial, hipStream_t st) {
   if (idw)
     launch_hvp_t<T, NPL, true>(G, s1, s2, sel1, sel2, qq, kk, kg, dots, qg, weight, avec, pbar, adot, d_s1, d_s2, ul,
-                               lsum, lam_colsum, partial, st);
+                               partial, st);
   else
     launch_hvp_t<T, NPL, false>(G, s1, s2, sel1, sel2, qq, kk, kg, dots, qg, weight, avec, pbar, adot, d_s1, d_s2,
-                                ul, lsum, lam_colsum, partial, st);
+                                ul, partial, st);
 }
 
 template <typename T, int NPL>
@@ -815,22 +800,21 @@ extern "C" int pkm_me_grad_hvp(const void* s1, const void* s2, const int64_t* se
                                int64_t num_tokens, int64_t heads, int64_t n_keys, int64_t topk, int score_type,
                                float weight, const float* qq, const float* kk, const float* kg, const float* dots,
                                const float* qg, const float* avec, const float* pbar, float* adot, void* d_s1,
-                               void* d_s2, float* ul, float* lsum, float* lam_colsum, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               void* d_s2, float* ul, void* workspace, size_t workspace_bytes, void* stream) {
   me::Geo G;
   int rc = me::check("pkm_me_grad_hvp", num_tokens, heads, n_keys, topk, dtype, score_type, &G);
   if (rc != PKM_OK) return rc;
   const bool idw = score_type == PKM_SCORE_IDW;
   PKM_REQUIRE(s1 && s2 && sel1 && sel2 && qg && avec && pbar && adot && d_s1 && d_s2 && ul,
               PKM_ERR_INVALID_ARGUMENT, "pkm_me_grad_hvp: null pointer");
-  PKM_REQUIRE(!idw || (qq && kk && kg && dots && lsum), PKM_ERR_INVALID_ARGUMENT,
-              "pkm_me_grad_hvp: idw scores need qq, kk, kg, dots and lsum");
+  PKM_REQUIRE(!idw || (qq && kk && kg && dots), PKM_ERR_INVALID_ARGUMENT,
+              "pkm_me_grad_hvp: idw scores need qq, kk, kg and dots");
   PKM_REQUIRE(workspace && workspace_bytes >= me::workspace_bytes(G), PKM_ERR_WORKSPACE,
               "pkm_me_grad_hvp: workspace %zu bytes < %zu", workspace_bytes, me::workspace_bytes(G));
   G.vec = me::vec_ok(n_keys, {s1, s2, dots, qg, kk, kg, avec, adot, d_s1, d_s2, ul});
   const int npl = me::npl_of(n_keys);
   PKM_ME_DISPATCH(me::launch_hvp, dtype, npl, G, idw ? 1 : 0, s1, s2, sel1, sel2, qq, kk, kg, dots, qg, weight, avec,
-                  (float*)pbar, adot, d_s1, d_s2, ul, lsum, lam_colsum, (float*)workspace, (hipStream_t)stream);
+                  (float*)pbar, adot, d_s1, d_s2, ul, (float*)workspace, (hipStream_t)stream);
   return pkm_check_launch("pkm_me_grad_hvp");
 }
 

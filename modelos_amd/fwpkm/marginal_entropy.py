@@ -12,12 +12,14 @@ The kernels take every (token, key) entry of the sub-score rows, lane-parallel
 them: a few more than topk for float32 scores, most of the row for 16-bit idw
 scores, which tie heavily); the products with the queries, the keys and the
 outer gradient are batched GEMMs over dense [2 heads, tokens, n] operands. The
-double backward is split as autograd splits the reference's graph: the part
-through the sub-scores comes back as their gradient (the retrieval's own
-backward carries it to the query and the keys, reading the key values the
-reference's saved tensors hold), the part with the sub-scores held fixed goes
-to the query and the keys directly (idw: the forward-time key values, those
-the reference's cdist copy holds; dot: no key values).
+double backward is split along the reference's graph: the part through the
+sub-scores comes back as their gradient, which the retrieval's own backward
+carries to the query and the keys with the reference's key-value semantics;
+for idw that gradient also carries the direct terms of the same form
+(lam (k - q), lam = dS u sigma, sent as dS sigma), and the rest of the part
+with the sub-scores held fixed (idw 2 U gbar for the query and -2 gbar sum_t U
+for the keys, from the forward-time key values; dot dS gbar) goes to the
+query and the keys directly.
 """
 from __future__ import annotations
 
@@ -107,27 +109,23 @@ class _AddrKeyGrad(torch.autograd.Function):
         adot = torch.empty((2, n), device=dev, dtype=torch.float32)
         d_s1 = torch.empty_like(s1)
         d_s2 = torch.empty_like(s2)
-        ul = torch.empty((2 * heads, tokens, 2 * n if idw else n), device=dev, dtype=torch.float32)
-        lsum = torch.empty((2 * heads, tokens), device=dev, dtype=torch.float32) if idw else None
-        lcs = torch.empty((2 * heads, n), device=dev, dtype=torch.float32) if idw else None
+        ul = torch.empty((2 * heads, tokens, n), device=dev, dtype=torch.float32)
         ws = _workspace(tokens, heads, n, dev)
         _lib.call("pkm_me_grad_hvp", _lib.ptr(s1), _lib.ptr(s2), _lib.ptr(sel1), _lib.ptr(sel2),
                   _lib.dtype_code(s1), tokens, heads, n, topk, _lib.SCORE_CODES[score_type], ctx.weight,
                   _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(kg), _lib.ptr(dots), _lib.ptr(qg), _lib.ptr(avec),
-                  _lib.ptr(pbar), _lib.ptr(adot), _lib.ptr(d_s1), _lib.ptr(d_s2), _lib.ptr(ul), _lib.ptr(lsum),
-                  _lib.ptr(lcs), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+                  _lib.ptr(pbar), _lib.ptr(adot), _lib.ptr(d_s1), _lib.ptr(d_s2), _lib.ptr(ul), _lib.ptr(ws),
+                  ws.numel(), _lib.stream_of(dev))
+        # the direct terms left beside the sub-scores' gradient: idw 2 U gbar and -2 gbar colsum(U),
+        # dot dS gbar
         d_query = d_keys = None
         if ctx.needs_input_grad[0]:
+            dq = torch.bmm(ul, gb)
             if idw:
-                # sum_j U_tj gbar_j + sum_j lam_tj k_j - lsum_t q_t
-                dq = 2.0 * (torch.bmm(ul, torch.cat((gb, kf), 1)) - lsum[:, :, None] * qb)
-            else:
-                dq = torch.bmm(ul, gb)
+                dq = 2.0 * dq
             d_query = dq.transpose(0, 1).reshape(ctx.query_shape).to(ctx.query_dtype)
         if idw and ctx.needs_input_grad[1]:
-            lam = ul[:, :, n:]
-            dk = torch.bmm(lam.transpose(1, 2), qb) - kf * lcs[:, :, None] - gb * cs[:, :, None]
-            d_keys = (2.0 * dk).reshape(2 * heads * n, half).to(ctx.keys_dtype)
+            d_keys = (-2.0 * gb * cs[:, :, None]).reshape(2 * heads * n, half).to(ctx.keys_dtype)
         return (d_query, d_keys, d_s1 if ctx.needs_input_grad[2] else None,
                 d_s2 if ctx.needs_input_grad[3] else None) + nones
 
