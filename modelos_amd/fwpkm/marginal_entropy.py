@@ -29,7 +29,7 @@ import torch
 
 from .. import _lib
 from ..embedding_bag import _aligned, _require_device
-from ..product_keys import SCORE_TYPES
+from ..product_keys import SCORE_TYPES, share_distance_products
 
 ME_MAX_N_KEYS = 1024
 _DTYPES = (torch.float32, torch.bfloat16, torch.float16)
@@ -53,7 +53,7 @@ class _AddrKeyGrad(torch.autograd.Function):
     batch b = 2h + c (head h, half c), the key table's row blocks."""
 
     @staticmethod
-    def forward(ctx, query, keys, s1, s2, sel1, sel2, heads, topk, weight, score_type):
+    def forward(ctx, query, keys, s1, s2, sel1, sel2, heads, topk, weight, score_type, share_with=None):
         ctx.set_materialize_grads(False)
         tokens, n = s1.shape[0], s1.shape[-1]
         half = keys.shape[1]
@@ -70,6 +70,9 @@ class _AddrKeyGrad(torch.autograd.Function):
             dots = torch.bmm(qb, kf.transpose(1, 2).contiguous())
             qq = (qb * qb).sum(-1).contiguous()
             kk = (kf * kf).sum(-1).contiguous()
+            if share_with is not None:
+                # the retrieval's backward needs the same products of the same operands
+                share_distance_products(share_with, dots, qq, kk)
         entropy = torch.empty(2, device=dev, dtype=torch.float32)
         coef = torch.empty((2 * heads, tokens, n), device=dev, dtype=torch.float32)
         avec = torch.empty((2, n), device=dev, dtype=torch.float32)
@@ -96,7 +99,7 @@ class _AddrKeyGrad(torch.autograd.Function):
     def backward(ctx, _d_entropy, gbar):
         qb, kf, s1, s2, sel1, sel2, avec, pbar, cs, qq, kk, dots = ctx.saved_tensors
         heads, topk, score_type = ctx.heads, ctx.topk, ctx.score_type
-        nones = (None,) * 6
+        nones = (None,) * 7
         if gbar is None:
             return (None, None, None, None) + nones
         tokens, n = s1.shape[0], s1.shape[-1]
@@ -153,11 +156,11 @@ def addr_loss_and_key_grad(query: torch.Tensor, keys: torch.Tensor, s1: torch.Te
     if st is None:
         raise NotImplementedError(f"addr_loss_and_key_grad: score type {score_type}")
     if create_graph:
-        entropy, g = _AddrKeyGrad.apply(query, keys, s1, s2, sel1, sel2, heads, topk, weight, st)
+        entropy, g = _AddrKeyGrad.apply(query, keys, s1, s2, sel1, sel2, heads, topk, weight, st, s1)
     else:
         with torch.no_grad():
             entropy, g = _AddrKeyGrad.apply(query.detach(), keys.detach(), s1.detach(), s2.detach(), sel1, sel2,
-                                            heads, topk, weight, st)
+                                            heads, topk, weight, st, s1)
     h1, h2 = entropy[0].to(s1.dtype), entropy[1].to(s1.dtype)
     return weight * (-1.0 * h1 + -1.0 * h2), g
 

@@ -219,7 +219,18 @@ def _idw_grad_coef(dS, qq, kk, dots):
     return U, rs, cs
 
 
-def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
+def share_distance_products(sub_scores: torch.Tensor, dots: torch.Tensor, qq: torch.Tensor, kk: torch.Tensor) -> None:
+    """Hands the float32 distance operands of an idw retrieval (dots [2 heads,
+    tokens, n] = <q_t, k_j>, qq [2 heads, tokens], kk [2 heads, n], taken from
+    the retrieval's own query and forward-time keys) to its backward node,
+    found through one of its sub-score outputs, so that the backward does not
+    form them again. No effect for other outputs or score types."""
+    node = sub_scores.grad_fn
+    if node is not None and getattr(node, "score_type", None) == "idw" and getattr(node, "sub_outputs", False):
+        node.shared_products = (dots, qq, kk)
+
+
+def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None, shared=None):
     """dq [tokens, heads, k_dim] and dkeys [2*heads*n, half] from the dense
     sub-score gradient dS [heads, 2, tokens, n] with one pair of batched GEMMs
     per (head, half) — the products autograd forms for the reference's einsum
@@ -234,7 +245,8 @@ def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
     strided half view works on a copy made at forward time, so every value
     it reads, first and second order, is the forward-time one. `keys_fwd` is
     that copy (idw); under create_graph it carries the table's own autograd
-    identity."""
+    identity. `shared`: (dots, qq, kk) already formed from the same query and
+    forward-time keys (share_distance_products), used outside create_graph."""
     half = keys.shape[1]
     N = dS.shape[2]
     Kh = keys.reshape(heads * 2, n, half)
@@ -253,7 +265,8 @@ def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
             kf = keys_fwd.reshape(heads * 2, n, half).float()
             if torch.is_grad_enabled():
                 kf = kf + (k32 - k32.detach())
-        dots = torch.bmm(q32, kf.transpose(1, 2).contiguous())
+        use_shared = shared is not None and not torch.is_grad_enabled()
+        dots = shared[0] if use_shared else torch.bmm(q32, kf.transpose(1, 2).contiguous())
         if torch.is_grad_enabled() or n > IDW_COEF_MAX_N:
             # differentiable in turn (a backward taken with create_graph), or more keys than the kernel takes
             d2 = (q32 * q32).sum(-1)[:, :, None] + (kf * kf).sum(-1)[:, None, :] - 2.0 * dots
@@ -261,7 +274,8 @@ def _grads_from_dense(query, keys, dS, heads, n, score_type, keys_fwd=None):
             rs, cs = U.sum(-1), U.sum(1)
         else:
             # the same U and its row and column sums in one pass (pkm_idw_grad_coef)
-            U, rs, cs = _idw_grad_coef(D, (q32 * q32).sum(-1), (kf * kf).sum(-1), dots)
+            qq, kk = (shared[1], shared[2]) if use_shared else ((q32 * q32).sum(-1), (kf * kf).sum(-1))
+            U, rs, cs = _idw_grad_coef(D, qq, kk, dots)
         dqh = 2.0 * (torch.bmm(U, kf) - q32 * rs[:, :, None])
         # float32 operands: the transposed view goes to the GEMM as it is
         dk = 2.0 * (torch.bmm(U.transpose(1, 2), q32) - kf * cs[:, :, None])
@@ -305,7 +319,8 @@ class ProductKeyTopK(torch.autograd.Function):
             d_s1 = d_s1.to(query.dtype) if d_s1 is not None else None
             d_s2 = d_s2.to(query.dtype) if d_s2 is not None else None
             dS = _DenseScoreGrad.apply(indices, d_scores.to(query.dtype), d_s1, d_s2, heads, n)
-            dq, dk = _grads_from_dense(query, keys, dS, heads, n, ctx.score_type, keys_fwd)
+            dq, dk = _grads_from_dense(query, keys, dS, heads, n, ctx.score_type, keys_fwd,
+                                       getattr(ctx, "shared_products", None))
         d_query = dq.to(query.dtype).reshape(ctx.query_shape) if ctx.needs_input_grad[0] else None
         d_keys = dk.to(keys.dtype) if ctx.needs_input_grad[1] else None
         return d_query, d_keys, None, None, None, None
