@@ -10,15 +10,21 @@
 // reading W and writing gW for all K rows.
 //
 // This design (own):
-//  1. sort:    stable LSD radix sort of (row, flat position) pairs, 2 passes of
-//              10/11-bit digits for up to 2^22 rows. Lookups whose index is out
-//              of [0, K) are dropped here (their psw-gradient is written as 0).
-//              The input is in position order and every pass is stable, so each
-//              row's occurrences end up in increasing position order: the
-//              float32 sums below have a fixed order, independent of the launch
-//              (no float atomics anywhere).
-//  2. offsets: row r starts at the first sorted position whose key is >= r
-//              (a binary search per row).
+//  1. sort:    stable sort of (row, flat position) pairs. Up to 2^22 rows: a
+//              radix pass buckets the lookups by the high 8/10/11-bit digit of
+//              the row, then a local pass sorts each bucket (2^B consecutive
+//              rows) by the low digit, segment by segment, and writes the row
+//              offsets and the occurrence metadata on the way. Other row
+//              counts: LSD radix passes. Lookups whose index is out of [0, K)
+//              are dropped here (their psw-gradient is written as 0). The input
+//              is in position order and every pass is stable, so each row's
+//              occurrences end up in increasing position order: the float32
+//              sums below have a fixed order, independent of the launch (no
+//              float atomics anywhere).
+//  2. offsets: row r starts at its bucket's start plus the counts of the
+//              bucket's lower rows (the local pass), or at the first sorted
+//              position whose key is >= r (a binary search per row, after LSD
+//              passes).
 //  3. heavy:   rows with more than T occurrences are cut into fixed chunks of
 //              T sorted occurrences; each chunk writes a float32 partial sum
 //              (2 slots per chunk: the row running in from the previous chunk
@@ -295,19 +301,34 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const int64_t* __restri
   for (int d = threadIdx.x; d < R; d += 256) hist[(int64_t)d * ntiles + blockIdx.x] = h[d];
 }
 
+// Segments of the local pass (LOCAL scatter): per segment its first item and
+// one past its last, then the segment count at [2 * max_segs].
+struct SegTab {
+  const uint32_t* tab;
+  int64_t max_segs;
+};
+
 // Stable scatter of one tile by digit, sub-tile by sub-tile. Each sub-tile is
 // first ordered by digit in LDS (per digit in item order), then written out in
 // that order, so each digit's run of the sub-tile goes to consecutive
 // addresses, right after the previous sub-tile's run of that digit: keys first,
 // then values, through one LDS buffer.
-template <bool FIRST, int BITS>
+// LOCAL: the block is one segment of the local pass (items [begin, end) of one
+// high-digit bucket, in order), its per-digit destinations given in ofs
+// [segment][digit]; the occurrence metadata {position / L, psw as float32
+// bits} of each item is written beside it when meta is not null.
+template <bool FIRST, int BITS, bool LOCAL = false>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __restrict__ idx,
                                                             const uint32_t* __restrict__ keys_in,
                                                             const uint32_t* __restrict__ vals_in, int64_t N,
                                                             const uint32_t* __restrict__ nvalid, int64_t K,
                                                             int shift, const uint32_t* __restrict__ ofs,
                                                             int64_t ntiles, uint32_t* __restrict__ keys_out,
-                                                            uint32_t* __restrict__ vals_out) {
+                                                            uint32_t* __restrict__ vals_out, SegTab seg = SegTab{},
+                                                            uint2* __restrict__ meta = nullptr,
+                                                            const void* __restrict__ psw = nullptr, int pdt = 0,
+                                                            uint32_t L32 = 1) {
+  static_assert(!(FIRST && LOCAL), "the local pass reads the bucketed keys");
   constexpr int R = 1 << BITS;
   constexpr int DPT = R / 256;  // digits per thread in the digit scan
   static_assert(R % 256 == 0, "digit count per thread");
@@ -317,22 +338,37 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
   __shared__ uint32_t wsum[4];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
+  int64_t first = (int64_t)blockIdx.x * kRadixTile;  // the block's first item
+  uint32_t lim;                                      // items below lim (non-first passes) are valid
+  int nsub = kRadixSubs;
   // per owned digit (thread t: digits DPT t .. DPT t + DPT - 1): the global
   // position of its next item in this tile
   uint32_t running[DPT];
+  if constexpr (LOCAL) {
+    const uint32_t nseg = seg.tab[2 * seg.max_segs];
+    if (blockIdx.x >= nseg) return;
+    const uint32_t b = seg.tab[2 * blockIdx.x], e = seg.tab[2 * blockIdx.x + 1];
+    first = b;
+    lim = e;
+    nsub = (int)((e - b + kRadixSub - 1) / kRadixSub);
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) running[j] = ofs[(int64_t)(threadIdx.x * DPT + j) * ntiles + blockIdx.x];
-  const uint32_t nv = FIRST ? 0u : *nvalid;
+    for (int j = 0; j < DPT; ++j) running[j] = ofs[(int64_t)blockIdx.x * R + threadIdx.x * DPT + j];
+  } else {
+    lim = FIRST ? 0u : *nvalid;
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) running[j] = ofs[(int64_t)(threadIdx.x * DPT + j) * ntiles + blockIdx.x];
+  }
+  const uint32_t nv = lim;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
 #pragma unroll 1
-  for (int sub = 0; sub < kRadixSubs; ++sub) {
+  for (int sub = 0; sub < nsub; ++sub) {
     for (int d = threadIdx.x; d < R; d += 256) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) wcnt[i][d] = 0;
     }
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kRadixTile + (int64_t)sub * kRadixSub + (int64_t)w * (kRadixItems * 64);
+    const int64_t base = first + (int64_t)sub * kRadixSub + (int64_t)w * (kRadixItems * 64);
     uint32_t k[kRadixItems], v[kRadixItems], pre[kRadixItems];
     uint32_t validmask = 0;
 #pragma unroll
@@ -419,10 +455,127 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
 #pragma unroll
     for (int i = 0; i < kRadixItems; ++i) {
       const uint32_t q = (uint32_t)(i * 256 + threadIdx.x);
-      if (q < nloc) vals_out[dst[i]] = stage[q];
+      if (q < nloc) {
+        const uint32_t val = stage[q];
+        vals_out[dst[i]] = val;
+        if (LOCAL && meta != nullptr)
+          meta[dst[i]] = make_uint2(val / L32, __float_as_uint(psw ? load_scalar(psw, pdt, val) : 1.f));
+      }
     }
     __syncthreads();  // stage and wcnt are reused by the next sub-tile
   }
+}
+
+// ---------------------------------------------------------------------------
+// Local pass of the two-level sort. The first pass buckets the lookups stably
+// by the high digit of the row (bits [B, 2 B)); each bucket holds the rows
+// b 2^B .. b 2^B + 2^B - 1 and its lookups in position order, so a stable
+// sort of each bucket by the low digit completes the sort by (row, position),
+// the order the single-digit passes give. Buckets are cut into segments of
+// at most kSegItems lookups (one workgroup each): per-segment digit counts,
+// then per bucket the digits' starts (the rows' offsets) and each segment's
+// share, then the segments' stable scatters, which also write the occurrence
+// metadata. A bucket's writes stay inside its own range of the outputs.
+// ---------------------------------------------------------------------------
+constexpr int kSegItems = 4 * kRadixSub;
+
+// One block: the segment table from the first pass's scanned digit offsets
+// (bucket b starts at ofs[b * ntiles], the next bucket's start or the valid
+// count ends it), and per bucket {first segment, one past its last, start}.
+__global__ __launch_bounds__(256) void seg_plan_kernel(const uint32_t* __restrict__ ofs, int64_t ntiles,
+                                                       int nbuckets, int R, const uint32_t* __restrict__ nvalid,
+                                                       uint32_t* __restrict__ tab, int64_t max_segs,
+                                                       uint32_t* __restrict__ bseg) {
+  __shared__ uint32_t lds4[4];
+  const uint32_t nv = *nvalid;
+  uint32_t carry = 0;
+  for (int b0 = 0; b0 < nbuckets; b0 += 256) {
+    const int b = b0 + (int)threadIdx.x;
+    uint32_t beg = 0, end = 0, ns = 0;
+    if (b < nbuckets) {
+      beg = ofs[(int64_t)b * ntiles];
+      end = b + 1 < R ? ofs[(int64_t)(b + 1) * ntiles] : nv;
+      if (b + 1 == nbuckets) end = nv;  // digits past the last bucket hold no lookups
+      ns = (end - beg + kSegItems - 1) / kSegItems;
+    }
+    uint32_t tot;
+    const uint32_t s0 = carry + block_exclusive_sum(ns, &tot, lds4);
+    if (b < nbuckets) {
+      bseg[3 * b] = s0;
+      bseg[3 * b + 1] = s0 + ns;
+      bseg[3 * b + 2] = beg;
+      for (uint32_t j = 0; j < ns; ++j) {
+        const uint32_t sb = beg + j * (uint32_t)kSegItems;
+        tab[2 * (s0 + j)] = sb;
+        tab[2 * (s0 + j) + 1] = end - sb < (uint32_t)kSegItems ? end : sb + (uint32_t)kSegItems;
+      }
+    }
+    carry += tot;
+  }
+  if (threadIdx.x == 0) tab[2 * max_segs] = carry;
+}
+
+// Per segment: counts of the low digit (keys & (2^BITS - 1)).
+template <int BITS>
+__global__ __launch_bounds__(256) void seg_hist_kernel(const uint32_t* __restrict__ keys, SegTab seg,
+                                                       uint32_t* __restrict__ hist) {
+  constexpr int R = 1 << BITS;
+  __shared__ uint32_t h[R];
+  if (blockIdx.x >= seg.tab[2 * seg.max_segs]) return;
+  for (int d = threadIdx.x; d < R; d += 256) h[d] = 0;
+  __syncthreads();
+  const uint32_t b = seg.tab[2 * blockIdx.x], e = seg.tab[2 * blockIdx.x + 1];
+  for (uint32_t i = b + threadIdx.x; i < e; i += 256) atomicAdd(&h[keys[i] & (R - 1)], 1u);
+  __syncthreads();
+  for (int d = threadIdx.x; d < R; d += 256) hist[(int64_t)blockIdx.x * R + d] = h[d];
+}
+
+// Per bucket: the digits' starts (row r = b 2^BITS + d starts at offs[r]) and
+// each segment's per-digit destination, in place of its counts.
+template <int BITS>
+__global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restrict__ bseg, int64_t K,
+                                                       uint32_t* __restrict__ hist, uint32_t* __restrict__ offs) {
+  constexpr int R = 1 << BITS;
+  constexpr int DPT = R / 256;
+  __shared__ uint32_t lds4[4];
+  const int b = blockIdx.x;
+  const uint32_t s0 = bseg[3 * b], s1 = bseg[3 * b + 1], start = bseg[3 * b + 2];
+  uint32_t tot[DPT], mine = 0;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = threadIdx.x * DPT + j;
+    uint32_t t = 0;
+    for (uint32_t s = s0; s < s1; ++s) t += hist[(int64_t)s * R + d];
+    tot[j] = t;
+    mine += t;
+  }
+  uint32_t all;
+  uint32_t run = block_exclusive_sum(mine, &all, lds4);
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = threadIdx.x * DPT + j;
+    const int64_t r = ((int64_t)b << BITS) + d;
+    if (r < K) offs[r] = start + run;
+    uint32_t at = start + run;
+    for (uint32_t s = s0; s < s1; ++s) {
+      const uint32_t c = hist[(int64_t)s * R + d];
+      hist[(int64_t)s * R + d] = at;
+      at += c;
+    }
+    run += tot[j];
+  }
+}
+
+// offs[K] <- the valid count; metadata entries past it (the padding and the
+// dropped lookups' share) <- 0.
+__global__ void meta_tail_kernel(const uint32_t* __restrict__ nvalid, int64_t K, int64_t n_total,
+                                 uint32_t* __restrict__ offs, uint2* __restrict__ meta) {
+  const uint32_t nv = *nvalid;
+  if (blockIdx.x == 0 && threadIdx.x == 0) offs[K] = nv;
+  if (meta == nullptr) return;
+  for (int64_t i = (int64_t)nv + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_total;
+       i += (int64_t)gridDim.x * blockDim.x)
+    meta[i] = make_uint2(0u, 0u);
 }
 
 // offs[r] <- the first sorted position whose key is >= r (a binary search of
@@ -1187,8 +1340,8 @@ static RadixPlan radix_plan(int64_t K) {
 
 struct BwdLayout {
   size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, long_rows, tickets,
-      invalid, total;
-  int64_t ntiles, nbins, nchunks, nmeta;
+      invalid, seg_tab, bseg, seg_hist, total;
+  int64_t ntiles, nbins, nchunks, nmeta, nbuckets, max_segs;
   RadixPlan plan;
 };
 
@@ -1236,6 +1389,19 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
   // out-of-range lookups: count, then positions
   l.invalid = off;
   off += align256((size_t)(N + 1) * 4);
+  // two-digit plans: the local pass's segment table, per-bucket segment ranges and per-segment digit counts
+  l.nbuckets = l.max_segs = 0;
+  l.seg_tab = l.bseg = l.seg_hist = off;
+  if (l.plan.passes == 2) {
+    l.nbuckets = cdiv(K, (int64_t)1 << l.plan.bits);
+    l.max_segs = cdiv(N, kSegItems) + l.nbuckets;
+    l.seg_tab = off;
+    off += align256((size_t)(2 * l.max_segs + 1) * 4);
+    l.bseg = off;
+    off += align256((size_t)(3 * l.nbuckets) * 4);
+    l.seg_hist = off;
+    off += align256((size_t)l.max_segs * ((size_t)1 << l.plan.bits) * 4);
+  }
   l.total = off;
   return l;
 }
@@ -1278,6 +1444,39 @@ static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], ui
                        (const uint32_t*)keys[cur], (const uint32_t*)vals[cur], N, nvalid, K, shift,
                        (const uint32_t*)hist, l.ntiles, keys[nxt], vals[nxt]);
   }
+}
+
+// Two-digit plans: a stable bucketing pass by the high digit (out-of-range
+// lookups dropped and listed), then the local pass per bucket (row offsets
+// and, with meta, the occurrence metadata included). Output in keys[1] /
+// vals[1], as the two single-digit passes leave it.
+template <int BITS>
+static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t* const vals[2], int64_t N, int64_t K,
+                           const BwdLayout& l, char* ws, uint32_t* hist, uint32_t* parts, uint32_t* invalid,
+                           uint32_t* offs, uint2* meta, const void* psw, int pdt, int64_t L, hipStream_t st) {
+  const uint32_t* nvalid = hist + l.nbins;  // the first pass's scan total
+  const dim3 grid((unsigned)l.ntiles), block(256);
+  hipLaunchKernelGGL((radix_hist_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr, N,
+                     (const uint32_t*)nullptr, K, BITS, hist, l.ntiles, invalid);
+  device_exclusive_sum(hist, l.nbins, parts, st);
+  hipLaunchKernelGGL((radix_scatter_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr,
+                     (const uint32_t*)nullptr, N, (const uint32_t*)nullptr, K, BITS, (const uint32_t*)hist, l.ntiles,
+                     keys[0], vals[0], SegTab{}, (uint2*)nullptr, (const void*)nullptr, 0, 1u);
+  uint32_t* tab = (uint32_t*)(ws + l.seg_tab);
+  uint32_t* bseg = (uint32_t*)(ws + l.bseg);
+  uint32_t* shist = (uint32_t*)(ws + l.seg_hist);
+  const SegTab seg{tab, l.max_segs};
+  hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(256), 0, st, (const uint32_t*)hist, l.ntiles, (int)l.nbuckets,
+                     1 << BITS, nvalid, tab, l.max_segs, bseg);
+  hipLaunchKernelGGL((seg_hist_kernel<BITS>), dim3((unsigned)l.max_segs), dim3(256), 0, st, (const uint32_t*)keys[0],
+                     seg, shist);
+  hipLaunchKernelGGL((seg_base_kernel<BITS>), dim3((unsigned)l.nbuckets), dim3(256), 0, st, (const uint32_t*)bseg, K,
+                     shist, offs);
+  hipLaunchKernelGGL((radix_scatter_kernel<false, BITS, true>), dim3((unsigned)l.max_segs), block, 0, st,
+                     (const int64_t*)nullptr, (const uint32_t*)keys[0], (const uint32_t*)vals[0], N, nvalid, K, 0,
+                     (const uint32_t*)shist, (int64_t)0, keys[1], vals[1], seg, meta, psw, pdt, (uint32_t)L);
+  hipLaunchKernelGGL(meta_tail_kernel, dim3(grid_for(kMetaPad + N, 256, 1024)), dim3(256), 0, st, nvalid, K,
+                     l.nmeta, offs, meta);
 }
 
 // Row-kernel prefetch depth (lookups per row reduced in the row kernel) for
@@ -1336,7 +1535,9 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
   if constexpr (LPG == 64) {
     uint2* meta = (uint2*)(ws + l.meta);
     hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(D, 256, 64)), dim3(256), 0, st, (uint32_t*)(ws + l.zrow), 0u, D);
-    if (N > 0)
+    if (N > 0 && l.plan.passes == 2) {
+      // written by the sort's local pass
+    } else if (N > 0)
       hipLaunchKernelGGL(occ_meta_kernel, dim3(grid_for(l.nmeta, 256, 16384)), dim3(256), 0, st, svals, nvalid,
                          l.nmeta, (uint32_t)L, psw, pdt, meta);
     else
@@ -1528,7 +1729,26 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
   const int64_t K = num_rows, N = bags * bag_size;
   const SortedView v = sorted_view(l, ws);
   hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, v.invalid, 0u, (int64_t)1);
-  if (N > 0) {
+  uint2* meta = c.lpg == 64 ? (uint2*)(ws + l.meta) : nullptr;  // read by the 64-lane row kernels
+  if (N > 0 && l.plan.passes == 2) {
+    // 1-2. stable sort of (row, position) by bucketing and local passes, with the row offsets and metadata
+    uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
+    uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
+    switch (l.plan.bits) {
+      case 8:
+        two_level_sort<8>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw, psw_dtype,
+                          bag_size, st);
+        break;
+      case 10:
+        two_level_sort<10>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw,
+                           psw_dtype, bag_size, st);
+        break;
+      default:
+        two_level_sort<11>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw,
+                           psw_dtype, bag_size, st);
+        break;
+    }
+  } else if (N > 0) {
     // 1. stable LSD radix sort of (row, position); out-of-range lookups dropped and listed
     uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
     uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
