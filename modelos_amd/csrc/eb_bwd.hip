@@ -123,6 +123,20 @@ __device__ __forceinline__ void sgd_store_row(const float* acc, const float* p, 
 // ---------------------------------------------------------------------------
 // Utilities
 // ---------------------------------------------------------------------------
+// The prepare phase's zeroed state in one launch: the out-of-range lookup
+// count, the long-row count and the zero row (n_zrow u32 words), each when not
+// null.
+__global__ void prep_fill_kernel(uint32_t* __restrict__ invalid, uint32_t* __restrict__ long_count,
+                                 uint32_t* __restrict__ zrow, int64_t n_zrow) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    invalid[0] = 0u;
+    if (long_count != nullptr) long_count[0] = 0u;
+  }
+  if (zrow == nullptr) return;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zrow; i += (int64_t)gridDim.x * blockDim.x)
+    zrow[i] = 0u;
+}
+
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = v;
@@ -481,13 +495,20 @@ constexpr int kSegItems = 4 * kRadixSub;
 
 // One block: the segment table from the first pass's scanned digit offsets
 // (bucket b starts at ofs[b * ntiles], the next bucket's start or the valid
-// count ends it), and per bucket {first segment, one past its last, start}.
+// count ends it), and per bucket {first segment, one past its last, start};
+// also offs[K] <- the valid count and, with meta, the metadata entries past it
+// (the padding and the dropped lookups' share) <- 0.
 __global__ __launch_bounds__(256) void seg_plan_kernel(const uint32_t* __restrict__ ofs, int64_t ntiles,
                                                        int nbuckets, int R, const uint32_t* __restrict__ nvalid,
                                                        uint32_t* __restrict__ tab, int64_t max_segs,
-                                                       uint32_t* __restrict__ bseg) {
+                                                       uint32_t* __restrict__ bseg, int64_t K,
+                                                       uint32_t* __restrict__ offs, uint2* __restrict__ meta,
+                                                       int64_t n_meta) {
   __shared__ uint32_t lds4[4];
   const uint32_t nv = *nvalid;
+  if (threadIdx.x == 0) offs[K] = nv;
+  if (meta != nullptr)
+    for (int64_t i = (int64_t)nv + threadIdx.x; i < n_meta; i += 256) meta[i] = make_uint2(0u, 0u);
   uint32_t carry = 0;
   for (int b0 = 0; b0 < nbuckets; b0 += 256) {
     const int b = b0 + (int)threadIdx.x;
@@ -564,18 +585,6 @@ __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restric
     }
     run += tot[j];
   }
-}
-
-// offs[K] <- the valid count; metadata entries past it (the padding and the
-// dropped lookups' share) <- 0.
-__global__ void meta_tail_kernel(const uint32_t* __restrict__ nvalid, int64_t K, int64_t n_total,
-                                 uint32_t* __restrict__ offs, uint2* __restrict__ meta) {
-  const uint32_t nv = *nvalid;
-  if (blockIdx.x == 0 && threadIdx.x == 0) offs[K] = nv;
-  if (meta == nullptr) return;
-  for (int64_t i = (int64_t)nv + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_total;
-       i += (int64_t)gridDim.x * blockDim.x)
-    meta[i] = make_uint2(0u, 0u);
 }
 
 // offs[r] <- the first sorted position whose key is >= r (a binary search of
@@ -1297,14 +1306,20 @@ __global__ void occ_meta_kernel(const uint32_t* __restrict__ svals, const uint32
 }
 
 
-// gpsw[position] <- psw-gradient dots computed in sorted order.
+// gpsw[position] <- psw-gradient dots computed in sorted order; gpsw <- 0 at
+// the positions the sort listed as out-of-range lookups (invalid: count, then
+// positions).
 __global__ void gpsw_scatter_kernel(const uint32_t* __restrict__ svals, const float* __restrict__ dsorted,
-                                    const uint32_t* __restrict__ nvalid, int64_t N, void* __restrict__ gpsw, int pdt) {
+                                    const uint32_t* __restrict__ nvalid, int64_t N, void* __restrict__ gpsw, int pdt,
+                                    const uint32_t* __restrict__ invalid) {
   const uint32_t nv = *nvalid;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N; i += (int64_t)gridDim.x * blockDim.x) {
     if (i >= (int64_t)nv) break;
     store_scalar(gpsw, pdt, svals[i], dsorted[i]);
   }
+  const uint32_t nbad = invalid[0];
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < nbad; i += gridDim.x * blockDim.x)
+    store_scalar(gpsw, pdt, invalid[1 + i], 0.f);
 }
 
 // gpsw[p] <- 0 for the positions the sort listed as out-of-range lookups.
@@ -1467,7 +1482,7 @@ static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t
   uint32_t* shist = (uint32_t*)(ws + l.seg_hist);
   const SegTab seg{tab, l.max_segs};
   hipLaunchKernelGGL(seg_plan_kernel, dim3(1), dim3(256), 0, st, (const uint32_t*)hist, l.ntiles, (int)l.nbuckets,
-                     1 << BITS, nvalid, tab, l.max_segs, bseg);
+                     1 << BITS, nvalid, tab, l.max_segs, bseg, K, offs, meta, l.nmeta);
   hipLaunchKernelGGL((seg_hist_kernel<BITS>), dim3((unsigned)l.max_segs), dim3(256), 0, st, (const uint32_t*)keys[0],
                      seg, shist);
   hipLaunchKernelGGL((seg_base_kernel<BITS>), dim3((unsigned)l.nbuckets), dim3(256), 0, st, (const uint32_t*)bseg, K,
@@ -1475,8 +1490,6 @@ static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t
   hipLaunchKernelGGL((radix_scatter_kernel<false, BITS, true>), dim3((unsigned)l.max_segs), block, 0, st,
                      (const int64_t*)nullptr, (const uint32_t*)keys[0], (const uint32_t*)vals[0], N, nvalid, K, 0,
                      (const uint32_t*)shist, (int64_t)0, keys[1], vals[1], seg, meta, psw, pdt, (uint32_t)L);
-  hipLaunchKernelGGL(meta_tail_kernel, dim3(grid_for(kMetaPad + N, 256, 1024)), dim3(256), 0, st, nvalid, K,
-                     l.nmeta, offs, meta);
 }
 
 // Row-kernel prefetch depth (lookups per row reduced in the row kernel) for
@@ -1489,9 +1502,9 @@ static int rows_prefetch(int64_t N, int64_t K) {
 
 // Prepare the row kernel's list: the light rows longer than 2 U (the row
 // kernel reduces up to 2 U in place).
+// (long_rows[K], the count, was zeroed by prep_fill_kernel.)
 static void prepare_rows_dyn(int64_t K, int U, const uint32_t* offs, uint32_t* long_rows, hipStream_t st) {
   uint32_t* long_count = long_rows + K;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, long_count, 0u, (int64_t)1);
   const int64_t lwg = cdiv(K, 1024) < 256 ? cdiv(K, 1024) : 256;
   hipLaunchKernelGGL(list_long_rows_kernel, dim3((unsigned)lwg), dim3(256), 0, st, offs, K, (uint32_t)(2 * U),
                      cdiv(cdiv(K, lwg), 256) * 256, long_rows, long_count);
@@ -1534,7 +1547,7 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
                            hipStream_t st) {
   if constexpr (LPG == 64) {
     uint2* meta = (uint2*)(ws + l.meta);
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(D, 256, 64)), dim3(256), 0, st, (uint32_t*)(ws + l.zrow), 0u, D);
+    // (the zero row was filled by prep_fill_kernel)
     if (N > 0 && l.plan.passes == 2) {
       // written by the sort's local pass
     } else if (N > 0)
@@ -1591,7 +1604,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     }
     if (N > 0 && gpsw != nullptr)
       hipLaunchKernelGGL(gpsw_scatter_kernel, dim3(grid_for(N, 256, 16384)), dim3(256), 0, st, svals,
-                         (const float*)dsorted, nvalid, N, gpsw, pdt);
+                         (const float*)dsorted, nvalid, N, gpsw, pdt, (const uint32_t*)(ws + l.invalid));
   } else {
     static_assert(!ACC, "the accumulating reduction runs on 64-lane rows");
     if (N > 0)
@@ -1728,7 +1741,13 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
   char* ws = (char*)workspace;
   const int64_t K = num_rows, N = bags * bag_size;
   const SortedView v = sorted_view(l, ws);
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, v.invalid, 0u, (int64_t)1);
+  // zeroed state: the out-of-range count, and for the 64-lane row kernels the long-row count and the zero row
+  {
+    const bool rows64 = c.lpg == 64;
+    hipLaunchKernelGGL(prep_fill_kernel, dim3(rows64 ? grid_for(dim, 256, 64) : 1), dim3(256), 0, st, v.invalid,
+                       rows64 && K > 0 ? (uint32_t*)(ws + l.long_rows) + K : (uint32_t*)nullptr,
+                       rows64 ? (uint32_t*)(ws + l.zrow) : (uint32_t*)nullptr, rows64 ? dim : (int64_t)0);
+  }
   uint2* meta = c.lpg == 64 ? (uint2*)(ws + l.meta) : nullptr;  // read by the 64-lane row kernels
   if (N > 0 && l.plan.passes == 2) {
     // 1-2. stable sort of (row, position) by bucketing and local passes, with the row offsets and metadata
@@ -1831,7 +1850,7 @@ static int eb_bwd_reduce(const char* fn, bool acc, const void* weight, int64_t n
 #undef PKM_REDUCE
   PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "%s: no kernel for lpg=%d vpl=%d%s", fn, c.lpg, c.vpl,
               acc ? " (accumulating: 64-lane rows, gradient in the table's dtype)" : "");
-  if (N > 0 && gpsw != nullptr)
+  if (N > 0 && gpsw != nullptr && c.lpg != 64)  // (64-lane rows: inside gpsw_scatter_kernel)
     hipLaunchKernelGGL(zero_invalid_gpsw_kernel, dim3(64), dim3(256), 0, st, (const uint32_t*)v.invalid, gpsw,
                        psw_dtype);
   return pkm_check_launch(fn);
@@ -1926,7 +1945,7 @@ extern "C" int pkm_eb_bwd_sgd(const void* values, int64_t num_rows, int64_t dim,
     ok = dispatch_reduce<bf16_t, bf16_t>(false, c, values, num_rows, dim, psw, psw_dtype, grad_out, bag_size, v.offs,
                                          v.keys, v.vals, v.nvalid, N, l, ws, nullptr, grad_psw, st, &S);
   PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd_sgd: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
-  if (N > 0 && grad_psw != nullptr)
+  if (N > 0 && grad_psw != nullptr && c.lpg != 64)  // (64-lane rows: inside gpsw_scatter_kernel)
     hipLaunchKernelGGL(zero_invalid_gpsw_kernel, dim3(64), dim3(256), 0, st, (const uint32_t*)v.invalid, grad_psw,
                        psw_dtype);
   return pkm_check_launch("pkm_eb_bwd_sgd");
