@@ -552,10 +552,15 @@ __global__ __launch_bounds__(256) void seg_hist_kernel(const uint32_t* __restric
 }
 
 // Per bucket: the digits' starts (row r = b 2^BITS + d starts at offs[r]) and
-// each segment's per-digit destination, in place of its counts.
+// each segment's per-digit destination, in place of its counts. With
+// long_rows: the bucket's rows of more than T and at most kHeavyT lookups are
+// appended to the long-row list (one atomic per bucket for its range; the
+// list's order does not matter to the kernel that reads it).
 template <int BITS>
 __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restrict__ bseg, int64_t K,
-                                                       uint32_t* __restrict__ hist, uint32_t* __restrict__ offs) {
+                                                       uint32_t* __restrict__ hist, uint32_t* __restrict__ offs,
+                                                       uint32_t T, uint32_t* __restrict__ long_rows,
+                                                       uint32_t* __restrict__ long_count) {
   constexpr int R = 1 << BITS;
   constexpr int DPT = R / 256;
   __shared__ uint32_t lds4[4];
@@ -584,6 +589,25 @@ __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restric
       at += c;
     }
     run += tot[j];
+  }
+  if (long_rows == nullptr) return;
+  __shared__ uint32_t base;
+  uint32_t nl = 0;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int64_t r = ((int64_t)b << BITS) + threadIdx.x * DPT + j;
+    nl += (r < K && tot[j] > T && tot[j] <= (uint32_t)kHeavyT) ? 1u : 0u;
+  }
+  uint32_t nall;
+  uint32_t at = block_exclusive_sum(nl, &nall, lds4);
+  if (nall == 0) return;
+  if (threadIdx.x == 0) base = atomicAdd(long_count, nall);
+  __syncthreads();
+  at += base;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int64_t r = ((int64_t)b << BITS) + threadIdx.x * DPT + j;
+    if (r < K && tot[j] > T && tot[j] <= (uint32_t)kHeavyT) long_rows[at++] = (uint32_t)r;
   }
 }
 
@@ -1468,7 +1492,8 @@ static void radix_pass(int pass, const int64_t* idx, uint32_t* const keys[2], ui
 template <int BITS>
 static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t* const vals[2], int64_t N, int64_t K,
                            const BwdLayout& l, char* ws, uint32_t* hist, uint32_t* parts, uint32_t* invalid,
-                           uint32_t* offs, uint2* meta, const void* psw, int pdt, int64_t L, hipStream_t st) {
+                           uint32_t* offs, uint2* meta, const void* psw, int pdt, int64_t L, uint32_t long_min,
+                           uint32_t* long_rows, hipStream_t st) {
   const uint32_t* nvalid = hist + l.nbins;  // the first pass's scan total
   const dim3 grid((unsigned)l.ntiles), block(256);
   hipLaunchKernelGGL((radix_hist_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr, N,
@@ -1486,7 +1511,7 @@ static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t
   hipLaunchKernelGGL((seg_hist_kernel<BITS>), dim3((unsigned)l.max_segs), dim3(256), 0, st, (const uint32_t*)keys[0],
                      seg, shist);
   hipLaunchKernelGGL((seg_base_kernel<BITS>), dim3((unsigned)l.nbuckets), dim3(256), 0, st, (const uint32_t*)bseg, K,
-                     shist, offs);
+                     shist, offs, long_min, long_rows, long_rows != nullptr ? long_rows + K : (uint32_t*)nullptr);
   hipLaunchKernelGGL((radix_scatter_kernel<false, BITS, true>), dim3((unsigned)l.max_segs), block, 0, st,
                      (const int64_t*)nullptr, (const uint32_t*)keys[0], (const uint32_t*)vals[0], N, nvalid, K, 0,
                      (const uint32_t*)shist, (int64_t)0, keys[1], vals[1], seg, meta, psw, pdt, (uint32_t)L);
@@ -1494,10 +1519,13 @@ static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t
 
 // Row-kernel prefetch depth (lookups per row reduced in the row kernel) for
 // rows of 64 * VPL vectors: 8 when the lookups average more than ~3 per row.
+static int rows_prefetch_of(int vpl, int64_t N, int64_t K) {
+  if (vpl <= 2) return N > 3 * K ? 8 : 4;
+  return vpl == 4 ? 2 : 1;
+}
 template <int VPL>
 static int rows_prefetch(int64_t N, int64_t K) {
-  if (VPL <= 2) return N > 3 * K ? 8 : 4;
-  return VPL == 4 ? 2 : 1;
+  return rows_prefetch_of(VPL, N, K);
 }
 
 // Prepare the row kernel's list: the light rows longer than 2 U (the row
@@ -1556,7 +1584,7 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
     else
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * l.nmeta, 256, 4096)), dim3(256), 0, st,
                          (uint32_t*)meta, 0u, 2 * l.nmeta);
-    if (K > 0)
+    if (K > 0 && !(N > 0 && l.plan.passes == 2))  // (the two-level sort lists the long rows itself)
       prepare_rows_dyn(K, rows_prefetch<VPL>(N, K), offs, (uint32_t*)(ws + l.long_rows), st);
   }
 }
@@ -1750,23 +1778,27 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
   }
   uint2* meta = c.lpg == 64 ? (uint2*)(ws + l.meta) : nullptr;  // read by the 64-lane row kernels
   if (N > 0 && l.plan.passes == 2) {
-    // 1-2. stable sort of (row, position) by bucketing and local passes, with the row offsets and metadata
+    // 1-2. stable sort of (row, position) by bucketing and local passes, with the row offsets, the metadata and
+    // the 64-lane row kernel's long-row list
     uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
     uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
+    uint32_t* long_rows = c.lpg == 64 ? (uint32_t*)(ws + l.long_rows) : nullptr;
+    const uint32_t long_min = (uint32_t)(2 * rows_prefetch_of(c.vpl, N, K));
+#define PKM_TWO_LEVEL(B_)                                                                                      \
+  two_level_sort<B_>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw, psw_dtype, \
+                     bag_size, long_min, long_rows, st)
     switch (l.plan.bits) {
       case 8:
-        two_level_sort<8>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw, psw_dtype,
-                          bag_size, st);
+        PKM_TWO_LEVEL(8);
         break;
       case 10:
-        two_level_sort<10>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw,
-                           psw_dtype, bag_size, st);
+        PKM_TWO_LEVEL(10);
         break;
       default:
-        two_level_sort<11>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw,
-                           psw_dtype, bag_size, st);
+        PKM_TWO_LEVEL(11);
         break;
     }
+#undef PKM_TWO_LEVEL
   } else if (N > 0) {
     // 1. stable LSD radix sort of (row, position); out-of-range lookups dropped and listed
     uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
