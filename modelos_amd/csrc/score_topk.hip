@@ -1302,22 +1302,21 @@ static_assert(kTrigger + 31 <= kBuf && kBuf <= 64, "slot budget");
 __host__ __device__ constexpr int word_key(int w) { return 32 * (w >> 3) + 8 * ((w & 7) >> 1) + 2 * (w & 1); }
 
 // Append the two scores of word p (keys key, key + 1) that can reach theta;
-// cb is the lane's slot count times the slot stride (kThreads words). Both
-// slots cb and cb + 1 are written by one instruction: slot cb takes r0 if it
-// passes and r1 otherwise, slot cb + 1 takes r1, and the count moves by the
-// number that pass, so the slots below the count are exactly the passing
-// scores in order (slot cb + 1 lies past the count unless both pass, and is
-// overwritten later).
-__device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* buf, uint32_t& cb, float tau,
+// ns is the lane's slot count. Both slots ns and ns + 1 are written by one
+// instruction: slot ns takes r0 if it passes and r1 otherwise, slot ns + 1
+// takes r1, and the count moves by the number that pass (two carry-in adds),
+// so the slots below the count are exactly the passing scores in order (slot
+// ns + 1 lies past the count unless both pass, and is overwritten later).
+__device__ __forceinline__ void append_pair(uint32_t p, uint32_t key, uint32_t* buf, uint32_t& ns, float tau,
                                             uint32_t hi_mask) {
   const uint32_t r0 = (p << 16) | (0xFFFFu - key);
   const uint32_t r1 = (p & hi_mask) | (0xFFFEu - key);
   const bool p0 = !(__uint_as_float(r0) < tau);
   const bool p1 = !(__uint_as_float(r1) < tau);
-  uint32_t* s = (uint32_t*)((unsigned char*)buf + cb);
+  uint32_t* s = buf + ns * kThreads;
   s[0] = p0 ? r0 : r1;
   s[kThreads] = r1;
-  cb += (p0 ? kThreads * 4u : 0u) + (p1 ? kThreads * 4u : 0u);
+  ns += (uint32_t)p0 + (uint32_t)p1;
 }
 
 // global_load_lds_dwordx4: lane i's 16 bytes at src go to LDS at dst + 16 i
@@ -1421,8 +1420,7 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
   uint32_t P[kWpb];
 #pragma unroll
   for (int i = 0; i < kWpb; ++i) P[i] = 0u;
-  uint32_t cb = 0;  // slot count x slot stride in bytes
-  constexpr uint32_t SB = kThreads * 4u;
+  uint32_t ns = 0;  // slot count
   // +inf until the second block's words are appended (P holds no scores, then
   // the first block's, which are in T already); tau_first once they are
   float tau = __uint_as_float(0x7F800000u), tau_first = 0.f;
@@ -1478,7 +1476,7 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
                                                         __builtin_bit_cast(bf16x8_t, bq[st]), X[kt], 0, 0, 0);
 #pragma unroll
         for (int q = (t * kWpb) / STEPS; q < ((t + 1) * kWpb) / STEPS; ++q)
-          append_pair(P[q], kprev + word_key(q), buf, cb, tau, hi_mask);
+          append_pair(P[q], kprev + word_key(q), buf, ns, tau, hi_mask);
         if (t >= KS) {
           // tile 0 is complete: its words replace the appended ones
 #pragma unroll
@@ -1511,12 +1509,12 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
       }
     } else {
 #pragma unroll
-      for (int q = 0; q < kWpb; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, cb, tau, hi_mask);
+      for (int q = 0; q < kWpb; ++q) append_pair(P[q], (uint32_t)(nb - 1) * kKB + word_key(q), buf, ns, tau, hi_mask);
     }
     if (j == 1) tau = tau_first;
     bool need;
     if (j < nb) {
-      const bool mine = __builtin_amdgcn_ballot_w64(cb >= kTrigger * SB) != 0;
+      const bool mine = __builtin_amdgcn_ballot_w64(ns >= kTrigger) != 0;
       if (lane == 0) flags[(j & 1) * kWaves + w] = mine ? 1u : 0u;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -1525,14 +1523,13 @@ __global__ __launch_bounds__(kThreads, 1) void pkm_score_stream_kernel(
       for (int v = 0; v < kWaves; ++v) any |= flags[(j & 1) * kWaves + v];
       need = any != 0;
     } else {
-      need = __builtin_amdgcn_ballot_w64(cb > 0u) != 0;
+      need = __builtin_amdgcn_ballot_w64(ns > 0u) != 0;
     }
     if (need) {
       // every slot: [0, 32), then [32, kBuf) where a lane holds more than 32
-      const uint32_t cnt = cb / SB;
-      merge_span<0>(T, buf, cnt);
-      if (__builtin_amdgcn_ballot_w64(cnt > 32u) != 0) merge_span<32>(T, buf, cnt);
-      cb = 0u;
+      merge_span<0>(T, buf, ns);
+      if (__builtin_amdgcn_ballot_w64(ns > 32u) != 0) merge_span<32>(T, buf, ns);
+      ns = 0u;
       if (j < nb) tau = tau_of(T);
     }
   }
