@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const int64_t* __res
 // share, then the segments' stable scatters, which also write the occurrence
 // metadata. A bucket's writes stay inside its own range of the outputs.
 // ---------------------------------------------------------------------------
-constexpr int kSegItems = 4 * kRadixSub;
+constexpr int kSegItems = kRadixSub;  // one sub-tile per segment: a hot bucket spreads over many workgroups
 
 // One block: the segment table from the first pass's scanned digit offsets
 // (bucket b starts at ofs[b * ntiles], the next bucket's start or the valid
