@@ -124,13 +124,17 @@ __device__ __forceinline__ void sgd_store_row(const float* acc, const float* p, 
 // Utilities
 // ---------------------------------------------------------------------------
 // The prepare phase's zeroed state in one launch: the out-of-range lookup
-// count, the long-row count and the zero row (n_zrow u32 words), each when not
-// null.
+// count, the long-row count, the hot-row count and lo flag (2 words) and the
+// zero row (n_zrow u32 words), each when not null.
 __global__ void prep_fill_kernel(uint32_t* __restrict__ invalid, uint32_t* __restrict__ long_count,
-                                 uint32_t* __restrict__ zrow, int64_t n_zrow) {
+                                 uint32_t* __restrict__ hot_state, uint32_t* __restrict__ zrow, int64_t n_zrow) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     invalid[0] = 0u;
     if (long_count != nullptr) long_count[0] = 0u;
+    if (hot_state != nullptr) {
+      hot_state[0] = 0u;
+      hot_state[1] = 0u;
+    }
   }
   if (zrow == nullptr) return;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_zrow; i += (int64_t)gridDim.x * blockDim.x)
@@ -551,16 +555,39 @@ __global__ __launch_bounds__(256) void seg_hist_kernel(const uint32_t* __restric
   for (int d = threadIdx.x; d < R; d += 256) hist[(int64_t)blockIdx.x * R + d] = h[d];
 }
 
+// Append the rows r = base_row + DPT t + j (j < DPT, r < K) whose flag is set
+// to list (count at *count): one atomic per block for the block's range; the
+// list's order does not matter to the kernels that read it.
+template <int DPT>
+__device__ __forceinline__ void append_rows(const bool (&flag)[DPT], int64_t base_row, uint32_t* __restrict__ list,
+                                            uint32_t* __restrict__ count, uint32_t* lds4, uint32_t* base) {
+  uint32_t nl = 0;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) nl += flag[j] ? 1u : 0u;
+  uint32_t nall;
+  uint32_t at = block_exclusive_sum(nl, &nall, lds4);
+  if (nall == 0) return;
+  if (threadIdx.x == 0) *base = atomicAdd(count, nall);
+  __syncthreads();
+  at += *base;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j)
+    if (flag[j]) list[at++] = (uint32_t)(base_row + threadIdx.x * DPT + j);
+  __syncthreads();  // *base is reused
+}
+
 // Per bucket: the digits' starts (row r = b 2^BITS + d starts at offs[r]) and
 // each segment's per-digit destination, in place of its counts. With
 // long_rows: the bucket's rows of more than T and at most kHeavyT lookups are
-// appended to the long-row list (one atomic per bucket for its range; the
-// list's order does not matter to the kernel that reads it).
+// appended to the long-row list; with hot_rows, its rows of at least H
+// lookups to the hot-row list.
 template <int BITS>
 __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restrict__ bseg, int64_t K,
                                                        uint32_t* __restrict__ hist, uint32_t* __restrict__ offs,
                                                        uint32_t T, uint32_t* __restrict__ long_rows,
-                                                       uint32_t* __restrict__ long_count) {
+                                                       uint32_t* __restrict__ long_count, uint32_t H,
+                                                       uint32_t* __restrict__ hot_rows,
+                                                       uint32_t* __restrict__ hot_count) {
   constexpr int R = 1 << BITS;
   constexpr int DPT = R / 256;
   __shared__ uint32_t lds4[4];
@@ -590,24 +617,20 @@ __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restric
     }
     run += tot[j];
   }
-  if (long_rows == nullptr) return;
   __shared__ uint32_t base;
-  uint32_t nl = 0;
+  const int64_t row0 = (int64_t)b << BITS;
+  if (long_rows != nullptr) {
+    bool fl[DPT];
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int64_t r = ((int64_t)b << BITS) + threadIdx.x * DPT + j;
-    nl += (r < K && tot[j] > T && tot[j] <= (uint32_t)kHeavyT) ? 1u : 0u;
+    for (int j = 0; j < DPT; ++j)
+      fl[j] = row0 + threadIdx.x * DPT + j < K && tot[j] > T && tot[j] <= (uint32_t)kHeavyT;
+    append_rows<DPT>(fl, row0, long_rows, long_count, lds4, &base);
   }
-  uint32_t nall;
-  uint32_t at = block_exclusive_sum(nl, &nall, lds4);
-  if (nall == 0) return;
-  if (threadIdx.x == 0) base = atomicAdd(long_count, nall);
-  __syncthreads();
-  at += base;
+  if (hot_rows != nullptr) {
+    bool fl[DPT];
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int64_t r = ((int64_t)b << BITS) + threadIdx.x * DPT + j;
-    if (r < K && tot[j] > T && tot[j] <= (uint32_t)kHeavyT) long_rows[at++] = (uint32_t)r;
+    for (int j = 0; j < DPT; ++j) fl[j] = row0 + threadIdx.x * DPT + j < K && tot[j] >= H;
+    append_rows<DPT>(fl, row0, hot_rows, hot_count, lds4, &base);
   }
 }
 
@@ -751,7 +774,7 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
                                                            const uint32_t* __restrict__ svals,
                                                            const uint32_t* __restrict__ nvalid, int64_t nchunks,
                                                            float* __restrict__ partials, void* __restrict__ gpsw,
-                                                           float* __restrict__ dsorted) {
+                                                           float* __restrict__ dsorted, uint32_t hot_min) {
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
   constexpr int GPW = 64 / LPG;
@@ -771,7 +794,7 @@ __global__ __launch_bounds__(256) void eb_bwd_heavy_kernel(const TW* __restrict_
     const uint32_t r = cand[t];
     if (t == 1 && r == cand[0]) break;
     const uint32_t rb = offs[r], re = offs[r + 1];
-    if (re - rb <= (uint32_t)kHeavyT) continue;
+    if (re - rb <= (uint32_t)kHeavyT || re - rb >= hot_min) continue;  // light, or reduced on the matrix cores
     const uint32_t s_beg = rb > i_beg ? rb : i_beg;
     const uint32_t s_end = re < i_end ? re : i_end;
     const int slot = rb > i_beg ? 1 : 0;
@@ -1129,7 +1152,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
     const TW* __restrict__ W, int64_t K, int64_t D, int want_dot, const TG* __restrict__ g,
     const uint32_t* __restrict__ offs, const uint2* __restrict__ meta, const float* __restrict__ partials,
     const TW* __restrict__ zrow, TW* __restrict__ dummy_row, TW* __restrict__ gW, float* __restrict__ dsorted,
-    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk, uint32_t long_min, SgdArgs S) {
+    uint32_t dummy_slot, uint32_t* __restrict__ tickets, uint32_t blk, uint32_t long_min, uint32_t hot_min,
+    SgdArgs S) {
   static_assert(kDynRC * U <= 64, "a chunk's metadata must fit one load per lane");
   constexpr int EPV = VecTraits<TW>::EPV;
   constexpr int NE = VPL * EPV;
@@ -1175,7 +1199,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
     M.beg = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i);
     M.end = (uint32_t)__builtin_amdgcn_readlane((int)C.off, i + 1);
     const uint32_t cnt = M.end - M.beg;
-    skip = cnt > long_min && cnt <= (uint32_t)kHeavyT;  // listed for the long-row kernel
+    // listed for the long-row kernel, or a hot row (the matrix-core products write it)
+    skip = (cnt > long_min && cnt <= (uint32_t)kHeavyT) || cnt >= hot_min;
     M.nh = cnt <= (uint32_t)U ? cnt : 0u;
     row = C.row0 + (uint32_t)i;
 #pragma unroll
@@ -1193,7 +1218,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
     if constexpr (ACC) {
       // the pending gradient of a row this kernel writes (one with lookups, not left to the long-row kernel)
       const uint32_t cnt = M.end - M.beg;
-      const bool mine = row < K32 && cnt > 0 && !(cnt > long_min && cnt <= (uint32_t)kHeavyT);
+      const bool mine = row < K32 && cnt > 0 && !(cnt > long_min && cnt <= (uint32_t)kHeavyT) && cnt < hot_min;
       const char* prow = mine ? (const char*)gW + (uint64_t)row * rowbytes : zb;
 #pragma unroll
       for (int v = 0; v < VPL; ++v) P[v] = ld16(prow + lane_byte + v * 1024u);
@@ -1233,7 +1258,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
     }
   };
   auto process = [&](const RowMeta<U>& M, uint32_t row, bool skip, RowData<VPL, U, NV>& R, const uint4* P) {
-    if (skip) return;  // longer than 2 U (and light): reduced by the long-row kernel
+    if (skip) return;  // longer than 2 U (and light): reduced by the long-row kernel; or hot
     float acc[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) acc[e] = 0.f;
@@ -1354,6 +1379,503 @@ __global__ void zero_invalid_gpsw_kernel(const uint32_t* __restrict__ invalid, v
 }
 
 // ---------------------------------------------------------------------------
+// Hot rows on the matrix cores. A row with at least hot_min lookups (a
+// sizeable share of the bags: hot_min >= bags / 16) is reduced as a row of
+// two dense products instead of one gradient-row read per lookup:
+//   gW[hot[i]] = sum_b C[i, b] G[b]     C[i, b] = sum of psw over the row's lookups in bag b
+//   E[i, b]    = <W[hot[i]], G[b]>      psw-gradient of each lookup of the row in bag b
+// with G the upstream gradient [bags, D]: bf16 operands, float32 sums, on
+// v_mfma_f32_16x16x32_bf16. C is never materialised. The row's lookups,
+// sorted by position and hence by bag, are merged per bag into entries (the
+// weights of one bag summed in float32, in position order), split into chunks
+// of 32 bags, and each MFMA tile of C is built in LDS from the entries. A
+// merged weight that bf16 does not hold exactly (a bag holding the row twice,
+// float32 weights) is carried as hi + lo, both bf16; lo entries are read, and
+// lo tiles multiplied, only in the chunks that have one. The sums run in a
+// fixed order (deterministic), but not in position order, so they may differ
+// from the light rows' in the last float32 bits.
+// ---------------------------------------------------------------------------
+constexpr int kHotKC = 32;         // bags per chunk (one MFMA k-step)
+constexpr int kHotM = 64;          // hot rows per gradient-product tile
+constexpr int kHotN = 256;         // table columns per gradient-product tile
+constexpr int kHotDM = 128;        // hot rows per dot-product tile
+constexpr int kHotDN = 128;        // bags per dot-product tile
+constexpr int kHotDK = 64;         // dims per chunk of the dot product
+constexpr int kHotThreads = 256;   // 4 waves of 64 x 64
+constexpr uint32_t kHotLo = 0x80000000u;  // chunk-pointer flag: the row's chunk holds a lo entry
+constexpr int kHotLoList = 256;    // lo chunks one row lists before it flags all of its chunks
+
+// For each listed row i (row r = hot[i], count at hot[hr_max]; sorted
+// occurrences [offs[r], offs[r+1])): the row's entries, one per distinct bag
+// in bag order, written over the start of the row's own occurrence range of
+// ent (bag % 32 | hi << 16) and ent_lo (lo); chunk pointers, chunk-major
+// (index c * hr_max + i), pc (first entry, | kHotLo if the chunk holds a lo)
+// and po (first occurrence) of the row's first bag >= 32 c, for c = 0..nc (c =
+// nc: the row's ends); any_lo <- 1 if some lo is nonzero. A block per row,
+// grid-stride over the list (every block reads the count).
+__global__ __launch_bounds__(256) void hot_list_kernel(const uint32_t* __restrict__ hot, int64_t hr_max,
+                                                       const uint32_t* __restrict__ offs,
+                                                       const uint2* __restrict__ meta, uint32_t nc,
+                                                       uint32_t* __restrict__ pc, uint32_t* __restrict__ po,
+                                                       uint32_t* __restrict__ ent, uint16_t* __restrict__ ent_lo,
+                                                       uint32_t* __restrict__ any_lo) {
+  __shared__ uint32_t lds4[4];
+  __shared__ uint32_t lo_chunks[kHotLoList];
+  __shared__ uint32_t n_lo;
+  const uint32_t n = hot[hr_max];
+  const size_t H = (size_t)hr_max;
+  for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
+    const uint32_t r = hot[i];
+    const uint32_t beg = offs[r], end = offs[r + 1];
+    if (threadIdx.x == 0) n_lo = 0u;
+    __syncthreads();
+    uint32_t carry = 0;  // entries of the row's earlier occurrence tiles
+    for (uint32_t j0 = beg; j0 < end; j0 += 256) {
+      const uint32_t j = j0 + threadIdx.x;
+      uint32_t bag = 0, prev = 0;
+      bool start = false;
+      if (j < end) {
+        bag = meta[j].x;
+        prev = j > beg ? meta[j - 1].x : 0u;
+        start = j == beg || bag != prev;
+      }
+      uint32_t tot;
+      const uint32_t k = carry + block_exclusive_sum(start ? 1u : 0u, &tot, lds4);
+      if (start) {
+        // chunks (chunk of the previous occurrence, chunk of this one] start here
+        const uint32_t c = bag / kHotKC;
+        for (uint32_t cc = j == beg ? 0u : prev / kHotKC + 1u; cc <= c; ++cc) {
+          pc[cc * H + i] = beg + k;
+          po[cc * H + i] = j;
+        }
+        float s = __uint_as_float(meta[j].y);
+        for (uint32_t t = j + 1; t < end && meta[t].x == bag; ++t) s += __uint_as_float(meta[t].y);
+        const uint32_t hi = f32_to_bf16_bits(s);
+        const uint32_t lo = f32_to_bf16_bits(s - bf16_to_f32(hi));
+        ent[beg + k] = (bag % kHotKC) | (hi << 16);
+        ent_lo[beg + k] = (uint16_t)lo;
+        if ((lo & 0x7FFFu) != 0u) {
+          *any_lo = 1u;
+          const uint32_t at = atomicAdd(&n_lo, 1u);
+          if (at < (uint32_t)kHotLoList) lo_chunks[at] = c;
+        }
+      }
+      carry += tot;
+    }
+    const uint32_t c_end = end > beg ? meta[end - 1].x / kHotKC + 1u : 0u;
+    for (uint32_t cc = c_end + threadIdx.x; cc <= nc; cc += 256) {
+      pc[cc * H + i] = beg + carry;
+      po[cc * H + i] = end;
+    }
+    __syncthreads();  // every pointer of the row written, n_lo final
+    const uint32_t nl = n_lo;
+    if (nl > (uint32_t)kHotLoList) {
+      for (uint32_t cc = threadIdx.x; cc < nc; cc += 256) pc[cc * H + i] |= kHotLo;
+    } else {
+      for (uint32_t t = threadIdx.x; t < nl; t += 256) atomicOr(&pc[lo_chunks[t] * H + i], kHotLo);
+    }
+    __syncthreads();  // n_lo and lo_chunks before the next row
+  }
+}
+
+// [rows][32] and [rows][64] bf16 LDS tiles: the 16-byte slots of a row are
+// rotated by the row (eight consecutive rows read at one slot cover all banks).
+__device__ __forceinline__ int hot_swz32(int row, int col) {
+  return row * 32 + ((((col >> 3) ^ (row >> 1)) & 3) << 3) + (col & 7);
+}
+__device__ __forceinline__ int hot_swz64(int row, int col) {
+  return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+}
+
+// Tile t of mt x nt -> (m, n), m fastest. With 8 | nt, the tiles of
+// workgroups on XCD x (t % 8 = x for a grid of a multiple of 8) take the
+// n-tiles [x nt / 8, (x + 1) nt / 8): one XCD's L2 serves each operand column.
+__device__ __forceinline__ void hot_tile(uint32_t t, uint32_t mt, uint32_t nt, uint32_t& m, uint32_t& n) {
+  if ((nt & 7u) == 0u) {
+    const uint32_t per = nt >> 3, x = t & 7u, j = t >> 3;
+    m = j % mt;
+    n = x * per + j / mt;
+  } else {
+    m = t % mt;
+    n = t / mt;
+  }
+}
+
+typedef __bf16 hot_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float hot_f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void hot_mma(const uint4& a, const uint4& b, hot_f32x4_t& c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(hot_bf16x8_t, a),
+                                              __builtin_bit_cast(hot_bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Gt[d][b] = G[b][d] for b < bags, 0 for bags <= b < 32 nc (the gradient
+// product's bag operand, bag-contiguous), and with Wh != NULL, Wh[i] =
+// W[hot[i]] (the dot product's row operand, contiguous); nothing without hot
+// rows. Tiles of 32 bags x 64 columns through LDS, grid-stride.
+__global__ __launch_bounds__(256) void hot_operands_kernel(const uint32_t* __restrict__ hot, int64_t hr_max,
+                                                           const bf16_t* __restrict__ G, int64_t B, uint32_t nc,
+                                                           int64_t D, uint16_t* __restrict__ Gt,
+                                                           const bf16_t* __restrict__ W, uint16_t* __restrict__ Wh) {
+  __shared__ uint16_t tile[32][64 + 2];
+  const uint32_t count = hot[hr_max];
+  if (count == 0) return;
+  const int tid = threadIdx.x;
+  const int64_t Bp = (int64_t)nc * kHotKC;
+  const int64_t ncol = D / 64;
+  const int64_t tiles = (int64_t)nc * ncol;
+  const uint16_t* g16 = (const uint16_t*)G;
+  for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+    const int64_t b0 = (t / ncol) * kHotKC, d0 = (t % ncol) * 64;
+    {
+      const int bl = tid >> 3, part = tid & 7;  // bag b0 + bl, columns d0 + 8 part
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (b0 + bl < B) v = ld16(g16 + (b0 + bl) * D + d0 + 8 * part);
+      const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        tile[bl][8 * part + 2 * e] = (uint16_t)(x[e] & 0xFFFFu);
+        tile[bl][8 * part + 2 * e + 1] = (uint16_t)(x[e] >> 16);
+      }
+    }
+    __syncthreads();
+    {
+      const int col = tid >> 2, grp = tid & 3;  // column d0 + col, bags b0 + 8 grp .. + 7
+      uint32_t x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        x[e] = (uint32_t)tile[8 * grp + 2 * e][col] | ((uint32_t)tile[8 * grp + 2 * e + 1][col] << 16);
+      *(uint4*)(Gt + (d0 + col) * Bp + b0 + 8 * grp) = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+    __syncthreads();
+  }
+  if (Wh == nullptr) return;
+  const int64_t per_row = D / 8;  // 16-byte pieces
+  const int64_t n16 = (int64_t)count * per_row;
+  for (int64_t k = (int64_t)blockIdx.x * 256 + tid; k < n16; k += (int64_t)gridDim.x * 256) {
+    const int64_t i = k / per_row, c = k % per_row;
+    *(uint4*)(Wh + i * D + 8 * c) = ld16((const uint16_t*)W + (int64_t)hot[i] * D + 8 * c);
+  }
+}
+
+// gW[hot[i], n0 + col] for a tile of 64 hot rows x 256 columns: the sum over
+// the bags' chunks of C-tile x Gt-tile. Wave w builds the C tile's rows
+// 16 w .. 16 w + 15 from their entries, two rows per load (32 lanes a row: a
+// chunk holds at most 32 distinct bags), and multiplies all 64 rows by its
+// 64 columns of the Gt tile. C tiles triple-buffered and Gt tiles
+// double-buffered in LDS, one barrier per chunk; a chunk's entries and Gt
+// rows are loaded two chunks ahead, into alternating register stages (every
+// load issued on every path, at clamped addresses, so the waits stay
+// partial); each stage carries the chunk pointers of its next chunk. ACC: the
+// sum is added to the gradient gW already holds (rounded to bf16 first, as
+// the light rows do).
+template <bool ACC>
+__global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))) void hot_grad_kernel(
+    const uint32_t* __restrict__ hot, int64_t hr_max, const uint32_t* __restrict__ pc, uint32_t nc,
+    const uint32_t* __restrict__ ent, const uint16_t* __restrict__ ent_lo, const uint16_t* __restrict__ Gt,
+    int64_t D, bf16_t* __restrict__ gW) {
+  constexpr int AT = kHotM * kHotKC;  // bf16 per C tile (4 KB)
+  constexpr int BT = kHotN * kHotKC;  // bf16 per Gt tile (16 KB)
+  __shared__ __align__(16) uint16_t Ah[3 * AT];
+  __shared__ __align__(16) uint16_t Al[3 * AT];
+  __shared__ __align__(16) uint16_t Bt[2 * BT];
+  __shared__ uint32_t rows[kHotM];
+  __shared__ uint32_t lo_tag[3];  // chunk + 1 of the last chunk that put a lo entry into the slot
+  const uint32_t count = hot[hr_max];
+  const bool any_lo = hot[hr_max + 1] != 0u;
+  const uint32_t mt = (count + kHotM - 1) / kHotM, nt = (uint32_t)(D / kHotN);
+  const size_t H = (size_t)hr_max;
+  const int64_t Bp = (int64_t)nc * kHotKC;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int eh = lane >> 5, el = lane & 31;  // entries: row 16 w + 2 s + eh of slot s, entry el of its chunk
+  const int gcol = tid >> 2, gpart = tid & 3;  // Gt: columns gcol + 64 u, bags 8 gpart .. + 7 of the chunk
+  // loaded values are kept as loaded (a select on one would wait for it); okm / flm: slots with an entry /
+  // with a lo flag, from the pointers
+  struct Stage {
+    uint32_t p0, p1;  // chunk pointers (flagged) of the stage's next chunk, for the lane's row 16 w + r
+    uint32_t okm, flm;
+    uint32_t e[8];
+    uint32_t lo[8];
+    uint4 g[4];
+  };
+  for (uint32_t t = blockIdx.x; t < mt * nt; t += gridDim.x) {
+    uint32_t m, n;
+    hot_tile(t, mt, nt, m, n);
+    const uint32_t i0 = m * kHotM;
+    const int64_t n0 = (int64_t)n * kHotN;
+    if (tid < kHotM) rows[tid] = i0 + tid < count ? hot[i0 + tid] : 0u;
+    if (tid < 3) lo_tag[tid] = 0u;
+    // the lane's row for the chunk pointers; a row past the count reads row 0's (its sums are never stored)
+    const uint32_t prow = i0 + 16 * w + r;
+    const size_t prow_c = prow < count ? prow : 0u;
+    const uint16_t* gbase = Gt + (n0 + gcol) * Bp + 8 * gpart;
+    // load chunk c (pointers S.p0 / S.p1 = its own), then S.p0 / S.p1 <- chunk c + 2's
+    auto load = [&](Stage& S, uint32_t c) {
+      uint32_t k[8];
+      S.okm = S.flm = 0u;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const uint32_t p0f = (uint32_t)__shfl((int)S.p0, 2 * s + eh);
+        const uint32_t p1 = (uint32_t)__shfl((int)S.p1, 2 * s + eh) & ~kHotLo;
+        const uint32_t kk = (p0f & ~kHotLo) + (uint32_t)el;
+        const bool ok = kk < p1;
+        k[s] = ok ? kk : 0u;
+        S.okm |= ok ? 1u << s : 0u;
+        S.flm |= (ok && (p0f & kHotLo) != 0u) ? 1u << s : 0u;
+      }
+      const uint32_t c2 = c + 2 < nc ? c + 2 : nc, c3 = c + 3 < nc ? c + 3 : nc;
+      S.p0 = pc[c2 * H + prow_c];
+      S.p1 = pc[c3 * H + prow_c];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        S.e[s] = ent[k[s]];
+        S.lo[s] = ent_lo[k[s]];
+      }
+      const int64_t cb = (int64_t)(c < nc ? c : nc - 1) * kHotKC;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) S.g[u] = ld16(gbase + 64 * u * Bp + cb);
+    };
+    auto put = [&](const Stage& S, int slot, uint32_t c, uint16_t* Bs) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if ((S.okm >> s) & 1u) {
+          const int at = slot * AT + hot_swz32(16 * w + 2 * s + eh, (int)(S.e[s] % kHotKC));
+          Ah[at] = (uint16_t)(S.e[s] >> 16);
+          if (((S.flm >> s) & 1u) && (S.lo[s] & 0x7FFFu) != 0u) {
+            Al[at] = (uint16_t)S.lo[s];
+            lo_tag[slot] = c + 1u;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) *(uint4*)(Bs + hot_swz32(gcol + 64 * u, 8 * gpart)) = S.g[u];
+    };
+    auto zero = [&](uint16_t* T) { *(uint4*)(T + 8 * tid) = make_uint4(0u, 0u, 0u, 0u); };
+    hot_f32x4_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = hot_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](int slot, uint32_t c, const uint16_t* Bs) {
+      uint4 a[4], b[4];
+#pragma unroll
+      for (int mt_ = 0; mt_ < 4; ++mt_) a[mt_] = *(const uint4*)(Ah + slot * AT + hot_swz32(16 * mt_ + r, 8 * q));
+#pragma unroll
+      for (int nt_ = 0; nt_ < 4; ++nt_) b[nt_] = *(const uint4*)(Bs + hot_swz32(64 * w + 16 * nt_ + r, 8 * q));
+#pragma unroll
+      for (int nt_ = 0; nt_ < 4; ++nt_)
+#pragma unroll
+        for (int mt_ = 0; mt_ < 4; ++mt_) hot_mma(a[mt_], b[nt_], acc[mt_][nt_]);
+      if (lo_tag[slot] == c + 1u) {  // uniform
+#pragma unroll
+        for (int mt_ = 0; mt_ < 4; ++mt_) a[mt_] = *(const uint4*)(Al + slot * AT + hot_swz32(16 * mt_ + r, 8 * q));
+#pragma unroll
+        for (int nt_ = 0; nt_ < 4; ++nt_)
+#pragma unroll
+          for (int mt_ = 0; mt_ < 4; ++mt_) hot_mma(a[mt_], b[nt_], acc[mt_][nt_]);
+      }
+    };
+    // stage c & 1 holds chunk c; chunk pointers of chunks 0 and 1 to start with
+    Stage s0, s1;
+    s0.p0 = pc[prow_c];
+    s0.p1 = pc[H + prow_c];
+    s1.p0 = s0.p1;
+    s1.p1 = pc[(nc >= 2 ? 2 : nc) * H + prow_c];
+    zero(Ah);
+    zero(Ah + AT);
+    if (any_lo) {
+      zero(Al);
+      zero(Al + AT);
+    }
+    load(s0, 0);
+    load(s1, 1);
+    __syncthreads();
+    put(s0, 0, 0u, Bt);
+    load(s0, 2);
+    __syncthreads();
+    // iteration c: put chunk c + 1 (its stage), reload that stage with chunk c + 3, multiply chunk c. Both
+    // bodies of a trip run on every path (an odd count ends with an empty one) and every load is issued in
+    // each: the waits for a stage's loads stay partial.
+    auto body = [&](uint32_t c, int ia, Stage& S) {
+      const int ia1 = ia == 2 ? 0 : ia + 1, ia2 = ia1 == 2 ? 0 : ia1 + 1;
+      // slot ia2 held chunk c - 1 (multiplied before the last barrier); a slot never used holds tag 0
+      zero(Ah + ia2 * AT);
+      if (any_lo && lo_tag[ia2] == c) zero(Al + ia2 * AT);
+      if (c + 1 < nc) put(S, ia1, c + 1, Bt + ((c + 1) & 1) * BT);
+      load(S, c + 3);
+      if (c < nc) mma(ia, c, Bt + (c & 1) * BT);
+      __syncthreads();
+    };
+    int ia = 0;
+    for (uint32_t c = 0; c < nc; c += 2) {
+      body(c, ia, s1);
+      ia = ia == 2 ? 0 : ia + 1;
+      body(c + 1, ia, s0);
+      ia = ia == 2 ? 0 : ia + 1;
+    }
+    // acc[mt][nt][e]: tile row 16 mt + 4 q + e, column 64 w + 16 nt + r
+    uint16_t* out = (uint16_t*)gW;
+#pragma unroll
+    for (int mt_ = 0; mt_ < 4; ++mt_) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * mt_ + 4 * q + e;
+        if (i0 + row < count) {
+          const int64_t base = (int64_t)rows[row] * D + n0 + 64 * w + r;
+#pragma unroll
+          for (int nt_ = 0; nt_ < 4; ++nt_) {
+            float v = acc[mt_][nt_][e];
+            if constexpr (ACC) v = bf16_to_f32(out[base + 16 * nt_]) + round_to<bf16_t>(v);
+            out[base + 16 * nt_] = (uint16_t)f32_to_bf16_bits(v);
+          }
+        }
+      }
+    }
+    __syncthreads();  // rows and tags before the next tile
+  }
+}
+
+// dsorted[j] = <Wh[i], G[bag of j]> for the occurrences j of the hot rows:
+// tiles of 128 hot rows x 128 bags, the dense product over D in chunks of 64
+// dims (both operands row-major, copied straight into LDS, double-buffered,
+// one barrier per chunk; loaded two chunks ahead into alternating register
+// stages), then the tile through LDS to the tile's occurrences (po: the rows'
+// occurrences by 32-bag chunk, chunk-major).
+__global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))) void hot_dot_kernel(
+    const uint32_t* __restrict__ hot, int64_t hr_max, const uint32_t* __restrict__ po, uint32_t nc,
+    const uint2* __restrict__ meta, const uint16_t* __restrict__ Wh, const bf16_t* __restrict__ G, int64_t B,
+    int64_t D, float* __restrict__ dsorted) {
+  constexpr int T = kHotDM * kHotDK;  // bf16 per operand tile (16 KB)
+  constexpr int EP = kHotDN + 4;      // E row pitch (floats)
+  static_assert(4 * T * 2 <= kHotDM * EP * 4, "operand tiles fit the E buffer");
+  __shared__ __align__(16) uint32_t smem[kHotDM * EP];  // 2 x (W tile, G tile), or E [row][bag]
+  uint16_t* As = (uint16_t*)smem;
+  uint16_t* Bs = As + 2 * T;
+  float* E = (float*)smem;
+  const uint32_t count = hot[hr_max];
+  const uint32_t mt = (count + kHotDM - 1) / kHotDM, nt = (uint32_t)((B + kHotDN - 1) / kHotDN);
+  const size_t H = (size_t)hr_max;
+  const int nk = (int)(D / kHotDK);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
+  const int r = lane & 15, q = lane >> 4;
+  const int lrow = tid >> 3, lslot = tid & 7;  // operand loads: rows lrow + 32 u, 16-byte slot
+  const uint32_t* meta32 = (const uint32_t*)meta;
+  const uint16_t* g16 = (const uint16_t*)G;
+  struct Stage {
+    uint4 a[4], b[4];
+  };
+  for (uint32_t t = blockIdx.x; t < mt * nt; t += gridDim.x) {
+    uint32_t m, n;
+    hot_tile(t, mt, nt, m, n);
+    const uint32_t i0 = m * kHotDM;
+    const int64_t b0 = (int64_t)n * kHotDN;
+    const uint16_t* wp[4];
+    const uint16_t* gp[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t rr = i0 + lrow + 32 * u;
+      wp[u] = Wh + (int64_t)(rr < count ? rr : count - 1) * D + 8 * lslot;
+      const int64_t b = b0 + lrow + 32 * u < B ? b0 + lrow + 32 * u : B - 1;
+      gp[u] = g16 + b * D + 8 * lslot;
+    }
+    auto load = [&](Stage& S, int k) {
+      const int kc = (k < nk ? k : nk - 1) * kHotDK;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        S.a[u] = ld16(wp[u] + kc);
+        S.b[u] = ld16(gp[u] + kc);
+      }
+    };
+    auto put = [&](const Stage& S, int buf) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        *(uint4*)(As + buf * T + hot_swz64(lrow + 32 * u, 8 * lslot)) = S.a[u];
+        *(uint4*)(Bs + buf * T + hot_swz64(lrow + 32 * u, 8 * lslot)) = S.b[u];
+      }
+    };
+    hot_f32x4_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = hot_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](int buf) {
+#pragma unroll
+      for (int ks = 0; ks < kHotDK / 32; ++ks) {
+        uint4 a[4], b[4];
+#pragma unroll
+        for (int mt_ = 0; mt_ < 4; ++mt_)
+          a[mt_] = *(const uint4*)(As + buf * T + hot_swz64(64 * wm + 16 * mt_ + r, 32 * ks + 8 * q));
+#pragma unroll
+        for (int nt_ = 0; nt_ < 4; ++nt_)
+          b[nt_] = *(const uint4*)(Bs + buf * T + hot_swz64(64 * wn + 16 * nt_ + r, 32 * ks + 8 * q));
+#pragma unroll
+        for (int nt_ = 0; nt_ < 4; ++nt_)
+#pragma unroll
+          for (int mt_ = 0; mt_ < 4; ++mt_) hot_mma(a[mt_], b[nt_], acc[mt_][nt_]);
+      }
+    };
+    // stage k & 1 holds chunk k; iteration k: put chunk k + 1, reload its stage with chunk k + 3, multiply chunk k
+    Stage s0, s1;
+    load(s0, 0);
+    load(s1, 1);
+    put(s0, 0);
+    load(s0, 2);
+    __syncthreads();
+    // both bodies of a trip run on every path (an odd count ends with an empty one): partial waits
+    auto body = [&](int k, Stage& S) {
+      if (k + 1 < nk) put(S, (k + 1) & 1);  // its buffer was last read by chunk k - 1, before the last barrier
+      load(S, k + 3);
+      if (k < nk) mma(k & 1);
+      __syncthreads();
+    };
+    for (int k = 0; k < nk; k += 2) {
+      body(k, s1);
+      body(k + 1, s0);
+    }
+    // E tile through LDS: acc[mt][nt][e] is tile row 64 wm + 16 mt + 4 q + e, bag 64 wn + 16 nt + r
+#pragma unroll
+    for (int mt_ = 0; mt_ < 4; ++mt_)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int nt_ = 0; nt_ < 4; ++nt_) E[(64 * wm + 16 * mt_ + 4 * q + e) * EP + 64 * wn + 16 * nt_ + r] = acc[mt_][nt_][e];
+    __syncthreads();
+    // wave w: tile rows 32 w .. 32 w + 31; lanes < 32 hold a row's occurrence range in the tile's 4 chunks
+    const uint32_t cb = (uint32_t)(b0 / kHotKC), ce = cb + kHotDN / kHotKC < nc ? cb + kHotDN / kHotKC : nc;
+    uint32_t pA = 0, pB = 0;
+    if (lane < 32 && i0 + 32 * w + lane < count) {
+      pA = po[cb * H + i0 + 32 * w + lane];
+      pB = po[ce * H + i0 + 32 * w + lane];
+    }
+    uint32_t len = pB - pA;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint32_t x = (uint32_t)__shfl_xor((int)len, o);
+      len = x > len ? x : len;
+    }
+    for (uint32_t p = 0; p < len; p += 64) {
+      uint32_t bag[32];
+#pragma unroll
+      for (int qq = 0; qq < 32; ++qq) {
+        const uint32_t j0 = (uint32_t)__builtin_amdgcn_readlane((int)pA, qq);
+        const uint32_t j1 = (uint32_t)__builtin_amdgcn_readlane((int)pB, qq);
+        const uint32_t j = j0 + p + (uint32_t)lane;
+        bag[qq] = j < j1 ? meta32[2 * (size_t)j] : 0xFFFFFFFFu;
+      }
+#pragma unroll
+      for (int qq = 0; qq < 32; ++qq) {
+        if (bag[qq] != 0xFFFFFFFFu) {
+          const uint32_t j = (uint32_t)__builtin_amdgcn_readlane((int)pA, qq) + p + (uint32_t)lane;
+          const uint32_t col = bag[qq] - (uint32_t)b0;
+          dsorted[j] = E[(32 * w + qq) * EP + (col < (uint32_t)kHotDN ? col : 0u)];
+        }
+      }
+    }
+    __syncthreads();  // E before the next tile
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -1379,12 +1901,16 @@ static RadixPlan radix_plan(int64_t K) {
 
 struct BwdLayout {
   size_t offs, keys0, vals0, keys1, vals1, hist, parts, partials, meta, dsorted, zrow, dummy_row, long_rows, tickets,
-      invalid, seg_tab, bseg, seg_hist, total;
+      invalid, seg_tab, bseg, seg_hist, hot_rows, hot_pc, hot_po, hot_ent, hot_lo, total;
   int64_t ntiles, nbins, nchunks, nmeta, nbuckets, max_segs;
+  // hot rows: at least hot_min lookups; at most hr_max of them; nc chunks of 32 bags
+  int64_t hot_min, hr_max, hot_nc;
+  size_t hot_gt, hot_wh;  // the gradient transposed [D][32 nc] and the hot rows' table rows [hr_max][D] (bf16)
   RadixPlan plan;
 };
 
-static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
+static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t bags, int64_t L) {
+  const int64_t N = bags * L;
   BwdLayout l;
   l.plan = radix_plan(K);
   size_t off = 0;
@@ -1441,6 +1967,27 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t N) {
     l.seg_hist = off;
     off += align256((size_t)l.max_segs * ((size_t)1 << l.plan.bits) * 4);
   }
+  // two-digit plans: the hot rows' list (count and lo flag after it), chunk pointers and merged entries
+  l.hot_min = bags / 16 > (int64_t)kHeavyT ? bags / 16 : (int64_t)kHeavyT + 1;
+  l.hr_max = (l.plan.passes == 2 && N > 0) ? (N / l.hot_min < K ? N / l.hot_min : K) : 0;
+  l.hot_nc = cdiv(bags, kHotKC);
+  l.hot_rows = l.hot_pc = l.hot_po = l.hot_ent = l.hot_lo = l.hot_gt = l.hot_wh = off;
+  if (l.hr_max > 0) {
+    l.hot_rows = off;
+    off += align256((size_t)(l.hr_max + 2) * 4);
+    l.hot_pc = off;
+    off += align256((size_t)l.hr_max * (size_t)(l.hot_nc + 1) * 4);
+    l.hot_po = off;
+    off += align256((size_t)l.hr_max * (size_t)(l.hot_nc + 1) * 4);
+    l.hot_ent = off;
+    off += align256((size_t)N * 4);
+    l.hot_lo = off;
+    off += align256((size_t)N * 2);
+    l.hot_gt = off;
+    off += align256((size_t)D * (size_t)(l.hot_nc * kHotKC) * 2);
+    l.hot_wh = off;
+    off += align256((size_t)l.hr_max * (size_t)D * 2);
+  }
   l.total = off;
   return l;
 }
@@ -1493,7 +2040,7 @@ template <int BITS>
 static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t* const vals[2], int64_t N, int64_t K,
                            const BwdLayout& l, char* ws, uint32_t* hist, uint32_t* parts, uint32_t* invalid,
                            uint32_t* offs, uint2* meta, const void* psw, int pdt, int64_t L, uint32_t long_min,
-                           uint32_t* long_rows, hipStream_t st) {
+                           uint32_t* long_rows, uint32_t* hot_rows, hipStream_t st) {
   const uint32_t* nvalid = hist + l.nbins;  // the first pass's scan total
   const dim3 grid((unsigned)l.ntiles), block(256);
   hipLaunchKernelGGL((radix_hist_kernel<true, BITS>), grid, block, 0, st, idx, (const uint32_t*)nullptr, N,
@@ -1511,7 +2058,8 @@ static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t
   hipLaunchKernelGGL((seg_hist_kernel<BITS>), dim3((unsigned)l.max_segs), dim3(256), 0, st, (const uint32_t*)keys[0],
                      seg, shist);
   hipLaunchKernelGGL((seg_base_kernel<BITS>), dim3((unsigned)l.nbuckets), dim3(256), 0, st, (const uint32_t*)bseg, K,
-                     shist, offs, long_min, long_rows, long_rows != nullptr ? long_rows + K : (uint32_t*)nullptr);
+                     shist, offs, long_min, long_rows, long_rows != nullptr ? long_rows + K : (uint32_t*)nullptr,
+                     (uint32_t)l.hot_min, hot_rows, hot_rows != nullptr ? hot_rows + l.hr_max : (uint32_t*)nullptr);
   hipLaunchKernelGGL((radix_scatter_kernel<false, BITS, true>), dim3((unsigned)l.max_segs), block, 0, st,
                      (const int64_t*)nullptr, (const uint32_t*)keys[0], (const uint32_t*)vals[0], N, nvalid, K, 0,
                      (const uint32_t*)shist, (int64_t)0, keys[1], vals[1], seg, meta, psw, pdt, (uint32_t)L);
@@ -1526,6 +2074,16 @@ static int rows_prefetch_of(int vpl, int64_t N, int64_t K) {
 template <int VPL>
 static int rows_prefetch(int64_t N, int64_t K) {
   return rows_prefetch_of(VPL, N, K);
+}
+
+// Whether the hot rows go to the matrix cores (for a bf16 table of 64-lane
+// rows, the lookups sorted by the two-level sort): rows of whole 256-column
+// tiles, and room for at least one hot row.
+static bool hot_rows_enabled(const BwdLayout& l, int64_t D) { return l.hr_max > 0 && D % kHotN == 0; }
+
+static unsigned hot_grid(int64_t tiles) {
+  const int64_t g = tiles < 1024 ? tiles : 1024;
+  return (unsigned)((g + 7) / 8 * 8);  // a multiple of 8: each workgroup stays on one XCD's tiles
 }
 
 // Prepare the row kernel's list: the light rows longer than 2 U (the row
@@ -1545,7 +2103,7 @@ template <typename TW, typename TG, int VPL, int U, bool SGD, bool ACC>
 static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, const void* g, const uint32_t* offs,
                             const uint2* meta, const float* partials, const void* zrow, void* dummy_row, void* gW,
                             float* dsorted, uint32_t dummy_slot, uint32_t* long_rows, uint32_t* tickets,
-                            uint32_t long_min, const SgdArgs& S, hipStream_t st) {
+                            uint32_t long_min, uint32_t hot_min, const SgdArgs& S, hipStream_t st) {
   const uint32_t* long_count = long_rows + K;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, tickets, 0u,
                      (int64_t)kDynGroups * kDynSub * kCtrStride);
@@ -1558,7 +2116,7 @@ static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, c
   KernelSpan span("eb_bwd_rows", st);
   hipLaunchKernelGGL((eb_bwd_rows_dyn_kernel<TW, TG, VPL, U, SGD, ACC>), dim3((unsigned)wgs), dim3(256), 0, st, (const TW*)W,
                      K, D, want_dot, (const TG*)g, offs, meta, partials, (const TW*)zrow, (TW*)dummy_row, (TW*)gW,
-                     dsorted, dummy_slot, tickets, blk, long_min, S);
+                     dsorted, dummy_slot, tickets, blk, long_min, hot_min, S);
   const int64_t rb = cdiv(K, 4 * 64);
   const unsigned lb = (unsigned)(rb < 1024 ? rb : 1024);
   hipLaunchKernelGGL((eb_bwd_long_rows_kernel<TW, TG, VPL, U, SGD, ACC>), dim3(lb), dim3(256), 0, st, (const TW*)W, D,
@@ -1572,7 +2130,7 @@ static void launch_rows_dyn(const void* W, int64_t K, int64_t D, int want_dot, c
 template <typename TW, int LPG, int VPL>
 static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64_t L, const uint32_t* offs,
                            const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l, char* ws,
-                           hipStream_t st) {
+                           bool hot, hipStream_t st) {
   if constexpr (LPG == 64) {
     uint2* meta = (uint2*)(ws + l.meta);
     // (the zero row was filled by prep_fill_kernel)
@@ -1586,6 +2144,17 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
                          (uint32_t*)meta, 0u, 2 * l.nmeta);
     if (K > 0 && !(N > 0 && l.plan.passes == 2))  // (the two-level sort lists the long rows itself)
       prepare_rows_dyn(K, rows_prefetch<VPL>(N, K), offs, (uint32_t*)(ws + l.long_rows), st);
+    if constexpr (std::is_same<TW, bf16_t>::value) {
+      if (hot && hot_rows_enabled(l, D)) {
+        // the hot rows the sort listed: merged entries and chunk pointers
+        const uint32_t* hot_list = (const uint32_t*)(ws + l.hot_rows);
+        const unsigned gb = (unsigned)(l.hr_max < 1024 ? l.hr_max : 1024);
+        hipLaunchKernelGGL(hot_list_kernel, dim3(gb), dim3(256), 0, st, hot_list, l.hr_max, offs,
+                           (const uint2*)(ws + l.meta), (uint32_t)l.hot_nc, (uint32_t*)(ws + l.hot_pc),
+                           (uint32_t*)(ws + l.hot_po), (uint32_t*)(ws + l.hot_ent), (uint16_t*)(ws + l.hot_lo),
+                           (uint32_t*)(ws + l.hot_rows) + l.hr_max + 1);
+      }
+    }
   }
 }
 
@@ -1602,10 +2171,33 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     const uint2* meta = (const uint2*)(ws + l.meta);
     float* dsorted = (float*)(ws + l.dsorted);
     void* zrow = ws + l.zrow;
+    // hot rows on the matrix cores (bf16 table and gradient; not in the SGD epilogue)
+    constexpr bool kHotTypes = std::is_same<TW, bf16_t>::value && std::is_same<TG, bf16_t>::value && !SGD;
+    const bool hot = kHotTypes && N > 0 && hot_rows_enabled(l, D);
+    const uint32_t hot_min = hot ? (uint32_t)l.hot_min : 0xFFFFFFFFu;
+    if constexpr (kHotTypes) {
+      if (hot) {
+        const uint32_t* hot_list = (const uint32_t*)(ws + l.hot_rows);
+        const int64_t bags = N / L;
+        uint16_t* Gt = (uint16_t*)(ws + l.hot_gt);
+        uint16_t* Wh = gpsw != nullptr ? (uint16_t*)(ws + l.hot_wh) : nullptr;
+        hipLaunchKernelGGL(hot_operands_kernel, dim3(grid_for(l.hot_nc * (D / 64), 1, 2048)), dim3(256), 0, st,
+                           hot_list, l.hr_max, (const bf16_t*)g, bags, (uint32_t)l.hot_nc, D, Gt, (const bf16_t*)W,
+                           Wh);
+        hipLaunchKernelGGL((hot_grad_kernel<ACC>), dim3(hot_grid(cdiv(l.hr_max, kHotM) * (D / kHotN))),
+                           dim3(kHotThreads), 0, st, hot_list, l.hr_max, (const uint32_t*)(ws + l.hot_pc),
+                           (uint32_t)l.hot_nc, (const uint32_t*)(ws + l.hot_ent), (const uint16_t*)(ws + l.hot_lo),
+                           (const uint16_t*)Gt, D, (bf16_t*)gW);
+        if (gpsw != nullptr)
+          hipLaunchKernelGGL(hot_dot_kernel, dim3(hot_grid(cdiv(l.hr_max, kHotDM) * cdiv(bags, kHotDN))),
+                             dim3(kHotThreads), 0, st, hot_list, l.hr_max, (const uint32_t*)(ws + l.hot_po),
+                             (uint32_t)l.hot_nc, meta, (const uint16_t*)Wh, (const bf16_t*)g, bags, D, dsorted);
+      }
+    }
     if (N > 0)
       hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, TG, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D,
                          psw, pdt, (const TG*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
-                         dsorted);
+                         dsorted, hot_min);
     if (K > 0) {
       const int want_dot = gpsw != nullptr ? 1 : 0;
       // the prefetch depth the lists were prepared for (rows longer than twice it go to the
@@ -1618,7 +2210,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
       uint32_t* long_rows = (uint32_t*)(ws + l.long_rows);
       uint32_t* tickets = (uint32_t*)(ws + l.tickets);
 #define PKM_ROWS(U_) \
-  launch_rows_dyn<TW, TG, VPL, U_, SGD, ACC>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, S, st)
+  launch_rows_dyn<TW, TG, VPL, U_, SGD, ACC>(W, K, D, want_dot, g, offs, meta, partials, zrow, dummy, gW, dsorted, dslot, long_rows, tickets, long_min, hot_min, S, st)
       if constexpr (VPL <= 2 && NV == 1) {
         if (u0 == 8) PKM_ROWS(8); else PKM_ROWS(4);
       } else if constexpr (VPL <= 2) {
@@ -1638,7 +2230,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     if (N > 0)
       hipLaunchKernelGGL((eb_bwd_heavy_kernel<TW, TG, LPG, VPL>), dim3(hb), dim3(256), 0, st, (const TW*)W, K, D,
                          psw, pdt, (const TG*)g, (uint32_t)L, offs, skeys, svals, nvalid, l.nchunks, partials, gpsw,
-                         (float*)nullptr);
+                         (float*)nullptr, 0xFFFFFFFFu);
     if (K == 0) return;
     const int rows_per_group = 4;
     const int64_t groups = cdiv(K, rows_per_group);
@@ -1657,12 +2249,12 @@ static bool dispatch_reduce(bool prepare, const GroupCfg& c, const void* W, int6
                             const void* g, int64_t L, const uint32_t* offs, const uint32_t* skeys,
                             const uint32_t* svals, const uint32_t* nvalid, int64_t N, const BwdLayout& l,
                             char* ws, void* gW, void* gpsw, hipStream_t st, const SgdArgs* sgd = nullptr,
-                            bool acc = false) {
+                            bool acc = false, bool hot = true) {
   static const SgdArgs no_sgd = {};
 #define PKM_RED_CASE(LPG_, VPL_)                                                                                  \
   if (c.lpg == LPG_ && c.vpl == VPL_) {                                                                           \
     if (prepare) {                                                                                                \
-      launch_prepare<TW, LPG_, VPL_>(K, D, psw, pdt, L, offs, svals, nvalid, N, l, ws, st);                       \
+      launch_prepare<TW, LPG_, VPL_>(K, D, psw, pdt, L, offs, svals, nvalid, N, l, ws, hot, st);                  \
     } else if (sgd == nullptr && acc) {                                                                         \
       if constexpr (LPG_ == 64 && std::is_same<TW, TG>::value)                                                    \
         launch_reduce<TW, TG, LPG_, VPL_, false, true>(W, K, D, psw, pdt, g, L, offs, skeys, svals, nvalid, N, l, \
@@ -1703,7 +2295,7 @@ using namespace pkm;
 
 extern "C" size_t pkm_eb_bwd_workspace_size(int64_t num_rows, int64_t dim, int64_t bags, int64_t bag_size) {
   if (num_rows < 0 || dim <= 0 || bags < 0 || bag_size < 0) return 0;
-  return bwd_layout(num_rows, dim, bags * bag_size).total;
+  return bwd_layout(num_rows, dim, bags, bag_size).total;
 }
 
 namespace pkm {
@@ -1728,7 +2320,7 @@ static int eb_bwd_check(const char* fn, int64_t num_rows, int64_t dim, int weigh
   const int epv = weight_dtype == PKM_DTYPE_F32 ? 4 : 8;
   PKM_REQUIRE(choose_group_cfg(dim, epv, true, c), PKM_ERR_UNSUPPORTED,
               "%s: dim %lld not supported (need dim/%d = LPG*VPL with LPG<=64, VPL<=8)", fn, (long long)dim, epv);
-  *l = bwd_layout(num_rows, dim, N);
+  *l = bwd_layout(num_rows, dim, bags, bag_size);
   PKM_REQUIRE(workspace != nullptr && workspace_bytes >= l->total, PKM_ERR_WORKSPACE,
               "%s: workspace of %zu bytes given, %zu needed", fn, workspace_bytes, l->total);
   PKM_REQUIRE((uintptr_t)workspace % 256 == 0, PKM_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned",
@@ -1757,9 +2349,12 @@ static SortedView sorted_view(const BwdLayout& l, char* ws) {
 
 }  // namespace pkm
 
-extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,
-                                  const void* psw, int psw_dtype, int64_t bags, int64_t bag_size, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
+namespace pkm {
+// pkm_eb_bwd_prepare; hot: also list the hot rows for the matrix-core
+// products (the reductions other than the SGD epilogue use them).
+static int eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices, const void* psw,
+                          int psw_dtype, int64_t bags, int64_t bag_size, void* workspace, size_t workspace_bytes,
+                          bool hot, void* stream) {
   GroupCfg c;
   BwdLayout l;
   const int rc = eb_bwd_check("pkm_eb_bwd_prepare", num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags,
@@ -1769,11 +2364,14 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
   char* ws = (char*)workspace;
   const int64_t K = num_rows, N = bags * bag_size;
   const SortedView v = sorted_view(l, ws);
-  // zeroed state: the out-of-range count, and for the 64-lane row kernels the long-row count and the zero row
+  hot = hot && c.lpg == 64 && weight_dtype == PKM_DTYPE_BF16 && hot_rows_enabled(l, dim);
+  // zeroed state: the out-of-range count, and for the 64-lane row kernels the long-row count, the hot-row
+  // state and the zero row
   {
     const bool rows64 = c.lpg == 64;
     hipLaunchKernelGGL(prep_fill_kernel, dim3(rows64 ? grid_for(dim, 256, 64) : 1), dim3(256), 0, st, v.invalid,
                        rows64 && K > 0 ? (uint32_t*)(ws + l.long_rows) + K : (uint32_t*)nullptr,
+                       hot ? (uint32_t*)(ws + l.hot_rows) + l.hr_max : (uint32_t*)nullptr,
                        rows64 ? (uint32_t*)(ws + l.zrow) : (uint32_t*)nullptr, rows64 ? dim : (int64_t)0);
   }
   uint2* meta = c.lpg == 64 ? (uint2*)(ws + l.meta) : nullptr;  // read by the 64-lane row kernels
@@ -1783,10 +2381,11 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
     uint32_t* keys[2] = {(uint32_t*)(ws + l.keys0), (uint32_t*)(ws + l.keys1)};
     uint32_t* vals[2] = {(uint32_t*)(ws + l.vals0), (uint32_t*)(ws + l.vals1)};
     uint32_t* long_rows = c.lpg == 64 ? (uint32_t*)(ws + l.long_rows) : nullptr;
+    uint32_t* hot_rows = hot ? (uint32_t*)(ws + l.hot_rows) : nullptr;
     const uint32_t long_min = (uint32_t)(2 * rows_prefetch_of(c.vpl, N, K));
 #define PKM_TWO_LEVEL(B_)                                                                                      \
   two_level_sort<B_>(indices, keys, vals, N, K, l, ws, v.hist, v.parts, v.invalid, v.offs, meta, psw, psw_dtype, \
-                     bag_size, long_min, long_rows, st)
+                     bag_size, long_min, long_rows, hot_rows, st)
     switch (l.plan.bits) {
       case 8:
         PKM_TWO_LEVEL(8);
@@ -1832,12 +2431,20 @@ extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtyp
                                 v.nvalid, N, l, ws, nullptr, nullptr, st);
   else if (weight_dtype == PKM_DTYPE_BF16)
     ok = dispatch_reduce<bf16_t>(true, c, nullptr, K, dim, psw, psw_dtype, nullptr, bag_size, v.offs, v.keys, v.vals,
-                                 v.nvalid, N, l, ws, nullptr, nullptr, st);
+                                 v.nvalid, N, l, ws, nullptr, nullptr, st, nullptr, false, hot);
   else
     ok = dispatch_reduce<f16_t>(true, c, nullptr, K, dim, psw, psw_dtype, nullptr, bag_size, v.offs, v.keys, v.vals,
                                 v.nvalid, N, l, ws, nullptr, nullptr, st);
   PKM_REQUIRE(ok, PKM_ERR_UNSUPPORTED, "pkm_eb_bwd_prepare: no kernel for lpg=%d vpl=%d", c.lpg, c.vpl);
   return pkm_check_launch("pkm_eb_bwd_prepare");
+}
+}  // namespace pkm
+
+extern "C" int pkm_eb_bwd_prepare(int64_t num_rows, int64_t dim, int weight_dtype, const int64_t* indices,
+                                  const void* psw, int psw_dtype, int64_t bags, int64_t bag_size, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  return eb_bwd_prepare(num_rows, dim, weight_dtype, indices, psw, psw_dtype, bags, bag_size, workspace,
+                        workspace_bytes, true, stream);
 }
 
 namespace pkm {
@@ -1962,8 +2569,8 @@ extern "C" int pkm_eb_bwd_sgd(const void* values, int64_t num_rows, int64_t dim,
               "pkm_eb_bwd_sgd: grad_psw given without psw");
   PKM_REQUIRE(((uintptr_t)values | (uintptr_t)grad_out | (uintptr_t)new_values | (uintptr_t)scaled_grad) % 16 == 0,
               PKM_ERR_INVALID_ARGUMENT, "pkm_eb_bwd_sgd: values, grad_out and outputs must be 16-byte aligned");
-  rc = pkm_eb_bwd_prepare(num_rows, dim, dtype, indices, psw, psw_dtype, bags, bag_size, workspace, workspace_bytes,
-                          stream);
+  rc = eb_bwd_prepare(num_rows, dim, dtype, indices, psw, psw_dtype, bags, bag_size, workspace, workspace_bytes,
+                      false, stream);
   if (rc != PKM_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
@@ -2047,7 +2654,7 @@ extern "C" int pkm_eb_bwd_noalloc(const void* weight, int64_t num_rows, int64_t 
   PKM_REQUIRE(bags * bag_size < ((int64_t)1 << 31) && num_rows < ((int64_t)1 << 31) - 1, PKM_ERR_INVALID_ARGUMENT,
               "pkm_eb_bwd_noalloc: bags*bag_size=%lld must be < 2^31 and num_rows=%lld < 2^31-1",
               (long long)(bags * bag_size), (long long)num_rows);
-  const size_t need = bwd_layout(num_rows, dim, bags * bag_size).total;
+  const size_t need = bwd_layout(num_rows, dim, bags, bag_size).total;
   PKM_REQUIRE(need <= kNoallocScratchBytes, PKM_ERR_WORKSPACE,
               "pkm_eb_bwd_noalloc: these sizes (num_rows=%lld dim=%lld bags=%lld bag_size=%lld) need %zu bytes of "
               "scratch, more than the fixed %zu bytes; use pkm_eb_bwd with a workspace",

@@ -445,6 +445,84 @@ def test_backward_large_gradient_parity(B, L, K, D, dtype, device):
     assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
 
 
+# Hot rows of a bf16 table with 64-lane rows (at least max(257, bags / 16)
+# lookups) are reduced as dense products on the matrix cores, their weights
+# merged per bag. Rows in ~40% of the bags, a row held up to three times by one
+# bag, a row at exactly the threshold and one just below it, a hot last row,
+# a bag count that is not a multiple of the 32-bag chunk or the 128-bag tile,
+# bf16 and float32 weights: elementwise against the oracle's sums of |terms|,
+# and bitwise run-to-run.
+def _hot_matrix_indices(B, L, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(20, K - 1, (B, L), generator=g)
+    idx[torch.rand(B, generator=g) < 0.4, 0] = 7
+    v = torch.rand(B, generator=g)
+    idx[v < 0.3, 1] = 8
+    idx[v < 0.1, 2] = 8
+    idx[v < 0.05, 3] = 8
+    hot_min = max(257, B // 16)
+    bags = torch.randperm(B, generator=g)
+    idx[bags[:hot_min], 4] = 9
+    idx[bags[:hot_min - 1], 5] = 10
+    idx[torch.rand(B, generator=g) < 0.5, 6] = K - 1
+    idx[bags[-3:], 7] = -1
+    return idx
+
+
+@pytest.mark.parametrize("psw_dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("B,L,K,D", [(2000, 12, 30000, 512), (1000, 16, 5000, 2048), (4100, 8, 9000, 1024)])
+def test_backward_hot_rows_matrix_cores(B, L, K, D, psw_dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    W, _, p, g = eb_inputs(B, L, K, D, torch.bfloat16, seed=41 + D, psw_dtype=psw_dtype)
+    idx = _hot_matrix_indices(B, L, K, seed=42 + D)
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    cW, cp = ref.eb_backward(idx, W.abs(), p.abs(), g.abs())
+    assert_rel_close(gW, eW, REL_TOL[torch.bfloat16], "grad_weight", cond=cW)
+    assert_rel_close(gp, ep, 1e-4 if psw_dtype == torch.float32 else REL_TOL[psw_dtype], "grad_psw", cond=cp)
+    assert (gp.cpu()[idx < 0] == 0).all()
+    gW2, gp2 = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
+
+
+# The merged weight of a hot row's bag is carried as bf16 hi + lo: sums that
+# cancel down to the lo parts come out exact. Row 5: weight 1 + 2^-8 (float32
+# weights; bf16 weights hold 1) in the even bags, -1 in the odd ones; row 6:
+# held twice by the even bags (weights 1 and 2^-8, merged 1 + 2^-8), once by
+# the odd ones (weight -1). Every partial sum is exact in float32, so the two
+# rows' gradients are exact: 2 g (row 5: 0 for bf16 weights) and 2 g.
+@pytest.mark.parametrize("psw_dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("D", [512, 1024])
+def test_backward_hot_rows_merged_weights_exact(D, psw_dtype, device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K = 1024, 4, 64
+    gen = torch.Generator().manual_seed(61)
+    W = (torch.randn((K, D), generator=gen) * 0.05).to(torch.bfloat16)
+    idx = torch.randint(10, K, (B, L), generator=gen)
+    p = torch.rand((B, L), generator=gen).to(psw_dtype)
+    even = torch.arange(B) % 2 == 0
+    w5 = 1 + 2.0**-8 if psw_dtype == torch.float32 else 1.0
+    idx[:, 0] = 5
+    p[:, 0] = torch.where(even, torch.tensor(w5), torch.tensor(-1.0)).to(psw_dtype)
+    idx[:, 1] = 6
+    p[:, 1] = torch.where(even, torch.tensor(1.0), torch.tensor(-1.0)).to(psw_dtype)
+    idx[even, 2] = 6
+    p[even, 2] = 2.0**-8
+    col = torch.arange(D) % 3
+    g = (1.0 + col).expand(B, D).to(torch.bfloat16).contiguous()  # 1, 2, 3 in every bag
+    gW, gp = eb.eb_backward(*_dev(idx, W, p, g, device=device))
+    gW = gW.cpu().float()
+    want5 = (2.0 * (1.0 + col) if psw_dtype == torch.float32 else torch.zeros(D)).float()
+    assert torch.equal(gW[5], want5)
+    assert torch.equal(gW[6], (2.0 * (1.0 + col)).float())
+    eW, ep = ref.eb_backward(idx, W, p, g)
+    cW, cp = ref.eb_backward(idx, W.abs(), p.abs(), g.abs())
+    assert_rel_close(gW, eW, REL_TOL[torch.bfloat16], "grad_weight", cond=cW)
+    assert_rel_close(gp, ep, 1e-4 if psw_dtype == torch.float32 else REL_TOL[psw_dtype], "grad_psw", cond=cp)
+
+
 # Rows longer than the row kernel's prefetch but below the heavy threshold
 # (5..250 lookups), packed into the first 64-row windows, beside two heavy rows
 # and uniform rows: with more than 3 lookups per row on average (the 8-slot
