@@ -579,15 +579,14 @@ __device__ __forceinline__ void append_rows(const bool (&flag)[DPT], int64_t bas
 // Per bucket: the digits' starts (row r = b 2^BITS + d starts at offs[r]) and
 // each segment's per-digit destination, in place of its counts. With
 // long_rows: the bucket's rows of more than T and at most kHeavyT lookups are
-// appended to the long-row list; with hot_rows, its rows of at least H
-// lookups to the hot-row list.
+// appended to the long-row list; with hot_bcnt: the number of its rows of at
+// least H lookups (hot rows, listed in row order by hot_order_kernel).
 template <int BITS>
 __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restrict__ bseg, int64_t K,
                                                        uint32_t* __restrict__ hist, uint32_t* __restrict__ offs,
                                                        uint32_t T, uint32_t* __restrict__ long_rows,
                                                        uint32_t* __restrict__ long_count, uint32_t H,
-                                                       uint32_t* __restrict__ hot_rows,
-                                                       uint32_t* __restrict__ hot_count) {
+                                                       uint32_t* __restrict__ hot_bcnt) {
   constexpr int R = 1 << BITS;
   constexpr int DPT = R / 256;
   __shared__ uint32_t lds4[4];
@@ -626,12 +625,47 @@ __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restric
       fl[j] = row0 + threadIdx.x * DPT + j < K && tot[j] > T && tot[j] <= (uint32_t)kHeavyT;
     append_rows<DPT>(fl, row0, long_rows, long_count, lds4, &base);
   }
-  if (hot_rows != nullptr) {
-    bool fl[DPT];
+  if (hot_bcnt != nullptr) {
+    uint32_t nh = 0;
 #pragma unroll
-    for (int j = 0; j < DPT; ++j) fl[j] = row0 + threadIdx.x * DPT + j < K && tot[j] >= H;
-    append_rows<DPT>(fl, row0, hot_rows, hot_count, lds4, &base);
+    for (int j = 0; j < DPT; ++j) nh += (row0 + threadIdx.x * DPT + j < K && tot[j] >= H) ? 1u : 0u;
+    uint32_t nall;
+    block_exclusive_sum(nh, &nall, lds4);
+    if (threadIdx.x == 0) hot_bcnt[b] = nall;
   }
+}
+
+// The hot rows (at least H lookups) in row order: bucket b (rows
+// [b 2^BITS, (b + 1) 2^BITS)) writes its rows after the hot rows of the
+// buckets before it (hot_bcnt: per-bucket counts); the last bucket writes the
+// count at hot[hr_max]. Rows in order keep a tile's hot rows, and their
+// merged entries, close together in memory.
+template <int BITS>
+__global__ __launch_bounds__(256) void hot_order_kernel(const uint32_t* __restrict__ hot_bcnt, int64_t nbuckets,
+                                                        const uint32_t* __restrict__ offs, int64_t K, uint32_t H,
+                                                        uint32_t* __restrict__ hot, int64_t hr_max) {
+  constexpr int DPT = (1 << BITS) / 256;
+  __shared__ uint32_t lds4[4];
+  const int64_t b = blockIdx.x;
+  uint32_t pre = 0;
+  for (int64_t x = threadIdx.x; x < b; x += 256) pre += hot_bcnt[x];
+  uint32_t prefix;
+  block_exclusive_sum(pre, &prefix, lds4);
+  const int64_t row0 = (b << BITS) + (int64_t)threadIdx.x * DPT;
+  bool fl[DPT];
+  uint32_t nh = 0;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int64_t r = row0 + j;
+    fl[j] = r < K && offs[r + 1] - offs[r] >= H;
+    nh += fl[j] ? 1u : 0u;
+  }
+  uint32_t total;
+  uint32_t at = prefix + block_exclusive_sum(nh, &total, lds4);
+#pragma unroll
+  for (int j = 0; j < DPT; ++j)
+    if (fl[j]) hot[at++] = (uint32_t)(row0 + j);
+  if (b == nbuckets - 1 && threadIdx.x == 0) hot[hr_max] = prefix + total;
 }
 
 // offs[r] <- the first sorted position whose key is >= r (a binary search of
@@ -1557,6 +1591,19 @@ __global__ __launch_bounds__(256) void hot_operands_kernel(const uint32_t* __res
   }
 }
 
+// Bag splits of the gradient product (split-K): the largest power of two S
+// that keeps S x (row tiles) x (column tiles) <= kHotTiles workgroup tiles, at
+// least 8 chunks per split and the S partial row blocks within part_rows.
+// S = 1: the product writes gW itself; else float32 partials, summed in split
+// order by hot_finish_kernel.
+constexpr uint32_t kHotTiles = 2048;
+__device__ __forceinline__ uint32_t hot_splits(uint32_t count, int64_t D, uint32_t nc, int64_t part_rows) {
+  const uint32_t mt = (count + kHotM - 1) / kHotM, nt = (uint32_t)(D / kHotN);
+  uint32_t S = 1;
+  while (S < 64 && 2 * S * mt * nt <= kHotTiles && nc >= 16 * S && (int64_t)(2 * S * mt) * kHotM <= part_rows) S *= 2;
+  return S;
+}
+
 // gW[hot[i], n0 + col] for a tile of 64 hot rows x 256 columns: the sum over
 // the bags' chunks of C-tile x Gt-tile. Wave w builds the C tile's rows
 // 16 w .. 16 w + 15 from their entries, two rows per load (32 lanes a row: a
@@ -1565,14 +1612,15 @@ __global__ __launch_bounds__(256) void hot_operands_kernel(const uint32_t* __res
 // double-buffered in LDS, one barrier per chunk; a chunk's entries and Gt
 // rows are loaded two chunks ahead, into alternating register stages (every
 // load issued on every path, at clamped addresses, so the waits stay
-// partial); each stage carries the chunk pointers of its next chunk. ACC: the
-// sum is added to the gradient gW already holds (rounded to bf16 first, as
-// the light rows do).
+// partial); each stage carries the chunk pointers of its next chunk. With S >
+// 1 bag splits, tile (m, n, s) sums the chunks [s nc / S, (s + 1) nc / S) into
+// the float32 partial rows s mt 64 + (hot row index). ACC: the sum is added to
+// the gradient gW already holds (rounded to bf16 first, as the light rows do).
 template <bool ACC>
 __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))) void hot_grad_kernel(
     const uint32_t* __restrict__ hot, int64_t hr_max, const uint32_t* __restrict__ pc, uint32_t nc,
     const uint32_t* __restrict__ ent, const uint16_t* __restrict__ ent_lo, const uint16_t* __restrict__ Gt,
-    int64_t D, bf16_t* __restrict__ gW) {
+    int64_t D, bf16_t* __restrict__ gW, float* __restrict__ part, int64_t part_rows) {
   constexpr int AT = kHotM * kHotKC;  // bf16 per C tile (4 KB)
   constexpr int BT = kHotN * kHotKC;  // bf16 per Gt tile (16 KB)
   __shared__ __align__(16) uint16_t Ah[3 * AT];
@@ -1583,6 +1631,7 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
   const uint32_t count = hot[hr_max];
   const bool any_lo = hot[hr_max + 1] != 0u;
   const uint32_t mt = (count + kHotM - 1) / kHotM, nt = (uint32_t)(D / kHotN);
+  const uint32_t NS = hot_splits(count, D, nc, part_rows);
   const size_t H = (size_t)hr_max;
   const int64_t Bp = (int64_t)nc * kHotKC;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -1598,9 +1647,11 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
     uint32_t lo[8];
     uint4 g[4];
   };
-  for (uint32_t t = blockIdx.x; t < mt * nt; t += gridDim.x) {
-    uint32_t m, n;
-    hot_tile(t, mt, nt, m, n);
+  for (uint32_t t = blockIdx.x; t < mt * NS * nt; t += gridDim.x) {
+    uint32_t ms, n;
+    hot_tile(t, mt * NS, nt, ms, n);
+    const uint32_t m = ms % mt, sp = ms / mt;
+    const uint32_t cb = (uint32_t)((uint64_t)sp * nc / NS), ce = (uint32_t)((uint64_t)(sp + 1) * nc / NS);
     const uint32_t i0 = m * kHotM;
     const int64_t n0 = (int64_t)n * kHotN;
     if (tid < kHotM) rows[tid] = i0 + tid < count ? hot[i0 + tid] : 0u;
@@ -1615,15 +1666,23 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
       S.okm = S.flm = 0u;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const uint32_t p0f = (uint32_t)__shfl((int)S.p0, 2 * s + eh);
-        const uint32_t p1 = (uint32_t)__shfl((int)S.p1, 2 * s + eh) & ~kHotLo;
-        const uint32_t kk = (p0f & ~kHotLo) + (uint32_t)el;
+        // rows 2 s (lanes 0-31) and 2 s + 1 (lanes 32-63) of the wave: lane reads, no LDS round trips
+        const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)S.p0, 2 * s);
+        const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane((int)S.p0, 2 * s + 1);
+        const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)S.p1, 2 * s);
+        const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane((int)S.p1, 2 * s + 1);
+        const uint32_t p0f = eh ? b0 : a0;
+        const uint32_t p1 = (eh ? b1 : a1) & ~kHotLo;
+        const uint32_t p0 = p0f & ~kHotLo;
+        const uint32_t kk = p0 + (uint32_t)el;
         const bool ok = kk < p1;
-        k[s] = ok ? kk : 0u;
+        // a lane past the chunk reads the entry before the row's chunk (in bounds, the lanes' own lines;
+        // one index shared by every such lane of the grid would make one hot cache line)
+        k[s] = ok ? kk : (p0 > 0u ? p0 - 1u : 0u);
         S.okm |= ok ? 1u << s : 0u;
         S.flm |= (ok && (p0f & kHotLo) != 0u) ? 1u << s : 0u;
       }
-      const uint32_t c2 = c + 2 < nc ? c + 2 : nc, c3 = c + 3 < nc ? c + 3 : nc;
+      const uint32_t c2 = c + 2 < ce ? c + 2 : ce, c3 = c + 3 < ce ? c + 3 : ce;
       S.p0 = pc[c2 * H + prow_c];
       S.p1 = pc[c3 * H + prow_c];
 #pragma unroll
@@ -1631,9 +1690,9 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
         S.e[s] = ent[k[s]];
         S.lo[s] = ent_lo[k[s]];
       }
-      const int64_t cb = (int64_t)(c < nc ? c : nc - 1) * kHotKC;
+      const int64_t bc = (int64_t)(c < ce ? c : ce - 1) * kHotKC;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) S.g[u] = ld16(gbase + 64 * u * Bp + cb);
+      for (int u = 0; u < 4; ++u) S.g[u] = ld16(gbase + 64 * u * Bp + bc);
     };
     auto put = [&](const Stage& S, int slot, uint32_t c, uint16_t* Bs) {
 #pragma unroll
@@ -1675,39 +1734,41 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
           for (int mt_ = 0; mt_ < 4; ++mt_) hot_mma(a[mt_], b[nt_], acc[mt_][nt_]);
       }
     };
-    // stage c & 1 holds chunk c; chunk pointers of chunks 0 and 1 to start with
+    // stage (c - cb) & 1 holds chunk c; chunk pointers of chunks cb and cb + 1 to start with
     Stage s0, s1;
-    s0.p0 = pc[prow_c];
-    s0.p1 = pc[H + prow_c];
+    s0.p0 = pc[cb * H + prow_c];
+    s0.p1 = pc[(cb + 1) * H + prow_c];
     s1.p0 = s0.p1;
-    s1.p1 = pc[(nc >= 2 ? 2 : nc) * H + prow_c];
+    s1.p1 = pc[(cb + 2 < ce ? cb + 2 : ce) * H + prow_c];
     zero(Ah);
     zero(Ah + AT);
     if (any_lo) {
       zero(Al);
       zero(Al + AT);
+      zero(Al + 2 * AT);
     }
-    load(s0, 0);
-    load(s1, 1);
+    load(s0, cb);
+    load(s1, cb + 1);
     __syncthreads();
-    put(s0, 0, 0u, Bt);
-    load(s0, 2);
+    put(s0, 0, cb, Bt + (cb & 1) * BT);
+    load(s0, cb + 2);
     __syncthreads();
     // iteration c: put chunk c + 1 (its stage), reload that stage with chunk c + 3, multiply chunk c. Both
     // bodies of a trip run on every path (an odd count ends with an empty one) and every load is issued in
     // each: the waits for a stage's loads stay partial.
     auto body = [&](uint32_t c, int ia, Stage& S) {
       const int ia1 = ia == 2 ? 0 : ia + 1, ia2 = ia1 == 2 ? 0 : ia1 + 1;
-      // slot ia2 held chunk c - 1 (multiplied before the last barrier); a slot never used holds tag 0
+      // slot ia2 held chunk c - 1 (multiplied before the last barrier); its lo tile was put to only if
+      // its tag says so (the tags start at 0 and the lo tiles zeroed)
       zero(Ah + ia2 * AT);
       if (any_lo && lo_tag[ia2] == c) zero(Al + ia2 * AT);
-      if (c + 1 < nc) put(S, ia1, c + 1, Bt + ((c + 1) & 1) * BT);
+      if (c + 1 < ce) put(S, ia1, c + 1, Bt + ((c + 1) & 1) * BT);
       load(S, c + 3);
-      if (c < nc) mma(ia, c, Bt + (c & 1) * BT);
+      if (c < ce) mma(ia, c, Bt + (c & 1) * BT);
       __syncthreads();
     };
     int ia = 0;
-    for (uint32_t c = 0; c < nc; c += 2) {
+    for (uint32_t c = cb; c < ce; c += 2) {
       body(c, ia, s1);
       ia = ia == 2 ? 0 : ia + 1;
       body(c + 1, ia, s0);
@@ -1721,17 +1782,59 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
       for (int e = 0; e < 4; ++e) {
         const int row = 16 * mt_ + 4 * q + e;
         if (i0 + row < count) {
-          const int64_t base = (int64_t)rows[row] * D + n0 + 64 * w + r;
+          if (NS > 1) {
+            float* prow = part + ((int64_t)sp * mt * kHotM + i0 + row) * D + n0 + 64 * w + r;
 #pragma unroll
-          for (int nt_ = 0; nt_ < 4; ++nt_) {
-            float v = acc[mt_][nt_][e];
-            if constexpr (ACC) v = bf16_to_f32(out[base + 16 * nt_]) + round_to<bf16_t>(v);
-            out[base + 16 * nt_] = (uint16_t)f32_to_bf16_bits(v);
+            for (int nt_ = 0; nt_ < 4; ++nt_) prow[16 * nt_] = acc[mt_][nt_][e];
+          } else {
+            const int64_t base = (int64_t)rows[row] * D + n0 + 64 * w + r;
+#pragma unroll
+            for (int nt_ = 0; nt_ < 4; ++nt_) {
+              float v = acc[mt_][nt_][e];
+              if constexpr (ACC) v = bf16_to_f32(out[base + 16 * nt_]) + round_to<bf16_t>(v);
+              out[base + 16 * nt_] = (uint16_t)f32_to_bf16_bits(v);
+            }
           }
         }
       }
     }
     __syncthreads();  // rows and tags before the next tile
+  }
+}
+
+// With S > 1 bag splits: gW[hot[i]] = bf16(sum over the splits, in split
+// order, of the float32 partial rows) (ACC: added to the pending gradient as
+// the product's own epilogue does); nothing with one split.
+template <bool ACC>
+__global__ __launch_bounds__(256) void hot_finish_kernel(const uint32_t* __restrict__ hot, int64_t hr_max,
+                                                         uint32_t nc, int64_t D, const float* __restrict__ part,
+                                                         int64_t part_rows, bf16_t* __restrict__ gW) {
+  const uint32_t count = hot[hr_max];
+  const uint32_t NS = hot_splits(count, D, nc, part_rows);
+  if (NS == 1) return;
+  const int64_t rows_per_split = (int64_t)((count + kHotM - 1) / kHotM) * kHotM;
+  const int64_t per_row = D / 4;
+  const int64_t n4 = (int64_t)count * per_row;
+  uint16_t* out = (uint16_t*)gW;
+  for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < n4; k += (int64_t)gridDim.x * 256) {
+    const int64_t i = k / per_row, c = 4 * (k % per_row);
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t sp = 0; sp < NS; ++sp) {
+      const float4 v = *(const float4*)(part + (sp * rows_per_split + i) * D + c);
+      a[0] += v.x;
+      a[1] += v.y;
+      a[2] += v.z;
+      a[3] += v.w;
+    }
+    uint16_t* o = out + (int64_t)hot[i] * D + c;
+    uint32_t b[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = a[e];
+      if constexpr (ACC) v = bf16_to_f32(o[e]) + round_to<bf16_t>(v);
+      b[e] = f32_to_bf16_bits(v);
+    }
+    *(uint2*)o = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
   }
 }
 
@@ -1905,7 +2008,8 @@ struct BwdLayout {
   int64_t ntiles, nbins, nchunks, nmeta, nbuckets, max_segs;
   // hot rows: at least hot_min lookups; at most hr_max of them; nc chunks of 32 bags
   int64_t hot_min, hr_max, hot_nc;
-  size_t hot_gt, hot_wh;  // the gradient transposed [D][32 nc] and the hot rows' table rows [hr_max][D] (bf16)
+  size_t hot_gt, hot_wh, hot_bcnt, hot_part;
+  int64_t hot_part_rows;  // float32 partial rows of the gradient product's bag splits  // the gradient transposed [D][32 nc] and the hot rows' table rows [hr_max][D] (bf16)
   RadixPlan plan;
 };
 
@@ -1971,7 +2075,8 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t bags, int64_t L) {
   l.hot_min = bags / 16 > (int64_t)kHeavyT ? bags / 16 : (int64_t)kHeavyT + 1;
   l.hr_max = (l.plan.passes == 2 && N > 0) ? (N / l.hot_min < K ? N / l.hot_min : K) : 0;
   l.hot_nc = cdiv(bags, kHotKC);
-  l.hot_rows = l.hot_pc = l.hot_po = l.hot_ent = l.hot_lo = l.hot_gt = l.hot_wh = off;
+  l.hot_rows = l.hot_pc = l.hot_po = l.hot_ent = l.hot_lo = l.hot_gt = l.hot_wh = l.hot_bcnt = l.hot_part = off;
+  l.hot_part_rows = 0;
   if (l.hr_max > 0) {
     l.hot_rows = off;
     off += align256((size_t)(l.hr_max + 2) * 4);
@@ -1987,6 +2092,13 @@ static BwdLayout bwd_layout(int64_t K, int64_t D, int64_t bags, int64_t L) {
     off += align256((size_t)D * (size_t)(l.hot_nc * kHotKC) * 2);
     l.hot_wh = off;
     off += align256((size_t)l.hr_max * (size_t)D * 2);
+    l.hot_bcnt = off;
+    off += align256((size_t)l.nbuckets * 4);
+    // up to 4 splits of every hot row, at most 128 MiB
+    const int64_t cap = ((int64_t)128 << 20) / (D * 4);
+    l.hot_part_rows = 4 * cdiv(l.hr_max, kHotM) * kHotM < cap ? 4 * cdiv(l.hr_max, kHotM) * kHotM : cap;
+    l.hot_part = off;
+    off += align256((size_t)l.hot_part_rows * (size_t)D * 4);
   }
   l.total = off;
   return l;
@@ -2059,7 +2171,11 @@ static void two_level_sort(const int64_t* idx, uint32_t* const keys[2], uint32_t
                      seg, shist);
   hipLaunchKernelGGL((seg_base_kernel<BITS>), dim3((unsigned)l.nbuckets), dim3(256), 0, st, (const uint32_t*)bseg, K,
                      shist, offs, long_min, long_rows, long_rows != nullptr ? long_rows + K : (uint32_t*)nullptr,
-                     (uint32_t)l.hot_min, hot_rows, hot_rows != nullptr ? hot_rows + l.hr_max : (uint32_t*)nullptr);
+                     (uint32_t)l.hot_min, hot_rows != nullptr ? (uint32_t*)(ws + l.hot_bcnt) : (uint32_t*)nullptr);
+  if (hot_rows != nullptr)
+    hipLaunchKernelGGL((hot_order_kernel<BITS>), dim3((unsigned)l.nbuckets), dim3(256), 0, st,
+                       (const uint32_t*)(ws + l.hot_bcnt), l.nbuckets, (const uint32_t*)offs, K, (uint32_t)l.hot_min,
+                       hot_rows, l.hr_max);
   hipLaunchKernelGGL((radix_scatter_kernel<false, BITS, true>), dim3((unsigned)l.max_segs), block, 0, st,
                      (const int64_t*)nullptr, (const uint32_t*)keys[0], (const uint32_t*)vals[0], N, nvalid, K, 0,
                      (const uint32_t*)shist, (int64_t)0, keys[1], vals[1], seg, meta, psw, pdt, (uint32_t)L);
@@ -2148,7 +2264,7 @@ static void launch_prepare(int64_t K, int64_t D, const void* psw, int pdt, int64
       if (hot && hot_rows_enabled(l, D)) {
         // the hot rows the sort listed: merged entries and chunk pointers
         const uint32_t* hot_list = (const uint32_t*)(ws + l.hot_rows);
-        const unsigned gb = (unsigned)(l.hr_max < 1024 ? l.hr_max : 1024);
+        const unsigned gb = (unsigned)(l.hr_max < 8192 ? l.hr_max : 8192);  // a block per row, up to 8192
         hipLaunchKernelGGL(hot_list_kernel, dim3(gb), dim3(256), 0, st, hot_list, l.hr_max, offs,
                            (const uint2*)(ws + l.meta), (uint32_t)l.hot_nc, (uint32_t*)(ws + l.hot_pc),
                            (uint32_t*)(ws + l.hot_po), (uint32_t*)(ws + l.hot_ent), (uint16_t*)(ws + l.hot_lo),
@@ -2184,10 +2300,15 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
         hipLaunchKernelGGL(hot_operands_kernel, dim3(grid_for(l.hot_nc * (D / 64), 1, 2048)), dim3(256), 0, st,
                            hot_list, l.hr_max, (const bf16_t*)g, bags, (uint32_t)l.hot_nc, D, Gt, (const bf16_t*)W,
                            Wh);
-        hipLaunchKernelGGL((hot_grad_kernel<ACC>), dim3(hot_grid(cdiv(l.hr_max, kHotM) * (D / kHotN))),
+        const int64_t tiles = cdiv(l.hr_max, kHotM) * (D / kHotN);
+        float* part = (float*)(ws + l.hot_part);
+        hipLaunchKernelGGL((hot_grad_kernel<ACC>), dim3(hot_grid(tiles > (int64_t)kHotTiles ? tiles : kHotTiles)),
                            dim3(kHotThreads), 0, st, hot_list, l.hr_max, (const uint32_t*)(ws + l.hot_pc),
                            (uint32_t)l.hot_nc, (const uint32_t*)(ws + l.hot_ent), (const uint16_t*)(ws + l.hot_lo),
-                           (const uint16_t*)Gt, D, (bf16_t*)gW);
+                           (const uint16_t*)Gt, D, (bf16_t*)gW, part, l.hot_part_rows);
+        hipLaunchKernelGGL((hot_finish_kernel<ACC>), dim3(grid_for(l.hr_max * (D / 4), 256, 4096)), dim3(256), 0, st,
+                           hot_list, l.hr_max, (uint32_t)l.hot_nc, D, (const float*)part, l.hot_part_rows,
+                           (bf16_t*)gW);
         if (gpsw != nullptr)
           hipLaunchKernelGGL(hot_dot_kernel, dim3(hot_grid(cdiv(l.hr_max, kHotDM) * cdiv(bags, kHotDN))),
                              dim3(kHotThreads), 0, st, hot_list, l.hr_max, (const uint32_t*)(ws + l.hot_po),
