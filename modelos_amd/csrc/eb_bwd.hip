@@ -1243,25 +1243,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRowVecs<T
       M.w[u] = (uint32_t)u < M.nh ? __int_as_float(__builtin_amdgcn_readlane((int)C.mw, i * U + u)) : 0.f;
     }
   };
+  // Rows and slots with nothing to read (tail rows past K, unused prefetch slots, W of a row without dots)
+  // load through a size-0 buffer resource: zeros, no memory access, same instructions.
   auto issue = [&](const RowMeta<U>& M, uint32_t row, RowData<VPL, U, NV>& R, uint4* P) {
-    // the SGD epilogue reads every table row (empty ones included); tail rows past K read the zero row
+    // the SGD epilogue reads every table row (empty ones included)
     const bool read_w = SGD ? row < K32 : (want_dot && M.nh);
-    const char* wrow = read_w ? Wb + (uint64_t)row * rowbytes : zb;
+    const auto wr = row_rsrc(Wb + (uint64_t)(read_w ? row : 0u) * rowbytes, read_w ? (uint32_t)rowbytes : 0u);
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_nt(wrow + lane_byte + v * 1024u);  // read once: keep L2 for g
+    for (int v = 0; v < VPL; ++v) R.wraw[v] = ld16_rsrc<2>(wr, lane_byte + v * 1024u);  // nt: keep L2 for g
     if constexpr (ACC) {
       // the pending gradient of a row this kernel writes (one with lookups, not left to the long-row kernel)
       const uint32_t cnt = M.end - M.beg;
       const bool mine = row < K32 && cnt > 0 && !(cnt > long_min && cnt <= (uint32_t)kHeavyT) && cnt < hot_min;
-      const char* prow = mine ? (const char*)gW + (uint64_t)row * rowbytes : zb;
+      const auto pr = row_rsrc((const char*)gW + (uint64_t)(mine ? row : 0u) * rowbytes, mine ? (uint32_t)rowbytes : 0u);
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) P[v] = ld16(prow + lane_byte + v * 1024u);
+      for (int v = 0; v < VPL; ++v) P[v] = ld16_rsrc<0>(pr, lane_byte + v * 1024u);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const char* grow = (uint32_t)u < M.nh ? gb + (uint64_t)M.b[u] * growbytes : zb;
+      const bool used = (uint32_t)u < M.nh;
+      const auto gr = row_rsrc(gb + (uint64_t)(used ? M.b[u] : 0u) * growbytes, used ? (uint32_t)growbytes : 0u);
 #pragma unroll
-      for (int v = 0; v < VPL * NV; ++v) R.gvec[u][v] = ld16(grow + glane_byte + (v / NV) * 1024u * NV + (v % NV) * 16u);
+      for (int v = 0; v < VPL * NV; ++v) R.gvec[u][v] = ld16_rsrc<0>(gr, glane_byte + (v / NV) * 1024u * NV + (v % NV) * 16u);
     }
   };
   const int dot_slot = dot_slot_of<U>(lane);

@@ -228,6 +228,19 @@ __device__ __forceinline__ void st16_nt(void* p, const uint4& v) {
   __builtin_nontemporal_store(x, (u32x4_t*)p);
 }
 
+// 16-byte loads through a buffer resource over one row (wave-uniform base and
+// size): a row given size 0 reads zeros without a memory access, in the same
+// instruction as a present row (the loads' count does not depend on the data,
+// so the compiler's waits on them stay partial). AUX: cache policy (2 = nt).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* row, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, (int)bytes, 0x00020000);
+}
+template <int AUX>
+__device__ __forceinline__ uint4 ld16_rsrc(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX);
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 // ---------------------------------------------------------------------------
 // Lane-group broadcast and reduction. A "group" is LPG consecutive lanes of a
 // wave64 (LPG a power of two); the source lane index is relative to the group.
