@@ -927,6 +927,10 @@ def run_stress(args, dev, steps=3, warmup=1):
     counts = torch.bincount(flat, minlength=n * n)
     U, top = int((counts > 0).sum()), int(counts.max())
     heavy = int((counts > 256).sum())
+    # rows of at least max(257, bags / 16) lookups: the value backward's matrix-core products
+    hot_min = max(257, tokens // 16)
+    hot_rows = int((counts >= hot_min).sum())
+    hot_lookups = int(counts[counts >= hot_min].sum())
     del flat, counts
     ms_per_step, step_ms, calls, ktimer = timed_steps(step, steps)
 
@@ -942,7 +946,11 @@ def run_stress(args, dev, steps=3, warmup=1):
     sc_ms = med(("pkm_score_topk", (tokens, H, n, half)))
     rows = ktimer.ms("eb_bwd_rows")
     rows_ms = sorted(rows)[len(rows) // 2] if rows else None
-    log(f"stress: {ms_per_step:.3f} ms/step; gather {fwd_ms:.3f} ms, value backward {bwd_ms:.3f} ms, "
+    hot = ktimer.ms("eb_bwd_hot")
+    hot_ms = sorted(hot)[len(hot) // 2] if hot else None
+    hot_flops = 2 * 2 * hot_rows * tokens * D  # C G and W_hot G^T, dense
+    log(f"stress: {ms_per_step:.3f} ms/step; gather {fwd_ms:.3f} ms, value backward {bwd_ms:.3f} ms "
+        f"(hot-row products {hot_ms if hot_ms is None else round(hot_ms, 3)} ms for {hot_rows} rows), "
         f"scoring {sc_ms:.3f} ms; U={U}, hottest row {top} lookups, {heavy} rows over 256")
 
     def rate(work, ms, peak):
@@ -969,6 +977,11 @@ def run_stress(args, dev, steps=3, warmup=1):
         "value_backward": dict(rate(a_bwd, bwd_ms, HBM_PEAK_GBS) or {}, unit="GB/s", work=a_bwd,
                                row_reduction_ms=round(rows_ms, 4) if rows_ms else None,
                                note="entry point: sort, heavy-row chunk partials, row reduction, scatter"),
+        "hot_rows": dict(rate(hot_flops, hot_ms, MFMA_BF16_PEAK_TFLOPS) or {}, unit="TFLOP/s", work=hot_flops,
+                         rows=hot_rows, lookups=hot_lookups, threshold=hot_min,
+                         note="value backward's hot rows (at least max(257, bags/16) lookups) as two dense bf16 "
+                              "products, C G (table gradient) and W_hot G^T (psw-gradients): operand copies, "
+                              "products and split sums, one event pair"),
         "scoring": dict(rate(score_flops(tokens, H, n, k), sc_ms, MFMA_BF16_PEAK_TFLOPS) or {}, unit="TFLOP/s",
                         work=score_flops(tokens, H, n, k),
                         note="entry point (scoring + per-half top-64 tile kernel, cartesian top-64)"),

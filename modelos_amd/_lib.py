@@ -301,7 +301,7 @@ class KernelTimer:
     keeps the durations and turns timing off. `ms(kernel)` returns the
     durations of one kernel name in call order."""
 
-    KERNELS = ("eb_fwd", "eb_bwd2", "eb_bwd_rows", "score_topk")
+    KERNELS = ("eb_fwd", "eb_bwd2", "eb_bwd_rows", "eb_bwd_hot", "score_topk")
 
     def __init__(self):
         self.records: dict = {}

@@ -2296,6 +2296,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
     const uint32_t hot_min = hot ? (uint32_t)l.hot_min : 0xFFFFFFFFu;
     if constexpr (kHotTypes) {
       if (hot) {
+        KernelSpan span("eb_bwd_hot", st);
         const uint32_t* hot_list = (const uint32_t*)(ws + l.hot_rows);
         const int64_t bags = N / L;
         uint16_t* Gt = (uint16_t*)(ws + l.hot_gt);
