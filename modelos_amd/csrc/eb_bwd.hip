@@ -1434,7 +1434,8 @@ __global__ void zero_invalid_gpsw_kernel(const uint32_t* __restrict__ invalid, v
 // ---------------------------------------------------------------------------
 constexpr int kHotKC = 32;         // bags per chunk (one MFMA k-step)
 constexpr int kHotM = 64;          // hot rows per gradient-product tile
-constexpr int kHotN = 256;         // table columns per gradient-product tile
+constexpr int kHotN = 512;         // table columns per gradient-product tile
+constexpr int kHotGradThreads = 512;  // gradient product: 8 waves of 64 rows x 64 columns
 constexpr int kHotDM = 128;        // hot rows per dot-product tile
 constexpr int kHotDN = 128;        // bags per dot-product tile
 constexpr int kHotDK = 64;         // dims per chunk of the dot product
@@ -1599,7 +1600,7 @@ __global__ __launch_bounds__(256) void hot_operands_kernel(const uint32_t* __res
 // least 8 chunks per split and the S partial row blocks within part_rows.
 // S = 1: the product writes gW itself; else float32 partials, summed in split
 // order by hot_finish_kernel.
-constexpr uint32_t kHotTiles = 2048;
+constexpr uint32_t kHotTiles = 1024;
 __device__ __forceinline__ uint32_t hot_splits(uint32_t count, int64_t D, uint32_t nc, int64_t part_rows) {
   const uint32_t mt = (count + kHotM - 1) / kHotM, nt = (uint32_t)(D / kHotN);
   uint32_t S = 1;
@@ -1607,11 +1608,11 @@ __device__ __forceinline__ uint32_t hot_splits(uint32_t count, int64_t D, uint32
   return S;
 }
 
-// gW[hot[i], n0 + col] for a tile of 64 hot rows x 256 columns: the sum over
-// the bags' chunks of C-tile x Gt-tile. Wave w builds the C tile's rows
-// 16 w .. 16 w + 15 from their entries, two rows per load (32 lanes a row: a
+// gW[hot[i], n0 + col] for a tile of 64 hot rows x 512 columns: the sum over
+// the bags' chunks of C-tile x Gt-tile. Wave w of 8 builds the C tile's rows
+// 8 w .. 8 w + 7 from their entries, two rows per load (32 lanes a row: a
 // chunk holds at most 32 distinct bags), and multiplies all 64 rows by its
-// 64 columns of the Gt tile. C tiles triple-buffered and Gt tiles
+// 64 columns of the Gt tile (each C tile serves 512 columns). C tiles triple-buffered and Gt tiles
 // double-buffered in LDS, one barrier per chunk; a chunk's entries and Gt
 // rows are loaded two chunks ahead, into alternating register stages (every
 // load issued on every path, at clamped addresses, so the waits stay
@@ -1620,7 +1621,7 @@ __device__ __forceinline__ uint32_t hot_splits(uint32_t count, int64_t D, uint32
 // the float32 partial rows s mt 64 + (hot row index). ACC: the sum is added to
 // the gradient gW already holds (rounded to bf16 first, as the light rows do).
 template <bool ACC>
-__global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))) void hot_grad_kernel(
+__global__ __launch_bounds__(kHotGradThreads) __attribute__((amdgpu_waves_per_eu(2))) void hot_grad_kernel(
     const uint32_t* __restrict__ hot, int64_t hr_max, const uint32_t* __restrict__ pc, uint32_t nc,
     const uint32_t* __restrict__ ent, const uint16_t* __restrict__ ent_lo, const uint16_t* __restrict__ Gt,
     int64_t D, bf16_t* __restrict__ gW, float* __restrict__ part, int64_t part_rows) {
@@ -1639,15 +1640,15 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
   const int64_t Bp = (int64_t)nc * kHotKC;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int eh = lane >> 5, el = lane & 31;  // entries: row 16 w + 2 s + eh of slot s, entry el of its chunk
-  const int gcol = tid >> 2, gpart = tid & 3;  // Gt: columns gcol + 64 u, bags 8 gpart .. + 7 of the chunk
+  const int eh = lane >> 5, el = lane & 31;  // entries: row 8 w + 2 s + eh of slot s, entry el of its chunk
+  const int gcol = tid >> 2, gpart = tid & 3;  // Gt: columns gcol + 128 u, bags 8 gpart .. + 7 of the chunk
   // loaded values are kept as loaded (a select on one would wait for it); okm / flm: slots with an entry /
   // with a lo flag, from the pointers
   struct Stage {
-    uint32_t p0, p1;  // chunk pointers (flagged) of the stage's next chunk, for the lane's row 16 w + r
+    uint32_t p0, p1;  // chunk pointers (flagged) of the stage's next chunk, for the lane's row 8 w + (lane & 7)
     uint32_t okm, flm;
-    uint32_t e[8];
-    uint32_t lo[8];
+    uint32_t e[4];
+    uint32_t lo[4];
     uint4 g[4];
   };
   for (uint32_t t = blockIdx.x; t < mt * NS * nt; t += gridDim.x) {
@@ -1660,15 +1661,15 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
     if (tid < kHotM) rows[tid] = i0 + tid < count ? hot[i0 + tid] : 0u;
     if (tid < 3) lo_tag[tid] = 0u;
     // the lane's row for the chunk pointers; a row past the count reads row 0's (its sums are never stored)
-    const uint32_t prow = i0 + 16 * w + r;
+    const uint32_t prow = i0 + 8 * w + (lane & 7);
     const size_t prow_c = prow < count ? prow : 0u;
     const uint16_t* gbase = Gt + (n0 + gcol) * Bp + 8 * gpart;
     // load chunk c (pointers S.p0 / S.p1 = its own), then S.p0 / S.p1 <- chunk c + 2's
     auto load = [&](Stage& S, uint32_t c) {
-      uint32_t k[8];
+      uint32_t k[4];
       S.okm = S.flm = 0u;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < 4; ++s) {
         // rows 2 s (lanes 0-31) and 2 s + 1 (lanes 32-63) of the wave: lane reads, no LDS round trips
         const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)S.p0, 2 * s);
         const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane((int)S.p0, 2 * s + 1);
@@ -1689,19 +1690,19 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
       S.p0 = pc[c2 * H + prow_c];
       S.p1 = pc[c3 * H + prow_c];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < 4; ++s) {
         S.e[s] = ent[k[s]];
         S.lo[s] = ent_lo[k[s]];
       }
       const int64_t bc = (int64_t)(c < ce ? c : ce - 1) * kHotKC;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) S.g[u] = ld16(gbase + 64 * u * Bp + bc);
+      for (int u = 0; u < 4; ++u) S.g[u] = ld16(gbase + 128 * u * Bp + bc);
     };
     auto put = [&](const Stage& S, int slot, uint32_t c, uint16_t* Bs) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < 4; ++s) {
         if ((S.okm >> s) & 1u) {
-          const int at = slot * AT + hot_swz32(16 * w + 2 * s + eh, (int)(S.e[s] % kHotKC));
+          const int at = slot * AT + hot_swz32(8 * w + 2 * s + eh, (int)(S.e[s] % kHotKC));
           Ah[at] = (uint16_t)(S.e[s] >> 16);
           if (((S.flm >> s) & 1u) && (S.lo[s] & 0x7FFFu) != 0u) {
             Al[at] = (uint16_t)S.lo[s];
@@ -1710,9 +1711,11 @@ __global__ __launch_bounds__(kHotThreads) __attribute__((amdgpu_waves_per_eu(2))
         }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) *(uint4*)(Bs + hot_swz32(gcol + 64 * u, 8 * gpart)) = S.g[u];
+      for (int u = 0; u < 4; ++u) *(uint4*)(Bs + hot_swz32(gcol + 128 * u, 8 * gpart)) = S.g[u];
     };
-    auto zero = [&](uint16_t* T) { *(uint4*)(T + 8 * tid) = make_uint4(0u, 0u, 0u, 0u); };
+    auto zero = [&](uint16_t* T) {
+      if (tid < AT / 8) *(uint4*)(T + 8 * tid) = make_uint4(0u, 0u, 0u, 0u);
+    };
     hot_f32x4_t acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -2307,7 +2310,7 @@ static void launch_reduce(const void* W, int64_t K, int64_t D, const void* psw, 
         const int64_t tiles = cdiv(l.hr_max, kHotM) * (D / kHotN);
         float* part = (float*)(ws + l.hot_part);
         hipLaunchKernelGGL((hot_grad_kernel<ACC>), dim3(hot_grid(tiles > (int64_t)kHotTiles ? tiles : kHotTiles)),
-                           dim3(kHotThreads), 0, st, hot_list, l.hr_max, (const uint32_t*)(ws + l.hot_pc),
+                           dim3(kHotGradThreads), 0, st, hot_list, l.hr_max, (const uint32_t*)(ws + l.hot_pc),
                            (uint32_t)l.hot_nc, (const uint32_t*)(ws + l.hot_ent), (const uint16_t*)(ws + l.hot_lo),
                            (const uint16_t*)Gt, D, (bf16_t*)gW, part, l.hot_part_rows);
         hipLaunchKernelGGL((hot_finish_kernel<ACC>), dim3(grid_for(l.hr_max * (D / 4), 256, 4096)), dim3(256), 0, st,
