@@ -79,6 +79,10 @@ size_t pkm_eb_bwd_workspace_size(int64_t num_rows, int64_t dim, int64_t bags, in
  * PKM_ERR_UNSUPPORTED (a caller widens a 16-bit gradient to float32 first,
  * which is exact).
  * workspace: device buffer of at least pkm_eb_bwd_workspace_size() bytes.
+ * Rows with at least max(257, bags / 16) lookups (a BF16 table and grad_out,
+ * dim a multiple of 512) are reduced as dense bf16 matrix products on the
+ * matrix cores, their weights merged per bag: float32 sums in a fixed order
+ * (deterministic), not in position order as the other rows' are.
  *
  * Replaces embedding_bag_bw_rev_indices
  *   (pkm/xformer_embeddingbag.py:331-386, fwpkm/xformer_embeddingbag_legacy.py:170-227),
