@@ -470,7 +470,8 @@ def _hot_matrix_indices(B, L, K, seed):
 
 
 @pytest.mark.parametrize("psw_dtype", [torch.bfloat16, torch.float32], ids=str)
-@pytest.mark.parametrize("B,L,K,D", [(2000, 12, 30000, 512), (1000, 16, 5000, 2048), (4100, 8, 9000, 1024)])
+@pytest.mark.parametrize("B,L,K,D", [(2000, 12, 30000, 512), (1000, 16, 5000, 2048), (4100, 8, 9000, 1024),
+                                     (1000, 8, 3000, 4096)])
 def test_backward_hot_rows_matrix_cores(B, L, K, D, psw_dtype, device):
     from modelos_amd import embedding_bag as eb
 
@@ -484,6 +485,21 @@ def test_backward_hot_rows_matrix_cores(B, L, K, D, psw_dtype, device):
     assert (gp.cpu()[idx < 0] == 0).all()
     gW2, gp2 = eb.eb_backward(*_dev(idx, W, p, g, device=device))
     assert torch.equal(gW, gW2) and torch.equal(gp, gp2)
+
+
+# Unweighted bags (every weight 1) with hot rows: a bag holding a hot row k
+# times merges to weight k; no psw-gradients (no dot product).
+def test_backward_hot_rows_unweighted(device):
+    from modelos_amd import embedding_bag as eb
+
+    B, L, K, D = 1500, 10, 8000, 1024
+    W, _, _, g = eb_inputs(B, L, K, D, torch.bfloat16, seed=63, psw=False)
+    idx = _hot_matrix_indices(B, L, K, seed=64)
+    gW, gp = eb.eb_backward(*_dev(idx, W, None, g, device=device))
+    assert gp is None
+    eW, _ = ref.eb_backward(idx, W, None, g)
+    cW, _ = ref.eb_backward(idx, W.abs(), None, g.abs())
+    assert_rel_close(gW, eW, REL_TOL[torch.bfloat16], "grad_weight", cond=cW)
 
 
 # The merged weight of a hot row's bag is carried as bf16 hi + lo: sums that
