@@ -592,29 +592,63 @@ __global__ __launch_bounds__(256) void seg_base_kernel(const uint32_t* __restric
   __shared__ uint32_t lds4[4];
   const int b = blockIdx.x;
   const uint32_t s0 = bseg[3 * b], s1 = bseg[3 * b + 1], start = bseg[3 * b + 2];
+  // the thread's DPT consecutive digits of a segment: one or two 16-byte vectors (one word for DPT = 1); each
+  // pass walks the bucket's segments once
+  static_assert(DPT == 1 || DPT % 4 == 0, "digits per thread: 1 or a multiple of 4");
+  auto seg_row = [&](uint32_t s) { return hist + (int64_t)s * R + threadIdx.x * DPT; };
+  auto load_row = [&](uint32_t s, uint32_t (&v)[DPT]) {
+    if constexpr (DPT == 1) {
+      v[0] = *seg_row(s);
+    } else {
+#pragma unroll
+      for (int q = 0; q < DPT / 4; ++q) {
+        const uint4 x = *(const uint4*)(seg_row(s) + 4 * q);
+        v[4 * q] = x.x;
+        v[4 * q + 1] = x.y;
+        v[4 * q + 2] = x.z;
+        v[4 * q + 3] = x.w;
+      }
+    }
+  };
+  auto store_row = [&](uint32_t s, const uint32_t (&v)[DPT]) {
+    if constexpr (DPT == 1) {
+      *seg_row(s) = v[0];
+    } else {
+#pragma unroll
+      for (int q = 0; q < DPT / 4; ++q)
+        *(uint4*)(seg_row(s) + 4 * q) = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+  };
   uint32_t tot[DPT], mine = 0;
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int d = threadIdx.x * DPT + j;
-    uint32_t t = 0;
-    for (uint32_t s = s0; s < s1; ++s) t += hist[(int64_t)s * R + d];
-    tot[j] = t;
-    mine += t;
+  for (int j = 0; j < DPT; ++j) tot[j] = 0;
+#pragma unroll 4
+  for (uint32_t s = s0; s < s1; ++s) {
+    uint32_t v[DPT];
+    load_row(s, v);
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) tot[j] += v[j];
   }
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) mine += tot[j];
   uint32_t all;
   uint32_t run = block_exclusive_sum(mine, &all, lds4);
+  uint32_t at[DPT];
 #pragma unroll
   for (int j = 0; j < DPT; ++j) {
     const int d = threadIdx.x * DPT + j;
     const int64_t r = ((int64_t)b << BITS) + d;
     if (r < K) offs[r] = start + run;
-    uint32_t at = start + run;
-    for (uint32_t s = s0; s < s1; ++s) {
-      const uint32_t c = hist[(int64_t)s * R + d];
-      hist[(int64_t)s * R + d] = at;
-      at += c;
-    }
+    at[j] = start + run;
     run += tot[j];
+  }
+#pragma unroll 4
+  for (uint32_t s = s0; s < s1; ++s) {
+    uint32_t v[DPT];
+    load_row(s, v);
+    store_row(s, at);
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) at[j] += v[j];
   }
   __shared__ uint32_t base;
   const int64_t row0 = (int64_t)b << BITS;
