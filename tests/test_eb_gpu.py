@@ -651,14 +651,17 @@ def test_backward_prepared_rejects_other_lookups(device):
         eb.eb_backward(didx.clone(), dW, dp, dg, prepared=prep)
 
 
-@pytest.mark.parametrize("K", [70000, 3000])
-def test_backward_prepared_workspace_serves_two_reductions(K, device):
+@pytest.mark.parametrize("K,hot", [(70000, False), (3000, False), (3000, True)])
+def test_backward_prepared_workspace_serves_two_reductions(K, hot, device):
     """One prepared workspace, two reductions with different upstream
     gradients (retain_graph, or the same lookups reused): each reduction
-    clears its own row-schedule counters, so both equal pkm_eb_bwd's."""
+    clears its own row-schedule counters, and leaves the hot-row lists the
+    prepare built intact, so both equal pkm_eb_bwd's."""
     from modelos_amd import embedding_bag as eb
 
     W, idx, p, g = eb_inputs(512, 256, K, 1024, torch.bfloat16, seed=47)
+    if hot:
+        idx = _hot_indices(512, 256, K, seed=49)  # rows 3, 4, 5 reach the hot threshold
     g2 = (torch.randn(g.shape, generator=torch.Generator().manual_seed(48)) * 0.5).to(g.dtype)
     dW, didx, dp, dg, dg2 = _dev(W, idx, p, g, g2, device=device)
     prep = eb.eb_backward_prepare(didx, dW, dp)
