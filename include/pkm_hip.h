@@ -274,6 +274,25 @@ int pkm_score_topk(const void* query, const void* keys, int64_t num_tokens, int6
                    void* out_sub_scores1, void* out_sub_scores2, void* stream);
 
 /*
+ * pkm_score_topk with a workspace: the same arguments and results (bit for
+ * bit), plus a device buffer of at least
+ * pkm_score_topk_workspace_size(heads, n_keys, half, dtype) bytes (the keys'
+ * size), 16-byte aligned. Where the tile kernel runs (knn above 32, IDW
+ * scores, F32, other half widths), the keys are first copied into it with
+ * each block of 16 keys stored chunk-major, so the kernel's key loads read
+ * whole cache lines. A NULL or smaller workspace gives pkm_score_topk.
+ * Replaces the same reference calls as pkm_score_topk (pkm/memory.py:250-289,
+ * fwpkm/fwpkm.py:853-934); the workspace has no counterpart there.
+ */
+size_t pkm_score_topk_workspace_size(int64_t heads, int64_t n_keys, int64_t half, int dtype);
+int pkm_score_topk_ws(const void* query, const void* keys, int64_t num_tokens, int64_t heads,
+                      int64_t n_keys, int64_t half, int64_t knn, int score_type, int dtype,
+                      void* out_scores, int64_t* out_indices,
+                      int64_t* out_sub_indices1, int64_t* out_sub_indices2,
+                      void* out_sub_scores1, void* out_sub_scores2,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Dense gradient of the two sub-score matrices from the gradient of the
  * selected scores (scores[t,h,j] = s_0[i_0] + s_1[i_1], id = i_0 * n_keys + i_1):
  *   d_sub_dense[h, c, t, i] = sum_{j : i_c(indices[t,h,j]) == i} d_scores[t,h,j]

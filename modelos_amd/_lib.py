@@ -87,6 +87,20 @@ SIGNATURES = {
         ],
     ),
     "pkm_count_invalid_indices": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "pkm_score_topk_workspace_size": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
+    "pkm_score_topk_ws": (
+        c_int,
+        [
+            c_void_p, c_void_p,  # query, keys
+            c_int64, c_int64, c_int64, c_int64, c_int64,  # num_tokens, heads, n_keys, half, knn
+            c_int, c_int,  # score_type, dtype
+            c_void_p, c_void_p,  # out_scores, out_indices
+            c_void_p, c_void_p,  # out_sub_indices1, out_sub_indices2
+            c_void_p, c_void_p,  # out_sub_scores1, out_sub_scores2
+            c_void_p, c_size_t,  # workspace, workspace_bytes
+            c_void_p,  # stream
+        ],
+    ),
     "pkm_score_topk": (
         c_int,
         [
@@ -345,12 +359,18 @@ _SIZE_ARGS = {
     "pkm_eb_bwd_sgd": (1, 2),
     "pkm_eb_bwd2_sgd": (4, 5),
     "pkm_score_topk": (2, 3, 4, 5),  # num_tokens, heads, n_keys, half
+    "pkm_score_topk_ws": (2, 3, 4, 5),
     "pkm_score_grad_sparse": (3, 4, 5, 6),  # num_tokens, heads, n_keys, half
     "pkm_rmsnorm_fwd": (2, 3),  # rows, dim
     "pkm_rmsnorm_bwd": (4, 5),
     "pkm_me_grad_fwd": (5, 6, 7),  # num_tokens, heads, n_keys
     "pkm_me_grad_hvp": (5, 6, 7),
 }
+
+# entry points timed under another's name: the workspace form of the scoring
+# entry is the same operation (its key pack included)
+_TIMED_AS = {"pkm_score_topk_ws": "pkm_score_topk"}
+
 
 
 def call(name: str, *args) -> None:
@@ -363,7 +383,8 @@ def call(name: str, *args) -> None:
     status = getattr(lib, name)(*args)
     if timer is not None:
         end.record()
-        timer.events.append(((name, tuple(args[i] for i in _SIZE_ARGS.get(name, ()))), start, end))
+        key = _TIMED_AS.get(name, name)
+        timer.events.append(((key, tuple(args[i] for i in _SIZE_ARGS.get(name, ()))), start, end))
     if status != 0:
         msg = lib.pkm_last_error_string().decode(errors="replace")
         raise PkmError(name, status, msg)

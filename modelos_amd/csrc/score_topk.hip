@@ -579,7 +579,7 @@ __device__ __forceinline__ void cartesian_rows(const typename Sel<TIN>::Key* l0r
 // ---------------------------------------------------------------------------
 template <typename TIN, int IDW, int TM, int KSC>
 __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
-    const TIN* __restrict__ Q, const TIN* __restrict__ Kt, int64_t Ntok, int H, int n, int half, int knn,
+    const TIN* __restrict__ Q, const TIN* __restrict__ Kt, int kpack, int64_t Ntok, int H, int n, int half, int knn,
     TIN* __restrict__ out_scores, int64_t* __restrict__ out_idx, int64_t* __restrict__ out_i1,
     int64_t* __restrict__ out_i2, TIN* __restrict__ out_s1, TIN* __restrict__ out_s2) {
   typedef Sel<TIN> SL;
@@ -632,8 +632,11 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
   // so the A fragment of a k-step is one lane-invariant offset away from a
   // per-lane base, and the 8 lanes an LDS cycle serves hit distinct banks.
   const int qlane = (lane & 15) * 4 + ((lane >> 4) ^ ((lane >> 2) & 3));
-  // key chunk of lane (column lane & 15, quarter lane >> 4) inside a tile row block
-  const int klane = (lane & 15) * CH + (lane >> 4);
+  // key chunk of lane (column lane & 15, quarter lane >> 4) inside a tile row
+  // block, and the chunk stride of a k-step: row-major keys, or tiles packed
+  // chunk-major by score_keys_pack_kernel (a k-step's operands one contiguous KB)
+  const int klane = kpack ? lane : (lane & 15) * CH + (lane >> 4);
+  const int kss = kpack ? 64 : 4;
   const int ncol = n / 16;
   // this wave's column tiles are w, w + 8, ...; batches of CB of them
   const int ntw = (ncol - w + kWaves - 1) / kWaves;
@@ -721,7 +724,7 @@ __global__ __launch_bounds__(kThreads) void pkm_score_topk_kernel(
       for (int k = 0; k < CB; ++k) {
         const int tile = w + kWaves * (CB * jb + k);
         const int tl = tile < ncol ? tile : 0;
-        b[k] = (Kc4 + (16 * tl * CH + 4 * ks))[klane];
+        b[k] = (Kc4 + (16 * tl * CH + kss * ks))[klane];
       }
     };
     auto load_a = [&](uint4* a, int ks) {
@@ -1625,7 +1628,7 @@ static int launch_cartesian(int64_t Ntok, int H, int n, int knn, int lds_max, vo
 }
 
 template <typename TIN, int IDW, int TM, int KSC>
-static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
+static int launch_score_tm(const void* q, const void* keys, int kpack, int64_t Ntok, int H, int n, int half, int knn,
                            size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
                            int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
   static std::atomic<uint64_t> lds_enabled{0};
@@ -1635,7 +1638,7 @@ static int launch_score_tm(const void* q, const void* keys, int64_t Ntok, int H,
   {
     KernelSpan span("score_topk", st);
     hipLaunchKernelGGL((pkm_score_topk_kernel<TIN, IDW, TM, KSC>), dim3((unsigned)blocks), dim3(kThreads), lds, st,
-                       (const TIN*)q, (const TIN*)keys, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
+                       (const TIN*)q, (const TIN*)keys, kpack, Ntok, H, n, half, knn, (TIN*)out_scores, out_idx, out_i1,
                        out_i2, (TIN*)out_s1, (TIN*)out_s2);
   }
   if constexpr (sizeof(typename Sel<TIN>::Key) == 4) return launch_cartesian<TIN>(Ntok, H, n, knn, lds_max, out_scores, out_idx, st);
@@ -1663,38 +1666,38 @@ static int launch_stream(const void* q, const void* keys, int64_t Ntok, int H, i
 // Kernel variant for (TM, k-steps per half): the k-step counts of the common
 // half key dims (128, 256, 512 elements) are compile-time.
 template <typename TIN, int IDW, int TM>
-static int launch_score_ks(const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
+static int launch_score_ks(const void* q, const void* keys, int kpack, int64_t Ntok, int H, int n, int half, int knn,
                            size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
                            int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
   switch (half / Sel<TIN>::KSTEP) {
     case 4:
-      return launch_score_tm<TIN, IDW, TM, 4>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+      return launch_score_tm<TIN, IDW, TM, 4>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
                                               out_i1, out_i2, out_s1, out_s2, st);
     case 8:
-      return launch_score_tm<TIN, IDW, TM, 8>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+      return launch_score_tm<TIN, IDW, TM, 8>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
                                               out_i1, out_i2, out_s1, out_s2, st);
     case 16:
-      return launch_score_tm<TIN, IDW, TM, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+      return launch_score_tm<TIN, IDW, TM, 16>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
                                                out_i1, out_i2, out_s1, out_s2, st);
     default:
-      return launch_score_tm<TIN, IDW, TM, 0>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
+      return launch_score_tm<TIN, IDW, TM, 0>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx,
                                               out_i1, out_i2, out_s1, out_s2, st);
   }
 }
 
 template <typename TIN, int IDW>
-static int launch_score(int TM, const void* q, const void* keys, int64_t Ntok, int H, int n, int half, int knn,
+static int launch_score(int TM, const void* q, const void* keys, int kpack, int64_t Ntok, int H, int n, int half, int knn,
                         size_t lds, int lds_max, void* out_scores, int64_t* out_idx, int64_t* out_i1,
                         int64_t* out_i2, void* out_s1, void* out_s2, hipStream_t st) {
   switch (TM) {
     case 64:
-      return launch_score_ks<TIN, IDW, 64>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+      return launch_score_ks<TIN, IDW, 64>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
                                            out_i2, out_s1, out_s2, st);
     case 32:
-      return launch_score_ks<TIN, IDW, 32>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+      return launch_score_ks<TIN, IDW, 32>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
                                            out_i2, out_s1, out_s2, st);
     default:
-      return launch_score_ks<TIN, IDW, 16>(q, keys, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
+      return launch_score_ks<TIN, IDW, 16>(q, keys, kpack, Ntok, H, n, half, knn, lds, lds_max, out_scores, out_idx, out_i1,
                                            out_i2, out_s1, out_s2, st);
   }
 }
@@ -1709,10 +1712,27 @@ int score_topk_generic(const void* query, const void* keys, int64_t num_tokens, 
                        int64_t* out_i1, int64_t* out_i2, void* out_s1, void* out_s2, int lds_max, hipStream_t st);
 }
 
-extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_tokens, int64_t heads, int64_t n_keys,
-                              int64_t half, int64_t knn, int score_type, int dtype, void* out_scores,
-                              int64_t* out_indices, int64_t* out_sub_indices1, int64_t* out_sub_indices2,
-                              void* out_sub_scores1, void* out_sub_scores2, void* stream) {
+namespace pkm {
+// Key tiles in the order the tile kernel's k-steps read them: within each
+// block of 16 consecutive keys (a column tile), 16-byte chunk c of the 16 keys
+// becomes contiguous (chunk-major), so the B operands of one k-step are one
+// contiguous KB instead of 64 bytes of 16 rows each. One thread per chunk.
+__global__ __launch_bounds__(256) void score_keys_pack_kernel(const uint4* __restrict__ K, uint4* __restrict__ P,
+                                                              int64_t chunks, int CH) {
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= chunks) return;
+  const int64_t tsz = 16 * (int64_t)CH;
+  const int64_t tile = o / tsz;
+  const int w = (int)(o - tile * tsz);
+  P[o] = K[tile * tsz + (int64_t)(w & 15) * CH + (w >> 4)];
+}
+}  // namespace pkm
+
+static int score_topk_impl(const void* query, const void* keys, int64_t num_tokens, int64_t heads, int64_t n_keys,
+                           int64_t half, int64_t knn, int score_type, int dtype, void* out_scores,
+                           int64_t* out_indices, int64_t* out_sub_indices1, int64_t* out_sub_indices2,
+                           void* out_sub_scores1, void* out_sub_scores2, void* workspace, size_t workspace_bytes,
+                           void* stream) {
   PKM_REQUIRE(dtype == PKM_DTYPE_F32 || dtype == PKM_DTYPE_BF16 || dtype == PKM_DTYPE_F16, PKM_ERR_UNSUPPORTED,
               "pkm_score_topk: dtype %d not supported (float32, bfloat16 and float16 are)", dtype);
   PKM_REQUIRE(score_type == PKM_SCORE_DOT || score_type == PKM_SCORE_IDW, PKM_ERR_INVALID_ARGUMENT,
@@ -1775,23 +1795,58 @@ extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_t
   PKM_REQUIRE(blocks < ((int64_t)1 << 31), PKM_ERR_INVALID_ARGUMENT, "pkm_score_topk: grid too large");
   int rc;
   const int H = (int)heads, n = (int)n_keys, hf = (int)half, k = (int)knn;
+  // with a workspace of the keys' size: the keys packed tile-major first (one
+  // pass over the table), so the kernel's key loads use whole cache lines
+  const size_t key_bytes_all = (size_t)(2 * heads * n_keys) * (size_t)half * (dtype == PKM_DTYPE_BF16 ? 2 : 4);
+  const int kpack = workspace != nullptr && workspace_bytes >= key_bytes_all && (uintptr_t)workspace % 16 == 0;
+  if (kpack) {
+    const int64_t chunks = (int64_t)(key_bytes_all / 16);
+    const int CH = (int)(half * (dtype == PKM_DTYPE_BF16 ? 2 : 4) / 16);
+    hipLaunchKernelGGL(score_keys_pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st,
+                       (const uint4*)keys, (uint4*)workspace, chunks, CH);
+    keys = workspace;
+  }
   if (dtype == PKM_DTYPE_BF16) {
     rc = score_type == PKM_SCORE_DOT
-             ? launch_score<bf16_t, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+             ? launch_score<bf16_t, 0>(TM, query, keys, kpack, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
                                        out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
                                        out_sub_scores2, st)
-             : launch_score<bf16_t, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+             : launch_score<bf16_t, 1>(TM, query, keys, kpack, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
                                        out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
                                        out_sub_scores2, st);
   } else {
     rc = score_type == PKM_SCORE_DOT
-             ? launch_score<float, 0>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+             ? launch_score<float, 0>(TM, query, keys, kpack, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
                                       out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
                                       out_sub_scores2, st)
-             : launch_score<float, 1>(TM, query, keys, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
+             : launch_score<float, 1>(TM, query, keys, kpack, num_tokens, H, n, hf, k, (size_t)lds, lds_max, out_scores,
                                       out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1,
                                       out_sub_scores2, st);
   }
   if (rc != PKM_OK) return rc;
   return pkm_check_launch("pkm_score_topk");
+}
+
+extern "C" int pkm_score_topk(const void* query, const void* keys, int64_t num_tokens, int64_t heads, int64_t n_keys,
+                              int64_t half, int64_t knn, int score_type, int dtype, void* out_scores,
+                              int64_t* out_indices, int64_t* out_sub_indices1, int64_t* out_sub_indices2,
+                              void* out_sub_scores1, void* out_sub_scores2, void* stream) {
+  return score_topk_impl(query, keys, num_tokens, heads, n_keys, half, knn, score_type, dtype, out_scores,
+                         out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, nullptr, 0,
+                         stream);
+}
+
+extern "C" size_t pkm_score_topk_workspace_size(int64_t heads, int64_t n_keys, int64_t half, int dtype) {
+  if (heads < 1 || n_keys < 1 || half < 1) return 0;
+  return (size_t)(2 * heads * n_keys * half) * (dtype == PKM_DTYPE_F32 ? 4 : 2);
+}
+
+extern "C" int pkm_score_topk_ws(const void* query, const void* keys, int64_t num_tokens, int64_t heads,
+                                 int64_t n_keys, int64_t half, int64_t knn, int score_type, int dtype,
+                                 void* out_scores, int64_t* out_indices, int64_t* out_sub_indices1,
+                                 int64_t* out_sub_indices2, void* out_sub_scores1, void* out_sub_scores2,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  return score_topk_impl(query, keys, num_tokens, heads, n_keys, half, knn, score_type, dtype, out_scores,
+                         out_indices, out_sub_indices1, out_sub_indices2, out_sub_scores1, out_sub_scores2, workspace,
+                         workspace_bytes, stream);
 }

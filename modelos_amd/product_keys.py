@@ -111,12 +111,14 @@ def score_topk(
         i2 = torch.empty((N, heads, knn), dtype=torch.long, device=dev)
         s1 = torch.empty((N, heads, n), dtype=dt, device=dev)
         s2 = torch.empty((N, heads, n), dtype=dt, device=dev)
+    # workspace for the keys packed tile-major (taken by the tile kernel only)
+    ws = torch.empty(keys.numel() * keys.element_size(), dtype=torch.uint8, device=dev)
     _lib.call(
-        "pkm_score_topk",
+        "pkm_score_topk_ws",
         _lib.ptr(query), _lib.ptr(keys), N, heads, n, half, knn,
         _lib.SCORE_CODES[score_type], _lib.dtype_code(query),
         _lib.ptr(scores), _lib.ptr(indices), _lib.ptr(i1), _lib.ptr(i2), _lib.ptr(s1), _lib.ptr(s2),
-        _lib.stream_of(dev),
+        _lib.ptr(ws), ws.numel(), _lib.stream_of(dev),
     )
     if sub_outputs:
         return scores, indices, i1, i2, s1, s2
